@@ -1,0 +1,305 @@
+"""ctypes binding of libming_hip.so (include/ming_hip.h) for tests and benches.
+
+The product is the C ABI; this module only declares its structs and
+functions and converts torch device tensors into `ming_tensor` views.  It
+raises when the library is missing: there is no fallback path.
+
+Mirrors of the reference interface (sbusso/ming-tts-serve):
+  Context.lm_layer      <- ming_fused.lmLayer      src/ming_fused.zig:597
+  LmModel               <- QStack.fuse/decodeFused src/ming_model.zig:510-544
+  Context.qgemv         <- mlx_quantized_matmul    src/mlx.zig:279
+  Context.quantize      <- mlx_quantize            src/mlx.zig:292
+  Context.dequantize    <- mlx_dequantize          src/mlx.zig:288
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libming_hip.so")
+
+MING_OK = 0
+MING_E_SHAPE = 1
+MING_E_CTX_OVER_CAPACITY = 2
+MING_E_HIP = 3
+MING_E_NOT_INIT = 4
+MING_E_ARG = 5
+MING_E_UNSUPPORTED = 6
+MING_E_TIMEOUT = 7
+
+DT_BF16, DT_F32, DT_U32, DT_I32 = 1, 2, 3, 4
+W_BF16, W_AFFINE = 0, 1
+LM_AUTO, LM_KERNELS, LM_PERSISTENT = 0, 1, 2
+
+c_void_p = ctypes.c_void_p
+c_i32 = ctypes.c_int32
+c_i64 = ctypes.c_int64
+c_f32 = ctypes.c_float
+
+
+class Tensor(ctypes.Structure):
+    _fields_ = [("data", c_void_p), ("dtype", c_i32), ("ndim", c_i32), ("shape", c_i64 * 4)]
+
+
+class Linear(ctypes.Structure):
+    _fields_ = [
+        ("kind", c_i32), ("out_features", c_i32), ("in_features", c_i32), ("group_size", c_i32),
+        ("bits", c_i32), ("global_scale", c_f32), ("w", c_void_p), ("scales", c_void_p), ("biases", c_void_p),
+    ]
+
+
+class LmCfg(ctypes.Structure):
+    _fields_ = [
+        ("hidden", c_i32), ("heads", c_i32), ("kv_heads", c_i32), ("head_dim", c_i32), ("inter", c_i32),
+        ("vocab", c_i32), ("n_layers", c_i32), ("eps", c_f32), ("log2_theta", c_f32),
+    ]
+
+
+class LmLayerW(ctypes.Structure):
+    _fields_ = [("ln1", c_void_p), ("ln2", c_void_p)] + [
+        (n, Linear) for n in ("wq", "wk", "wv", "wo", "wg", "wu", "wd")
+    ] + [("bq", c_void_p), ("bk", c_void_p), ("bv", c_void_p)]
+
+
+class Kv(ctypes.Structure):
+    _fields_ = [
+        ("k", c_void_p), ("v", c_void_p), ("n_layers", c_i32), ("kv_heads", c_i32), ("head_dim", c_i32),
+        ("capacity", c_i32), ("len", c_i32),
+    ]
+
+
+class LmOut(ctypes.Structure):
+    _fields_ = [("qkv", c_void_p), ("o", c_void_p), ("x1", c_void_p), ("hh", c_void_p), ("x2", c_void_p)]
+
+
+_lib = None
+
+
+def lib():
+    """Load libming_hip.so once (raises OSError if it is not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise OSError(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+    L = ctypes.CDLL(LIB_PATH)
+    P = ctypes.POINTER
+    sig = {
+        "ming_ctx_create": (c_i32, [P(c_void_p), c_i32]),
+        "ming_ctx_destroy": (c_i32, [c_void_p]),
+        "ming_ctx_set_stream": (c_i32, [c_void_p, c_void_p]),
+        "ming_ctx_stream": (c_void_p, [c_void_p]),
+        "ming_sync": (c_i32, [c_void_p]),
+        "ming_last_error": (ctypes.c_char_p, [c_void_p]),
+        "ming_status_str": (ctypes.c_char_p, [c_i32]),
+        "ming_fused_enabled": (c_i32, []),
+        "ming_dit_enabled": (c_i32, []),
+        "ming_lm_enabled": (c_i32, []),
+        "ming_set_force_off": (None, [c_i32]),
+        "ming_malloc": (c_i32, [c_void_p, ctypes.c_size_t, P(c_void_p)]),
+        "ming_free": (c_i32, [c_void_p, c_void_p]),
+        "ming_memcpy_htod": (c_i32, [c_void_p, c_void_p, c_void_p, ctypes.c_size_t]),
+        "ming_memcpy_dtoh": (c_i32, [c_void_p, c_void_p, c_void_p, ctypes.c_size_t]),
+        "ming_memset": (c_i32, [c_void_p, c_void_p, c_i32, ctypes.c_size_t]),
+        "ming_qgemv": (c_i32, [c_void_p, P(Tensor), P(Tensor), P(Tensor), P(Tensor), c_f32, c_i32, c_i32, P(Tensor)]),
+        "ming_qgemv_f32": (c_i32, [c_void_p, P(Tensor), P(Tensor), P(Tensor), P(Tensor), c_f32, c_i32, c_i32,
+                                   P(Tensor)]),
+        "ming_dequantize": (c_i32, [c_void_p, P(Tensor), P(Tensor), P(Tensor), c_i32, c_i32, c_f32, P(Tensor)]),
+        "ming_quantize": (c_i32, [c_void_p, P(Tensor), c_i32, c_i32, P(Tensor), P(Tensor), P(Tensor)]),
+        "ming_lm_layer": (c_i32, [c_void_p, P(LmCfg), P(LmLayerW), c_void_p, c_i32, P(Kv), c_i32, P(LmOut)]),
+        "ming_lm_model_create": (c_i32, [c_void_p, P(LmCfg), P(LmLayerW), c_void_p, P(Linear), P(Linear),
+                                         P(c_void_p)]),
+        "ming_lm_model_destroy": (c_i32, [c_void_p]),
+        "ming_lm_model_set_mode": (c_i32, [c_void_p, c_i32]),
+        "ming_lm_step": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, P(Kv), c_void_p, c_void_p, c_void_p]),
+        "ming_lm_generate": (c_i32, [c_void_p, c_void_p, P(Kv), c_i32, c_void_p]),
+        "ming_lm_model_trace": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+        "ming_synth_stream": (ctypes.c_uint64, [ctypes.c_uint64, ctypes.c_char_p]),
+        "ming_synth_normal_bf16": (None, [ctypes.c_uint64, c_f32, c_f32, c_void_p, ctypes.c_size_t, c_i32]),
+        "ming_synth_uniform_i32": (None, [ctypes.c_uint64, c_i32, c_void_p, ctypes.c_size_t]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = L
+    return L
+
+
+def exported_symbols():
+    """Names of every function the ctypes table declares (all must resolve)."""
+    lib()
+    return [n for n in dir(_lib) if n.startswith("ming_")]
+
+
+class MingError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__(f"{lib().ming_status_str(status).decode()} ({status}): {msg}")
+        self.status = status
+
+
+# ---- torch helpers ----------------------------------------------------------
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def tensor(t, dtype=None):
+    """ming_tensor view of a contiguous torch tensor (u32 data travel as int32)."""
+    torch = _torch()
+    assert t.is_contiguous(), "ming tensors are row-major contiguous"
+    if dtype is None:
+        dtype = {torch.bfloat16: DT_BF16, torch.float32: DT_F32, torch.int32: DT_I32}[t.dtype]
+    shape = list(t.shape)
+    assert len(shape) <= 4
+    return Tensor(t.data_ptr(), dtype, len(shape), (c_i64 * 4)(*(shape + [0] * (4 - len(shape)))))
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def linear(w, scales=None, biases=None, global_scale=1.0, out_features=None, in_features=None):
+    """ming_linear from torch tensors: bf16 [N,K] or affine (int32 [N,K/8], bf16 scales/biases)."""
+    if scales is None:
+        n, k = w.shape
+        return Linear(W_BF16, n, k, 0, 0, 1.0, w.data_ptr(), None, None)
+    n = w.shape[0]
+    k = w.shape[1] * 8
+    return Linear(W_AFFINE, out_features or n, in_features or k, 64, 4, float(global_scale), w.data_ptr(),
+                  scales.data_ptr(), biases.data_ptr())
+
+
+class Context:
+    """A ming_ctx bound to torch's current stream on `device`."""
+
+    def __init__(self, device=0, use_torch_stream=True):
+        L = lib()
+        h = c_void_p()
+        st = L.ming_ctx_create(ctypes.byref(h), device)
+        if st:
+            raise MingError(st, "ming_ctx_create failed")
+        self.h = h
+        self.L = L
+        if use_torch_stream:
+            torch = _torch()
+            self.set_stream(torch.cuda.current_stream(device).cuda_stream)
+
+    def close(self):
+        if self.h:
+            self.L.ming_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def check(self, st):
+        if st:
+            raise MingError(st, self.L.ming_last_error(self.h).decode())
+
+    def set_stream(self, s):
+        self.check(self.L.ming_ctx_set_stream(self.h, c_void_p(s)))
+
+    def sync(self):
+        self.check(self.L.ming_sync(self.h))
+
+    # ---- MLX-affine linear algebra ----
+    def qgemv(self, x, w, scales, biases, y, global_scale=1.0, f32=False):
+        f = self.L.ming_qgemv_f32 if f32 else self.L.ming_qgemv
+        tx, tw, ts, tb, ty = tensor(x), tensor(w, DT_U32), tensor(scales), tensor(biases), tensor(y)
+        self.check(f(self.h, ctypes.byref(tx), ctypes.byref(tw), ctypes.byref(ts), ctypes.byref(tb),
+                     float(global_scale), 64, 4, ctypes.byref(ty)))
+
+    def quantize(self, w, wq, scales, biases):
+        tw, tq, ts, tb = tensor(w), tensor(wq, DT_U32), tensor(scales), tensor(biases)
+        self.check(self.L.ming_quantize(self.h, ctypes.byref(tw), 64, 4, ctypes.byref(tq), ctypes.byref(ts),
+                                        ctypes.byref(tb)))
+
+    def dequantize(self, wq, scales, biases, out, global_scale=1.0):
+        tq, ts, tb, to = tensor(wq, DT_U32), tensor(scales), tensor(biases), tensor(out)
+        self.check(self.L.ming_dequantize(self.h, ctypes.byref(tq), ctypes.byref(ts), ctypes.byref(tb), 64, 4,
+                                          float(global_scale), ctypes.byref(to)))
+
+    # ---- Qwen2 decode ----
+    def lm_layer(self, cfg, layer_w, x, pos, kv, layer, out):
+        self.check(self.L.ming_lm_layer(self.h, ctypes.byref(cfg), ctypes.byref(layer_w), ptr(x), int(pos),
+                                        ctypes.byref(kv), int(layer), ctypes.byref(out)))
+
+
+class LmModel:
+    """ming_lm_model: prepared decode stack (QStack.fuse)."""
+
+    def __init__(self, ctx, cfg, layers, final_norm, head, embed):
+        self.ctx = ctx
+        self.cfg = cfg
+        self._layers = (LmLayerW * len(layers))(*layers)
+        self._head = head
+        self._embed = embed
+        h = c_void_p()
+        ctx.check(ctx.L.ming_lm_model_create(ctx.h, ctypes.byref(cfg), self._layers, ptr(final_norm),
+                                             ctypes.byref(head), ctypes.byref(embed), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.ctx.L.ming_lm_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_mode(self, mode):
+        self.ctx.check(self.ctx.L.ming_lm_model_set_mode(self.h, int(mode)))
+
+    def step(self, kv, token=None, x_in=None, hidden=None, logits=None, argmax=None):
+        self.ctx.check(self.ctx.L.ming_lm_step(self.ctx.h, self.h, ptr(token), ptr(x_in), ctypes.byref(kv),
+                                               ptr(hidden), ptr(logits), ptr(argmax)))
+
+    def trace(self):
+        """dict of per-layer activations of the last step (torch bf16 device tensors)."""
+        torch = _torch()
+        c = self.cfg
+        H, L, nq = c.hidden, c.n_layers, c.hidden + 2 * c.kv_heads * c.head_dim
+        t = dict(x=torch.empty((L + 1, H), dtype=torch.bfloat16, device="cuda"),
+                 x1=torch.empty((L, H), dtype=torch.bfloat16, device="cuda"),
+                 att=torch.empty((L, H), dtype=torch.bfloat16, device="cuda"),
+                 qkv=torch.empty((L, nq), dtype=torch.bfloat16, device="cuda"),
+                 hh=torch.empty((L, c.inter), dtype=torch.bfloat16, device="cuda"))
+        self.ctx.check(self.ctx.L.ming_lm_model_trace(self.h, *(ptr(t[k]) for k in ("x", "x1", "att", "qkv", "hh"))))
+        return t
+
+    def generate(self, kv, n_steps, tokens):
+        self.ctx.check(self.ctx.L.ming_lm_generate(self.ctx.h, self.h, ctypes.byref(kv), int(n_steps), ptr(tokens)))
+
+
+# ---- synthetic inputs ---------------------------------------------------------
+
+
+def synth_stream(seed, name):
+    return lib().ming_synth_stream(int(seed), name.encode())
+
+
+def synth_normal_bf16(seed, name, n, mean=0.0, std=1.0, threads=None):
+    """numpy uint16 (bf16 bits) [n] of bf16(mean + std * N(0,1))."""
+    import numpy as np
+
+    out = np.empty(int(n), dtype=np.uint16)
+    lib().ming_synth_normal_bf16(synth_stream(seed, name), float(mean), float(std),
+                                 out.ctypes.data_as(c_void_p), out.size, int(threads or min(16, os.cpu_count() or 1)))
+    return out
+
+
+def synth_uniform_i32(seed, name, n, hi):
+    import numpy as np
+
+    out = np.empty(int(n), dtype=np.int32)
+    lib().ming_synth_uniform_i32(synth_stream(seed, name), int(hi), out.ctypes.data_as(c_void_p), out.size)
+    return out

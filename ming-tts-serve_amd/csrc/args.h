@@ -1,0 +1,64 @@
+// Plain argument blocks shared by the host glue and the kernels (no device
+// code, so host-only translation units can include it).
+#pragma once
+
+#include <stdint.h>
+
+namespace ming {
+
+// Weights of one linear as the kernels see them.
+struct LinearDev {
+    int32_t kind;  // 0 bf16, 1 affine 4-bit / group 64
+    int32_t N, K;
+    float gscale;
+    const uint32_t* w;   // affine: u32 [N, K/8]; bf16: bf16 [N, K] viewed as u32 pairs
+    const uint16_t* s;   // bf16 [N, K/64]
+    const uint16_t* b;   // bf16 [N, K/64]
+};
+
+// fused.LmLayer (src/ming_fused.zig:576-589) as the kernels see it.
+struct LayerDev {
+    const uint16_t *ln1, *ln2;
+    LinearDev q, k, v, o, g, u, d;
+    const uint16_t *bq, *bk, *bv;
+};
+
+// Everything one decode step touches.  Activations of every layer are kept
+// (x[l] is layer l's input, x[n_layers] the stack output), which also lets
+// tests read any intermediate.
+struct StepArgs {
+    const LayerDev* layers;   // device array [n_layers] (persistent schedule)
+    int n_layers, H, heads, kvh, hd, I;
+    float eps, log2_theta;
+    const uint16_t* final_norm;
+    LinearDev head;           // tied LM head [V, H]
+    LinearDev embed;          // embedding table [V, H]
+    uint16_t* kc;             // [n_layers][kvh][cap][hd]
+    uint16_t* vc;
+    int cap;
+    int pos;                  // position of this token (= cached length before the step)
+    const int32_t* token_in;  // device id, or null: x[0] already holds the input row
+    int32_t* argmax_out;      // device i32, or null
+    // Activations of layer l: input x + l*sx, output xo + l*sx, x1 + l*sx,
+    // att + l*sx, qkv + l*sq, hh + l*sh.  The stack uses one buffer per layer
+    // (xo = x + H, so x[l + 1] is layer l's output); a single-layer call
+    // passes caller buffers with zero strides.
+    uint16_t* x;
+    uint16_t* xo;
+    uint16_t* x1;
+    uint16_t* att;
+    uint16_t* qkv;
+    uint16_t* hh;
+    int64_t sx, sq, sh;
+    float* part;              // attention partials [kvh][nsplit][grp][hd + 2]
+    int split_len;            // positions per attention split (multiple of 64)
+    uint16_t* hidden;         // [H] final-normed hidden (bf16)
+    float* logits;            // [V] f32, or null
+    float* amax_v;            // [kMaxParts] argmax partials
+    int32_t* amax_i;
+    int32_t* flags;           // [0] error flag, [1] grid barrier counter
+};
+
+constexpr int kMaxParts = 4096;
+
+}  // namespace ming

@@ -1,0 +1,116 @@
+// Device helpers shared by the gfx950 kernels: bf16 rounding, the MLX-affine
+// 4-bit unpack into bf16 pairs, wave reductions, and bounded spin waits.
+//
+// Numerics: storage is bf16, accumulation f32, and values are rounded to bf16
+// (round to nearest even) at the points where the reference's MLX graph
+// materialises a bf16 array (src/ming_fused.zig:17-25).  The library is built
+// with -ffp-contract=off, so an expression rounds exactly as written; fused
+// multiply-adds appear only where a kernel calls fmaf() or a dot builtin.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ming {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// ---- bf16 -----------------------------------------------------------------
+
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// f32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float rb(float f) { return bf2f(f2bf(f)); }
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+// acc + a.lo*b.lo + a.hi*b.hi with bf16 pairs packed in u32 (v_dot2c_f32_bf16).
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), acc,
+                                           false);
+}
+
+// ---- MLX affine 4-bit unpack ------------------------------------------------
+// A u32 word holds 8 nibbles, element 8j+i in bits [4i, 4i+4) (low first).
+// OR-ing a nibble q into the mantissa of bf16(128) gives bf16(128 + q)
+// exactly, so one v_and_or_b32 turns two nibbles into a bf16 pair.  The pairs
+// are (q0,q4), (q1,q5), (q2,q6), (q3,q7); the activation vector is staged in
+// the same pair order, and the +128 offset is removed in the group epilogue:
+//   sum_k (s q_k + b) x_k = s * sum_k (128 + q_k) x_k + (b - 128 s) * sum_k x_k.
+constexpr uint32_t kQ4Magic = 0x43004300u;  // bf16(128) | bf16(128) << 16
+
+__device__ __forceinline__ void q4_pairs(uint32_t w, uint32_t& p0, uint32_t& p1, uint32_t& p2, uint32_t& p3) {
+    p0 = (w & 0x000f000fu) | kQ4Magic;
+    p1 = ((w >> 4) & 0x000f000fu) | kQ4Magic;
+    p2 = ((w >> 8) & 0x000f000fu) | kQ4Magic;
+    p3 = ((w >> 12) & 0x000f000fu) | kQ4Magic;
+}
+
+// Dot product of one 8-element word of nibbles with the pair-ordered
+// activations xp[0..3] = (x0,x4),(x1,x5),(x2,x6),(x3,x7).
+__device__ __forceinline__ float q4_word_dot(uint32_t w, const uint32_t* xp, float acc) {
+    uint32_t p0, p1, p2, p3;
+    q4_pairs(w, p0, p1, p2, p3);
+    acc = dot2(p0, xp[0], acc);
+    acc = dot2(p1, xp[1], acc);
+    acc = dot2(p2, xp[2], acc);
+    acc = dot2(p3, xp[3], acc);
+    return acc;
+}
+
+// ---- reductions -------------------------------------------------------------
+
+template <int W>
+__device__ __forceinline__ float team_sum(float v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+template <int W>
+__device__ __forceinline__ float team_max(float v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// Block-wide sum over blockDim.x threads (multiple of 64); `red` holds one
+// float per wave.  All threads get the result.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = team_sum<kWave>(v);
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, nw = blockDim.x / kWave;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int i = 0; i < nw; i++) s += red[i];
+    return s;
+}
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = team_max<kWave>(v);
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, nw = blockDim.x / kWave;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = -INFINITY;
+    for (int i = 0; i < nw; i++) s = fmaxf(s, red[i]);
+    return s;
+}
+
+// ---- loads ------------------------------------------------------------------
+
+__device__ __forceinline__ uint4 ldg4(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+}  // namespace ming

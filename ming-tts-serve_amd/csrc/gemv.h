@@ -1,0 +1,128 @@
+// Batch-1 (and few-row) GEMV building blocks for gfx950.
+//
+// The activation vector is staged once per workgroup in LDS; a "team" of T
+// lanes (32 or 64) owns one weight row and walks it in 16-byte chunks, so a
+// team's loads of a row are contiguous and one wave instruction covers
+// 64 x 16 B.  Partial sums stay in f32 and meet with a team reduction.
+//
+// MLX-affine 4-bit rows: a 16 B chunk is 4 u32 words = 32 nibbles = half a
+// quantization group of 64.  The staged activations are bf16 pairs in nibble
+// pair order (see q4_pairs) laid out [word j][chunk c][pair p] so that the
+// lanes of one ds_read_b128 hit consecutive 16 B (no LDS bank conflicts), and
+// xh[c] holds the f32 sum of chunk c's 32 activations for the +128 offset
+// correction and the bias term.
+//
+// bf16 rows: a 16 B chunk is 8 weights, dotted with the activations in their
+// natural pair order with v_dot2c_f32_bf16.
+#pragma once
+
+#include "args.h"
+#include "common.h"
+
+namespace ming {
+
+// LDS image of one activation vector of K elements (K % 64 == 0).
+struct XStage {
+    uint32_t* xs;  // K/2 u32
+    float* xh;     // K/32 f32 (affine only)
+};
+
+__host__ __device__ constexpr int xstage_words(int K) { return K / 2 + K / 32; }
+
+// Stage bf16 x [K] (global or LDS) for an affine matrix.  All threads of the
+// block participate; ends with __syncthreads().
+__device__ __forceinline__ void stage_q4(const uint16_t* x, int K, XStage st) {
+    const int NC = K / 32, nw = K / 8;
+    for (int wi = threadIdx.x; wi < nw; wi += blockDim.x) {
+        const int c = wi >> 2, j = wi & 3;
+        const uint4 v = *reinterpret_cast<const uint4*>(x + 8 * wi);
+        // v holds x[8wi+0..7] as pairs (0,1),(2,3),(4,5),(6,7); build (0,4),(1,5),(2,6),(3,7).
+        uint4 o;
+        o.x = (v.x & 0xffffu) | (v.z << 16);
+        o.y = (v.x >> 16) | (v.z & 0xffff0000u);
+        o.z = (v.y & 0xffffu) | (v.w << 16);
+        o.w = (v.y >> 16) | (v.w & 0xffff0000u);
+        *reinterpret_cast<uint4*>(st.xs + (j * NC + c) * 4) = o;
+    }
+    // chunk sums: thread per chunk, in element order
+    for (int c = threadIdx.x; c < NC; c += blockDim.x) {
+        float s = 0.0f;
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + 32 * c);
+        for (int i = 0; i < 16; i++) {
+            const uint32_t u = p[i];
+            s += bf_lo(u);
+            s += bf_hi(u);
+        }
+        st.xh[c] = s;
+    }
+    __syncthreads();
+}
+
+// Stage bf16 x [K] for a bf16 matrix (natural order).
+__device__ __forceinline__ void stage_bf16(const uint16_t* x, int K, XStage st) {
+    for (int i = threadIdx.x; i < K / 8; i += blockDim.x)
+        reinterpret_cast<uint4*>(st.xs)[i] = reinterpret_cast<const uint4*>(x)[i];
+    __syncthreads();
+}
+
+__device__ __forceinline__ void stage_x(const LinearDev& L, const uint16_t* x, XStage st) {
+    if (L.kind == 1)
+        stage_q4(x, L.K, st);
+    else
+        stage_bf16(x, L.K, st);
+}
+
+// Partial dot of affine row n over the chunks c = tl, tl+T, ... (no team
+// reduction; the caller reduces).  Global scale not applied.
+template <int T>
+__device__ __forceinline__ float q4_row_partial(const LinearDev& L, int n, const XStage& st, int tl) {
+    const int NC = L.K / 32, G = L.K / 64;
+    const uint32_t* wrow = L.w + (size_t)n * (L.K / 8);
+    const uint16_t* srow = L.s + (size_t)n * G;
+    const uint16_t* brow = L.b + (size_t)n * G;
+    float acc = 0.0f;
+    for (int c = tl; c < NC; c += T) {
+        const uint4 w = ldg4(wrow + 4 * c);
+        const float s = bf2f(srow[c >> 1]), b = bf2f(brow[c >> 1]);
+        const uint4 x0 = *reinterpret_cast<const uint4*>(st.xs + (0 * NC + c) * 4);
+        const uint4 x1 = *reinterpret_cast<const uint4*>(st.xs + (1 * NC + c) * 4);
+        const uint4 x2 = *reinterpret_cast<const uint4*>(st.xs + (2 * NC + c) * 4);
+        const uint4 x3 = *reinterpret_cast<const uint4*>(st.xs + (3 * NC + c) * 4);
+        float a0 = q4_word_dot(w.x, reinterpret_cast<const uint32_t*>(&x0), 0.0f);
+        float a1 = q4_word_dot(w.y, reinterpret_cast<const uint32_t*>(&x1), 0.0f);
+        a0 = q4_word_dot(w.z, reinterpret_cast<const uint32_t*>(&x2), a0);
+        a1 = q4_word_dot(w.w, reinterpret_cast<const uint32_t*>(&x3), a1);
+        const float a = a0 + a1;
+        acc = fmaf(s, a, acc);
+        acc = fmaf(b - 128.0f * s, st.xh[c], acc);
+    }
+    return acc;
+}
+
+// Partial dot of bf16 row n over 16 B chunks c = tl, tl+T, ...
+template <int T>
+__device__ __forceinline__ float bf16_row_partial(const LinearDev& L, int n, const XStage& st, int tl) {
+    const int NC = L.K / 8;
+    const uint32_t* wrow = L.w + (size_t)n * (L.K / 2);
+    float a0 = 0.0f, a1 = 0.0f;
+    for (int c = tl; c < NC; c += T) {
+        const uint4 w = ldg4(wrow + 4 * c);
+        const uint4 x = *reinterpret_cast<const uint4*>(st.xs + 4 * c);
+        a0 = dot2(w.x, x.x, a0);
+        a1 = dot2(w.y, x.y, a1);
+        a0 = dot2(w.z, x.z, a0);
+        a1 = dot2(w.w, x.w, a1);
+    }
+    return a0 + a1;
+}
+
+// Full row dot (team-reduced, global scale applied): every lane of the team
+// gets the f32 accumulator of row n.
+template <int T>
+__device__ __forceinline__ float row_dot(const LinearDev& L, int n, const XStage& st, int tl) {
+    float a = L.kind == 1 ? q4_row_partial<T>(L, n, st, tl) : bf16_row_partial<T>(L, n, st, tl);
+    a = team_sum<T>(a);
+    return L.kind == 1 ? a * L.gscale : a;
+}
+
+}  // namespace ming

@@ -1,0 +1,163 @@
+// Standalone MLX-affine kernels: quantized GEMV (mlx_quantized_matmul with
+// transpose_w=true, src/mlx.zig:279), dequantize (src/mlx.zig:288) and
+// quantize (src/mlx.zig:292).  4-bit values, groups of 64, bf16 scales and
+// biases, and the f32 global scale of the reference's mlx-c patch
+// (patches/mlxc-gather-qmm-global-scale.patch:10-18).
+#include "gemv.h"
+#include "internal.h"
+
+namespace ming {
+
+namespace {
+
+constexpr int kBlock = 256;
+
+// y[m, n] for M activation rows.  Each wave owns 64/T rows at a time; the grid
+// strides over rows so that the LDS staging is amortised on large N.
+template <int T>
+__global__ __launch_bounds__(kBlock) void qgemv_kernel(int M, const uint16_t* __restrict__ x, LinearDev L,
+                                                       uint16_t* __restrict__ y_bf16, float* __restrict__ y_f32) {
+    extern __shared__ uint32_t smem[];
+    XStage st{smem, reinterpret_cast<float*>(smem + L.K / 2)};
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int team = lane / T, tl = lane % T;
+    constexpr int kRowsPerWave = kWave / T;
+    const int waves_total = gridDim.x * (kBlock / kWave);
+    for (int m = 0; m < M; m++) {
+        stage_x(L, x + (size_t)m * L.K, st);
+        for (int r0 = (blockIdx.x * (kBlock / kWave) + wave) * kRowsPerWave; r0 < L.N;
+             r0 += waves_total * kRowsPerWave) {
+            const int n = r0 + team;
+            const bool ok = n < L.N;
+            const float a = row_dot<T>(L, ok ? n : r0, st, tl);
+            if (ok && tl == 0) {
+                if (y_f32) y_f32[(size_t)m * L.N + n] = a;
+                if (y_bf16) y_bf16[(size_t)m * L.N + n] = f2bf(a);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// One thread per u32 word (8 values): bf16(g * (s*q + b)).
+__global__ void dequantize_kernel(const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
+                                  const uint16_t* __restrict__ b, int64_t N, int64_t K, float g,
+                                  uint16_t* __restrict__ out) {
+    const int64_t nw = N * (K / 8);
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nw; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t n = i / (K / 8), kw = i % (K / 8);
+        const int64_t gi = n * (K / 64) + kw / 8;
+        const float sc = bf2f(s[gi]), bi = bf2f(b[gi]);
+        const uint32_t word = w[i];
+        uint32_t o[4];
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            float v0 = sc * (float)((word >> (8 * p)) & 0xfu) + bi;
+            float v1 = sc * (float)((word >> (8 * p + 4)) & 0xfu) + bi;
+            if (g != 1.0f) {
+                v0 *= g;
+                v1 *= g;
+            }
+            o[p] = pack_bf2(v0, v1);
+        }
+        *reinterpret_cast<uint4*>(out + 8 * i) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+// One thread per group of 64: the MLX affine quantizer (min/max, edge
+// snapped so that zero is exact, rint, clamp), all in f32 with correctly
+// rounded division, as the CPU algorithm it restates.
+__global__ void quantize_kernel(const uint16_t* __restrict__ w, int64_t N, int64_t K, uint32_t* __restrict__ wq,
+                                uint16_t* __restrict__ s, uint16_t* __restrict__ b) {
+    const int64_t ng = N * (K / 64);
+    const float n_bins = 15.0f, eps = 1e-7f;
+    for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < ng; gi += (int64_t)gridDim.x * blockDim.x) {
+        const uint4* src = reinterpret_cast<const uint4*>(w + gi * 64);
+        uint32_t v[32];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint4 u = src[i];
+            v[4 * i] = u.x;
+            v[4 * i + 1] = u.y;
+            v[4 * i + 2] = u.z;
+            v[4 * i + 3] = u.w;
+        }
+        float wmin = INFINITY, wmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const float a = bf_lo(v[i]), c = bf_hi(v[i]);
+            wmax = fmaxf(wmax, fmaxf(a, c));
+            wmin = fminf(wmin, fminf(a, c));
+        }
+        const bool mask = fabsf(wmin) > fabsf(wmax);
+        float scale = fmaxf((wmax - wmin) / n_bins, eps);
+        scale = mask ? scale : -scale;
+        const float edge = mask ? wmin : wmax;
+        const float q0 = rintf(edge / scale);
+        float bias = 0.0f;
+        if (q0 != 0.0f) {
+            scale = edge / q0;
+            bias = edge;
+        }
+        uint32_t out[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int e = 8 * j + k;
+                const float x = (e & 1) ? bf_hi(v[e >> 1]) : bf_lo(v[e >> 1]);
+                float q = rintf((x - bias) / scale);
+                q = fminf(fmaxf(q, 0.0f), n_bins);
+                word |= (uint32_t)q << (4 * k);
+            }
+            out[j] = word;
+        }
+        uint4* dst = reinterpret_cast<uint4*>(wq + gi * 8);
+        dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
+        dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
+        s[gi] = f2bf(scale);
+        b[gi] = f2bf(bias);
+    }
+}
+
+int grid_for(int64_t items, int per_block, int cap) {
+    int64_t g = (items + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return (int)g;
+}
+
+}  // namespace
+
+hipError_t launch_qgemv(hipStream_t st, int M, const uint16_t* x, const uint32_t* w, const uint16_t* s,
+                        const uint16_t* b, int N, int K, float gscale, uint16_t* y_bf16, float* y_f32) {
+    LinearDev L{1, N, K, gscale, w, s, b};
+    const size_t lds = sizeof(uint32_t) * xstage_words(K);
+    if (K / 32 <= 32) {
+        const int rows_per_block = (kBlock / kWave) * 2;
+        hipLaunchKernelGGL(qgemv_kernel<32>, dim3(grid_for(N, rows_per_block, 4096)), dim3(kBlock), lds, st, M, x,
+                           L, y_bf16, y_f32);
+    } else {
+        const int rows_per_block = kBlock / kWave;
+        hipLaunchKernelGGL(qgemv_kernel<64>, dim3(grid_for(N, rows_per_block, 4096)), dim3(kBlock), lds, st, M, x,
+                           L, y_bf16, y_f32);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_dequantize(hipStream_t st, const uint32_t* w, const uint16_t* s, const uint16_t* b, int64_t N,
+                             int64_t K, float gscale, uint16_t* out) {
+    hipLaunchKernelGGL(dequantize_kernel, dim3(grid_for(N * (K / 8), 256, 65536)), dim3(256), 0, st, w, s, b, N, K,
+                       gscale, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize(hipStream_t st, const uint16_t* w, int64_t N, int64_t K, uint32_t* wq, uint16_t* s,
+                           uint16_t* b) {
+    hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(N * (K / 64), 256, 65536)), dim3(256), 0, st, w, N, K, wq, s,
+                       b);
+    return hipGetLastError();
+}
+
+}  // namespace ming

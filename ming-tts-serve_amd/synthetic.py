@@ -1,0 +1,202 @@
+"""Synthetic random-init Qwen2 decode stacks for benches and tests.
+
+Weights are bf16(N(0, std)) from the library's counter-based generator
+(ming_synth_normal_bf16), one stream per tensor name (seed, name), with the
+reference checkpoint's key names (src/ming_model.zig:550-561, :938).  RMSNorm
+weights are 1.0 + N(0, norm_std) (1.0 exactly when norm_std == 0, the
+HF init).  With quant=True every linear is quantized on the GPU to MLX affine
+4-bit / group 64 (ming_quantize); the embedding table doubles as the tied LM
+head (Qwen2-0.5B convention).
+"""
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import (Context, Kv, Linear, LmCfg, LmLayerW, LmModel, W_AFFINE, W_BF16, linear, synth_normal_bf16)
+
+
+@dataclass
+class LmSpec:
+    hidden: int = 896
+    heads: int = 14
+    kv_heads: int = 2
+    head_dim: int = 64
+    inter: int = 4864
+    vocab: int = 151936
+    n_layers: int = 24
+    eps: float = 1e-6
+    theta: float = 1e6
+
+    @property
+    def kvd(self):
+        return self.kv_heads * self.head_dim
+
+    def cfg(self):
+        return LmCfg(self.hidden, self.heads, self.kv_heads, self.head_dim, self.inter, self.vocab, self.n_layers,
+                     self.eps, float(np.log2(np.float32(self.theta))))
+
+    def weight_bytes_q4(self):
+        """Bytes of all 4-bit linears incl. the tied head (0.5625 B/param)."""
+        H, I, kvd = self.hidden, self.inter, self.kvd
+        per_layer = H * H * 2 + 2 * kvd * H + 3 * H * I
+        return int((per_layer * self.n_layers + self.vocab * H) * 0.5625)
+
+
+QWEN2_05B = LmSpec()
+
+
+def _to_dev(arr_u16, shape, device):
+    import torch
+
+    t = torch.from_numpy(arr_u16.view(np.int16).reshape(shape))
+    return t.to(device).view(torch.bfloat16)
+
+
+class SyntheticLm:
+    """Device weights of a Qwen2 stack plus the C-ABI views of them."""
+
+    def __init__(self, ctx: Context, spec: LmSpec, seed=0, quant=True, std=0.02, norm_std=0.0, device="cuda",
+                 threads=None):
+        import torch
+
+        self.ctx, self.spec, self.seed, self.quant, self.device = ctx, spec, seed, quant, device
+        self.tensors = {}  # name -> dict(w=..., s=..., b=...) or bf16 tensor
+        H, I, kvd, V = spec.hidden, spec.inter, spec.kvd, spec.vocab
+
+        def normal(name, shape, mean=0.0, sd=std):
+            n = int(np.prod(shape))
+            return synth_normal_bf16(seed, name, n, mean, sd, threads)
+
+        def add_linear(name, N, K):
+            w = _to_dev(normal(name + ".weight", (N, K)), (N, K), device)
+            if not quant:
+                self.tensors[name] = dict(w=w)
+                return
+            wq = torch.empty((N, K // 8), dtype=torch.int32, device=device)
+            s = torch.empty((N, K // 64), dtype=torch.bfloat16, device=device)
+            b = torch.empty((N, K // 64), dtype=torch.bfloat16, device=device)
+            ctx.quantize(w, wq, s, b)
+            ctx.sync()
+            del w
+            self.tensors[name] = dict(w=wq, s=s, b=b)
+
+        def add_vec(name, n, mean=0.0, sd=std):
+            self.tensors[name] = _to_dev(normal(name, (n,), mean, sd), (n,), device)
+
+        def add_norm(name, n):
+            if norm_std == 0.0:
+                self.tensors[name] = torch.ones(n, dtype=torch.bfloat16, device=device)
+            else:
+                add_vec(name, n, 1.0, norm_std)
+
+        P = "model.model"
+        add_linear(f"{P}.embed_tokens", V, H)
+        for i in range(spec.n_layers):
+            L = f"{P}.layers.{i}"
+            add_norm(f"{L}.input_layernorm.weight", H)
+            add_norm(f"{L}.post_attention_layernorm.weight", H)
+            add_linear(f"{L}.self_attn.q_proj", H, H)
+            add_linear(f"{L}.self_attn.k_proj", kvd, H)
+            add_linear(f"{L}.self_attn.v_proj", kvd, H)
+            add_vec(f"{L}.self_attn.q_proj.bias", H)
+            add_vec(f"{L}.self_attn.k_proj.bias", kvd)
+            add_vec(f"{L}.self_attn.v_proj.bias", kvd)
+            add_linear(f"{L}.self_attn.o_proj", H, H)
+            add_linear(f"{L}.mlp.gate_proj", I, H)
+            add_linear(f"{L}.mlp.up_proj", I, H)
+            add_linear(f"{L}.mlp.down_proj", H, I)
+        add_norm(f"{P}.norm.weight", H)
+        self._build_views()
+
+    # ---- C-ABI views ----
+    def lin(self, name):
+        t = self.tensors[name]
+        if "s" in t:
+            return linear(t["w"], t["s"], t["b"])
+        return linear(t["w"])
+
+    def _build_views(self):
+        spec, P = self.spec, "model.model"
+        self.layers = []
+        for i in range(spec.n_layers):
+            L = f"{P}.layers.{i}"
+            self.layers.append(LmLayerW(
+                self.tensors[f"{L}.input_layernorm.weight"].data_ptr(),
+                self.tensors[f"{L}.post_attention_layernorm.weight"].data_ptr(),
+                self.lin(f"{L}.self_attn.q_proj"), self.lin(f"{L}.self_attn.k_proj"),
+                self.lin(f"{L}.self_attn.v_proj"), self.lin(f"{L}.self_attn.o_proj"),
+                self.lin(f"{L}.mlp.gate_proj"), self.lin(f"{L}.mlp.up_proj"), self.lin(f"{L}.mlp.down_proj"),
+                self.tensors[f"{L}.self_attn.q_proj.bias"].data_ptr(),
+                self.tensors[f"{L}.self_attn.k_proj.bias"].data_ptr(),
+                self.tensors[f"{L}.self_attn.v_proj.bias"].data_ptr()))
+        self.embed = self.lin(f"{P}.embed_tokens")
+        self.head = self.embed  # tied
+        self.final_norm = self.tensors[f"{P}.norm.weight"]
+        self.cfg = spec.cfg()
+
+    def model(self):
+        return LmModel(self.ctx, self.cfg, self.layers, self.final_norm, self.head, self.embed)
+
+    # ---- host copies (for the CPU checker) ----
+    def host(self, name):
+        """numpy copy of a tensor: bf16 -> uint16, packed -> uint32; dict for linears."""
+        import torch
+
+        t = self.tensors[name]
+
+        def cpu(x):
+            if x.dtype == torch.bfloat16:
+                return x.view(torch.int16).cpu().numpy().view(np.uint16)
+            return x.cpu().numpy().view(np.uint32)
+
+        if isinstance(t, dict):
+            return {k: cpu(v) for k, v in t.items()}
+        return cpu(t)
+
+
+class KvCache:
+    """In-place bf16 KV cache [n_layers][kv_heads][capacity][head_dim] on the device."""
+
+    def __init__(self, spec: LmSpec, capacity, device="cuda"):
+        import torch
+
+        shape = (spec.n_layers, spec.kv_heads, capacity, spec.head_dim)
+        self.k = torch.zeros(shape, dtype=torch.bfloat16, device=device)
+        self.v = torch.zeros(shape, dtype=torch.bfloat16, device=device)
+        self.kv = Kv(self.k.data_ptr(), self.v.data_ptr(), spec.n_layers, spec.kv_heads, spec.head_dim, capacity, 0)
+
+    @property
+    def len(self):
+        return self.kv.len
+
+    def fill_random(self, n, seed=0, std=1.0, threads=None):
+        """Rows [0, n) of every layer/head ~ bf16(N(0, std)); len = n."""
+        import torch
+
+        L, kvh, cap, hd = self.k.shape
+        for nm, t in (("kv.k", self.k), ("kv.v", self.v)):
+            arr = synth_normal_bf16(seed, nm, L * kvh * n * hd, 0.0, std, threads)
+            t[:, :, :n, :] = torch.from_numpy(arr.view(np.int16).reshape(L, kvh, n, hd)).to(t.device).view(
+                torch.bfloat16)
+        self.kv.len = n
+
+    def host(self):
+        import torch
+
+        return (self.k.view(torch.int16).cpu().numpy().view(np.uint16),
+                self.v.view(torch.int16).cpu().numpy().view(np.uint16))
+
+
+def lm_bytes_per_token(spec: LmSpec, ctx_len):
+    """Algorithmic HBM bytes of one 4-bit decode token at `ctx_len` cached
+    positions: 4-bit linears + tied head (0.5625 B/param), q/k/v biases and
+    norm weights, the KV read of ctx_len cached rows and the one-row append."""
+    H, kvd, L = spec.hidden, spec.kvd, spec.n_layers
+    small = L * (2 * H + (H + 2 * kvd)) * 2 + H * 2
+    kv_row = L * 2 * kvd * 2
+    return spec.weight_bytes_q4() + small + kv_row * ctx_len + kv_row
+
+
+__all__ = ["LmSpec", "QWEN2_05B", "SyntheticLm", "KvCache", "lm_bytes_per_token", "W_AFFINE", "W_BF16",
+           "Linear", "math"]

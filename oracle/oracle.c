@@ -1,0 +1,385 @@
+/*
+ * oracle.c -- CPU restatement of the reference's per-token loop (test
+ * infrastructure only; see oracle.h for scope and citations).
+ *
+ * Accumulation order: every dot product keeps 8 interleaved f32 partial sums
+ * (element k goes to partial k % 8) that are added pairwise at the end.  The
+ * order is fixed so that runs are reproducible; MLX's own order is not
+ * observable here, and any f32 order is within the bf16 tolerance of the
+ * parity tests.
+ */
+#include "oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ---- bf16 ---------------------------------------------------------------- */
+
+uint16_t or_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u); /* quiet NaN */
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+float or_f32(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+float or_rb(float f) { return or_f32(or_bf16(f)); }
+
+void or_to_bf16(const float* x, uint16_t* y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = or_bf16(x[i]);
+}
+
+void or_to_f32(const uint16_t* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = or_f32(x[i]);
+}
+
+static float sum8(const float* p) {
+    return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+}
+
+/* ---- MLX affine quantization --------------------------------------------- */
+
+/* Per group: scale = max((wmax - wmin) / n_bins, 1e-7), signed toward the
+ * larger-magnitude edge; the edge is snapped to an integer level q0 so that
+ * zero is exact (scale = edge / q0, bias = edge), unless q0 == 0 (bias 0).
+ * q = clamp(rint((w - bias) / scale), 0, n_bins), computed in f32 with the
+ * unrounded scale and bias; scale and bias are stored as bf16.
+ * (MLX 0.32 CPU `quantize`, mlx/backend/cpu/quantized.cpp.) */
+int or_quantize(const uint16_t* w, int64_t N, int64_t K, int group, int bits, uint32_t* wq,
+                uint16_t* scales, uint16_t* biases) {
+    if (bits != 4 && bits != 8) return -1;
+    if (K % group != 0 || (group * bits) % 32 != 0) return -1;
+    const float n_bins = (float)((1 << bits) - 1);
+    const float eps = 1e-7f;
+    const int el_per_int = 32 / bits;
+    const int64_t ng = K / group;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < N; r++) {
+        for (int64_t g = 0; g < ng; g++) {
+            const uint16_t* wg = w + r * K + g * group;
+            float wmin = INFINITY, wmax = -INFINITY;
+            for (int j = 0; j < group; j++) {
+                const float v = or_f32(wg[j]);
+                wmax = fmaxf(wmax, v);
+                wmin = fminf(wmin, v);
+            }
+            const int mask = fabsf(wmin) > fabsf(wmax);
+            float scale = fmaxf((wmax - wmin) / n_bins, eps);
+            scale = mask ? scale : -scale;
+            const float edge = mask ? wmin : wmax;
+            const float q0 = rintf(edge / scale);
+            float bias = 0.0f;
+            if (q0 != 0.0f) {
+                scale = edge / q0;
+                bias = edge;
+            }
+            uint32_t* out = wq + r * (K / el_per_int) + g * (group / el_per_int);
+            for (int j = 0; j < group / el_per_int; j++) {
+                uint32_t word = 0;
+                for (int k = 0; k < el_per_int; k++) {
+                    float v = or_f32(wg[j * el_per_int + k]);
+                    v = rintf((v - bias) / scale);
+                    v = fminf(fmaxf(v, 0.0f), n_bins);
+                    word |= (uint32_t)v << (k * bits);
+                }
+                out[j] = word;
+            }
+            scales[r * ng + g] = or_bf16(scale);
+            biases[r * ng + g] = or_bf16(bias);
+        }
+    }
+    return 0;
+}
+
+static inline uint32_t qval(const uint32_t* row, int64_t k, int bits) {
+    const int per = 32 / bits;
+    return (row[k / per] >> ((k % per) * bits)) & ((1u << bits) - 1u);
+}
+
+int or_dequantize(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases, int64_t N, int64_t K,
+                  int group, int bits, float gscale, uint16_t* out) {
+    if (bits != 4 && bits != 8) return -1;
+    if (K % group != 0) return -1;
+    const int64_t ng = K / group, wpr = K * bits / 32;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < N; r++) {
+        for (int64_t k = 0; k < K; k++) {
+            const float s = or_f32(scales[r * ng + k / group]);
+            const float b = or_f32(biases[r * ng + k / group]);
+            float v = s * (float)qval(wq + r * wpr, k, bits) + b;
+            if (gscale != 1.0f) v *= gscale;
+            out[r * K + k] = or_bf16(v);
+        }
+    }
+    return 0;
+}
+
+/* ---- linear layers -------------------------------------------------------- */
+
+static float dot_bf16(const uint16_t* w, const uint16_t* x, int64_t K) {
+    float p[8] = {0};
+    int64_t k = 0;
+    for (; k + 8 <= K; k += 8)
+        for (int j = 0; j < 8; j++) p[j] += or_f32(w[k + j]) * or_f32(x[k + j]);
+    for (; k < K; k++) p[k % 8] += or_f32(w[k]) * or_f32(x[k]);
+    return sum8(p);
+}
+
+/* Affine row: sum_k x_k * (s_g * q_k + b_g), dequantized value in f32. */
+static float dot_affine(const or_linear* L, int64_t n, const uint16_t* x) {
+    const int64_t K = L->K, ng = K / L->group, wpr = K * L->bits / 32;
+    const uint32_t* row = (const uint32_t*)L->w + n * wpr;
+    float p[8] = {0};
+    for (int64_t g = 0; g < ng; g++) {
+        const float s = or_f32(L->scales[n * ng + g]);
+        const float b = or_f32(L->biases[n * ng + g]);
+        const int64_t k0 = g * L->group;
+        for (int64_t k = k0; k < k0 + L->group; k++) {
+            const float wv = s * (float)qval(row, k, L->bits) + b;
+            p[k % 8] += or_f32(x[k]) * wv;
+        }
+    }
+    return sum8(p) * L->gscale;
+}
+
+void or_linear_acc(const or_linear* L, const uint16_t* x, int64_t M, float* y) {
+    const int64_t N = L->N, K = L->K;
+    for (int64_t m = 0; m < M; m++) {
+        const uint16_t* xr = x + m * K;
+        float* yr = y + m * N;
+        if (L->kind == OR_W_BF16) {
+            const uint16_t* W = (const uint16_t*)L->w;
+#pragma omp parallel for schedule(static)
+            for (int64_t n = 0; n < N; n++) yr[n] = dot_bf16(W + n * K, xr, K);
+        } else {
+#pragma omp parallel for schedule(static)
+            for (int64_t n = 0; n < N; n++) yr[n] = dot_affine(L, n, xr);
+        }
+    }
+}
+
+void or_linear_fwd(const or_linear* L, const uint16_t* x, int64_t M, const uint16_t* bias, uint16_t* y) {
+    const int64_t N = L->N;
+    float* acc = (float*)malloc(sizeof(float) * (size_t)(M * N));
+    or_linear_acc(L, x, M, acc);
+    for (int64_t m = 0; m < M; m++)
+        for (int64_t n = 0; n < N; n++) {
+            const float a = acc[m * N + n];
+            float v;
+            if (!bias)
+                v = a;
+            else if (L->kind == OR_W_BF16)
+                v = a + or_f32(bias[n]);             /* addmm: one rounding */
+            else
+                v = or_rb(a) + or_f32(bias[n]);      /* quantized_matmul, then + bias */
+            y[m * N + n] = or_bf16(v);
+        }
+    free(acc);
+}
+
+/* ---- element-wise / normalisation ---------------------------------------- */
+
+void or_rms_norm(const uint16_t* x, const uint16_t* w, int64_t M, int64_t n, float eps, uint16_t* out) {
+    for (int64_t m = 0; m < M; m++) {
+        const uint16_t* xr = x + m * n;
+        float p[8] = {0};
+        for (int64_t i = 0; i < n; i++) {
+            const float v = or_f32(xr[i]);
+            p[i % 8] += v * v;
+        }
+        const float inv = 1.0f / sqrtf(sum8(p) / (float)n + eps);
+        for (int64_t i = 0; i < n; i++)
+            out[m * n + i] = or_bf16(or_f32(w[i]) * or_rb(or_f32(xr[i]) * inv));
+    }
+}
+
+void or_rope(uint16_t* x, int nh, int hd, int pos, float log2_base) {
+    const int half = hd / 2;
+    for (int i = 0; i < half; i++) {
+        const float inv_freq = exp2f(-((float)i / (float)half) * log2_base);
+        const float th = (float)pos * inv_freq;
+        const float c = cosf(th), s = sinf(th);
+        for (int h = 0; h < nh; h++) {
+            uint16_t* r = x + h * hd;
+            const float x1 = or_f32(r[i]), x2 = or_f32(r[i + half]);
+            r[i] = or_bf16(x1 * c - x2 * s);
+            r[i + half] = or_bf16(x1 * s + x2 * c);
+        }
+    }
+}
+
+void or_swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* out) {
+    for (int64_t i = 0; i < n; i++) {
+        const float gv = or_f32(g[i]);
+        const float sg = or_rb(1.0f / (1.0f + expf(-gv)));
+        out[i] = or_bf16(or_rb(gv * sg) * or_f32(u[i]));
+    }
+}
+
+void or_gelu_approx(const uint16_t* x, int64_t n, uint16_t* out) {
+    const float c0 = or_rb(0.044715f), c1 = or_rb(0.7978845608f);
+    for (int64_t i = 0; i < n; i++) {
+        const float v = or_f32(x[i]);
+        const float x3 = or_rb(powf(v, 3.0f));
+        const float inner = or_rb(v + or_rb(c0 * x3));
+        const float th = or_rb(tanhf(or_rb(c1 * inner)));
+        out[i] = or_bf16(or_rb(0.5f * v) * or_rb(1.0f + th));
+    }
+}
+
+void or_add(const uint16_t* a, const uint16_t* b, int64_t n, uint16_t* out) {
+    for (int64_t i = 0; i < n; i++) out[i] = or_bf16(or_f32(a[i]) + or_f32(b[i]));
+}
+
+/* ---- Qwen2 decode --------------------------------------------------------- */
+
+void or_attention(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int heads, int kv_heads, int hd,
+                  int cap, int pos, float scale, uint16_t* out) {
+    const int grp = heads / kv_heads, n = pos + 1;
+#pragma omp parallel for schedule(static)
+    for (int h = 0; h < heads; h++) {
+        const int kvh = h / grp;
+        float* sc = (float*)malloc(sizeof(float) * (size_t)n);
+        float qs[256];
+        for (int d = 0; d < hd; d++) qs[d] = scale * or_f32(q[h * hd + d]);
+        float m = -INFINITY;
+        for (int j = 0; j < n; j++) {
+            const uint16_t* kr = kc + ((int64_t)kvh * cap + j) * hd;
+            float p[8] = {0};
+            for (int d = 0; d < hd; d++) p[d % 8] += qs[d] * or_f32(kr[d]);
+            sc[j] = sum8(p);
+            m = fmaxf(m, sc[j]);
+        }
+        float l = 0.0f;
+        for (int j = 0; j < n; j++) {
+            sc[j] = expf(sc[j] - m);
+            l += sc[j];
+        }
+        for (int d = 0; d < hd; d++) {
+            float a = 0.0f;
+            for (int j = 0; j < n; j++) a += sc[j] * or_f32(vc[((int64_t)kvh * cap + j) * hd + d]);
+            out[h * hd + d] = or_bf16(a / l);
+        }
+        free(sc);
+    }
+}
+
+void or_lm_layer_step(const or_lm_cfg* c, const or_lm_layer* l, const uint16_t* x, int pos, uint16_t* kc,
+                      uint16_t* vc, int cap, uint16_t* x_out, or_lm_trace* tr) {
+    const int H = c->hidden, hd = c->head_dim, kvd = c->kv_heads * hd, I = c->inter;
+    uint16_t* h = (uint16_t*)malloc(2 * (size_t)H);
+    uint16_t* q = (uint16_t*)malloc(2 * (size_t)H);
+    uint16_t* k = (uint16_t*)malloc(2 * (size_t)kvd);
+    uint16_t* v = (uint16_t*)malloc(2 * (size_t)kvd);
+    uint16_t* att = (uint16_t*)malloc(2 * (size_t)H);
+    uint16_t* o = (uint16_t*)malloc(2 * (size_t)H);
+    uint16_t* x1 = (uint16_t*)malloc(2 * (size_t)H);
+    uint16_t* h2 = (uint16_t*)malloc(2 * (size_t)H);
+    uint16_t* g = (uint16_t*)malloc(2 * (size_t)I);
+    uint16_t* u = (uint16_t*)malloc(2 * (size_t)I);
+    uint16_t* hh = (uint16_t*)malloc(2 * (size_t)I);
+    uint16_t* d = (uint16_t*)malloc(2 * (size_t)H);
+
+    or_rms_norm(x, l->ln1, 1, H, c->eps, h);
+    or_linear_fwd(&l->q, h, 1, l->bq, q);
+    or_linear_fwd(&l->k, h, 1, l->bk, k);
+    or_linear_fwd(&l->v, h, 1, l->bv, v);
+    or_rope(q, c->heads, hd, pos, c->log2_theta);
+    or_rope(k, c->kv_heads, hd, pos, c->log2_theta);
+    for (int kh = 0; kh < c->kv_heads; kh++) {
+        memcpy(kc + ((int64_t)kh * cap + pos) * hd, k + kh * hd, 2 * (size_t)hd);
+        memcpy(vc + ((int64_t)kh * cap + pos) * hd, v + kh * hd, 2 * (size_t)hd);
+    }
+    or_attention(q, kc, vc, c->heads, c->kv_heads, hd, cap, pos, 1.0f / sqrtf((float)hd), att);
+    or_linear_fwd(&l->o, att, 1, NULL, o);
+    or_add(x, o, H, x1);
+    or_rms_norm(x1, l->ln2, 1, H, c->eps, h2);
+    or_linear_fwd(&l->gate, h2, 1, NULL, g);
+    or_linear_fwd(&l->up, h2, 1, NULL, u);
+    or_swiglu(g, u, I, hh);
+    or_linear_fwd(&l->down, hh, 1, NULL, d);
+    or_add(x1, d, H, x_out);
+
+    if (tr) {
+        if (tr->h) memcpy(tr->h, h, 2 * (size_t)H);
+        if (tr->qkv) {
+            memcpy(tr->qkv, q, 2 * (size_t)H);
+            memcpy(tr->qkv + H, k, 2 * (size_t)kvd);
+            memcpy(tr->qkv + H + kvd, v, 2 * (size_t)kvd);
+        }
+        if (tr->att) memcpy(tr->att, att, 2 * (size_t)H);
+        if (tr->x1) memcpy(tr->x1, x1, 2 * (size_t)H);
+        if (tr->hh) memcpy(tr->hh, hh, 2 * (size_t)I);
+    }
+    free(h); free(q); free(k); free(v); free(att); free(o);
+    free(x1); free(h2); free(g); free(u); free(hh); free(d);
+}
+
+int or_lm_head(const or_lm_cfg* c, const uint16_t* norm, const or_linear* head, const uint16_t* x,
+               uint16_t* hidden_out, float* logits, uint16_t* logits_bf16, float* margin) {
+    const int H = c->hidden;
+    const int64_t V = head->N;
+    uint16_t hid[8192];
+    or_rms_norm(x, norm, 1, H, c->eps, hid);
+    if (hidden_out) memcpy(hidden_out, hid, 2 * (size_t)H);
+    float* lg = logits ? logits : (float*)malloc(sizeof(float) * (size_t)V);
+    or_linear_acc(head, hid, 1, lg);
+    int best = 0;
+    float b1 = -INFINITY, b2 = -INFINITY;
+    for (int64_t i = 0; i < V; i++) {
+        const float v = lg[i];
+        if (v > b1) {
+            b2 = b1;
+            b1 = v;
+            best = (int)i;
+        } else if (v > b2) {
+            b2 = v;
+        }
+    }
+    if (logits_bf16)
+        for (int64_t i = 0; i < V; i++) logits_bf16[i] = or_bf16(lg[i]);
+    if (margin) *margin = b1 - b2;
+    if (!logits) free(lg);
+    return best;
+}
+
+void or_embed(const or_linear* table, int id, uint16_t* out) {
+    const int64_t K = table->K;
+    if (table->kind == OR_W_BF16) {
+        memcpy(out, (const uint16_t*)table->w + (int64_t)id * K, 2 * (size_t)K);
+    } else {
+        const int64_t ng = K / table->group, wpr = K * table->bits / 32;
+        or_dequantize((const uint32_t*)table->w + (int64_t)id * wpr, table->scales + (int64_t)id * ng,
+                      table->biases + (int64_t)id * ng, 1, K, table->group, table->bits, table->gscale, out);
+    }
+}
+
+/* ---- CPU threads ---------------------------------------------------------- */
+
+void or_set_threads(int n) {
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}
+
+int or_get_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

@@ -1,0 +1,134 @@
+/*
+ * oracle.h -- CPU restatement of Ming-3.0-tts's per-token generation loop.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product library links, loads or
+ * calls this code.  It is the checker for the HIP path (tests/, the smoke
+ * entry and the cpu_baseline leg of bench.py) and nothing else.
+ *
+ * It restates the MLX graph path of the reference (MING_FUSED=0 semantics):
+ * bf16 storage, f32 accumulation, and a bf16 rounding at every point where
+ * MLX materialises a bf16 array.  Citations are to the reference tree
+ * (sbusso/ming-tts-serve).
+ *
+ *   LM layer graph ............ src/ming_model.zig:588-611
+ *   decode gate / final norm .. src/ming_model.zig:530-544, :566-575
+ *   rounding points ........... src/ming_fused.zig:17-25
+ *   swiglu / gelu op order .... src/ming_model.zig:800-862
+ *   DiT block graph ........... src/ming_model.zig:783-795
+ *   CFM / CFG / Euler ......... src/ming_model.zig:1161-1188, :1193-1203
+ *   flow schedule ............. src/ming_model.zig:1207-1215
+ *   aggregator ................ src/ming_model.zig:1042-1053
+ *   stop head ................. src/ming_model.zig:1033-1038
+ *
+ * The MLX-affine quantizer, dequantizer and quantized matmul restate the
+ * published MLX 0.32 CPU algorithm (mlx/backend/cpu/quantized.cpp), which the
+ * reference binds at src/mlx.zig:279-292 but never calls.
+ *
+ * Where each function is pinned (closed forms, library routines, brute force)
+ * is stated in the test that checks it (tests/test_oracle_*.py).
+ */
+#ifndef MING_ORACLE_H
+#define MING_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- bf16 ---------------------------------------------------------------- */
+uint16_t or_bf16(float f);             /* f32 -> bf16, round to nearest even */
+float or_f32(uint16_t h);              /* bf16 -> f32 (exact) */
+float or_rb(float f);                  /* round through bf16 */
+void or_to_bf16(const float* x, uint16_t* y, int64_t n);
+void or_to_f32(const uint16_t* x, float* y, int64_t n);
+
+/* ---- MLX affine quantization (mode "affine", transpose=true layout) ------ */
+/* w bf16 [N,K] -> wq u32 [N, K*bits/32], scales/biases bf16 [N, K/group]. */
+int or_quantize(const uint16_t* w, int64_t N, int64_t K, int group, int bits,
+                uint32_t* wq, uint16_t* scales, uint16_t* biases);
+/* -> bf16 [N,K]: bf16(gscale * (s*q + b)) */
+int or_dequantize(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+                  int64_t N, int64_t K, int group, int bits, float gscale, uint16_t* out);
+
+/* ---- linear layers -------------------------------------------------------- */
+enum { OR_W_BF16 = 0, OR_W_AFFINE = 1 };
+typedef struct {
+    int kind;                 /* OR_W_BF16 or OR_W_AFFINE */
+    int64_t N, K;             /* out_features, in_features */
+    const void* w;            /* bf16 [N,K] or u32 [N,K*bits/32] */
+    const uint16_t* scales;   /* bf16 [N,K/group] (affine) */
+    const uint16_t* biases;   /* bf16 [N,K/group] (affine) */
+    float gscale;             /* global scale (affine); 1.0 = plain MLX affine */
+    int group, bits;
+} or_linear;
+
+/* y[n] = f32 accumulation of W x (no rounding). rows x[M][K] -> y[M][N]. */
+void or_linear_acc(const or_linear* L, const uint16_t* x, int64_t M, float* y);
+/* MLX linear output: bf16 [M,N].
+ *   bf16 weights:  addmm  -> bf16(acc + bias)                (one rounding)
+ *   affine weights: quantized_matmul then + bias -> bf16(bf16(acc) + bias)  */
+void or_linear_fwd(const or_linear* L, const uint16_t* x, int64_t M, const uint16_t* bias, uint16_t* y);
+
+/* ---- element-wise / normalisation ---------------------------------------- */
+/* MLX fast::rms_norm: out = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))), rows [M][n]. */
+void or_rms_norm(const uint16_t* x, const uint16_t* w, int64_t M, int64_t n, float eps, uint16_t* out);
+/* MLX fast::rope, traditional=false: pairs (d, d + hd/2); x [nh][hd] bf16 in place. */
+void or_rope(uint16_t* x, int nh, int hd, int pos, float log2_base);
+/* compiled swiglu: bf16(bf16(g * bf16(sigmoid(g))) * u) */
+void or_swiglu(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* out);
+/* compiled mlx.nn.gelu_approx with bf16 weak scalars, every op rounded */
+void or_gelu_approx(const uint16_t* x, int64_t n, uint16_t* out);
+/* bf16 add */
+void or_add(const uint16_t* a, const uint16_t* b, int64_t n, uint16_t* out);
+
+/* ---- Qwen2 decode --------------------------------------------------------- */
+typedef struct {
+    int hidden, heads, kv_heads, head_dim, inter;
+    float eps, log2_theta;
+} or_lm_cfg;
+
+typedef struct {
+    const uint16_t *ln1, *ln2;
+    or_linear q, k, v, o, gate, up, down;
+    const uint16_t *bq, *bk, *bv;
+} or_lm_layer;
+
+/* Intermediates of one layer (all optional, bf16 unless noted). */
+typedef struct {
+    uint16_t* h;    /* rms(x, ln1)        [hidden] */
+    uint16_t* qkv;  /* roped q | roped k | v  [hidden + 2*kv_heads*head_dim] */
+    uint16_t* att;  /* attention output   [hidden] */
+    uint16_t* x1;   /* x + o_proj         [hidden] */
+    uint16_t* hh;   /* swiglu             [inter] */
+} or_lm_trace;
+
+/* GQA decode attention of one token at position `pos` over the cache rows
+ * [0, pos] (the new row already appended).  q [heads][hd] bf16;
+ * kc/vc [kv_heads][cap][hd] bf16; out [heads][hd] bf16. */
+void or_attention(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int heads, int kv_heads,
+                  int hd, int cap, int pos, float scale, uint16_t* out);
+
+/* One Qwen2 layer on x [hidden] at position pos.  k/v are appended in place
+ * at row pos of kc/vc ([kv_heads][cap][hd]).  x_out [hidden]. */
+void or_lm_layer_step(const or_lm_cfg* c, const or_lm_layer* l, const uint16_t* x, int pos,
+                      uint16_t* kc, uint16_t* vc, int cap, uint16_t* x_out, or_lm_trace* tr);
+
+/* Final norm + tied LM head + greedy argmax.  hidden_out bf16 [hidden];
+ * logits f32 [vocab] (accumulator before rounding; may be NULL);
+ * returns the argmax over the f32 logits, lowest index on ties. */
+int or_lm_head(const or_lm_cfg* c, const uint16_t* norm, const or_linear* head, const uint16_t* x,
+               uint16_t* hidden_out, float* logits, uint16_t* logits_bf16, float* margin);
+
+/* Embedding row gather: bf16 table [V,H] or affine-quantized table. */
+void or_embed(const or_linear* table, int id, uint16_t* out);
+
+/* ---- CPU threads ---------------------------------------------------------- */
+void or_set_threads(int n);
+int or_get_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,116 @@
+"""GPU parity of the MLX-affine kernels (ming_quantize / ming_dequantize /
+ming_qgemv) against the oracle, at the five GEMV shapes of the 4-bit sweep:
+[896x896], [896x128] (k/v proj), [896x4864], [4864x896], [896x151936]
+(lm_head), given as [in x out].
+
+Bars: quantize and dequantize bit-exact; qgemv bf16 outputs within
+|d| <= 2e-2 + 1e-2 |ref|, f32 accumulators within 1e-4 + 1e-5 |ref|; global
+scale 2^k exact (a power-of-two factor commutes with rounding)."""
+import numpy as np
+import pytest
+import torch
+
+from lmkit import assert_close_bf16
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(896, 896), (896, 128), (896, 4864), (4864, 896), (896, 151936)]  # [in, out]
+
+
+def dev_u16(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda().view(torch.bfloat16)
+
+
+def host_u16(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def make(ming, ctx, K, N, seed=0, std=0.02):
+    print(f"[qgemv] shape in={K} out={N} seed={seed}", flush=True)
+    w = ming.synth_normal_bf16(seed, f"w{K}x{N}", N * K, 0.0, std).reshape(N, K)
+    x = ming.synth_normal_bf16(seed, f"x{K}", K, 0.0, 1.0)
+    wd = dev_u16(w)
+    wq = torch.empty((N, K // 8), dtype=torch.int32, device="cuda")
+    s = torch.empty((N, K // 64), dtype=torch.bfloat16, device="cuda")
+    b = torch.empty((N, K // 64), dtype=torch.bfloat16, device="cuda")
+    ctx.quantize(wd, wq, s, b)
+    ctx.sync()
+    return w, x, wq, s, b
+
+
+@pytest.mark.parametrize("K,N", SHAPES)
+def test_quantize_dequantize_bit_exact(ming, oracle, ctx, K, N):
+    w, x, wq, s, b = make(ming, ctx, K, N)
+    rq, rs, rb_ = oracle.quantize(w)
+    assert np.array_equal(wq.cpu().numpy().view(np.uint32), rq), "packed nibbles differ"
+    assert np.array_equal(host_u16(s), rs), "scales differ"
+    assert np.array_equal(host_u16(b), rb_), "biases differ"
+    out = torch.empty((N, K), dtype=torch.bfloat16, device="cuda")
+    ctx.dequantize(wq, s, b, out)
+    ctx.sync()
+    assert np.array_equal(host_u16(out), oracle.dequantize(rq, rs, rb_)), "dequantized weights differ"
+
+
+@pytest.mark.parametrize("K,N", SHAPES)
+def test_qgemv_matches_oracle(ming, oracle, ctx, K, N):
+    w, x, wq, s, b = make(ming, ctx, K, N)
+    L = oracle.Linear(wq.cpu().numpy().view(np.uint32), host_u16(s), host_u16(b))
+    ref_acc = oracle.linear_acc(L, x)
+    ref = oracle.linear(L, x)
+    xd = dev_u16(x)
+    y = torch.empty(N, dtype=torch.bfloat16, device="cuda")
+    yf = torch.empty(N, dtype=torch.float32, device="cuda")
+    ctx.qgemv(xd, wq, s, b, y)
+    ctx.qgemv(xd, wq, s, b, yf, f32=True)
+    ctx.sync()
+    got_acc = yf.cpu().numpy()
+    d = np.abs(got_acc.astype(np.float64) - ref_acc)
+    assert (d <= 1e-4 + 1e-5 * np.abs(ref_acc)).all(), f"f32 accumulators: max|d| {d.max():.3e}"
+    md = assert_close_bf16(host_u16(y), ref, f"qgemv [{K}x{N}]")
+    # the bf16 output is the rounding of the f32 accumulator
+    assert np.array_equal(host_u16(y), oracle.to_bf16(got_acc))
+    print(f"[qgemv] [{K}x{N}] max|d| bf16 {md:.3e} f32 {d.max():.3e}", flush=True)
+
+
+@pytest.mark.parametrize("g", [1.0, 2.0, 0.5, 3.0])
+def test_global_scale(ming, oracle, ctx, g):
+    K, N = 896, 4864
+    w, x, wq, s, b = make(ming, ctx, K, N, seed=1)
+    xd = dev_u16(x)
+    y1 = torch.empty(N, dtype=torch.bfloat16, device="cuda")
+    yg = torch.empty(N, dtype=torch.bfloat16, device="cuda")
+    ctx.qgemv(xd, wq, s, b, y1, global_scale=1.0)
+    ctx.qgemv(xd, wq, s, b, yg, global_scale=g)
+    ctx.sync()
+    L1 = oracle.Linear(wq.cpu().numpy().view(np.uint32), host_u16(s), host_u16(b))
+    if g == 1.0:
+        assert np.array_equal(host_u16(yg), host_u16(y1))
+    if g in (2.0, 0.5):  # power of two: exact scaling of the rounded output
+        assert np.array_equal(oracle.to_f32(host_u16(yg)), (oracle.to_f32(host_u16(y1)) * g).astype(np.float32))
+    Lg = oracle.Linear(L1.w, L1.s, L1.b, gscale=g)
+    assert_close_bf16(host_u16(yg), oracle.linear(Lg, x), f"global scale {g}")
+    # dequantize applies the same factor
+    out = torch.empty((N, K), dtype=torch.bfloat16, device="cuda")
+    ctx.dequantize(wq, s, b, out, global_scale=g)
+    ctx.sync()
+    assert np.array_equal(host_u16(out), oracle.dequantize(L1.w, L1.s, L1.b, gscale=g))
+
+
+def test_qgemv_multirow(ming, oracle, ctx):
+    K, N, M = 896, 4864, 4
+    w, x, wq, s, b = make(ming, ctx, K, N, seed=2)
+    xs = ming.synth_normal_bf16(5, "xm", M * K, 0.0, 1.0).reshape(M, K)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    ctx.qgemv(dev_u16(xs), wq, s, b, y)
+    ctx.sync()
+    L = oracle.Linear(wq.cpu().numpy().view(np.uint32), host_u16(s), host_u16(b))
+    assert_close_bf16(host_u16(y), oracle.linear(L, xs), "qgemv M=4")
+
+
+def test_qgemv_shape_errors(ming, ctx):
+    K, N = 896, 128
+    w, x, wq, s, b = make(ming, ctx, K, N)
+    y = torch.empty(N + 1, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ming.MingError) as e:
+        ctx.qgemv(dev_u16(x), wq, s, b, y)
+    assert e.value.status == ming.MING_E_SHAPE
