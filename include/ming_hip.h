@@ -62,8 +62,11 @@ typedef struct ming_ctx ming_ctx;
 
 int ming_ctx_create(ming_ctx** out, int device);
 int ming_ctx_destroy(ming_ctx* ctx);
-/* Run on a caller-owned hipStream_t (NULL = the context's own stream). */
+/* Run on a caller-owned hipStream_t, used as given: NULL is HIP's null
+ * (default) stream.  A new context runs on a stream of its own until this is
+ * called; ming_ctx_use_own_stream() returns to it. */
 int ming_ctx_set_stream(ming_ctx* ctx, void* hip_stream);
+int ming_ctx_use_own_stream(ming_ctx* ctx);
 void* ming_ctx_stream(ming_ctx* ctx);
 /* The eval point (mlx_eval, src/ming_model.zig:269-274); also reports any
  * device-side error flag (MING_E_TIMEOUT). */
@@ -191,6 +194,14 @@ enum ming_lm_mode {
     MING_LM_PERSISTENT = 2   /* one persistent kernel per token */
 };
 int ming_lm_model_set_mode(ming_lm_model* m, int32_t mode);
+
+/* Per-stage timing of the persistent schedule (the reference's MING_PROFILE
+ * step timing, src/ming_model.zig:1394-1410, at stage granularity): with a
+ * device buffer of u64 [n_stamps][grid] set, every workgroup writes the
+ * device wall clock (wall_clock64) at each stage boundary of later steps.
+ * NULL turns it off.  ming_lm_model_profile_shape gives the buffer shape. */
+int ming_lm_model_profile(ming_lm_model* m, void* stamps_dev);
+int ming_lm_model_profile_shape(ming_lm_model* m, int32_t* n_stamps, int32_t* grid);
 
 /* One decode step: QStack.decodeFused (src/ming_model.zig:530-544) plus the
  * tied LM head and greedy argmax.  Input: if `token_dev` is non-NULL, the

@@ -87,6 +87,7 @@ def lib():
         "ming_ctx_create": (c_i32, [P(c_void_p), c_i32]),
         "ming_ctx_destroy": (c_i32, [c_void_p]),
         "ming_ctx_set_stream": (c_i32, [c_void_p, c_void_p]),
+        "ming_ctx_use_own_stream": (c_i32, [c_void_p]),
         "ming_ctx_stream": (c_void_p, [c_void_p]),
         "ming_sync": (c_i32, [c_void_p]),
         "ming_last_error": (ctypes.c_char_p, [c_void_p]),
@@ -110,6 +111,8 @@ def lib():
                                          P(c_void_p)]),
         "ming_lm_model_destroy": (c_i32, [c_void_p]),
         "ming_lm_model_set_mode": (c_i32, [c_void_p, c_i32]),
+        "ming_lm_model_profile": (c_i32, [c_void_p, c_void_p]),
+        "ming_lm_model_profile_shape": (c_i32, [c_void_p, P(c_i32), P(c_i32)]),
         "ming_lm_step": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, P(Kv), c_void_p, c_void_p, c_void_p]),
         "ming_lm_generate": (c_i32, [c_void_p, c_void_p, P(Kv), c_i32, c_void_p]),
         "ming_lm_model_trace": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),

@@ -14,9 +14,10 @@ namespace ming {
 
 hipError_t launch_lm_layer(hipStream_t st, const StepArgs& a, const LayerDev& Ld, int l);
 hipError_t launch_lm_step_kernels(hipStream_t st, const StepArgs& a, const LayerDev* host_layers);
-hipError_t launch_lm_step_persistent(hipStream_t st, const StepArgs& a, int grid);
+hipError_t launch_lm_step_tagged(hipStream_t st, const StepArgs& a, int q4, int grid);
 hipError_t launch_copy_token(hipStream_t st, const int32_t* src, int32_t* dst);
-int persistent_grid(int num_cus);
+int tagged_grid(int num_cus);
+int tagged_split_len(int n);
 int attn_split_len(int n);
 size_t attn_part_floats(int kvh, int heads, int hd, int n);
 
@@ -193,9 +194,11 @@ struct ming_lm_model {
     const uint16_t* final_norm = nullptr;
     int mode = MING_LM_AUTO;
     int pgrid = 0;
+    uint32_t epoch = 0;   // tag of the last persistent step (tags start at 1)
+    uint64_t* tstamp = nullptr;  // optional stage-boundary stamps (ming_lm_model_profile)
     // workspace
     DevBuf x, x1, att, qkv, hh, part, hidden, amax_v, amax_i;
-    size_t part_floats = 0;
+    DevBuf tx, tq, ta, tx1, th, counters;  // tagged hand-off buffers, arrival counters
 };
 
 namespace {
@@ -248,7 +251,13 @@ int ming_ctx_destroy(ming_ctx* ctx) {
 
 int ming_ctx_set_stream(ming_ctx* ctx, void* s) {
     if (!alive(ctx)) return MING_E_NOT_INIT;
-    ctx->stream = s ? static_cast<hipStream_t>(s) : ctx->own_stream;
+    ctx->stream = static_cast<hipStream_t>(s);
+    return MING_OK;
+}
+
+int ming_ctx_use_own_stream(ming_ctx* ctx) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    ctx->stream = ctx->own_stream;
     return MING_OK;
 }
 
@@ -263,6 +272,7 @@ int ming_sync(ming_ctx* ctx) {
     if (st) return st;
     if (flag) {
         (void)hipMemset(ctx->dev_flags, 0, sizeof(int32_t));
+        ctx->timeout_seen = true;
         return set_err(ctx, MING_E_TIMEOUT, "a device-side wait exceeded its spin limit");
     }
     return MING_OK;
@@ -453,6 +463,9 @@ int ming_lm_model_create(ming_ctx* ctx, const ming_lm_cfg* cfg, const ming_lm_la
     if ((st = check_linear(ctx, *head, cfg->vocab, cfg->hidden, "head")) ||
         (st = check_linear(ctx, *embed, cfg->vocab, cfg->hidden, "embed")))
         return st;
+    for (int i = 0; i < cfg->n_layers; i++)
+        if (layers[i].wq.kind != head->kind)
+            return set_err(ctx, MING_E_UNSUPPORTED, "the LM head and every layer must share one weight kind");
     auto* m = new ming_lm_model;
     m->ctx = ctx;
     m->cfg = *cfg;
@@ -472,11 +485,19 @@ int ming_lm_model_create(ming_ctx* ctx, const ming_lm_cfg* cfg, const ming_lm_la
     if (e == hipSuccess) e = m->hidden.ensure(sizeof(uint16_t) * (size_t)H);
     if (e == hipSuccess) e = m->amax_v.ensure(sizeof(float) * kMaxParts);
     if (e == hipSuccess) e = m->amax_i.ensure(sizeof(int32_t) * kMaxParts);
+    if (e == hipSuccess) e = m->tx.ensure(sizeof(uint64_t) * (size_t)(L + 1) * (H / 2));
+    if (e == hipSuccess) e = m->tq.ensure(sizeof(uint64_t) * (size_t)L * (nq / 2));
+    if (e == hipSuccess) e = m->ta.ensure(sizeof(uint64_t) * (size_t)L * (H / 2));
+    if (e == hipSuccess) e = m->tx1.ensure(sizeof(uint64_t) * (size_t)L * (H / 2));
+    if (e == hipSuccess) e = m->th.ensure(sizeof(uint64_t) * (size_t)L * (I / 2));
+    if (e == hipSuccess) e = m->counters.ensure(sizeof(int32_t) * (size_t)(L * cfg->kv_heads + 1));
+    for (DevBuf* b : {&m->tx, &m->tq, &m->ta, &m->tx1, &m->th, &m->counters})
+        if (e == hipSuccess) e = hipMemset(b->p, 0, b->bytes);
     if (e != hipSuccess) {
         ming_lm_model_destroy(m);
         return hip_check(ctx, e, "lm_model workspace");
     }
-    m->pgrid = persistent_grid(ctx->num_cus);
+    m->pgrid = tagged_grid(ctx->num_cus);
     *out = m;
     return MING_OK;
 }
@@ -484,9 +505,23 @@ int ming_lm_model_create(ming_ctx* ctx, const ming_lm_cfg* cfg, const ming_lm_la
 int ming_lm_model_destroy(ming_lm_model* m) {
     if (!m) return MING_E_NOT_INIT;
     if (m->d_layers) (void)hipFree(m->d_layers);
-    for (DevBuf* b : {&m->x, &m->x1, &m->att, &m->qkv, &m->hh, &m->part, &m->hidden, &m->amax_v, &m->amax_i})
+    for (DevBuf* b : {&m->x, &m->x1, &m->att, &m->qkv, &m->hh, &m->part, &m->hidden, &m->amax_v, &m->amax_i,
+                      &m->tx, &m->tq, &m->ta, &m->tx1, &m->th, &m->counters})
         b->release();
     delete m;
+    return MING_OK;
+}
+
+int ming_lm_model_profile(ming_lm_model* m, void* stamps_dev) {
+    if (!m) return MING_E_NOT_INIT;
+    m->tstamp = static_cast<uint64_t*>(stamps_dev);
+    return MING_OK;
+}
+
+int ming_lm_model_profile_shape(ming_lm_model* m, int32_t* n_stamps, int32_t* grid) {
+    if (!m) return MING_E_NOT_INIT;
+    if (n_stamps) *n_stamps = 3 + 10 * m->cfg.n_layers;
+    if (grid) *grid = m->pgrid;
     return MING_OK;
 }
 
@@ -557,10 +592,34 @@ static int lm_step_impl(ming_ctx* ctx, ming_lm_model* m, const int32_t* token_de
                         hipMemcpyAsync(a.x, x_in, sizeof(uint16_t) * c->hidden, hipMemcpyDeviceToDevice, ctx->stream),
                         "copy x_in")))
         return st;
-    const bool persistent = (m->mode == MING_LM_PERSISTENT || m->mode == MING_LM_AUTO) && m->pgrid > 0;
-    if (persistent)
-        st = hip_check(ctx, launch_lm_step_persistent(ctx->stream, a, m->pgrid), "lm_step persistent launch");
-    else
+    // The persistent schedule runs every attention split on its own
+    // workgroup and merges at most 64 splits per kv head.
+    const int tsl = tagged_split_len(kv->len + 1);
+    const int nsplit = (kv->len + 1 + tsl - 1) / tsl;
+    const bool fits = m->pgrid > 0 && c->kv_heads * nsplit <= m->pgrid && nsplit <= 64;
+    const bool persistent = (m->mode == MING_LM_PERSISTENT || m->mode == MING_LM_AUTO) && fits;
+    if (m->mode == MING_LM_PERSISTENT && !fits)
+        return set_err(ctx, MING_E_UNSUPPORTED, "lm_step: context too long for the persistent schedule");
+    if (persistent) {
+        if (ctx->timeout_seen) {  // a timed-out step may have left arrival counters raised
+            if ((st = hip_check(ctx, hipMemsetAsync(m->counters.p, 0, m->counters.bytes, ctx->stream),
+                                "reset counters")))
+                return st;
+            ctx->timeout_seen = false;
+        }
+        a.tx = static_cast<uint64_t*>(m->tx.p);
+        a.tq = static_cast<uint64_t*>(m->tq.p);
+        a.ta = static_cast<uint64_t*>(m->ta.p);
+        a.tx1 = static_cast<uint64_t*>(m->tx1.p);
+        a.th = static_cast<uint64_t*>(m->th.p);
+        a.counters = static_cast<int32_t*>(m->counters.p);
+        a.tstamp = m->tstamp;
+        a.split_len = tsl;
+        a.epoch = ++m->epoch;
+        if (a.epoch == 0) a.epoch = ++m->epoch;
+        st = hip_check(ctx, launch_lm_step_tagged(ctx->stream, a, m->head.kind == 1, m->pgrid),
+                       "lm_step persistent launch");
+    } else
         st = hip_check(ctx, launch_lm_step_kernels(ctx->stream, a, m->layers.data()), "lm_step launch");
     if (st) return st;
     kv->len += 1;

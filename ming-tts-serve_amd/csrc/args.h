@@ -57,6 +57,16 @@ struct StepArgs {
     float* amax_v;            // [kMaxParts] argmax partials
     int32_t* amax_i;
     int32_t* flags;           // [0] error flag, [1] grid barrier counter
+    // Tagged hand-off buffers of the persistent schedule: u64 words holding a
+    // pair of bf16 values (low half) and the step's epoch (high half).
+    uint64_t* tx;             // [n_layers + 1][H/2]   layer inputs / stack output
+    uint64_t* tq;             // [n_layers][(H + 2*kvh*hd)/2]
+    uint64_t* ta;             // [n_layers][H/2]       merged attention
+    uint64_t* tx1;            // [n_layers][H/2]
+    uint64_t* th;             // [n_layers][I/2]
+    int32_t* counters;        // [n_layers * kvh] attention arrivals, [n_layers * kvh] head arrivals
+    uint32_t epoch;
+    uint64_t* tstamp;         // optional [n_stamps][grid] wall-clock stamps per stage boundary
 };
 
 constexpr int kMaxParts = 4096;

@@ -71,18 +71,41 @@ __device__ __forceinline__ float q4_word_dot(uint32_t w, const uint32_t* xp, flo
 
 // ---- reductions -------------------------------------------------------------
 
-template <int W>
-__device__ __forceinline__ float team_sum(float v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+// Butterfly reductions over aligned teams of W lanes (W = 2..64) on VALU
+// data paths: DPP quad_perm for lane distance 1 and 2, DPP half-row and row
+// mirrors to complete 8- and 16-lane groups, and gfx950's permlane16/32 swaps
+// across rows.  Each step combines two values symmetrically, so every lane of
+// a team ends with the bit-identical result.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+template <int W, class Op>
+__device__ __forceinline__ float team_reduce(float v, Op op) {
+    if (W > 1) v = op(v, dpp<0xB1>(v));   // quad_perm [1,0,3,2]
+    if (W > 2) v = op(v, dpp<0x4E>(v));   // quad_perm [2,3,0,1]
+    if (W > 4) v = op(v, dpp<0x141>(v));  // row_half_mirror
+    if (W > 8) v = op(v, dpp<0x140>(v));  // row_mirror
+    if (W > 16) {
+        const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = op(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    }
+    if (W > 32) {
+        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = op(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    }
     return v;
 }
 
 template <int W>
+__device__ __forceinline__ float team_sum(float v) {
+    return team_reduce<W>(v, [](float a, float b) { return a + b; });
+}
+
+template <int W>
 __device__ __forceinline__ float team_max(float v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
+    return team_reduce<W>(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 // Block-wide sum over blockDim.x threads (multiple of 64); `red` holds one

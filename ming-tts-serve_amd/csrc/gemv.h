@@ -33,6 +33,9 @@ __host__ __device__ constexpr int xstage_words(int K) { return K / 2 + K / 32; }
 // block participate; ends with __syncthreads().
 __device__ __forceinline__ void stage_q4(const uint16_t* x, int K, XStage st) {
     const int NC = K / 32, nw = K / 8;
+    // blockDim.x and nw are multiples of 4, so the 4 words of a chunk are
+    // handled by 4 adjacent lanes in the same iteration; their sums meet
+    // with two lane exchanges.
     for (int wi = threadIdx.x; wi < nw; wi += blockDim.x) {
         const int c = wi >> 2, j = wi & 3;
         const uint4 v = *reinterpret_cast<const uint4*>(x + 8 * wi);
@@ -43,17 +46,10 @@ __device__ __forceinline__ void stage_q4(const uint16_t* x, int K, XStage st) {
         o.z = (v.y & 0xffffu) | (v.w << 16);
         o.w = (v.y >> 16) | (v.w & 0xffff0000u);
         *reinterpret_cast<uint4*>(st.xs + (j * NC + c) * 4) = o;
-    }
-    // chunk sums: thread per chunk, in element order
-    for (int c = threadIdx.x; c < NC; c += blockDim.x) {
-        float s = 0.0f;
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + 32 * c);
-        for (int i = 0; i < 16; i++) {
-            const uint32_t u = p[i];
-            s += bf_lo(u);
-            s += bf_hi(u);
-        }
-        st.xh[c] = s;
+        float s = ((bf_lo(v.x) + bf_hi(v.x)) + (bf_lo(v.y) + bf_hi(v.y))) +
+                  ((bf_lo(v.z) + bf_hi(v.z)) + (bf_lo(v.w) + bf_hi(v.w)));
+        s = team_sum<4>(s);
+        if (j == 0) st.xh[c] = s;
     }
     __syncthreads();
 }
@@ -123,6 +119,107 @@ __device__ __forceinline__ float row_dot(const LinearDev& L, int n, const XStage
     float a = L.kind == 1 ? q4_row_partial<T>(L, n, st, tl) : bf16_row_partial<T>(L, n, st, tl);
     a = team_sum<T>(a);
     return L.kind == 1 ? a * L.gscale : a;
+}
+
+// ---- register-prefetched rows ----------------------------------------------
+// A lane's share of one weight row: NCH 16-byte chunks c = c0 + tl + T*j and,
+// for affine rows, each chunk's (scale, bias) pair packed in a u32.  Loading
+// is split from computing so that a stage can issue its weight loads before
+// the activation vector is ready (the HBM latency then overlaps the
+// normalisation and LDS staging).  Q4 selects the weight format at compile
+// time (1: MLX affine 4-bit, 0: bf16).
+template <int NCH>
+struct RowRegs {
+    uint4 w[NCH];
+    uint32_t sb[NCH];
+};
+
+template <int Q4>
+__device__ __forceinline__ int row_chunks(const LinearDev& L) { return Q4 ? L.K / 32 : L.K / 8; }
+
+template <int Q4, int T, int NCH>
+__device__ __forceinline__ void row_load(const LinearDev& L, int n, int tl, int c0, RowRegs<NCH>& r) {
+    const int NC = row_chunks<Q4>(L), G = L.K / 64;
+    const uint32_t* wrow = L.w + (size_t)n * (Q4 ? L.K / 8 : L.K / 2);
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+        const int c = c0 + tl + T * j;
+        if (c < NC) {
+            r.w[j] = ldg4(wrow + 4 * c);
+            if (Q4)
+                r.sb[j] = (uint32_t)L.s[(size_t)n * G + (c >> 1)] | ((uint32_t)L.b[(size_t)n * G + (c >> 1)] << 16);
+        } else {
+            r.w[j] = make_uint4(0, 0, 0, 0);
+            r.sb[j] = 0u;
+        }
+    }
+}
+
+// Partial (not team-reduced) dot of the chunks held in r.
+template <int Q4, int T, int NCH>
+__device__ __forceinline__ float row_compute(const LinearDev& L, const RowRegs<NCH>& r, const XStage& st, int tl,
+                                             int c0) {
+    const int NC = row_chunks<Q4>(L);
+    float acc = 0.0f;
+    if (Q4) {
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int c = c0 + tl + T * j;
+            if (c < NC) {
+                const uint4 x0 = *reinterpret_cast<const uint4*>(st.xs + (0 * NC + c) * 4);
+                const uint4 x1 = *reinterpret_cast<const uint4*>(st.xs + (1 * NC + c) * 4);
+                const uint4 x2 = *reinterpret_cast<const uint4*>(st.xs + (2 * NC + c) * 4);
+                const uint4 x3 = *reinterpret_cast<const uint4*>(st.xs + (3 * NC + c) * 4);
+                float a0 = q4_word_dot(r.w[j].x, reinterpret_cast<const uint32_t*>(&x0), 0.0f);
+                float a1 = q4_word_dot(r.w[j].y, reinterpret_cast<const uint32_t*>(&x1), 0.0f);
+                a0 = q4_word_dot(r.w[j].z, reinterpret_cast<const uint32_t*>(&x2), a0);
+                a1 = q4_word_dot(r.w[j].w, reinterpret_cast<const uint32_t*>(&x3), a1);
+                const float s = bf_lo(r.sb[j]), b = bf_hi(r.sb[j]);
+                acc = fmaf(s, a0 + a1, acc);
+                acc = fmaf(b - 128.0f * s, st.xh[c], acc);
+            }
+        }
+    } else {
+        float a1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int c = c0 + tl + T * j;
+            if (c < NC) {
+                const uint4 x = *reinterpret_cast<const uint4*>(st.xs + 4 * c);
+                acc = dot2(r.w[j].x, x.x, acc);
+                a1 = dot2(r.w[j].y, x.y, a1);
+                acc = dot2(r.w[j].z, x.z, acc);
+                a1 = dot2(r.w[j].w, x.w, a1);
+            }
+        }
+        acc += a1;
+    }
+    return acc;
+}
+
+// Row n with its first batch of chunks already in `first`; the remaining
+// batches (rows longer than T*NCH chunks) are loaded here.  Team-reduced,
+// global scale applied.
+template <int Q4, int T, int NCH>
+__device__ __forceinline__ float row_dot_pf(const LinearDev& L, int n, const XStage& st, int tl,
+                                            const RowRegs<NCH>& first) {
+    float acc = row_compute<Q4, T, NCH>(L, first, st, tl, 0);
+    const int NC = row_chunks<Q4>(L);
+    for (int c0 = T * NCH; c0 < NC; c0 += T * NCH) {
+        RowRegs<NCH> r;
+        row_load<Q4, T, NCH>(L, n, tl, c0, r);
+        acc += row_compute<Q4, T, NCH>(L, r, st, tl, c0);
+    }
+    acc = team_sum<T>(acc);
+    return Q4 ? acc * L.gscale : acc;
+}
+
+template <int Q4>
+__device__ __forceinline__ void stage_xk(const uint16_t* x, int K, XStage st) {
+    if (Q4)
+        stage_q4(x, K, st);
+    else
+        stage_bf16(x, K, st);
 }
 
 }  // namespace ming

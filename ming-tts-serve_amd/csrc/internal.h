@@ -39,6 +39,7 @@ struct ming_ctx {
     size_t max_lds = 0;
     bool alive = false;
     ming::DevBuf part;                // attention partials of ming_lm_layer
+    bool timeout_seen = false;        // ming_sync saw the device error flag
 };
 
 namespace ming {
