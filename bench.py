@@ -37,7 +37,7 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--ctx", type=int, default=2048)
-    p.add_argument("--mode", choices=["auto", "kernels", "persistent"], default="auto")
+    p.add_argument("--mode", choices=["auto", "kernels", "persistent", "direct"], default="auto")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     return p.parse_args()
@@ -59,7 +59,8 @@ def main():
     t0 = time.time()
     syn = S.SyntheticLm(ctx, spec, seed=0, quant=True)
     m = syn.model()
-    m.set_mode({"auto": ming.LM_AUTO, "kernels": ming.LM_KERNELS, "persistent": ming.LM_PERSISTENT}[args.mode])
+    m.set_mode({"auto": ming.LM_AUTO, "kernels": ming.LM_KERNELS, "persistent": ming.LM_PERSISTENT,
+                "direct": ming.LM_PERSISTENT_DIRECT}[args.mode])
     cache = S.KvCache(spec, args.ctx + 1)
     cache.fill_random(args.ctx, seed=1)
     torch.cuda.synchronize()

@@ -18,6 +18,10 @@ hipError_t launch_lm_step_tagged(hipStream_t st, const StepArgs& a, int q4, int 
 hipError_t launch_copy_token(hipStream_t st, const int32_t* src, int32_t* dst);
 int tagged_grid(int num_cus);
 int tagged_split_len(int n);
+int tagged_hubs(int grid);
+int tagged_img_stride(int H, int I);
+int tagged_max_layers();
+int tagged_units_per_worker();
 int attn_split_len(int n);
 size_t attn_part_floats(int kvh, int heads, int hd, int n);
 
@@ -199,6 +203,8 @@ struct ming_lm_model {
     // workspace
     DevBuf x, x1, att, qkv, hh, part, hidden, amax_v, amax_i;
     DevBuf tx, tq, ta, tx1, th, counters;  // tagged hand-off buffers, arrival counters
+    DevBuf img, hflag, hubtab;             // per-XCD hub images, their flags, hub XCC ids
+    int img_stride = 0, nflag = 0;
 };
 
 namespace {
@@ -491,7 +497,12 @@ int ming_lm_model_create(ming_ctx* ctx, const ming_lm_cfg* cfg, const ming_lm_la
     if (e == hipSuccess) e = m->tx1.ensure(sizeof(uint64_t) * (size_t)L * (H / 2));
     if (e == hipSuccess) e = m->th.ensure(sizeof(uint64_t) * (size_t)L * (I / 2));
     if (e == hipSuccess) e = m->counters.ensure(sizeof(int32_t) * (size_t)(L * cfg->kv_heads + 1));
-    for (DevBuf* b : {&m->tx, &m->tq, &m->ta, &m->tx1, &m->th, &m->counters})
+    m->img_stride = tagged_img_stride(H, I);
+    m->nflag = (4 * L + 1 + 31) / 32 * 32;  // whole 128-byte lines per hub
+    if (e == hipSuccess) e = m->img.ensure(sizeof(uint32_t) * (size_t)kMaxHubs * kImgSlots * m->img_stride);
+    if (e == hipSuccess) e = m->hflag.ensure(sizeof(uint32_t) * (size_t)kMaxHubs * m->nflag);
+    if (e == hipSuccess) e = m->hubtab.ensure(sizeof(uint64_t) * 32);
+    for (DevBuf* b : {&m->tx, &m->tq, &m->ta, &m->tx1, &m->th, &m->counters, &m->img, &m->hflag, &m->hubtab})
         if (e == hipSuccess) e = hipMemset(b->p, 0, b->bytes);
     if (e != hipSuccess) {
         ming_lm_model_destroy(m);
@@ -506,7 +517,7 @@ int ming_lm_model_destroy(ming_lm_model* m) {
     if (!m) return MING_E_NOT_INIT;
     if (m->d_layers) (void)hipFree(m->d_layers);
     for (DevBuf* b : {&m->x, &m->x1, &m->att, &m->qkv, &m->hh, &m->part, &m->hidden, &m->amax_v, &m->amax_i,
-                      &m->tx, &m->tq, &m->ta, &m->tx1, &m->th, &m->counters})
+                      &m->tx, &m->tq, &m->ta, &m->tx1, &m->th, &m->counters, &m->img, &m->hflag, &m->hubtab})
         b->release();
     delete m;
     return MING_OK;
@@ -527,7 +538,7 @@ int ming_lm_model_profile_shape(ming_lm_model* m, int32_t* n_stamps, int32_t* gr
 
 int ming_lm_model_set_mode(ming_lm_model* m, int32_t mode) {
     if (!m) return MING_E_NOT_INIT;
-    if (mode < MING_LM_AUTO || mode > MING_LM_PERSISTENT) return set_err(m->ctx, MING_E_ARG, "unknown mode");
+    if (mode < MING_LM_AUTO || mode > MING_LM_PERSISTENT_DIRECT) return set_err(m->ctx, MING_E_ARG, "unknown mode");
     m->mode = mode;
     return MING_OK;
 }
@@ -596,9 +607,16 @@ static int lm_step_impl(ming_ctx* ctx, ming_lm_model* m, const int32_t* token_de
     // workgroup and merges at most 64 splits per kv head.
     const int tsl = tagged_split_len(kv->len + 1);
     const int nsplit = (kv->len + 1 + tsl - 1) / tsl;
-    const bool fits = m->pgrid > 0 && c->kv_heads * nsplit <= m->pgrid && nsplit <= 64;
-    const bool persistent = (m->mode == MING_LM_PERSISTENT || m->mode == MING_LM_AUTO) && fits;
-    if (m->mode == MING_LM_PERSISTENT && !fits)
+    const bool want_persistent =
+        m->mode == MING_LM_PERSISTENT || m->mode == MING_LM_PERSISTENT_DIRECT || m->mode == MING_LM_AUTO;
+    const int nhubs = m->mode == MING_LM_PERSISTENT_DIRECT ? 0 : tagged_hubs(m->pgrid);
+    const int workers = m->pgrid - nhubs;
+    const int nq = c->hidden + 2 * c->kv_heads * c->head_dim;
+    const int upw = tagged_units_per_worker();
+    const bool fits = m->pgrid > 0 && c->kv_heads * nsplit <= workers && nsplit <= 64 && nq / 4 <= upw * workers &&
+                      c->hidden / 2 <= upw * workers && c->n_layers <= tagged_max_layers();
+    const bool persistent = want_persistent && fits;
+    if (want_persistent && m->mode != MING_LM_AUTO && !fits)
         return set_err(ctx, MING_E_UNSUPPORTED, "lm_step: context too long for the persistent schedule");
     if (persistent) {
         if (ctx->timeout_seen) {  // a timed-out step may have left arrival counters raised
@@ -614,6 +632,12 @@ static int lm_step_impl(ming_ctx* ctx, ming_lm_model* m, const int32_t* token_de
         a.th = static_cast<uint64_t*>(m->th.p);
         a.counters = static_cast<int32_t*>(m->counters.p);
         a.tstamp = m->tstamp;
+        a.nhubs = nhubs;
+        a.img = static_cast<uint32_t*>(m->img.p);
+        a.img_stride = m->img_stride;
+        a.hflag = static_cast<uint32_t*>(m->hflag.p);
+        a.nflag = m->nflag;
+        a.hubtab = static_cast<uint64_t*>(m->hubtab.p);
         a.split_len = tsl;
         a.epoch = ++m->epoch;
         if (a.epoch == 0) a.epoch = ++m->epoch;

@@ -67,7 +67,19 @@ struct StepArgs {
     int32_t* counters;        // [n_layers * kvh] attention arrivals, [n_layers * kvh] head arrivals
     uint32_t epoch;
     uint64_t* tstamp;         // optional [n_stamps][grid] wall-clock stamps per stage boundary
+    // Hubs of the persistent schedule (one workgroup per XCD): each publishes
+    // the staged GEMV input of every stage into memory that the other
+    // workgroups of its XCD read through their shared L2.
+    int nhubs;                // 0: every workgroup stages its own inputs
+    uint32_t* img;            // [kMaxHubs][kImgSlots][img_stride] stage images
+    int img_stride;           // u32 words per image slot
+    uint32_t* hflag;          // [kMaxHubs][nflag] epoch of each published image
+    int nflag;                // flag words per hub (>= 4 * n_layers + 1)
+    uint64_t* hubtab;         // [kMaxHubs] tagged XCC id of each hub
 };
+
+constexpr int kMaxHubs = 8;
+constexpr int kImgSlots = 5;  // q/k/v, o_proj, gate/up, down, LM head
 
 constexpr int kMaxParts = 4096;
 

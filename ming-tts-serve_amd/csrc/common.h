@@ -108,14 +108,23 @@ __device__ __forceinline__ float team_max(float v) {
     return team_reduce<W>(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also
+// drains every outstanding global load of the calling wave (its fence waits
+// for the memory counters); this one lets weight prefetches stay in flight.
+__device__ __forceinline__ void lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Block-wide sum over blockDim.x threads (multiple of 64); `red` holds one
 // float per wave.  All threads get the result.
 __device__ __forceinline__ float block_sum(float v, float* red) {
     v = team_sum<kWave>(v);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, nw = blockDim.x / kWave;
-    __syncthreads();
+    lds_sync();
     if (lane == 0) red[wave] = v;
-    __syncthreads();
+    lds_sync();
     float s = 0.0f;
     for (int i = 0; i < nw; i++) s += red[i];
     return s;
@@ -124,16 +133,38 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 __device__ __forceinline__ float block_max(float v, float* red) {
     v = team_max<kWave>(v);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, nw = blockDim.x / kWave;
-    __syncthreads();
+    lds_sync();
     if (lane == 0) red[wave] = v;
-    __syncthreads();
+    lds_sync();
     float s = -INFINITY;
     for (int i = 0; i < nw; i++) s = fmaxf(s, red[i]);
     return s;
 }
 
-// ---- loads ------------------------------------------------------------------
+// ---- global memory -------------------------------------------------------------
+// Accesses through these views compile to global_* instructions.  Through a
+// generic pointer whose origin the compiler cannot see (one loaded from an
+// argument block) they would be flat_* instructions, which also count against
+// the LDS counter: the next LDS access would then wait for them, which turns a
+// weight prefetch into a stall.
+#define MING_GLOBAL __attribute__((address_space(1)))
 
-__device__ __forceinline__ uint4 ldg4(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+template <class T>  // scalar T
+__device__ __forceinline__ T gld(const T* p) {
+    return *(const MING_GLOBAL T*)p;
+}
+template <class T>  // scalar T
+__device__ __forceinline__ void gst(T* p, T v) {
+    *(MING_GLOBAL T*)p = v;
+}
+__device__ __forceinline__ void gst(uint4* p, uint4 v) {
+    *(MING_GLOBAL u32x4_t*)p = u32x4_t{v.x, v.y, v.z, v.w};
+}
+__device__ __forceinline__ uint4 ldg4(const void* p) {
+    const u32x4_t v = *(const MING_GLOBAL u32x4_t*)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 }  // namespace ming

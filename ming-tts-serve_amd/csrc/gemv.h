@@ -29,6 +29,22 @@ struct XStage {
 
 __host__ __device__ constexpr int xstage_words(int K) { return K / 2 + K / 32; }
 
+// One group of 8 activations x[8g..8g+7], held as the bf16 pairs
+// (0,1),(2,3),(4,5),(6,7) in v: returns the nibble pair order
+// (0,4),(1,5),(2,6),(3,7) that goes to xs word j = g % 4 of chunk c = g / 4
+// (at (j * NC + c) * 4), and the f32 sum of the 8 values (the 4 groups of a
+// chunk add up to xh[c]).
+__device__ __forceinline__ uint4 q4_group(uint4 v, float& s) {
+    uint4 o;
+    o.x = (v.x & 0xffffu) | (v.z << 16);
+    o.y = (v.x >> 16) | (v.z & 0xffff0000u);
+    o.z = (v.y & 0xffffu) | (v.w << 16);
+    o.w = (v.y >> 16) | (v.w & 0xffff0000u);
+    s = ((bf_lo(v.x) + bf_hi(v.x)) + (bf_lo(v.y) + bf_hi(v.y))) +
+        ((bf_lo(v.z) + bf_hi(v.z)) + (bf_lo(v.w) + bf_hi(v.w)));
+    return o;
+}
+
 // Stage bf16 x [K] (global or LDS) for an affine matrix.  All threads of the
 // block participate; ends with __syncthreads().
 __device__ __forceinline__ void stage_q4(const uint16_t* x, int K, XStage st) {
@@ -38,16 +54,9 @@ __device__ __forceinline__ void stage_q4(const uint16_t* x, int K, XStage st) {
     // with two lane exchanges.
     for (int wi = threadIdx.x; wi < nw; wi += blockDim.x) {
         const int c = wi >> 2, j = wi & 3;
-        const uint4 v = *reinterpret_cast<const uint4*>(x + 8 * wi);
-        // v holds x[8wi+0..7] as pairs (0,1),(2,3),(4,5),(6,7); build (0,4),(1,5),(2,6),(3,7).
-        uint4 o;
-        o.x = (v.x & 0xffffu) | (v.z << 16);
-        o.y = (v.x >> 16) | (v.z & 0xffff0000u);
-        o.z = (v.y & 0xffffu) | (v.w << 16);
-        o.w = (v.y >> 16) | (v.w & 0xffff0000u);
+        float s;
+        const uint4 o = q4_group(*reinterpret_cast<const uint4*>(x + 8 * wi), s);
         *reinterpret_cast<uint4*>(st.xs + (j * NC + c) * 4) = o;
-        float s = ((bf_lo(v.x) + bf_hi(v.x)) + (bf_lo(v.y) + bf_hi(v.y))) +
-                  ((bf_lo(v.z) + bf_hi(v.z)) + (bf_lo(v.w) + bf_hi(v.w)));
         s = team_sum<4>(s);
         if (j == 0) st.xh[c] = s;
     }
@@ -123,15 +132,19 @@ __device__ __forceinline__ float row_dot(const LinearDev& L, int n, const XStage
 
 // ---- register-prefetched rows ----------------------------------------------
 // A lane's share of one weight row: NCH 16-byte chunks c = c0 + tl + T*j and,
-// for affine rows, each chunk's (scale, bias) pair packed in a u32.  Loading
-// is split from computing so that a stage can issue its weight loads before
-// the activation vector is ready (the HBM latency then overlaps the
-// normalisation and LDS staging).  Q4 selects the weight format at compile
+// for affine rows, each chunk's scale and bias (bf16 bits, zero-extended).
+// Loading is split from computing so that a stage can issue its weight loads
+// before the activation vector is ready (the HBM latency then overlaps the
+// wait for the input).  Nothing touches the loaded registers until the
+// compute step: an ALU use right after the load would make the compiler wait
+// for it there.  Lanes past the end of the row load the row's last chunk
+// again (same cache line) and mask it in the compute step, so the number of
+// loads does not depend on the lane.  Q4 selects the weight format at compile
 // time (1: MLX affine 4-bit, 0: bf16).
 template <int NCH>
 struct RowRegs {
     uint4 w[NCH];
-    uint32_t sb[NCH];
+    uint32_t s[NCH], b[NCH];
 };
 
 template <int Q4>
@@ -143,17 +156,17 @@ __device__ __forceinline__ void row_load(const LinearDev& L, int n, int tl, int 
     const uint32_t* wrow = L.w + (size_t)n * (Q4 ? L.K / 8 : L.K / 2);
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
-        const int c = c0 + tl + T * j;
-        if (c < NC) {
-            r.w[j] = ldg4(wrow + 4 * c);
-            if (Q4)
-                r.sb[j] = (uint32_t)L.s[(size_t)n * G + (c >> 1)] | ((uint32_t)L.b[(size_t)n * G + (c >> 1)] << 16);
+        const int c = min(c0 + tl + T * j, NC - 1);
+        r.w[j] = ldg4(wrow + 4 * c);
+        if (Q4) {
+            r.s[j] = gld(L.s + (size_t)n * G + (c >> 1));
+            r.b[j] = gld(L.b + (size_t)n * G + (c >> 1));
         } else {
-            r.w[j] = make_uint4(0, 0, 0, 0);
-            r.sb[j] = 0u;
+            r.s[j] = r.b[j] = 0u;
         }
     }
 }
+
 
 // Partial (not team-reduced) dot of the chunks held in r.
 template <int Q4, int T, int NCH>
@@ -174,7 +187,7 @@ __device__ __forceinline__ float row_compute(const LinearDev& L, const RowRegs<N
                 float a1 = q4_word_dot(r.w[j].y, reinterpret_cast<const uint32_t*>(&x1), 0.0f);
                 a0 = q4_word_dot(r.w[j].z, reinterpret_cast<const uint32_t*>(&x2), a0);
                 a1 = q4_word_dot(r.w[j].w, reinterpret_cast<const uint32_t*>(&x3), a1);
-                const float s = bf_lo(r.sb[j]), b = bf_hi(r.sb[j]);
+                const float s = bf2f((uint16_t)r.s[j]), b = bf2f((uint16_t)r.b[j]);
                 acc = fmaf(s, a0 + a1, acc);
                 acc = fmaf(b - 128.0f * s, st.xh[c], acc);
             }

@@ -1,19 +1,34 @@
 // One persistent kernel per decode token (the whole of QStack.decodeFused,
 // src/ming_model.zig:530-544, plus the tied LM head and argmax), with the
-// stages handing their outputs over through tagged words instead of grid
-// barriers.
+// stages handing their outputs over through tagged words and per-XCD hubs
+// instead of grid barriers.
 //
-// Hand-off: a stage's output vector is written as u64 words {bf16 pair, epoch}
-// with device-coherent (sc1) stores, and a consumer polls the words it needs
-// with device-coherent loads until every tag equals the step's epoch.  Data
-// and flag travel in one single-copy-atomic word, so no fence (no L2
-// write-back or invalidate) is needed and a hand-off costs one cross-XCD
-// store->load trip.  Buffers start zeroed and epochs start at 1, so a stale
-// word never matches.
+// Producers: a stage's output vector is written as u64 words {bf16 pair,
+// epoch} with device-coherent (sc1) stores.  Data and tag travel in one
+// single-copy-atomic word, so no fence (no L2 write-back or invalidate) is
+// needed.  Buffers start zeroed and epochs start at 1, so a stale word never
+// matches.
 //
-// Overlap: every workgroup issues the weight loads of its next units (and
-// attention workgroups their first K/V tile) before it polls for the stage's
-// input, so HBM latency is hidden behind the dependency chain.
+// Hubs: workgroups 0..7 run one per XCD (the dispatcher places workgroup i on
+// XCD i % 8; every workgroup reads its XCC id, and a workgroup whose XCD has
+// no hub polls and stages its inputs itself).  A hub polls each stage's input
+// vector with device-coherent loads, rms-normalises it where the stage does,
+// builds the GEMV stage image (nibble pair order plus chunk sums) and writes
+// it with ordinary stores, which stay in its XCD's L2.  A flag raised after
+// the image's stores have completed tells the workers of the XCD to copy the
+// image into LDS with device-scope loads, which the L2 serves because the
+// lines were written on this XCD.  A broadcast to 248 workgroups thus costs 8
+// device-coherent readers instead of 248, and a waiting worker polls one
+// word instead of the whole vector.
+//
+// Overlap: in a worker, wave 0 receives each stage's input while waves 1..7
+// have the stage's weight loads in flight.  Vector loads complete in issue
+// order, so a wave with outstanding weight loads could not see a poll result
+// before its weights; the split keeps the receive path free of them.  A
+// worker issues a stage's loads as soon as it enters the stage, which for
+// most workers is long before the input arrives (they skip the stages in
+// between), and attention workers issue their first K/V tile before they wait
+// for q.
 //
 // Attention splits meet through a per-(layer, kv head) arrival counter: the
 // workgroup that arrives last merges the partials.  The LM head's
@@ -22,8 +37,7 @@
 //
 // Every wait is bounded: past the spin limit a workgroup raises flags[0] and
 // continues, so the grid always drains; the host reports MING_E_TIMEOUT.
-// The kernel needs all workgroups co-resident (cooperative launch, one per
-// CU).
+// The kernel needs all workgroups co-resident (cooperative launch).
 #include "gemv.h"
 #include "internal.h"
 
@@ -33,14 +47,20 @@ namespace {
 
 constexpr int kT = 512;          // threads per workgroup (8 waves, 2 per SIMD)
 constexpr int kW = kT / kWave;   // waves per workgroup
+constexpr int kCW = kW - 1;      // compute waves (1..7); wave 0 receives each stage's input
 constexpr int kLds = 12288;      // LDS words (48 KB)
-constexpr int kXsOff = 0;        // XStage, K <= 8192: 4352 words
-constexpr int kRecvOff = 4400;   // received payloads, <= 4096 words
-constexpr int kHtOff = 8496;     // rms output, <= 2048 bf16
+constexpr int kXsOff = 0;        // stage image, K <= 8192: 4352 words (+3 copy padding)
 constexpr int kRedOff = 9520;    // reduction scratch (64 words)
 constexpr int kFlagOff = 9584;   // broadcast flags (16 words)
+constexpr int kLayOff = 12288;   // the layer table, copied once per launch: a stage's weight pointers and
+                                 // shapes are then LDS reads, not global loads that would queue behind prefetches
+constexpr int kMaxLdsLayers = 48;
+constexpr int kLayWords = (int)(sizeof(LayerDev) / 4);
+constexpr int kLdsTotal = kLayOff + kMaxLdsLayers * kLayWords;
+static_assert(sizeof(LayerDev) % 8 == 0, "layer table entries must keep 8-byte alignment in LDS");
 constexpr unsigned kSpin = 1u << 22;
 constexpr int kTile = 64;
+constexpr int kSc1 = 16;         // buffer-load cache policy bit: device scope
 
 template <int Q4>
 struct Nc {
@@ -49,32 +69,33 @@ struct Nc {
     static constexpr int up_units = Q4 ? 2 : 1;
 };
 
-__device__ __forceinline__ void tstore(uint64_t* p, uint32_t payload, uint32_t tag) {
-    __hip_atomic_store(p, ((uint64_t)tag << 32) | payload, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t tload(const uint64_t* p) {
-    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void cstore(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float cload(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int flag_set(int32_t* flags) {
-    return __hip_atomic_load(flags, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// The thread index through an opaque move: values derived from it are
+// recomputed where they are used instead of being hoisted out of the layer
+// loop into registers that stay live (and spill) for the whole kernel.
+__device__ __forceinline__ int tix() {
+    int t;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
+    return t;
 }
 
-// Pollers back off between rounds (s_sleep of about 64 cycles per unit, up
-// to 4 units), so a few hundred workgroups waiting on one small vector do not
-// crowd out the stores they are waiting for.
-__device__ __forceinline__ void poll_pause(unsigned s) {
-    if (s < 2)
-        __builtin_amdgcn_s_sleep(1);
-    else if (s < 8)
-        __builtin_amdgcn_s_sleep(2);
-    else
-        __builtin_amdgcn_s_sleep(4);
+// Device-coherent accesses (relaxed, agent scope) through global-space views.
+template <class T>
+__device__ __forceinline__ void astore(T* p, T v) {
+    __hip_atomic_store((MING_GLOBAL T*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ T aload(const T* p) {
+    return __hip_atomic_load((MING_GLOBAL T*)const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void tstore(uint64_t* p, uint32_t payload, uint32_t tag) {
+    astore(p, ((uint64_t)tag << 32) | payload);
+}
+__device__ __forceinline__ uint64_t tload(const uint64_t* p) { return aload(p); }
+__device__ __forceinline__ void cstore(float* p, float v) { astore(p, v); }
+__device__ __forceinline__ float cload(const float* p) { return aload(p); }
+__device__ __forceinline__ int flag_set(int32_t* flags) { return aload(flags); }
+__device__ __forceinline__ void raise_flag(int32_t* flags) {
+    __hip_atomic_fetch_or((MING_GLOBAL int32_t*)flags, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Poll one tagged word until it carries `tag` (bounded); returns its payload.
@@ -83,11 +104,10 @@ __device__ __forceinline__ uint32_t trecv1(const uint64_t* p, uint32_t tag, int3
     unsigned s = 0;
     while ((uint32_t)(w >> 32) != tag) {
         if (++s >= kSpin) {
-            atomicOr(flags, 1);
+            raise_flag(flags);
             break;
         }
         if ((s & 255u) == 0 && flag_set(flags)) break;
-        poll_pause(s);
         w = tload(p);
     }
     return (uint32_t)w;
@@ -98,42 +118,49 @@ __device__ __forceinline__ uint32_t tfinish(const uint64_t* p, uint64_t w, uint3
     return (uint32_t)(w >> 32) == tag ? (uint32_t)w : trecv1(p, tag, flags);
 }
 
-// Whole tagged vector of n words (n <= 8 * blockDim.x) into LDS (u32
-// payloads); ends with a barrier.  A thread issues the loads of all its words
-// at once and re-polls only the stale ones, so the wait is one round trip
-// after the last producer, not one per word.
-__device__ void trecv(const uint64_t* src, int n, uint32_t tag, uint32_t* dst, int32_t* flags) {
-    constexpr int kMaxPer = 8;
-    uint64_t w[kMaxPer];
+// Poll the 4 words of each group g = tix() + p * kT (p = 0, 1; g < ng)
+// of a tagged vector until all carry `tag` (bounded); payloads into v[4p+j].
+// All loads are issued at once and only stale words are polled again, so the
+// wait ends one round trip after the last producer.
+__device__ __forceinline__ void trecv_groups(const uint64_t* src, int ng, uint32_t tag, uint32_t (&v)[8],
+                                             int32_t* flags) {
+    uint64_t w[8];
 #pragma unroll
-    for (int k = 0; k < kMaxPer; k++) {
-        const int i = threadIdx.x + k * blockDim.x;
-        w[k] = i < n ? tload(src + i) : ((uint64_t)tag << 32);
+    for (int k = 0; k < 8; k++) {
+        const int g = tix() + (k >> 2) * kT;
+        w[k] = g < ng ? tload(src + 4 * g + (k & 3)) : ((uint64_t)tag << 32);
     }
     unsigned s = 0;
     while (true) {
         bool ready = true;
 #pragma unroll
-        for (int k = 0; k < kMaxPer; k++) ready &= (uint32_t)(w[k] >> 32) == tag;
+        for (int k = 0; k < 8; k++) ready &= (uint32_t)(w[k] >> 32) == tag;
         if (ready) break;
         if (++s >= kSpin) {
-            atomicOr(flags, 1);
+            raise_flag(flags);
             break;
         }
         if ((s & 255u) == 0 && flag_set(flags)) break;
-        poll_pause(s);
 #pragma unroll
-        for (int k = 0; k < kMaxPer; k++) {
-            const int i = threadIdx.x + k * blockDim.x;
-            if ((uint32_t)(w[k] >> 32) != tag) w[k] = tload(src + i);
+        for (int k = 0; k < 8; k++) {
+            const int g = tix() + (k >> 2) * kT;
+            if ((uint32_t)(w[k] >> 32) != tag) w[k] = tload(src + 4 * g + (k & 3));
         }
     }
 #pragma unroll
-    for (int k = 0; k < kMaxPer; k++) {
-        const int i = threadIdx.x + k * blockDim.x;
-        if (i < n) dst[i] = (uint32_t)w[k];
+    for (int k = 0; k < 8; k++) v[k] = (uint32_t)w[k];
+}
+
+// Poll a hub flag until it carries `tag` (bounded).
+__device__ __forceinline__ void wait_flag(const uint32_t* f, uint32_t tag, int32_t* flags) {
+    unsigned s = 0;
+    while (aload(f) != tag) {
+        if (++s >= kSpin) {
+            raise_flag(flags);
+            break;
+        }
+        if ((s & 255u) == 0 && flag_set(flags)) break;
     }
-    __syncthreads();
 }
 
 // Optional profile: wall-clock stamps of this workgroup.  Slot 0 is the
@@ -141,66 +168,186 @@ __device__ void trecv(const uint64_t* src, int n, uint32_t tag, uint32_t* dst, i
 // slot 1 + 2 (5 l + s) when its input has arrived and the next slot when it is
 // done; the head takes the two slots after the last layer.
 __device__ __forceinline__ void stamp(const StepArgs& a, int k) {
-    if (a.tstamp && threadIdx.x == 0) a.tstamp[(size_t)k * gridDim.x + blockIdx.x] = wall_clock64();
+    if (a.tstamp && tix() == 0) gst(a.tstamp + (size_t)k * gridDim.x + blockIdx.x, (uint64_t)wall_clock64());
 }
 __device__ __forceinline__ int slot_in(int l, int s) { return 1 + 2 * (5 * l + s); }
+// A stage's "done" stamp, taken when every wave of the workgroup is done.
+__device__ __forceinline__ void done_stamp(const StepArgs& a, int k) {
+    if (a.tstamp) {
+        lds_sync();
+        stamp(a, k);
+    }
+}
 
+// A worker: W workers, this one is w; hub is the hub workgroup of its XCD
+// (or -1: stage inputs itself).
 struct Ctx {
     const StepArgs& a;
     uint32_t* lds;
-    int G, wg, wave, lane, team, tl;
+    int W, w, wave, lane, team, tl, hub;
 };
 
 __device__ __forceinline__ XStage xs_of(uint32_t* lds, int K) {
     return XStage{lds + kXsOff, reinterpret_cast<float*>(lds + kXsOff + K / 2)};
 }
-__device__ __forceinline__ uint16_t* recv16(uint32_t* lds) { return reinterpret_cast<uint16_t*>(lds + kRecvOff); }
 
-// MLX fast::rms_norm of x (LDS) into LDS.
-__device__ void rms_lds(const uint16_t* x, const uint16_t* w, int H, float eps, uint16_t* h, float* rd) {
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < H; i += blockDim.x) {
-        const float v = bf2f(x[i]);
-        ss += v * v;
+// ---- stage images ------------------------------------------------------------------
+// Receive the tagged bf16 vector src [K/2 words], optionally rms-normalise it
+// with norm_w (MLX fast::rms_norm: bf16(w * bf16(x * rsqrt(mean(x^2) + eps)))),
+// and write its GEMV stage image to dst (LDS or global): xs [K/2] and, for
+// affine weights, the chunk sums xh [K/32] right after it.  `hidden`, if not
+// null, receives the (normalised) vector.  Thread t owns the 8-value groups
+// t and t + kT (K <= 8192).  All threads of the block call it.
+template <int Q4, bool TO_LDS>
+__device__ __forceinline__ void build_image(const StepArgs& a, uint32_t* lds, const uint64_t* src, int K,
+                                            const uint16_t* norm_w, uint32_t* dst, uint16_t* hidden) {
+    // dst is LDS (a worker staging for itself) or global memory (a hub image)
+    auto put4 = [&](int word, uint4 v) {
+        if (TO_LDS)
+            *reinterpret_cast<uint4*>(dst + word) = v;
+        else
+            gst(reinterpret_cast<uint4*>(dst + word), v);
+    };
+    auto put1 = [&](int word, float v) {
+        if (TO_LDS)
+            reinterpret_cast<float*>(dst)[word] = v;
+        else
+            gst(reinterpret_cast<float*>(dst) + word, v);
+    };
+    const int ng = K / 8, NC = K / 32;
+    uint4 nw[2];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const int g = tix() + p * kT;
+        nw[p] = (norm_w && g < ng) ? ldg4(norm_w + 8 * g) : make_uint4(0, 0, 0, 0);
     }
-    ss = block_sum(ss, rd);
-    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-    for (int i = threadIdx.x; i < H; i += blockDim.x) h[i] = f2bf(bf2f(w[i]) * rb(bf2f(x[i]) * inv));
-    __syncthreads();
+    uint32_t v[8];
+    trecv_groups(src, ng, a.epoch, v, a.flags);
+    if (norm_w) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float lo = bf_lo(v[k]), hi = bf_hi(v[k]);
+            ss += lo * lo;
+            ss += hi * hi;
+        }
+        ss = block_sum(ss, reinterpret_cast<float*>(lds + kRedOff));
+        const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const uint32_t wn[4] = {nw[p].x, nw[p].y, nw[p].z, nw[p].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t x = v[4 * p + j];
+                v[4 * p + j] = pack_bf2(bf_lo(wn[j]) * rb(bf_lo(x) * inv), bf_hi(wn[j]) * rb(bf_hi(x) * inv));
+            }
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const int g = tix() + p * kT;
+        const bool act = g < ng;
+        const uint4 x = make_uint4(v[4 * p], v[4 * p + 1], v[4 * p + 2], v[4 * p + 3]);
+        if (hidden && act) gst(reinterpret_cast<uint4*>(hidden + 8 * g), x);
+        if (Q4) {
+            float s;
+            const uint4 o = q4_group(x, s);
+            if (act) put4(((g & 3) * NC + (g >> 2)) * 4, o);
+            s = team_sum<4>(s);  // ng is a multiple of 4: a quad of lanes is active or idle together
+            if (act && (g & 3) == 0) put1(K / 2 + (g >> 2), s);
+        } else if (act) {
+            put4(4 * g, x);
+        }
+    }
 }
 
-// Receive a tagged bf16 vector of K values, optionally rms-normalise it, and
-// stage it for a GEMV.
+// Worker: the stage image of flag fidx / image slot `slot` into LDS (xs at
+// kXsOff).  With a hub, wave 0 waits for its flag and copies the image (waves
+// 1..7 meanwhile have their weight loads in flight); without one, all waves
+// build it here.  The first barrier also ends the previous stage's use of LDS.
 template <int Q4>
-__device__ void recv_stage(const Ctx& c, const uint64_t* src, int K, const uint16_t* norm_w, uint16_t* h_out = nullptr) {
+__device__ __forceinline__ void get_image(const Ctx& c, int fidx, int slot, const uint64_t* src, int K,
+                                          const uint16_t* norm_w, uint16_t* hidden) {
     const StepArgs& a = c.a;
-    trecv(src, K / 2, a.epoch, c.lds + kRecvOff, a.flags);
-    const uint16_t* x = recv16(c.lds);
-    if (norm_w) {
-        uint16_t* h = reinterpret_cast<uint16_t*>(c.lds + kHtOff);
-        rms_lds(x, norm_w, K, a.eps, h, reinterpret_cast<float*>(c.lds + kRedOff));
-        if (h_out)
-            for (int i = threadIdx.x; i < K; i += blockDim.x) h_out[i] = h[i];
-        x = h;
+    if (c.hub < 0) {
+        lds_sync();
+        build_image<Q4, true>(a, c.lds, src, K, norm_w, c.lds + kXsOff, hidden);
+        lds_sync();
+        return;
     }
-    stage_xk<Q4>(x, K, xs_of(c.lds, K));
+    if (c.wave == 0 && c.lane == 0) wait_flag(a.hflag + (size_t)c.hub * a.nflag + fidx, a.epoch, a.flags);
+    lds_sync();
+    if (c.wave == 0) {
+        const int n4 = ((Q4 ? K / 2 + K / 32 : K / 2) + 3) / 4;
+        const uint32_t* img = a.img + ((size_t)c.hub * kImgSlots + slot) * a.img_stride;
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(img), 0, a.img_stride * 4, 0x00020000);
+        for (int i = c.lane; i < n4; i += kWave) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, i * 16, 0, kSc1);
+            reinterpret_cast<uint4*>(c.lds + kXsOff)[i] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+    }
+    lds_sync();
+}
+
+// Hub: build and publish one stage image, then raise its flag.  The barrier
+// waits for every thread's stores to complete (its release fence drains the
+// memory counters), so the flag is raised after the whole image is in L2.
+template <int Q4>
+__device__ __forceinline__ void hub_publish(const StepArgs& a, uint32_t* lds, const uint64_t* src, int K, const uint16_t* norm_w,
+                            uint32_t* img, uint32_t* flag, uint16_t* hidden) {
+    build_image<Q4, false>(a, lds, src, K, norm_w, img, hidden);
+    __syncthreads();
+    if (tix() == 0) gst(flag, a.epoch);
+}
+
+template <int Q4>
+__device__ __forceinline__ void hub_main(const StepArgs& a, const LayerDev* __restrict__ layers, uint32_t* lds, int b,
+                                         uint32_t xcc) {
+    if (tix() == 0) tstore(a.hubtab + b, xcc, a.epoch);
+    uint32_t* img = a.img + (size_t)b * kImgSlots * a.img_stride;
+    uint32_t* fl = a.hflag + (size_t)b * a.nflag;
+    const int H = a.H, L = a.n_layers;
+    const size_t st = a.img_stride;
+    for (int l = 0; l < L; l++) {
+        const LayerDev& Ld = layers[l];
+        hub_publish<Q4>(a, lds, a.tx + (size_t)l * (H / 2), H, Ld.ln1, img, fl + 4 * l, nullptr);
+        hub_publish<Q4>(a, lds, a.ta + (size_t)l * (H / 2), H, nullptr, img + st, fl + 4 * l + 1, nullptr);
+        hub_publish<Q4>(a, lds, a.tx1 + (size_t)l * (H / 2), H, Ld.ln2, img + 2 * st, fl + 4 * l + 2, nullptr);
+        hub_publish<Q4>(a, lds, a.th + (size_t)l * (a.I / 2), a.I, nullptr, img + 3 * st, fl + 4 * l + 3, nullptr);
+    }
+    hub_publish<Q4>(a, lds, a.tx + (size_t)L * (H / 2), H, a.final_norm, img + 4 * st, fl + 4 * L,
+                    b == 0 ? a.hidden : nullptr);
+}
+
+// Worker: the first hub whose XCC id equals this workgroup's, or -1.
+__device__ __forceinline__ int find_hub(const StepArgs& a, uint32_t* lds, uint32_t xcc) {
+    int* sel = reinterpret_cast<int*>(lds + kFlagOff + 1);
+    if (tix() < kWave) {
+        uint32_t hx = 0xffffffffu;
+        if ((int)tix() < a.nhubs) hx = trecv1(a.hubtab + tix(), a.epoch, a.flags);
+        const unsigned long long m = __ballot(hx == xcc);
+        if (tix() == 0) *sel = m ? __ffsll(m) - 1 : -1;
+    }
+    __syncthreads();
+    return *sel;
 }
 
 // ---- embed / input row -> tx[0] ----------------------------------------------
-__device__ void st_embed(const Ctx& c) {
+__device__ __forceinline__ void st_embed(const Ctx& c) {
     const StepArgs& a = c.a;
     const int nw = a.H / 2;
-    for (int i = c.wg * kT + threadIdx.x; i < nw; i += c.G * kT) {
+    for (int i = c.w * kT + tix(); i < nw; i += c.W * kT) {
         uint32_t v;
         if (a.token_in) {
             const LinearDev& E = a.embed;
-            int id = *a.token_in;
+            int id = gld(a.token_in);
             id = id < 0 ? 0 : (id >= E.N ? E.N - 1 : id);
             const int k = 2 * i;
             if (E.kind == 1) {
-                const uint32_t word = E.w[(size_t)id * (E.K / 8) + k / 8];
-                const float sc = bf2f(E.s[(size_t)id * (E.K / 64) + k / 64]);
-                const float bi = bf2f(E.b[(size_t)id * (E.K / 64) + k / 64]);
+                const uint32_t word = gld(E.w + (size_t)id * (E.K / 8) + k / 8);
+                const float sc = bf2f(gld(E.s + (size_t)id * (E.K / 64) + k / 64));
+                const float bi = bf2f(gld(E.b + (size_t)id * (E.K / 64) + k / 64));
                 float v0 = sc * (float)((word >> (4 * (k % 8))) & 0xfu) + bi;
                 float v1 = sc * (float)((word >> (4 * (k % 8) + 4)) & 0xfu) + bi;
                 if (E.gscale != 1.0f) {
@@ -209,11 +356,11 @@ __device__ void st_embed(const Ctx& c) {
                 }
                 v = pack_bf2(v0, v1);
             } else {
-                v = reinterpret_cast<const uint32_t*>(E.w)[((size_t)id * E.K + k) / 2];
+                v = gld(reinterpret_cast<const uint32_t*>(E.w) + ((size_t)id * E.K + k) / 2);
             }
-            reinterpret_cast<uint32_t*>(a.x)[i] = v;
+            gst(reinterpret_cast<uint32_t*>(a.x) + i, v);
         } else {
-            v = reinterpret_cast<const uint32_t*>(a.x)[i];
+            v = gld(reinterpret_cast<const uint32_t*>(a.x) + i);
         }
         tstore(a.tx + i, v, a.epoch);
     }
@@ -222,12 +369,8 @@ __device__ void st_embed(const Ctx& c) {
 // ---- LA: q/k/v + bias + rope ----------------------------------------------------
 // Unit = quad of rows (c, c+1, c+hd/2, c+hd/2+1) of the concatenated [q|k|v]
 // rows, c even; team 0 computes the first two, team 1 the other two, so each
-// output word (c, c+1) has one writer.  Units are packed: unit = wg*kW + wave.
-//
-// Every GEMV stage is split into `load` (issue this workgroup's weight loads
-// into registers) and `run` (wait for the input vector, compute, hand over).
-// The kernel issues stage s+1's loads before it runs stage s, so weights are
-// in flight one stage ahead across the whole chain, layers included.
+// output word (c, c+1) has one writer.  Units are packed on the compute waves:
+// unit = w*kCW + wave - 1.
 struct QkvGeom {
     bool any, has;
     int cr, which, base, r0;
@@ -238,9 +381,10 @@ __device__ __forceinline__ QkvGeom qkv_geom(const Ctx& c) {
     const int half = a.hd / 2, kvd = a.kvh * a.hd, nq = a.H + 2 * kvd;
     const int nunits = nq / 4, qpb = half / 2;  // quads per head block
     QkvGeom g;
-    g.any = c.wg * kW < nunits;
-    const int q = c.wg * kW + c.wave;
-    g.has = q < nunits;
+    const int u = c.w * kCW + c.wave - 1;
+    g.any = c.w * kCW < nunits;
+    g.has = c.wave > 0 && u < nunits;
+    const int q = max(0, min(u, nunits - 1));
     g.cr = (q / qpb) * a.hd + (q % qpb) * 2;  // concatenated row c
     g.which = g.cr < a.H ? 0 : (g.cr < a.H + kvd ? 1 : 2);
     g.base = g.which == 0 ? 0 : (g.which == 1 ? a.H : a.H + kvd);
@@ -248,54 +392,59 @@ __device__ __forceinline__ QkvGeom qkv_geom(const Ctx& c) {
     return g;
 }
 
+__device__ __forceinline__ bool in_qkv(const Ctx& c) { return qkv_geom(c).any; }
+
 template <int Q4>
 struct QkvW {
     RowRegs<Nc<Q4>::t32> w0, w1;
+    uint32_t bias[2];    // bias pairs (lr, lr+1) and (lr+hd/2, lr+hd/2+1)
+    float cs[2], sn[2];  // rope factors of dims d, d+1 (they do not depend on the input)
 };
 
 template <int Q4>
-__device__ void qkv_load(const Ctx& c, const LayerDev& Ld, QkvW<Q4>& W) {
-    const QkvGeom g = qkv_geom(c);
-    if (!g.has) return;
-    const LinearDev& L = g.which == 0 ? Ld.q : (g.which == 1 ? Ld.k : Ld.v);
-    row_load<Q4, 32, Nc<Q4>::t32>(L, g.r0, c.tl, 0, W.w0);
-    row_load<Q4, 32, Nc<Q4>::t32>(L, g.r0 + 1, c.tl, 0, W.w1);
-}
-
-template <int Q4>
-__device__ void st_qkv(const Ctx& c, const LayerDev& Ld, int l, const QkvW<Q4>& W) {
+__device__ __forceinline__ void st_qkv(const Ctx& c, const LayerDev& Ld, int l) {
     const StepArgs& a = c.a;
     const int half = a.hd / 2, kvd = a.kvh * a.hd, nq = a.H + 2 * kvd;
     const QkvGeom g = qkv_geom(c);
-    if (!g.any) return;
-    const bool has = g.has;
-    const int cr = g.cr, which = g.which, base = g.base, r0 = g.r0;
+    const int cr = g.cr, which = g.which, base = g.base, r0 = g.r0, lr = cr - base;
     const LinearDev& L = which == 0 ? Ld.q : (which == 1 ? Ld.k : Ld.v);
-    recv_stage<Q4>(c, a.tx + (size_t)l * (a.H / 2), a.H, Ld.ln1);
+    QkvW<Q4> W;
+    if (g.has) {
+        // MLX fast::rope, non-traditional: pairs (d, d + hd/2); computed
+        // before the weight loads are issued, as large angles may read
+        // reduction tables
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int d = (lr + i) % a.hd;
+            const float inv_freq = exp2f(-((float)d / (float)half) * a.log2_theta);
+            const float th = (float)a.pos * inv_freq;
+            W.cs[i] = cosf(th);
+            W.sn[i] = sinf(th);
+        }
+        asm volatile("" ::: "memory");
+        const uint32_t* b32 = reinterpret_cast<const uint32_t*>(which == 0 ? Ld.bq : (which == 1 ? Ld.bk : Ld.bv));
+        W.bias[0] = gld(b32 + lr / 2);
+        W.bias[1] = gld(b32 + (lr + half) / 2);
+        row_load<Q4, 32, Nc<Q4>::t32>(L, r0, c.tl, 0, W.w0);
+        row_load<Q4, 32, Nc<Q4>::t32>(L, r0 + 1, c.tl, 0, W.w1);
+    }
+    get_image<Q4>(c, 4 * l, 0, a.tx + (size_t)l * (a.H / 2), a.H, Ld.ln1, nullptr);
     stamp(a, slot_in(l, 0));
-    if (!has) return;
+    if (!g.has) return;
     const XStage st = xs_of(c.lds, a.H);
     const float acc0 = row_dot_pf<Q4, 32, Nc<Q4>::t32>(L, r0, st, c.tl, W.w0);
     const float acc1 = row_dot_pf<Q4, 32, Nc<Q4>::t32>(L, r0 + 1, st, c.tl, W.w1);
     const float v[4] = {__shfl(acc0, 0, kWave), __shfl(acc1, 0, kWave), __shfl(acc0, 32, kWave),
                         __shfl(acc1, 32, kWave)};
     if (c.lane != 0) return;
-    const uint16_t* bias = which == 0 ? Ld.bq : (which == 1 ? Ld.bk : Ld.bv);
-    const int lr = cr - base;
+    const float bias[4] = {bf_lo(W.bias[0]), bf_hi(W.bias[0]), bf_lo(W.bias[1]), bf_hi(W.bias[1])};
     float e[4];
-    const int off[4] = {0, 1, half, half + 1};
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float bv = bf2f(bias[lr + off[i]]);
-        e[i] = Q4 ? rb(rb(v[i]) + bv) : rb(v[i] + bv);
-    }
-    if (which < 2) {  // MLX fast::rope, non-traditional: pairs (d, d + hd/2)
+    for (int i = 0; i < 4; i++) e[i] = Q4 ? rb(rb(v[i]) + bias[i]) : rb(v[i] + bias[i]);
+    if (which < 2) {
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const int d = (lr + i) % a.hd;
-            const float inv_freq = exp2f(-((float)d / (float)half) * a.log2_theta);
-            const float th = (float)a.pos * inv_freq;
-            const float cs = cosf(th), sn = sinf(th);
+            const float cs = W.cs[i], sn = W.sn[i];
             const float x1 = e[i], x2 = e[i + 2];
             const float o1 = x1 * cs - x2 * sn, o2 = x1 * sn + x2 * cs;
             e[i] = rb(o1);
@@ -307,23 +456,23 @@ __device__ void st_qkv(const Ctx& c, const LayerDev& Ld, int l, const QkvW<Q4>& 
     tstore(tq + cr / 2, w_lo, a.epoch);
     tstore(tq + (cr + half) / 2, w_hi, a.epoch);
     uint32_t* pq = reinterpret_cast<uint32_t*>(a.qkv + l * a.sq);
-    pq[cr / 2] = w_lo;
-    pq[(cr + half) / 2] = w_hi;
+    gst(pq + cr / 2, w_lo);
+    gst(pq + (cr + half) / 2, w_hi);
     if (which > 0) {
         uint16_t* cache = which == 1 ? a.kc : a.vc;
         const int kh = lr / a.hd, d = lr % a.hd;
         uint32_t* dst = reinterpret_cast<uint32_t*>(cache + (((size_t)l * a.kvh + kh) * a.cap + a.pos) * a.hd);
-        dst[d / 2] = w_lo;
-        dst[(d + half) / 2] = w_hi;
+        gst(dst + d / 2, w_lo);
+        gst(dst + (d + half) / 2, w_hi);
     }
 }
 
 // ---- LB: split-K GQA attention + last-arriver merge ----------------------------
-// Unit = (kv head g, split of positions), on the last workgroups of the grid.
-// The split is walked in tiles of 64 positions: each thread loads one 16 B
-// chunk of K and one of V per tile (the next tile's loads are issued before
-// the current one is computed); scores use 8 lanes per position, the online
-// softmax one wave per head, P.V one thread per (head, dim).
+// Unit = (kv head g, split of positions), on the last workers.  The split is
+// walked in tiles of 64 positions: each thread loads one 16 B chunk of K and
+// one of V per tile (the next tile's loads are issued before the current one
+// is computed); scores use 8 lanes per position, the online softmax one wave
+// per head, P.V one thread per (head, dim).
 struct ALds {
     float* q;       // [8][64]
     uint16_t* k;    // [64][64]
@@ -350,41 +499,73 @@ __device__ __forceinline__ ALds alds(uint32_t* lds) {
     return s;
 }
 
-__device__ void st_attn(const Ctx& c, int l) {
+// This worker's attention unit: kv head g, positions [j0, j1) of ns splits.
+struct AttnGeom {
+    int u, ns, g, sp, j0, j1;
+};
+
+__device__ __forceinline__ AttnGeom attn_geom(const Ctx& c) {
     const StepArgs& a = c.a;
-    const int n = a.pos + 1, ns = (n + a.split_len - 1) / a.split_len, grp = a.heads / a.kvh, hd = a.hd;
-    const int U = a.kvh * ns;
-    const int u = c.G - 1 - c.wg;  // attention units on the last workgroups
-    if (u < 0 || u >= U) return;
-    const int g = u / ns, sp = u % ns;
-    const int j0 = sp * a.split_len, j1 = min(n, j0 + a.split_len);
+    AttnGeom q;
+    const int n = a.pos + 1;
+    q.ns = (n + a.split_len - 1) / a.split_len;
+    q.u = c.W - 1 - c.w;  // attention units on the last workers
+    q.g = q.u / q.ns;
+    q.sp = q.u % q.ns;
+    q.j0 = q.sp * a.split_len;
+    q.j1 = min(n, q.j0 + a.split_len);
+    return q;
+}
+
+__device__ __forceinline__ bool in_attn(const Ctx& c) {
+    const AttnGeom q = attn_geom(c);
+    return q.u >= 0 && q.u < c.a.kvh * q.ns;
+}
+
+// K/V chunk of this thread in a 64-position tile: cached rows (< pos) come
+// from the cache; row pos arrives with q through the tagged q|k|v.
+struct AttnTile {
+    uint4 k, v;
+};
+
+// Rows past the split or not yet cached load row min(row, ...) instead (the
+// loads take no branch); attn_tile_valid() tells which rows to zero.
+__device__ __forceinline__ void attn_tile_load(const Ctx& c, int l, const AttnGeom& q, int t0, AttnTile& r) {
+    const StepArgs& a = c.a;
+    const int row = t0 + tix() / 8, col = tix() % 8;
+    const int rr = max(0, min(row, min(q.j1, a.pos) - 1));
+    const size_t off = ((((size_t)l * a.kvh + q.g) * a.cap) + rr) * a.hd + 8 * col;
+    r.k = ldg4(a.kc + off);
+    r.v = ldg4(a.vc + off);
+}
+__device__ __forceinline__ bool attn_tile_valid(const Ctx& c, const AttnGeom& q, int t0) {
+    const int row = t0 + tix() / 8;
+    return row < q.j1 && row < c.a.pos;
+}
+
+// The first tile's loads, issued a stage ahead.
+__device__ __forceinline__ void attn_pre(const Ctx& c, int l, AttnTile& r) {
+    const AttnGeom q = attn_geom(c);
+    attn_tile_load(c, l, q, q.j0, r);
+}
+
+// Wait for this unit's q rows (and, in the split holding position pos, the
+// new k/v row) and stage them in LDS.
+__device__ __forceinline__ void attn_recv(const Ctx& c, int l) {
+    const StepArgs& a = c.a;
+    const AttnGeom q = attn_geom(c);
+    const int grp = a.heads / a.kvh, hd = a.hd, g = q.g, t = tix();
     const ALds S = alds(c.lds);
-    const int t = threadIdx.x;
-    const uint16_t* kbase = a.kc + (((size_t)l * a.kvh + g) * a.cap) * hd;
-    const uint16_t* vbase = a.vc + (((size_t)l * a.kvh + g) * a.cap) * hd;
-    const int trow = t / 8, tcol = t % 8;  // this thread's 16 B chunk of a 64 x 128 B tile
-    uint4 kr, vr;
-    // cached rows (< pos) come from the cache; row pos from the tagged q|k|v
-    auto load_tile = [&](int t0) {
-        const int row = t0 + trow;
-        if (row < j1 && row < a.pos) {
-            kr = ldg4(kbase + (size_t)row * hd + 8 * tcol);
-            vr = ldg4(vbase + (size_t)row * hd + 8 * tcol);
-        } else {
-            kr = make_uint4(0, 0, 0, 0);
-            vr = make_uint4(0, 0, 0, 0);
-        }
-    };
-    load_tile(j0);
     const int nq = a.H + 2 * a.kvh * hd;
     const uint64_t* tq = a.tq + (size_t)l * (nq / 2);
     const float scale = 1.0f / sqrtf((float)hd);
+    lds_sync();  // the previous stage is done with LDS
     for (int i = t; i < grp * hd / 2; i += kT) {
         const uint32_t w = trecv1(tq + (g * grp * hd) / 2 + i, a.epoch, a.flags);
         S.q[2 * i] = scale * bf_lo(w);
         S.q[2 * i + 1] = scale * bf_hi(w);
     }
-    if (j1 > a.pos && t < hd) {  // this split holds the new row
+    if (q.j1 > a.pos && t < hd) {  // this split holds the new row
         const uint64_t* src =
             t < hd / 2 ? tq + (a.H + g * hd) / 2 + t : tq + (a.H + a.kvh * hd + g * hd) / 2 + t - hd / 2;
         const uint32_t w = trecv1(src, a.epoch, a.flags);
@@ -395,20 +576,29 @@ __device__ void st_attn(const Ctx& c, int l) {
     }
     if (t < 32) S.ml[t] = (t % 4 == 0) ? -INFINITY : 0.0f;
     stamp(a, slot_in(l, 1));
+}
+
+__device__ __forceinline__ void attn_run(const Ctx& c, int l, AttnTile tile) {
+    const StepArgs& a = c.a;
+    const AttnGeom q = attn_geom(c);
+    const int ns = q.ns, g = q.g, sp = q.sp, j0 = q.j0, j1 = q.j1;
+    const int grp = a.heads / a.kvh, hd = a.hd, t = tix();
+    const ALds S = alds(c.lds);
     const int hp = t / 64, d = t % 64;  // P.V: thread owns dim d of head hp
     float acc = 0.0f;
     for (int t0 = j0; t0 < j1; t0 += kTile) {
         const int cnt = min(kTile, j1 - t0);
-        __syncthreads();
-        reinterpret_cast<uint4*>(S.k)[t] = kr;
-        reinterpret_cast<uint4*>(S.v)[t] = vr;
-        __syncthreads();
+        lds_sync();
+        const bool ok = attn_tile_valid(c, q, t0);
+        reinterpret_cast<uint4*>(S.k)[t] = ok ? tile.k : make_uint4(0, 0, 0, 0);
+        reinterpret_cast<uint4*>(S.v)[t] = ok ? tile.v : make_uint4(0, 0, 0, 0);
+        lds_sync();
         if (a.pos >= t0 && a.pos < t0 + cnt && t < hd / 2) {  // new row
             reinterpret_cast<uint32_t*>(S.k + (a.pos - t0) * hd)[t] = S.kn[t];
             reinterpret_cast<uint32_t*>(S.v + (a.pos - t0) * hd)[t] = S.vn[t];
         }
-        __syncthreads();
-        if (t0 + kTile < j1) load_tile(t0 + kTile);
+        lds_sync();
+        if (t0 + kTile < j1) attn_tile_load(c, l, q, t0 + kTile, tile);
         {   // scores: 8 lanes per position, 8 dims each
             const int p = t >> 3, qt = t & 7;
             const uint4 kk = *reinterpret_cast<const uint4*>(S.k + p * hd + qt * 8);
@@ -425,7 +615,7 @@ __device__ void st_attn(const Ctx& c, int l) {
                 if (qt == 0) S.p[h * kTile + p] = p < cnt ? s : -INFINITY;
             }
         }
-        __syncthreads();
+        lds_sync();
         if (c.wave < grp) {  // online softmax, one wave per head, lane = position
             const int h = c.wave;
             const float s = S.p[h * kTile + c.lane];
@@ -441,7 +631,7 @@ __device__ void st_attn(const Ctx& c, int l) {
                 S.ml[4 * h + 2] = corr;
             }
         }
-        __syncthreads();
+        lds_sync();
         if (hp < grp) {
             const float* ph = S.p + hp * kTile;
             float s0 = 0.0f, s1 = 0.0f;
@@ -453,7 +643,7 @@ __device__ void st_attn(const Ctx& c, int l) {
             acc = acc * S.ml[4 * hp + 2] + (s0 + s1);
         }
     }
-    __syncthreads();
+    lds_sync();
     // partials: device-coherent stores, completed before the arrival
     if (hp < grp) {
         float* out = a.part + ((size_t)(g * ns + sp) * grp + hp) * (hd + 2);
@@ -468,11 +658,11 @@ __device__ void st_attn(const Ctx& c, int l) {
     int* last = reinterpret_cast<int*>(c.lds + kFlagOff);
     if (t == 0) {
         int* ctr = a.counters + l * a.kvh + g;
-        const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int old = __hip_atomic_fetch_add((MING_GLOBAL int*)ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *last = old == ns - 1;
-        if (old == ns - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == ns - 1) astore(ctr, 0);
     }
-    __syncthreads();
+    lds_sync();
     if (!*last) return;
     // merge the ns (<= 64) splits of the grp heads of kv head g
     const float* pbase = a.part + (size_t)(g * ns) * grp * (hd + 2);
@@ -487,7 +677,7 @@ __device__ void st_attn(const Ctx& c, int l) {
         S.mw[h * 64 + c.lane] = w;
         if (c.lane == 0) S.mlsum[h] = lw;
     }
-    __syncthreads();
+    lds_sync();
     if (hp < grp) {
         constexpr int B = 8;
         float o = 0.0f;
@@ -506,80 +696,68 @@ __device__ void st_attn(const Ctx& c, int l) {
         if ((d & 1) == 0) {
             const uint32_t w = pack_bf2(val, nxt);
             tstore(a.ta + (size_t)l * (a.H / 2) + col / 2, w, a.epoch);
-            reinterpret_cast<uint32_t*>(a.att + l * a.sx)[col / 2] = w;
+            gst(reinterpret_cast<uint32_t*>(a.att + l * a.sx) + col / 2, w);
         }
     }
 }
 
-// ---- LC: o_proj + residual (unit = row pair, packed) -----------------------------
-template <int Q4>
-struct OW {
-    RowRegs<Nc<Q4>::t32> w;
-};
+// ---- LC: o_proj + residual (unit = row pair, packed on the compute waves) ------
+// O and down workers (the same set): row pairs 2p, 2p+1 with p = w*kCW + wave - 1.
+__device__ __forceinline__ bool in_rowpairs(const Ctx& c) { return c.w * kCW < c.a.H / 2; }
 
 template <int Q4>
-__device__ void o_load(const Ctx& c, const LayerDev& Ld, OW<Q4>& W) {
-    const int p = c.wg * kW + c.wave;
-    if (p < c.a.H / 2) row_load<Q4, 32, Nc<Q4>::t32>(Ld.o, 2 * p + c.team, c.tl, 0, W.w);
-}
-
-template <int Q4>
-__device__ void st_o(const Ctx& c, const LayerDev& Ld, int l, const OW<Q4>& W) {
+__device__ __forceinline__ void st_o(const Ctx& c, const LayerDev& Ld, int l) {
     const StepArgs& a = c.a;
-    const int nunits = a.H / 2;
-    if (c.wg * kW >= nunits) return;
-    const int p = c.wg * kW + c.wave;
-    const bool has = p < nunits;
+    const int p = c.w * kCW + c.wave - 1;
+    const bool has = c.wave > 0 && p < a.H / 2;
     const int r = 2 * p + c.team;
     const uint64_t* xsrc = a.tx + (size_t)l * (a.H / 2) + p;  // residual, produced two stages ago
-    const uint64_t xpre = has && c.lane == 0 ? tload(xsrc) : 0;
-    recv_stage<Q4>(c, a.ta + (size_t)l * (a.H / 2), a.H, nullptr);
+    uint64_t xpre = 0;
+    RowRegs<Nc<Q4>::t32> W;
+    if (has) {
+        if (c.lane == 0) xpre = tload(xsrc);
+        row_load<Q4, 32, Nc<Q4>::t32>(Ld.o, r, c.tl, 0, W);
+    }
+    get_image<Q4>(c, 4 * l + 1, 1, a.ta + (size_t)l * (a.H / 2), a.H, nullptr, nullptr);
     stamp(a, slot_in(l, 2));
     if (!has) return;
-    const float acc = row_dot_pf<Q4, 32, Nc<Q4>::t32>(Ld.o, r, xs_of(c.lds, a.H), c.tl, W.w);
+    const float acc = row_dot_pf<Q4, 32, Nc<Q4>::t32>(Ld.o, r, xs_of(c.lds, a.H), c.tl, W);
     const float a0 = __shfl(acc, 0, kWave), a1 = __shfl(acc, 32, kWave);
     if (c.lane == 0) {
         const uint32_t xw = tfinish(xsrc, xpre, a.epoch, a.flags);
         const uint32_t w = pack_bf2(bf_lo(xw) + rb(a0), bf_hi(xw) + rb(a1));
         tstore(a.tx1 + (size_t)l * (a.H / 2) + p, w, a.epoch);
-        reinterpret_cast<uint32_t*>(a.x1 + l * a.sx)[p] = w;
+        gst(reinterpret_cast<uint32_t*>(a.x1 + l * a.sx) + p, w);
     }
 }
 
 // ---- LD: rms(ln2) + gate/up + swiglu (unit = output pair, spread) -----------------
-// Unit p -> workgroup p % G, slot p / G; slot s -> wave s % kW.  Team 0 takes
-// the gate rows 2p, 2p+1, team 1 the up rows.
-template <int Q4>
-struct UpW {
-    RowRegs<Nc<Q4>::t32> w[Nc<Q4>::up_units][2];
-};
-
-__device__ __forceinline__ int up_slots(const Ctx& c) { return (c.a.I / 2 - c.wg + c.G - 1) / c.G; }
+// Unit p -> worker p % W, slot s = p / W; slot s -> compute wave 1 + s % kCW.
+// Team 0 takes the gate rows 2p, 2p+1, team 1 the up rows.
+__device__ __forceinline__ int up_slots(const Ctx& c) { return (c.a.I / 2 - c.w + c.W - 1) / c.W; }
 
 template <int Q4>
-__device__ void up_load(const Ctx& c, const LayerDev& Ld, UpW<Q4>& W) {
-    const int slots = up_slots(c);
-    const LinearDev& L = c.team == 0 ? Ld.g : Ld.u;
-#pragma unroll
-    for (int i = 0; i < Nc<Q4>::up_units; i++) {
-        const int s = c.wave + i * kW;
-        if (s < slots) {
-            const int p = c.wg + s * c.G;
-            row_load<Q4, 32, Nc<Q4>::t32>(L, 2 * p, c.tl, 0, W.w[i][0]);
-            row_load<Q4, 32, Nc<Q4>::t32>(L, 2 * p + 1, c.tl, 0, W.w[i][1]);
-        }
-    }
-}
-
-template <int Q4>
-__device__ void st_up(const Ctx& c, const LayerDev& Ld, int l, const UpW<Q4>& W) {
+__device__ __forceinline__ void st_up(const Ctx& c, const LayerDev& Ld, int l) {
     const StepArgs& a = c.a;
     constexpr int MU = Nc<Q4>::up_units;
     const int slots = up_slots(c);
     if (slots <= 0) return;
     const LinearDev& L = c.team == 0 ? Ld.g : Ld.u;
-    recv_stage<Q4>(c, a.tx1 + (size_t)l * (a.H / 2), a.H, Ld.ln2);
+    RowRegs<Nc<Q4>::t32> W[MU][2];
+    if (c.wave > 0) {
+#pragma unroll
+        for (int i = 0; i < MU; i++) {
+            const int s = c.wave - 1 + i * kCW;
+            if (s < slots) {
+                const int p = c.w + s * c.W;
+                row_load<Q4, 32, Nc<Q4>::t32>(L, 2 * p, c.tl, 0, W[i][0]);
+                row_load<Q4, 32, Nc<Q4>::t32>(L, 2 * p + 1, c.tl, 0, W[i][1]);
+            }
+        }
+    }
+    get_image<Q4>(c, 4 * l + 2, 2, a.tx1 + (size_t)l * (a.H / 2), a.H, Ld.ln2, nullptr);
     stamp(a, slot_in(l, 3));
+    if (c.wave == 0) return;
     const XStage st = xs_of(c.lds, a.H);
     auto finish = [&](int p, float acc0, float acc1) {
         const float g0 = rb(__shfl(acc0, 0, kWave)), g1 = rb(__shfl(acc1, 0, kWave));
@@ -588,22 +766,22 @@ __device__ void st_up(const Ctx& c, const LayerDev& Ld, int l, const UpW<Q4>& W)
             const float s0 = rb(1.0f / (1.0f + expf(-g0))), s1 = rb(1.0f / (1.0f + expf(-g1)));
             const uint32_t wv = pack_bf2(rb(g0 * s0) * u0, rb(g1 * s1) * u1);
             tstore(a.th + (size_t)l * (a.I / 2) + p, wv, a.epoch);
-            reinterpret_cast<uint32_t*>(a.hh + l * a.sh)[p] = wv;
+            gst(reinterpret_cast<uint32_t*>(a.hh + l * a.sh) + p, wv);
         }
     };
 #pragma unroll
     for (int i = 0; i < MU; i++) {
-        const int s = c.wave + i * kW;
+        const int s = c.wave - 1 + i * kCW;
         if (s < slots) {
-            const int p = c.wg + s * c.G;
-            const float acc0 = row_dot_pf<Q4, 32, Nc<Q4>::t32>(L, 2 * p, st, c.tl, W.w[i][0]);
-            const float acc1 = row_dot_pf<Q4, 32, Nc<Q4>::t32>(L, 2 * p + 1, st, c.tl, W.w[i][1]);
+            const int p = c.w + s * c.W;
+            const float acc0 = row_dot_pf<Q4, 32, Nc<Q4>::t32>(L, 2 * p, st, c.tl, W[i][0]);
+            const float acc1 = row_dot_pf<Q4, 32, Nc<Q4>::t32>(L, 2 * p + 1, st, c.tl, W[i][1]);
             finish(p, acc0, acc1);
         }
     }
-    // units beyond the prefetched ones (only when MU is small)
-    for (int s = c.wave + MU * kW; s < slots; s += kW) {
-        const int p = c.wg + s * c.G;
+    // units beyond the preloaded ones (only when a worker has more than MU * kCW)
+    for (int s = c.wave - 1 + MU * kCW; s < slots; s += kCW) {
+        const int p = c.w + s * c.W;
         RowRegs<Nc<Q4>::t32> r0, r1;
         row_load<Q4, 32, Nc<Q4>::t32>(L, 2 * p, c.tl, 0, r0);
         row_load<Q4, 32, Nc<Q4>::t32>(L, 2 * p + 1, c.tl, 0, r1);
@@ -613,45 +791,37 @@ __device__ void st_up(const Ctx& c, const LayerDev& Ld, int l, const UpW<Q4>& W)
     }
 }
 
-// ---- LE: down + residual (unit = row pair, packed) ---------------------------------
+// ---- LE: down + residual (unit = row pair, packed on the compute waves) --------------
 template <int Q4>
-struct DownW {
-    RowRegs<Nc<Q4>::down> w;
-};
-
-template <int Q4>
-__device__ void down_load(const Ctx& c, const LayerDev& Ld, DownW<Q4>& W) {
-    const int p = c.wg * kW + c.wave;
-    if (p < c.a.H / 2) row_load<Q4, 32, Nc<Q4>::down>(Ld.d, 2 * p + c.team, c.tl, 0, W.w);
-}
-
-template <int Q4>
-__device__ void st_down(const Ctx& c, const LayerDev& Ld, int l, const DownW<Q4>& W) {
+__device__ __forceinline__ void st_down(const Ctx& c, const LayerDev& Ld, int l) {
     const StepArgs& a = c.a;
-    const int nunits = a.H / 2;
-    if (c.wg * kW >= nunits) return;
-    const int p = c.wg * kW + c.wave;
-    const bool has = p < nunits;
+    const int p = c.w * kCW + c.wave - 1;
+    const bool has = c.wave > 0 && p < a.H / 2;
     const int r = 2 * p + c.team;
     const uint64_t* xsrc = a.tx1 + (size_t)l * (a.H / 2) + p;  // residual, produced two stages ago
-    const uint64_t xpre = has && c.lane == 0 ? tload(xsrc) : 0;
-    recv_stage<Q4>(c, a.th + (size_t)l * (a.I / 2), a.I, nullptr);
+    uint64_t xpre = 0;
+    RowRegs<Nc<Q4>::down> W;
+    if (has) {
+        if (c.lane == 0) xpre = tload(xsrc);
+        row_load<Q4, 32, Nc<Q4>::down>(Ld.d, r, c.tl, 0, W);
+    }
+    get_image<Q4>(c, 4 * l + 3, 3, a.th + (size_t)l * (a.I / 2), a.I, nullptr, nullptr);
     stamp(a, slot_in(l, 4));
     if (!has) return;
-    const float acc = row_dot_pf<Q4, 32, Nc<Q4>::down>(Ld.d, r, xs_of(c.lds, a.I), c.tl, W.w);
+    const float acc = row_dot_pf<Q4, 32, Nc<Q4>::down>(Ld.d, r, xs_of(c.lds, a.I), c.tl, W);
     const float a0 = __shfl(acc, 0, kWave), a1 = __shfl(acc, 32, kWave);
     if (c.lane == 0) {
         const uint32_t xw = tfinish(xsrc, xpre, a.epoch, a.flags);
         const uint32_t w2 = pack_bf2(bf_lo(xw) + rb(a0), bf_hi(xw) + rb(a1));
         tstore(a.tx + (size_t)(l + 1) * (a.H / 2) + p, w2, a.epoch);
-        reinterpret_cast<uint32_t*>(a.xo + l * a.sx)[p] = w2;
+        gst(reinterpret_cast<uint32_t*>(a.xo + l * a.sx) + p, w2);
     }
 }
 
 // ---- final norm + tied LM head + argmax ---------------------------------------------
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
 
-__device__ void block_best(float& bv, int& bi, float* rv, int* ri) {
+__device__ __forceinline__ void block_best(float& bv, int& bi, float* rv, int* ri) {
     for (int o = kWave / 2; o > 0; o >>= 1) {
         const float ov = __shfl_xor(bv, o, kWave);
         const int oi = __shfl_xor(bi, o, kWave);
@@ -660,14 +830,14 @@ __device__ void block_best(float& bv, int& bi, float* rv, int* ri) {
             bi = oi;
         }
     }
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    __syncthreads();
+    const int wave = tix() / kWave, lane = tix() % kWave;
+    lds_sync();
     if (lane == 0) {
         rv[wave] = bv;
         ri[wave] = bi;
     }
-    __syncthreads();
-    if (threadIdx.x == 0)
+    lds_sync();
+    if (tix() == 0)
         for (int w = 1; w < kW; w++)
             if (better(rv[w], ri[w], bv, bi)) {
                 bv = rv[w];
@@ -675,10 +845,11 @@ __device__ void block_best(float& bv, int& bi, float* rv, int* ri) {
             }
 }
 
-// The head keeps kHeadDepth row pairs per wave in flight: each register slot
-// is refilled with the row pair kHeadDepth positions further on as soon as it
-// has been used (slots are indexed statically, the loop is unrolled by the
-// depth), so the stream of head rows never waits for a whole batch.
+// The head keeps kHeadDepth row pairs per compute wave in flight: each
+// register slot is refilled with the row pair kHeadDepth positions further on
+// as soon as it has been used (slots are indexed statically, the loop is
+// unrolled by the depth), so the stream of head rows never waits for a whole
+// batch.  Loads past the last row pair reload the last one.
 constexpr int kHeadDepth = 8;
 
 template <int Q4>
@@ -688,41 +859,42 @@ struct HeadW {
 
 template <int Q4>
 __device__ __forceinline__ void head_slot_load(const Ctx& c, int p, RowRegs<Nc<Q4>::t32>& w) {
-    const int V = c.a.head.N, nunits = V / 2 + (V & 1);
-    if (p < nunits) row_load<Q4, 32, Nc<Q4>::t32>(c.a.head, min(2 * p + c.team, V - 1), c.tl, 0, w);
+    const int V = c.a.head.N;
+    row_load<Q4, 32, Nc<Q4>::t32>(c.a.head, min(2 * p + c.team, V - 1), c.tl, 0, w);
 }
 
 template <int Q4>
-__device__ void head_load(const Ctx& c, HeadW<Q4>& W) {
-    const int nw = c.G * kW, me = c.wg * kW + c.wave;
-#pragma unroll
-    for (int i = 0; i < kHeadDepth; i++) head_slot_load<Q4>(c, me + i * nw, W.w[i]);
-}
-
-template <int Q4>
-__device__ void st_head(const Ctx& c, HeadW<Q4>& W) {
+__device__ __forceinline__ void st_head(const Ctx& c) {
     const StepArgs& a = c.a;
     const int V = a.head.N, nunits = V / 2 + (V & 1);
-    const int nw = c.G * kW, me = c.wg * kW + c.wave;
-    recv_stage<Q4>(c, a.tx + (size_t)a.n_layers * (a.H / 2), a.H, a.final_norm,
-                   c.wg == 0 ? a.hidden : nullptr);
+    const int nw = c.W * kCW, me = c.w * kCW + c.wave - 1;
+    HeadW<Q4> W;
+    if (c.wave > 0) {
+#pragma unroll
+        for (int i = 0; i < kHeadDepth; i++) head_slot_load<Q4>(c, me + i * nw, W.w[i]);
+    }
+    // the hidden output comes from hub 0, or from worker 0 when there are no hubs
+    get_image<Q4>(c, 4 * a.n_layers, 4, a.tx + (size_t)a.n_layers * (a.H / 2), a.H, a.final_norm,
+                  a.nhubs == 0 && c.w == 0 ? a.hidden : nullptr);
     stamp(a, slot_in(a.n_layers, 0));
     const XStage st = xs_of(c.lds, a.H);
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int first = me; first < nunits; first += kHeadDepth * nw) {
+    if (c.wave > 0) {
+        for (int first = me; first < nunits; first += kHeadDepth * nw) {
 #pragma unroll
-        for (int i = 0; i < kHeadDepth; i++) {
-            const int p = first + i * nw;
-            if (p < nunits) {
-                const int r = min(2 * p + c.team, V - 1);
-                const float acc = row_dot_pf<Q4, 32, Nc<Q4>::t32>(a.head, r, st, c.tl, W.w[i]);
-                head_slot_load<Q4>(c, p + kHeadDepth * nw, W.w[i]);
-                if (c.tl == 0 && 2 * p + c.team < V) {
-                    if (a.logits) a.logits[r] = acc;
-                    if (better(acc, r, bv, bi)) {
-                        bv = acc;
-                        bi = r;
+            for (int i = 0; i < kHeadDepth; i++) {
+                const int p = first + i * nw;
+                if (p < nunits) {
+                    const int r = min(2 * p + c.team, V - 1);
+                    const float acc = row_dot_pf<Q4, 32, Nc<Q4>::t32>(a.head, r, st, c.tl, W.w[i]);
+                    head_slot_load<Q4>(c, p + kHeadDepth * nw, W.w[i]);
+                    if (c.tl == 0 && 2 * p + c.team < V) {
+                        if (a.logits) gst(a.logits + r, acc);
+                        if (better(acc, r, bv, bi)) {
+                            bv = acc;
+                            bi = r;
+                        }
                     }
                 }
             }
@@ -731,74 +903,98 @@ __device__ void st_head(const Ctx& c, HeadW<Q4>& W) {
     float* rv = reinterpret_cast<float*>(c.lds + kRedOff);
     int* ri = reinterpret_cast<int*>(c.lds + kRedOff + 16);
     block_best(bv, bi, rv, ri);
-    if (threadIdx.x == 0) {
-        cstore(a.amax_v + c.wg, bv);
-        __hip_atomic_store(a.amax_i + c.wg, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tix() == 0) {
+        cstore(a.amax_v + c.w, bv);
+        astore(a.amax_i + c.w, bi);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     int* last = reinterpret_cast<int*>(c.lds + kFlagOff);
-    if (threadIdx.x == 0) {
+    if (tix() == 0) {
         int* ctr = a.counters + a.n_layers * a.kvh;
-        const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *last = old == c.G - 1;
-        if (old == c.G - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int old = __hip_atomic_fetch_add((MING_GLOBAL int*)ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *last = old == c.W - 1;
+        if (old == c.W - 1) astore(ctr, 0);
     }
-    __syncthreads();
+    lds_sync();
     if (!*last) return;
     bv = -INFINITY;
     bi = 0x7fffffff;
-    for (int i = threadIdx.x; i < c.G; i += kT) {
+    for (int i = tix(); i < c.W; i += kT) {
         const float v = cload(a.amax_v + i);
-        const int ix = __hip_atomic_load(a.amax_i + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int ix = aload(a.amax_i + i);
         if (better(v, ix, bv, bi)) {
             bv = v;
             bi = ix;
         }
     }
     block_best(bv, bi, rv, ri);
-    if (threadIdx.x == 0 && a.argmax_out) *a.argmax_out = bi == 0x7fffffff ? 0 : bi;
+    if (tix() == 0 && a.argmax_out) gst(a.argmax_out, bi == 0x7fffffff ? 0 : bi);
 }
 
-
 template <int Q4>
-__global__ __launch_bounds__(kT) void decode_tagged_kernel(StepArgs a) {
-    __shared__ uint32_t lds[kLds];
-    const int lane = threadIdx.x % kWave;
-    const Ctx c{a, lds, (int)gridDim.x, (int)blockIdx.x, (int)(threadIdx.x / kWave), lane, lane / 32, lane % 32};
+__global__ __launch_bounds__(kT) void decode_tagged_kernel(StepArgs args, const LayerDev* __restrict__ layers) {
+    // Read the arguments in place, in the kernel-argument segment (uniform
+    // scalar loads), instead of letting the compiler copy the block to scratch
+    // for the references that the stages take.
+    (void)args;
+    const StepArgs& a = *(const StepArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    __shared__ __align__(16) uint32_t lds[kLdsTotal];
     stamp(a, 0);
-    QkvW<Q4> qw;
-    OW<Q4> ow;
-    UpW<Q4> uw;
-    DownW<Q4> dw;
-    qkv_load<Q4>(c, a.layers[0], qw);
-    st_embed(c);
-    for (int l = 0; l < a.n_layers; l++) {
-        const LayerDev& Ld = a.layers[l];
-        o_load<Q4>(c, Ld, ow);
-        st_qkv<Q4>(c, Ld, l, qw);
-        __syncthreads();
-        stamp(a, slot_in(l, 0) + 1);
-        st_attn(c, l);
-        __syncthreads();
-        stamp(a, slot_in(l, 1) + 1);
-        up_load<Q4>(c, Ld, uw);
-        st_o<Q4>(c, Ld, l, ow);
-        __syncthreads();
-        stamp(a, slot_in(l, 2) + 1);
-        down_load<Q4>(c, Ld, dw);
-        st_up<Q4>(c, Ld, l, uw);
-        __syncthreads();
-        stamp(a, slot_in(l, 3) + 1);
-        if (l + 1 < a.n_layers) qkv_load<Q4>(c, a.layers[l + 1], qw);
-        st_down<Q4>(c, Ld, l, dw);
-        __syncthreads();
-        stamp(a, slot_in(l, 4) + 1);
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xcc &= 0xfu;
+    const int nh = a.nhubs;
+    if ((int)blockIdx.x < nh) {
+        hub_main<Q4>(a, layers, lds, blockIdx.x, xcc);
+        return;
     }
-    HeadW<Q4> hw;
-    head_load<Q4>(c, hw);
-    st_head<Q4>(c, hw);
-    stamp(a, slot_in(a.n_layers, 0) + 1);
+    // the wave index is uniform across the wave: say so, so that per-wave
+    // selections (which rows, which linear) live in scalar registers
+    const int lane = tix() % kWave, wave = __builtin_amdgcn_readfirstlane(tix() / kWave);
+    const int W = (int)gridDim.x - nh, w = (int)blockIdx.x - nh;
+    {
+        const Ctx c0{a, lds, W, w, wave, lane, lane / 32, lane % 32, -1};
+        st_embed(c0);
+        // layer table into LDS (find_hub's barrier publishes it)
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(layers);
+        for (int i = tix(); i < a.n_layers * kLayWords; i += kT) lds[kLayOff + i] = gld(src + i);
+    }
+    const LayerDev* lay = reinterpret_cast<const LayerDev*>(lds + kLayOff);
+    const int hub = find_hub(a, lds, xcc);
+    const Ctx c0{a, lds, W, w, wave, lane, lane / 32, lane % 32, hub};
+    const bool pq = in_qkv(c0), pa = in_attn(c0), po = in_rowpairs(c0);
+    const int L = a.n_layers;
+    for (int l = 0; l < L; l++) {
+        const int ln = tix() % kWave;
+        const Ctx c{a, lds, W, w, wave, ln, ln / 32, ln % 32, hub};
+        const LayerDev& Ld = lay[l];
+        if (pq) {
+            st_qkv<Q4>(c, Ld, l);
+            done_stamp(a, slot_in(l, 0) + 1);
+        }
+        if (pa) {
+            AttnTile at;
+            attn_pre(c, l, at);
+            attn_recv(c, l);
+            attn_run(c, l, at);
+            done_stamp(a, slot_in(l, 1) + 1);
+        }
+        if (po) {
+            st_o<Q4>(c, Ld, l);
+            done_stamp(a, slot_in(l, 2) + 1);
+        }
+        st_up<Q4>(c, Ld, l);
+        done_stamp(a, slot_in(l, 3) + 1);
+        if (po) {
+            st_down<Q4>(c, Ld, l);
+            done_stamp(a, slot_in(l, 4) + 1);
+        }
+    }
+    const int ln = tix() % kWave;
+    const Ctx c{a, lds, W, w, wave, ln, ln / 32, ln % 32, hub};
+    st_head<Q4>(c);
+    done_stamp(a, slot_in(L, 0) + 1);
 }
 
 }  // namespace
@@ -812,9 +1008,24 @@ int tagged_split_len(int n) {
     return sl;
 }
 
+// Hubs for a grid of `grid` workgroups: one per XCD when the grid is large
+// enough to spare them.
+int tagged_hubs(int grid) { return grid >= 64 ? kMaxHubs : 0; }
+
+// u32 words of one image slot: the largest stage image (K = max(H, I)),
+// rounded up to 256 bytes.
+int tagged_img_stride(int H, int I) {
+    const int K = H > I ? H : I;
+    return (xstage_words(K) + 63) / 64 * 64;
+}
+
+int tagged_max_layers() { return kMaxLdsLayers; }
+int tagged_units_per_worker() { return kCW; }
+
 hipError_t launch_lm_step_tagged(hipStream_t st, const StepArgs& a, int q4, int grid) {
     StepArgs args = a;
-    void* params[] = {&args};
+    const LayerDev* layers = a.layers;
+    void* params[] = {&args, &layers};
     const void* f = q4 ? reinterpret_cast<const void*>(decode_tagged_kernel<1>)
                        : reinterpret_cast<const void*>(decode_tagged_kernel<0>);
     return hipLaunchCooperativeKernel(f, dim3(grid), dim3(kT), params, 0, st);

@@ -145,12 +145,15 @@ def check_step_teacher_forced(ming, m, cache_before, cache_after, orc, pos, toke
     return worst, float(d.max()), ram, margin
 
 
-@pytest.mark.parametrize("mode", ["kernels", "persistent"])
+MODES = {"kernels": "LM_KERNELS", "persistent": "LM_PERSISTENT", "direct": "LM_PERSISTENT_DIRECT"}
+
+
+@pytest.mark.parametrize("mode", ["kernels", "persistent", "direct"])
 @pytest.mark.parametrize("ctx_len", [512, 2048, 8192])
 def test_lm_step_matches_oracle(ming, ctx, q4_model, ctx_len, mode):
     S = syn_mod(ming)
     syn, m, orc = q4_model
-    md = ming.LM_KERNELS if mode == "kernels" else ming.LM_PERSISTENT
+    md = getattr(ming, MODES[mode])
     print(f"[lm_step] ctx={ctx_len} mode={mode}", flush=True)
     cache = S.KvCache(syn.spec, ctx_len + 4)
     cache.fill_random(ctx_len, seed=ctx_len)
@@ -165,12 +168,14 @@ def test_lm_step_matches_oracle(ming, ctx, q4_model, ctx_len, mode):
 
 
 def test_schedules_agree_and_deterministic(ming, ctx, q4_model):
-    """Each schedule is bit-for-bit reproducible; the two schedules (which
-    sum in different orders) agree within the bf16 tolerance."""
+    """Each schedule is bit-for-bit reproducible; the persistent kernel gives
+    the same bits with and without per-XCD hubs (the stage images are built by
+    the same code), and it agrees with the per-stage kernels (which sum in
+    different orders) within the bf16 tolerance."""
     S = syn_mod(ming)
     syn, m, _ = q4_model
     outs = {}
-    for mode in (ming.LM_KERNELS, ming.LM_PERSISTENT):
+    for mode in (ming.LM_KERNELS, ming.LM_PERSISTENT, ming.LM_PERSISTENT_DIRECT):
         for rep in range(3):
             cache = S.KvCache(syn.spec, 1100)
             cache.fill_random(1000, seed=7)
@@ -181,7 +186,8 @@ def test_schedules_agree_and_deterministic(ming, ctx, q4_model):
                     f"mode {mode} not reproducible (repeat {rep})"
             else:
                 outs[mode] = o
-    k, p = outs[ming.LM_KERNELS], outs[ming.LM_PERSISTENT]
+    k, p, d = outs[ming.LM_KERNELS], outs[ming.LM_PERSISTENT], outs[ming.LM_PERSISTENT_DIRECT]
+    assert p[0] == d[0] and np.array_equal(p[1], d[1]) and np.array_equal(p[2], d[2]), "hubs change the result"
     assert_close_bf16(p[1], k[1], "persistent vs kernels hidden", atol=0.2, rtol=0.1)
 
 
