@@ -8,12 +8,17 @@ norm -> LM head -> argmax, with the token fed back on the device.  Every
 step decodes at position 2048 (the cache length is reset before each step,
 so the appended row is rewritten in place and the context stays 2048).
 
-Prints one JSON line (see the keys below).  `roofline` prices the step
-kernel against HBM: algorithmic bytes per token (4-bit weights incl. the
-tied head at 0.5625 B/param, biases and norms, the KV read of 2048 rows and
-the one-row append) / measured time per token.  `cpu_baseline` times the
-oracle (the CPU restatement in oracle/, OpenMP over output rows) on the
-host cores on a bounded sample of the same workload.
+Prints one JSON line (see the keys below).  `value` is tokens/s over the
+timed region.  `roofline` prices the step kernel against HBM: algorithmic
+bytes per token (4-bit weights incl. the tied head at 0.5625 B/param, biases
+and norms, the KV read of 2048 rows and the one-row append) divided by the
+kernel's average launch duration, which events recorded around every launch
+on the launch stream measure inside the timed region (with the persistent
+schedule a step is one launch).  `traffic` is the HBM bytes per launch that
+rocprofv3's FETCH_SIZE/WRITE_SIZE counters measured for this workload,
+scaled by a plain copy's reading (profiles/); null for other workloads.
+`cpu_baseline` times the oracle (the CPU restatement in oracle/, OpenMP over
+output rows) on the host cores on a bounded sample of the same workload.
 """
 import argparse
 import importlib
@@ -75,18 +80,24 @@ def main():
     for _ in range(args.warmup):
         step()
     ctx.sync()
+    # the library launches on torch's current stream (Context binds it), so
+    # these events bracket each launch on its own stream
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record()
-    for _ in range(args.steps):
+    for i in range(args.steps):
+        ev[i][0].record()
         step()
+        ev[i][1].record()
     e1.record()
     torch.cuda.synchronize()
     ctx.sync()
     ms = e0.elapsed_time(e1) / args.steps
+    launch_ms = sum(a.elapsed_time(b) for a, b in ev) / args.steps
     tok_s = 1000.0 / ms
     bytes_tok = S.lm_bytes_per_token(spec, args.ctx)
-    achieved = bytes_tok / (ms * 1e-3) / 1e9
+    achieved = bytes_tok / (launch_ms * 1e-3) / 1e9
 
     cpu = None
     if not args.no_cpu:
@@ -120,12 +131,23 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "bytes_per_token": bytes_tok,
+            "traffic": measured_traffic(args),
+            "bytes_per_launch": bytes_tok,
+            "launch_ms": round(launch_ms, 5),
         },
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+
+
+def measured_traffic(args):
+    """HBM bytes per launch from the committed rocprofv3 counter runs, for
+    the workload they were taken on (ctx 2048, persistent schedule)."""
+    path = os.path.join(ROOT, "profiles", "decode_tagged_kernel_ctx2048_traffic.json")
+    if args.ctx != 2048 or args.mode not in ("auto", "persistent") or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)["traffic_bytes_per_dispatch"]
 
 
 def cpu_baseline(ming, S, syn, cache, args):

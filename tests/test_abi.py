@@ -1,0 +1,81 @@
+"""The C ABI on the CPU: libming_hip.so loads, exports every function that
+include/ming_hip.h declares, and its host-side contract holds without a GPU
+(argument checks, status strings, the MING_FUSED switches).  No kernel runs
+here.
+"""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ming_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)  # drop comments
+    text = re.sub(r"//[^\n]*", " ", text)
+    names = re.findall(r"\b(ming_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for must in ("ming_ctx_create", "ming_sync", "ming_last_error", "ming_qgemv", "ming_dequantize",
+                 "ming_quantize", "ming_lm_layer", "ming_lm_step", "ming_lm_generate", "ming_fused_enabled",
+                 "ming_dit_enabled", "ming_lm_enabled", "ming_set_force_off"):
+        assert must in names, must
+
+
+def test_library_exports_every_declared_function(ming):
+    lib = ctypes.CDLL(ming.LIB_PATH)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_status_strings(ming):
+    L = ming.lib()
+    seen = set()
+    for s in range(0, 8):
+        txt = L.ming_status_str(s).decode()
+        assert txt and txt not in seen
+        seen.add(txt)
+    assert L.ming_status_str(0).decode() == "ok"
+
+
+def test_null_context_is_not_init(ming):
+    L = ming.lib()
+    assert L.ming_sync(None) == ming.MING_E_NOT_INIT
+    assert L.ming_ctx_destroy(None) == ming.MING_E_NOT_INIT
+    assert L.ming_ctx_set_stream(None, None) == ming.MING_E_NOT_INIT
+    assert L.ming_last_error(None) is not None
+
+
+def test_ctx_create_rejects_null_out(ming):
+    assert ming.lib().ming_ctx_create(None, 0) == ming.MING_E_ARG
+
+
+@pytest.mark.parametrize("env,fused,dit,lm", [
+    ({}, 1, 1, 1),
+    ({"MING_FUSED": "0"}, 0, 0, 0),
+    ({"MING_FUSED_DIT": "0"}, 1, 0, 1),
+    ({"MING_FUSED_LM": "0"}, 1, 1, 0),
+])
+def test_fused_switches_follow_environment(env, fused, dit, lm):
+    # a fresh process per case: the switches read the environment like the reference's
+    # enabled()/ditEnabled()/lmEnabled()
+    code = ("import importlib,sys; sys.path.insert(0, %r); m = importlib.import_module('ming-tts-serve_amd'); "
+            "L = m.lib(); print(L.ming_fused_enabled(), L.ming_dit_enabled(), L.ming_lm_enabled()); "
+            "L.ming_set_force_off(1); print(L.ming_fused_enabled(), L.ming_dit_enabled(), L.ming_lm_enabled())"
+            % ROOT)
+    e = {k: v for k, v in os.environ.items() if not k.startswith("MING_FUSED")}
+    e.update(env)
+    out = subprocess.run([sys.executable, "-c", code], env=e, capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    first, second = out.stdout.split("\n")[:2]
+    assert first.split() == [str(fused), str(dit), str(lm)]
+    assert second.split() == ["0", "0", "0"]  # force_off wins

@@ -1,0 +1,253 @@
+"""Pins the oracle (the CPU restatement used as the parity checker) against
+facts that do not come from the oracle's own formulas: hand-derived known
+answers of the MLX affine format, f64 brute force, torch's textbook ops,
+exact invariants (power-of-two scaling, identity rotation, one-key
+attention) and tie-breaking.  Each check is chosen so that a plausible slip
+(nibble order, group index, scale sign, pairing, a dropped bias or weight, a
+transposed operand, a wrong kv-head mapping) fails it.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+RNG = np.random.default_rng(1234)
+
+
+def bf16(x):
+    return torch.from_numpy(np.asarray(x, np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def f32(h):
+    return oracle.to_f32(h)
+
+
+def rand_bf16(shape, std=1.0, rng=RNG):
+    return bf16(rng.normal(0, std, shape).astype(np.float32))
+
+
+# ---- MLX affine 4-bit format -----------------------------------------------------
+
+def test_dequant_packing_known_answer():
+    # word 0x76543210 holds q = 0..7 in nibble order (element 8j+i in bits 4i): with s = 1, b = 0
+    # the row dequantizes to 0..7, then 8..15 for 0xFEDCBA98
+    K = 64
+    wq = np.tile(np.array([0x76543210, 0xFEDCBA98], np.uint32), K // 16).reshape(1, K // 8)
+    s = bf16([1.0]).reshape(1, 1)
+    b = bf16([0.0]).reshape(1, 1)
+    got = f32(oracle.dequantize(wq, s, b))[0]
+    assert np.array_equal(got, np.tile(np.arange(16, dtype=np.float32), 4))
+
+
+def test_dequant_closed_form_random():
+    # value = bf16(s*q + b) with q the nibble of column k, s/b the group's bf16 pair (numpy restatement)
+    N, K = 37, 256
+    wq = RNG.integers(0, 2 ** 32, size=(N, K // 8), dtype=np.uint64).astype(np.uint32)
+    s = rand_bf16((N, K // 64), 0.05)
+    b = rand_bf16((N, K // 64), 0.5)
+    q = ((wq[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(N, K).astype(np.float32)
+    sk = np.repeat(f32(s), 64, axis=1)
+    bk = np.repeat(f32(b), 64, axis=1)
+    want = bf16(sk * q + bk)
+    assert np.array_equal(oracle.dequantize(wq, s, b), want)
+
+
+def test_quantize_known_answer_grid_and_zero_group():
+    # group 0: {0, 1/16, ..., 15/16} four times.  |min| <= |max| so the edge is the max:
+    # scale = -(15/16)/15 = -1/16, q0 = rint(edge/scale) = -15, scale = edge/q0 = -1/16,
+    # bias = 15/16 and q_k = rint((w_k - 15/16) / (-1/16)) = 15 - j (reversed), exact round trip.
+    # group 1: all zeros -> q = 0, bias 0, scale = -eps = -1e-7 (rounded to bf16).
+    j = np.tile(np.arange(16, dtype=np.float32), 4)
+    w = bf16(np.concatenate([j / 16.0, np.zeros(64, np.float32)]).reshape(1, 128))
+    wq, s, b = oracle.quantize(w)
+    assert f32(s)[0, 0] == -1.0 / 16 and f32(b)[0, 0] == 15.0 / 16
+    q = ((wq[0, :8, None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(64)
+    assert np.array_equal(q, (15 - j).astype(np.uint32))
+    assert np.all(wq[0, 8:] == 0) and f32(b)[0, 1] == 0.0 and s[0, 1] == bf16([-1e-7])[0]
+    assert np.array_equal(oracle.dequantize(wq, s, b), w)
+
+
+def test_quantize_negative_edge_and_error_bound():
+    # |min| > |max|: the min is the edge and the scale positive.  A dequantized value is within
+    # half a step of the input, plus q <= 15 times the bf16 rounding of the stored scale
+    # (<= 2^-8 |s|), plus the bf16 rounding of the result (<= 2^-9 |w|)
+    w = bf16(np.concatenate([np.linspace(-3.0, 1.0, 64), RNG.normal(0, 0.02, 64 * 7)]).reshape(2, 256)
+             .astype(np.float32))
+    wq, s, b = oracle.quantize(w)
+    assert f32(s)[0, 0] > 0 and f32(b)[0, 0] == -3.0
+    d = f32(oracle.dequantize(wq, s, b)) - f32(w)
+    step = np.repeat(np.abs(f32(s)), 64, axis=1)
+    assert np.all(np.abs(d) <= 0.5 * step + 15 * step * 2.0 ** -8 + np.abs(f32(w)) * 2.0 ** -8 + 1e-6)
+
+
+# ---- qGEMV --------------------------------------------------------------------------
+
+SHAPES = [(896, 896), (128, 896), (4864, 896), (896, 4864), (151936, 896)]  # (N, K) of the 5 real linears
+
+
+@pytest.mark.parametrize("N,K", SHAPES)
+def test_linear_acc_vs_f64(N, K):
+    rng = np.random.default_rng(N + K)
+    w = bf16(rng.normal(0, 0.02, (N, K)).astype(np.float32))
+    wq, s, b = oracle.quantize(w)
+    x = bf16(rng.normal(0, 1, K).astype(np.float32))
+    # f64 reference built from the packed nibbles (the accumulator sees s*q + b unrounded; only a
+    # materialised dequantized weight is rounded to bf16)
+    q = ((wq[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(N, K).astype(np.float64)
+    wd = np.repeat(f32(s).astype(np.float64), 64, axis=1) * q + np.repeat(f32(b).astype(np.float64), 64, axis=1)
+    for g in (1.0, 0.5, 3.0):
+        L = oracle.Linear(wq, s, b, gscale=g)
+        got = oracle.linear_acc(L, x).astype(np.float64)
+        want = g * (wd @ f32(x).astype(np.float64))
+        err = np.abs(got - want)
+        assert np.all(err <= 1e-4 + 1e-5 * np.abs(want)), f"{N}x{K} g={g}: max err {err.max():.3e}"
+
+
+def test_linear_bf16_weights_and_bias_rounding():
+    N, K = 64, 192
+    w = rand_bf16((N, K), 0.05)
+    x = rand_bf16(K)
+    bias = rand_bf16(N, 0.1)
+    L = oracle.Linear(w)
+    acc = f32(w).astype(np.float64) @ f32(x).astype(np.float64)
+    got = f32(oracle.linear(L, x, bias))
+    # addmm rounds once: bf16(acc + b)
+    assert np.all(np.abs(got - (acc + f32(bias))) <= np.abs(acc + f32(bias)) * 2 ** -8 + 1e-6)
+
+
+# ---- element-wise ----------------------------------------------------------------------
+
+def test_rms_norm_vs_torch_and_scale_invariance():
+    x = rand_bf16((3, 896))
+    w = rand_bf16(896, 0.5)
+    got = f32(oracle.rms_norm(x, w, eps=1e-6))
+    ref = torch.nn.functional.rms_norm(torch.from_numpy(f32(x)), (896,), torch.from_numpy(f32(w)), eps=1e-6)
+    assert np.all(np.abs(got - ref.numpy()) <= np.abs(ref.numpy()) * 2 ** -7 + 1e-6)
+    # with eps = 0 the norm is exactly invariant under x -> 2^k x
+    a = oracle.rms_norm(x, w, eps=0.0)
+    for k in (-3, 5):
+        assert np.array_equal(oracle.rms_norm(bf16(f32(x) * 2.0 ** k), w, eps=0.0), a)
+
+
+def test_rope_identity_and_rotation():
+    hd, nh, log2b = 64, 3, float(np.log2(np.float32(1e6)))
+    x = rand_bf16((nh, hd))
+    assert np.array_equal(oracle.rope(x, 0, log2b), x)  # pos 0 rotates by 0
+    for pos in (1, 17, 2047):
+        got = f32(oracle.rope(x, pos, log2b)).astype(np.float64)
+        d = np.arange(hd // 2)
+        th = pos * np.exp2(-(d / (hd // 2)) * log2b)
+        z = (f32(x)[:, :hd // 2] + 1j * f32(x)[:, hd // 2:]) * np.exp(1j * th)  # pairs (d, d + hd/2)
+        want = np.concatenate([z.real, z.imag], axis=1)
+        assert np.all(np.abs(got - want) <= np.abs(want) * 2 ** -7 + 2e-3 * (1 + pos / 1000)), pos
+
+
+def test_swiglu_and_gelu_vs_torch():
+    g, u = rand_bf16(4096, 2.0), rand_bf16(4096, 2.0)
+    want = torch.nn.functional.silu(torch.from_numpy(f32(g))) * torch.from_numpy(f32(u))
+    got = f32(oracle.swiglu(g, u))
+    assert np.all(np.abs(got - want.numpy()) <= np.abs(want.numpy()) * 2 ** -6 + 1e-5)
+    # gelu_approx rounds every op to bf16 (the reference's definition), so 1 + tanh(.) near 0 for
+    # large negative x carries an absolute error up to 2^-8, scaled by 0.5|x|
+    x = rand_bf16(4096, 2.0)
+    want = torch.nn.functional.gelu(torch.from_numpy(f32(x)), approximate="tanh").numpy()
+    got = f32(oracle.gelu_approx(x))
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2 ** -5 + np.abs(f32(x)) * 2 ** -7 + 1e-4)
+
+
+def ref_attention(q, kc, vc, n, scale):
+    heads, hd = q.shape
+    kvh = kc.shape[0]
+    out = np.empty((heads, hd))
+    for h in range(heads):
+        g = h // (heads // kvh)
+        s = (f32(q[h]).astype(np.float64) @ f32(kc[g, :n]).astype(np.float64).T) * scale
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ f32(vc[g, :n]).astype(np.float64)
+    return out
+
+
+def test_attention_vs_f64_and_gqa_mapping():
+    heads, kvh, hd, cap, pos = 14, 2, 64, 300, 257
+    q = rand_bf16((heads, hd))
+    kc = rand_bf16((kvh, cap, hd))
+    vc = rand_bf16((kvh, cap, hd))
+    vc[1] = bf16(f32(vc[1]) + 3.0)  # kv heads far apart: a wrong head mapping is visible
+    got = f32(oracle.attention(q, kc, vc, pos, 0.125))
+    want = ref_attention(q, kc, vc, pos + 1, 0.125)
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2 ** -7 + 2e-3)
+
+
+def test_attention_single_key_is_value():
+    q = rand_bf16((14, 64))
+    kc = rand_bf16((2, 8, 64))
+    vc = rand_bf16((2, 8, 64))
+    got = oracle.attention(q, kc, vc, 0, 0.125)
+    assert np.array_equal(got[:7], np.repeat(vc[0:1, 0], 7, axis=0))
+    assert np.array_equal(got[7:], np.repeat(vc[1:2, 0], 7, axis=0))
+
+
+# ---- a whole layer and the head -------------------------------------------------------------
+
+def test_layer_vs_torch_f32():
+    """The oracle's layer (bf16 rounding points) against a torch f32 layer written from the
+    Qwen2 definition with the same dequantized weights: equal within bf16 tolerance."""
+    H, heads, kvh, hd, I, pos = 128, 2, 1, 64, 256, 5
+    rng = np.random.default_rng(7)
+
+    def lin(n, k):
+        wq, s, b = oracle.quantize(bf16(rng.normal(0, 0.05, (n, k)).astype(np.float32)))
+        return oracle.Linear(wq, s, b), f32(oracle.dequantize(wq, s, b))
+
+    (q, Wq), (k, Wk), (v, Wv), (o, Wo) = lin(H, H), lin(kvh * hd, H), lin(kvh * hd, H), lin(H, H)
+    (gt, Wg), (up, Wu), (dn, Wd) = lin(I, H), lin(I, H), lin(H, I)
+    ln1, ln2 = bf16(1 + rng.normal(0, 0.1, H)), bf16(1 + rng.normal(0, 0.1, H))
+    bq, bk, bv = (bf16(rng.normal(0, 0.05, n)) for n in (H, kvh * hd, kvh * hd))
+    c = oracle.cfg(H, heads, kvh, hd, I)
+    layer = oracle.LmLayer(ln1, ln2, q, k, v, o, gt, up, dn, bq, bk, bv)
+    x = bf16(rng.normal(0, 1, H))
+    kc = bf16(rng.normal(0, 1, (kvh, 16, hd)))
+    vc = bf16(rng.normal(0, 1, (kvh, 16, hd)))
+    kc0, vc0 = kc.copy(), vc.copy()
+    got = f32(oracle.lm_layer_step(c, layer, x, pos, kc, vc))
+
+    T = lambda a: torch.from_numpy(np.asarray(a, np.float32)).double()
+    xt = T(f32(x))
+    rms = lambda t, w: t / torch.sqrt((t * t).mean() + 1e-6) * T(f32(w))
+    h = rms(xt, ln1)
+    qq = T(Wq) @ h + T(f32(bq))
+    kk = T(Wk) @ h + T(f32(bk))
+    vv = T(Wv) @ h + T(f32(bv))
+
+    def rope(t):
+        t = t.view(-1, hd)
+        d = torch.arange(hd // 2, dtype=torch.float64)
+        th = pos * torch.exp2(-(d / (hd // 2)) * np.log2(1e6))
+        a, b2 = t[:, :hd // 2], t[:, hd // 2:]
+        return torch.cat([a * torch.cos(th) - b2 * torch.sin(th), a * torch.sin(th) + b2 * torch.cos(th)], 1)
+
+    qq, kk = rope(qq), rope(kk)
+    K = torch.cat([T(f32(kc0[0, :pos])), kk], 0)
+    V = torch.cat([T(f32(vc0[0, :pos])), vv.view(1, hd)], 0)
+    att = torch.softmax(qq @ K.T / 8.0, dim=1) @ V
+    x1 = xt + T(Wo) @ att.reshape(-1)
+    h2 = rms(x1, ln2)
+    hh = torch.nn.functional.silu(T(Wg) @ h2) * (T(Wu) @ h2)
+    want = (x1 + T(Wd) @ hh).numpy()
+    assert np.all(np.abs(got - want) <= 2e-2 + 1e-2 * np.abs(want)), np.abs(got - want).max()
+    # the appended cache rows are the rotated k and the plain v
+    assert np.all(np.abs(f32(kc[0, pos]) - kk.numpy().reshape(-1)) <= 2e-2 + 1e-2 * np.abs(kk.numpy().reshape(-1)))
+    assert np.array_equal(kc[0, :pos], kc0[0, :pos]) and np.array_equal(vc[0, :pos], vc0[0, :pos])
+
+
+def test_head_argmax_ties_go_to_first_index():
+    H, V = 64, 40
+    c = oracle.cfg(H, 1, 1, 64, 128)
+    w = bf16(np.random.default_rng(3).normal(0, 0.01, (V, H)))
+    w[9] = bf16(np.full(H, 0.5, np.float32))
+    w[23] = w[9]  # the same row twice: equal top logits
+    head = oracle.Linear(w)
+    norm = bf16(np.ones(H, np.float32))
+    am, _, lg, _, margin = oracle.lm_head(c, norm, head, bf16(np.ones(H, np.float32)))
+    assert lg[9] == lg[23] == lg.max() and am == 9 and margin == 0.0
