@@ -227,6 +227,112 @@ int ming_lm_model_trace(ming_lm_model* m, void* x, void* x1, void* att, void* qk
  * tokens_dev[1..n] receive the argmaxes.  No host synchronisation inside. */
 int ming_lm_generate(ming_ctx* ctx, ming_lm_model* m, ming_kv* kv, int32_t n_steps, int32_t* tokens_dev);
 
+/* ---- DiT flow head and aggregator ------------------------------------------
+ * The reference's fused DiT path (src/ming_fused.zig:482-573) and its
+ * callers DitStack.forward (src/ming_model.zig:770-797), cfmSample (:1143),
+ * aggregate (:1154) and stopProb (:1033).  Rows: R = B*L <= 6 (CFM: 2 CFG
+ * halves x 3; aggregator 1 x 2); bf16 weights [out, in] with biases. */
+
+/* DiT shape (reference: 1024, 16, 64, 4096, eps 1e-6). */
+typedef struct {
+    int32_t hidden, heads, head_dim, ff;
+    float eps;
+} ming_dit_cfg;
+
+/* fused.Block (src/ming_fused.zig:482-500): linears are MING_W_BF16. */
+typedef struct {
+    const void *norm1, *norm2;                 /* bf16 [hidden] */
+    ming_linear wq, wk, wv, wo, w1, w2;
+    const void *bq, *bk, *bv, *bo, *b1, *b2;   /* bf16 */
+} ming_dit_block_w;
+
+/* BlockOut (src/ming_fused.zig:521): caller buffers, bf16.  qkv [3][R][hidden]
+ * (rotated q, rotated k, v), att/x1/x2 [R][hidden], hh [R][ff]. */
+typedef struct {
+    void *qkv, *att, *x1, *hh, *x2;
+} ming_dit_out;
+
+/* Rotary.precompute (src/ming_model.zig:698-704): cos/sin f32 [L][half] =
+ * cos/sin(l * inv_freq[i]) from the checkpoint's f32 inv_freq (host). */
+int ming_rotary_table(ming_ctx* ctx, const float* inv_freq_host, int32_t half, int32_t L, float* cos_dev,
+                      float* sin_dev);
+
+/* fused.block (src/ming_fused.zig:523-539): one DiT block on x [B, L, hidden]
+ * with rotary tables [L][head_dim/2]; all five outputs required. */
+int ming_dit_block(ming_ctx* ctx, const ming_dit_cfg* cfg, const ming_dit_block_w* w, const void* x, int32_t B,
+                   int32_t L, const float* cos_dev, const float* sin_dev, ming_dit_out* out);
+
+/* fused.single (src/ming_fused.zig:542-556): one kernel of a block.  which 0:
+ * A (rms + q/k/v + rotary + attention; out = attention [R][hidden], qkv_tmp
+ * receives q/k/v); 1: B (out = x + out_proj(in), in = attention); 2: C (out =
+ * gelu(ff1(rms(x)))); 3: D (out = x + ff2(in), in = hh). */
+int ming_dit_single(ming_ctx* ctx, int32_t which, const ming_dit_cfg* cfg, const ming_dit_block_w* w, const void* x,
+                    const void* in, int32_t B, int32_t L, const float* cos_dev, const float* sin_dev, void* qkv_tmp,
+                    void* out);
+
+/* fused.embed (src/ming_fused.zig:559-561): CFM input rows h [2][3][hidden] =
+ * [te + ce, xh, x_emb(y)] per CFG half; y [latent], te/ce [2][hidden], xh
+ * [hidden]. */
+int ming_cfm_embed(ming_ctx* ctx, const void* y, const ming_linear* x_emb, const void* bx, const void* te,
+                   const void* ce, const void* xh, void* h_out);
+
+/* fused.final (src/ming_fused.zig:565-573): final rms + linear on rows L-1
+ * and 2L-1 of h [2L][hidden], CFG combine, Euler step `step` (+ SDE when
+ * shift != 0).  dtt/sq bf16 [steps], sde bf16 [steps][latent]. */
+int ming_cfm_final(ming_ctx* ctx, const void* h, int32_t L, const void* norm, const ming_linear* wf, const void* bf,
+                   const void* y, const void* dtt, const void* sq, const void* sde, int32_t step, float cfg,
+                   float shift, void* y_out);
+
+/* Flow head weights (DitStack "flowloss.cfm.model" + embedders + final
+ * layer, src/ming_model.zig:955-965). */
+typedef struct {
+    ming_dit_cfg cfg;
+    int32_t n_blocks;
+    const ming_dit_block_w* blocks;            /* host array [n_blocks] */
+    const float* inv_freq;                     /* host f32 [head_dim/2] (rotary_embed.inv_freq) */
+    ming_linear x_emb, c_emb, t_mlp0, t_mlp2, final;
+    const void *bx, *bc, *bt0, *bt2, *final_norm, *bf;
+} ming_cfm_w;
+
+/* Aggregator weights (DitStack "linear_proj_audio", src/ming_model.zig:966-971). */
+typedef struct {
+    ming_dit_cfg cfg;
+    int32_t n_blocks;
+    const ming_dit_block_w* blocks;
+    const float* inv_freq;
+    ming_linear x_emb, final;
+    const void *bx, *cls, *final_norm, *bf;
+} ming_agg_w;
+
+typedef struct ming_cfm_model ming_cfm_model;
+typedef struct ming_agg_model ming_agg_model;
+
+/* Model.load's flow-head precomputation (src/ming_model.zig:976-1004):
+ * rotary table for L = 3, flow schedule, dt, sqrt|dt| and the 10 timestep
+ * embeddings; workspace for one sample.  Weights stay caller-owned. */
+int ming_cfm_model_create(ming_ctx* ctx, const ming_cfm_w* w, ming_cfm_model** out);
+int ming_cfm_model_destroy(ming_cfm_model* m);
+/* The model's flow schedule (host copies): t [steps+1], dt [steps], sq
+ * [steps], t_emb device pointer [steps][2][hidden]. */
+int ming_cfm_model_tables(ming_cfm_model* m, uint16_t* t, uint16_t* dt, uint16_t* sq, const void** t_emb_dev);
+/* cfmSample (src/ming_model.zig:1143-1151, :1161-1203): 10 Euler steps of
+ * the CFG DiT.  z [lm_hidden], hist/noise [latent], sde [steps][latent] (all
+ * device bf16) -> latent_out [latent]; shift = sigma * sqrt(temperature).
+ * y_steps (optional, device [steps][latent]) receives each step's latent. */
+int ming_cfm_sample(ming_ctx* ctx, ming_cfm_model* m, const void* z, const void* hist, const void* noise,
+                    const void* sde, float cfg, float sigma, float temperature, void* latent_out, void* y_steps);
+
+/* Aggregator precomputation (rotary table for L = 2) and workspace. */
+int ming_agg_model_create(ming_ctx* ctx, const ming_agg_w* w, ming_agg_model** out);
+int ming_agg_model_destroy(ming_agg_model* m);
+/* aggregate (src/ming_model.zig:1042-1053, :1154-1157): latent [latent] ->
+ * next LM input row out [lm_hidden]. */
+int ming_aggregate(ming_ctx* ctx, ming_agg_model* m, const void* latent, void* out);
+
+/* stopProb (src/ming_model.zig:1033-1038): p_dev (device f32) =
+ * softmax(f32(stop_head(z)))[1]; head [2, lm_hidden] bf16 with bias. */
+int ming_stop_prob(ming_ctx* ctx, const ming_linear* head, const void* bias, const void* z, float* p_dev);
+
 /* ---- synthetic inputs (host side; benches and tests) -----------------------
  * Counter-based splitmix64 + Box-Muller: element i of stream (seed, name) is
  * a pure function of (seed, fnv1a64(name), i), so any slice can be generated

@@ -10,6 +10,13 @@ Mirrors of the reference interface (sbusso/ming-tts-serve):
   Context.qgemv         <- mlx_quantized_matmul    src/mlx.zig:279
   Context.quantize      <- mlx_quantize            src/mlx.zig:292
   Context.dequantize    <- mlx_dequantize          src/mlx.zig:288
+  Context.dit_block     <- ming_fused.block        src/ming_fused.zig:523
+  Context.dit_single    <- ming_fused.single       src/ming_fused.zig:542
+  Context.cfm_embed     <- ming_fused.embed        src/ming_fused.zig:559
+  Context.cfm_final     <- ming_fused.final        src/ming_fused.zig:565
+  Context.stop_prob     <- stopProb                src/ming_model.zig:1033
+  CfmModel.sample       <- cfmSample               src/ming_model.zig:1143
+  AggModel.aggregate    <- aggregate               src/ming_model.zig:1154
 """
 import ctypes
 import os
@@ -71,6 +78,32 @@ class LmOut(ctypes.Structure):
     _fields_ = [("qkv", c_void_p), ("o", c_void_p), ("x1", c_void_p), ("hh", c_void_p), ("x2", c_void_p)]
 
 
+class DitCfg(ctypes.Structure):
+    _fields_ = [("hidden", c_i32), ("heads", c_i32), ("head_dim", c_i32), ("ff", c_i32), ("eps", c_f32)]
+
+
+class DitBlockW(ctypes.Structure):
+    _fields_ = [("norm1", c_void_p), ("norm2", c_void_p)] + [
+        (n, Linear) for n in ("wq", "wk", "wv", "wo", "w1", "w2")
+    ] + [(n, c_void_p) for n in ("bq", "bk", "bv", "bo", "b1", "b2")]
+
+
+class DitOut(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in ("qkv", "att", "x1", "hh", "x2")]
+
+
+class CfmW(ctypes.Structure):
+    _fields_ = [("cfg", DitCfg), ("n_blocks", c_i32), ("blocks", c_void_p), ("inv_freq", c_void_p)] + [
+        (n, Linear) for n in ("x_emb", "c_emb", "t_mlp0", "t_mlp2", "final")
+    ] + [(n, c_void_p) for n in ("bx", "bc", "bt0", "bt2", "final_norm", "bf")]
+
+
+class AggW(ctypes.Structure):
+    _fields_ = [("cfg", DitCfg), ("n_blocks", c_i32), ("blocks", c_void_p), ("inv_freq", c_void_p)] + [
+        (n, Linear) for n in ("x_emb", "final")
+    ] + [(n, c_void_p) for n in ("bx", "cls", "final_norm", "bf")]
+
+
 _lib = None
 
 
@@ -116,6 +149,23 @@ def lib():
         "ming_lm_step": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, P(Kv), c_void_p, c_void_p, c_void_p]),
         "ming_lm_generate": (c_i32, [c_void_p, c_void_p, P(Kv), c_i32, c_void_p]),
         "ming_lm_model_trace": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+        "ming_rotary_table": (c_i32, [c_void_p, c_void_p, c_i32, c_i32, c_void_p, c_void_p]),
+        "ming_dit_block": (c_i32, [c_void_p, P(DitCfg), P(DitBlockW), c_void_p, c_i32, c_i32, c_void_p, c_void_p,
+                                   P(DitOut)]),
+        "ming_dit_single": (c_i32, [c_void_p, c_i32, P(DitCfg), P(DitBlockW), c_void_p, c_void_p, c_i32, c_i32,
+                                    c_void_p, c_void_p, c_void_p, c_void_p]),
+        "ming_cfm_embed": (c_i32, [c_void_p, c_void_p, P(Linear), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+        "ming_cfm_final": (c_i32, [c_void_p, c_void_p, c_i32, c_void_p, P(Linear), c_void_p, c_void_p, c_void_p,
+                                   c_void_p, c_void_p, c_i32, c_f32, c_f32, c_void_p]),
+        "ming_cfm_model_create": (c_i32, [c_void_p, P(CfmW), P(c_void_p)]),
+        "ming_cfm_model_destroy": (c_i32, [c_void_p]),
+        "ming_cfm_model_tables": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, P(c_void_p)]),
+        "ming_cfm_sample": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_f32, c_f32, c_f32,
+                                    c_void_p, c_void_p]),
+        "ming_agg_model_create": (c_i32, [c_void_p, P(AggW), P(c_void_p)]),
+        "ming_agg_model_destroy": (c_i32, [c_void_p]),
+        "ming_aggregate": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p]),
+        "ming_stop_prob": (c_i32, [c_void_p, P(Linear), c_void_p, c_void_p, c_void_p]),
         "ming_synth_stream": (ctypes.c_uint64, [ctypes.c_uint64, ctypes.c_char_p]),
         "ming_synth_normal_bf16": (None, [ctypes.c_uint64, c_f32, c_f32, c_void_p, ctypes.c_size_t, c_i32]),
         "ming_synth_uniform_i32": (None, [ctypes.c_uint64, c_i32, c_void_p, ctypes.c_size_t]),
@@ -232,6 +282,99 @@ class Context:
     def lm_layer(self, cfg, layer_w, x, pos, kv, layer, out):
         self.check(self.L.ming_lm_layer(self.h, ctypes.byref(cfg), ctypes.byref(layer_w), ptr(x), int(pos),
                                         ctypes.byref(kv), int(layer), ctypes.byref(out)))
+
+
+    # ---- DiT flow head / aggregator pieces ----
+    def rotary_table(self, inv_freq, L, cos, sin):
+        """inv_freq: numpy f32 [half]; cos/sin: device f32 [L, half]."""
+        import numpy as np
+
+        inv = np.ascontiguousarray(inv_freq, dtype=np.float32)
+        self.check(self.L.ming_rotary_table(self.h, inv.ctypes.data_as(c_void_p), inv.size, int(L), ptr(cos),
+                                            ptr(sin)))
+
+    def dit_block(self, cfg, w, x, B, L, cos, sin, out):
+        self.check(self.L.ming_dit_block(self.h, ctypes.byref(cfg), ctypes.byref(w), ptr(x), int(B), int(L),
+                                         ptr(cos), ptr(sin), ctypes.byref(out)))
+
+    def dit_single(self, which, cfg, w, x, inp, B, L, cos, sin, qkv_tmp, out):
+        self.check(self.L.ming_dit_single(self.h, int(which), ctypes.byref(cfg), ctypes.byref(w), ptr(x), ptr(inp),
+                                          int(B), int(L), ptr(cos), ptr(sin), ptr(qkv_tmp), ptr(out)))
+
+    def cfm_embed(self, y, x_emb, bx, te, ce, xh, h_out):
+        self.check(self.L.ming_cfm_embed(self.h, ptr(y), ctypes.byref(x_emb), ptr(bx), ptr(te), ptr(ce), ptr(xh),
+                                         ptr(h_out)))
+
+    def cfm_final(self, h, L, norm, wf, bf, y, dt, sq, sde, step, cfg, shift, y_out):
+        self.check(self.L.ming_cfm_final(self.h, ptr(h), int(L), ptr(norm), ctypes.byref(wf), ptr(bf), ptr(y),
+                                         ptr(dt), ptr(sq), ptr(sde), int(step), float(cfg), float(shift),
+                                         ptr(y_out)))
+
+    def stop_prob(self, head, bias, z, p):
+        self.check(self.L.ming_stop_prob(self.h, ctypes.byref(head), ptr(bias), ptr(z), ptr(p)))
+
+
+class CfmModel:
+    """ming_cfm_model: the flow head's load-time tables plus one sample's workspace."""
+
+    def __init__(self, ctx, w):
+        self.ctx, self.w = ctx, w  # w: CfmW (its blocks array and inv_freq must stay alive)
+        h = c_void_p()
+        ctx.check(ctx.L.ming_cfm_model_create(ctx.h, ctypes.byref(w), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.ctx.L.ming_cfm_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tables(self):
+        """(t [11], dt [10], sq [10]) as numpy uint16 bf16 bits, and the t_emb device pointer."""
+        import numpy as np
+
+        t = np.empty(11, np.uint16)
+        dt = np.empty(10, np.uint16)
+        sq = np.empty(10, np.uint16)
+        te = c_void_p()
+        self.ctx.check(self.ctx.L.ming_cfm_model_tables(self.h, t.ctypes.data_as(c_void_p),
+                                                        dt.ctypes.data_as(c_void_p), sq.ctypes.data_as(c_void_p),
+                                                        ctypes.byref(te)))
+        return t, dt, sq, te.value
+
+    def sample(self, z, hist, noise, sde, cfg, sigma, temperature, latent_out, y_steps=None):
+        self.ctx.check(self.ctx.L.ming_cfm_sample(self.ctx.h, self.h, ptr(z), ptr(hist), ptr(noise), ptr(sde),
+                                                  float(cfg), float(sigma), float(temperature), ptr(latent_out),
+                                                  ptr(y_steps)))
+
+
+class AggModel:
+    """ming_agg_model: the aggregator's rotary table and workspace."""
+
+    def __init__(self, ctx, w):
+        self.ctx, self.w = ctx, w
+        h = c_void_p()
+        ctx.check(ctx.L.ming_agg_model_create(ctx.h, ctypes.byref(w), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.ctx.L.ming_agg_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def aggregate(self, latent, out):
+        self.ctx.check(self.ctx.L.ming_aggregate(self.ctx.h, self.h, ptr(latent), ptr(out)))
 
 
 class LmModel:

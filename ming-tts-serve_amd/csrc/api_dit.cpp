@@ -1,0 +1,515 @@
+// C-ABI glue of the DiT flow head and aggregator (include/ming_hip.h, "DiT
+// flow head and aggregator"): argument checks, the load-time tables of
+// Model.load (rotary tables, flow schedule, timestep embeddings;
+// src/ming_model.zig:976-1004) and the per-call launch sequences of
+// cfmSample / aggregate / stopProb (src/ming_model.zig:1033-1053, :1143-1203).
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "args.h"
+#include "internal.h"
+
+namespace ming {
+hipError_t launch_dit_stage(hipStream_t st, int which, const DitBlockDev& w, const uint16_t* x, const uint16_t* in,
+                            int B, int L, const float* cos_t, const float* sin_t, uint16_t* qkv, uint16_t* out);
+hipError_t launch_dit_block(hipStream_t st, const DitBlockDev& w, const uint16_t* x, int B, int L,
+                            const float* cos_t, const float* sin_t, uint16_t* qkv, uint16_t* att, uint16_t* x1,
+                            uint16_t* hh, uint16_t* x2);
+hipError_t launch_dit_linear(hipStream_t st, const uint16_t* x, int64_t xrow0, int64_t xstride, int R,
+                             const uint16_t* norm, float eps, const uint16_t* w, int N, int K, const uint16_t* bias,
+                             uint16_t* out, bool silu);
+hipError_t launch_cfm_embed(hipStream_t st, const uint16_t* y, const uint16_t* wx, const uint16_t* bx, int D,
+                            int latent, const uint16_t* te, const uint16_t* ce, const uint16_t* xh, uint16_t* rows);
+hipError_t launch_cfm_final(hipStream_t st, const uint16_t* h, int L, int D, const uint16_t* norm, float eps,
+                            const uint16_t* wf, const uint16_t* bf, int latent, const uint16_t* y, const uint16_t* dt,
+                            const uint16_t* sq, const uint16_t* sde, int step, float cfg, float shift,
+                            uint16_t* y_out);
+hipError_t launch_stop_prob(hipStream_t st, const uint16_t* z, const uint16_t* w, const uint16_t* b, int K, float* p);
+}  // namespace ming
+
+using namespace ming;
+
+namespace {
+
+constexpr int kFlowSteps = 10;  // FLOW_STEPS (src/ming_model.zig:48)
+constexpr int kMaxRows = 6;
+
+bool alive(const ming_ctx* c) { return c && c->alive; }
+
+// Host bf16 helpers for the load-time tables (round to nearest even).
+uint16_t hbf(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+float hf(uint16_t h) {
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+float hrb(float f) { return hf(hbf(f)); }
+
+int check_cfg(ming_ctx* ctx, const ming_dit_cfg* c) {
+    if (!c) return set_err(ctx, MING_E_ARG, "dit: null cfg");
+    if (c->hidden <= 0 || c->hidden % 64 != 0 || c->hidden > 4096 || c->ff <= 0 || c->ff % 64 != 0 || c->ff > 4096)
+        return set_err(ctx, MING_E_UNSUPPORTED, "dit: hidden and ff must be multiples of 64, at most 4096");
+    if (c->head_dim <= 0 || c->head_dim > 64 || c->head_dim % 2 != 0 || c->heads * c->head_dim != c->hidden)
+        return set_err(ctx, MING_E_UNSUPPORTED, "dit: heads * head_dim must equal hidden, head_dim even and <= 64");
+    return MING_OK;
+}
+
+int check_bf16(ming_ctx* ctx, const ming_linear& l, int N, int K, const char* what) {
+    if (l.kind != MING_W_BF16 || !l.w)
+        return set_err(ctx, MING_E_UNSUPPORTED, std::string(what) + ": DiT linears are bf16 [out, in]");
+    if (l.out_features != N || l.in_features != K)
+        return set_err(ctx, MING_E_SHAPE, std::string(what) + ": expected [" + std::to_string(N) + ", " +
+                                              std::to_string(K) + "], got [" + std::to_string(l.out_features) +
+                                              ", " + std::to_string(l.in_features) + "]");
+    if (K % 8 != 0) return set_err(ctx, MING_E_UNSUPPORTED, std::string(what) + ": in_features % 8 != 0");
+    return MING_OK;
+}
+
+int check_block(ming_ctx* ctx, const ming_dit_cfg* c, const ming_dit_block_w* w) {
+    if (!w) return set_err(ctx, MING_E_ARG, "dit: null block");
+    const int D = c->hidden, F = c->ff;
+    int st;
+    if ((st = check_bf16(ctx, w->wq, D, D, "wq")) || (st = check_bf16(ctx, w->wk, D, D, "wk")) ||
+        (st = check_bf16(ctx, w->wv, D, D, "wv")) || (st = check_bf16(ctx, w->wo, D, D, "wo")) ||
+        (st = check_bf16(ctx, w->w1, F, D, "ff1")) || (st = check_bf16(ctx, w->w2, D, F, "ff2")))
+        return st;
+    if (!w->norm1 || !w->norm2 || !w->bq || !w->bk || !w->bv || !w->bo || !w->b1 || !w->b2)
+        return set_err(ctx, MING_E_ARG, "dit: null norm or bias");
+    return MING_OK;
+}
+
+DitBlockDev block_dev(const ming_dit_cfg* c, const ming_dit_block_w* w) {
+    auto p = [](const void* v) { return static_cast<const uint16_t*>(v); };
+    DitBlockDev d;
+    d.D = c->hidden;
+    d.F = c->ff;
+    d.heads = c->heads;
+    d.hd = c->head_dim;
+    d.eps = c->eps;
+    d.norm1 = p(w->norm1);
+    d.norm2 = p(w->norm2);
+    d.wq = p(w->wq.w);
+    d.wk = p(w->wk.w);
+    d.wv = p(w->wv.w);
+    d.wo = p(w->wo.w);
+    d.w1 = p(w->w1.w);
+    d.w2 = p(w->w2.w);
+    d.bq = p(w->bq);
+    d.bk = p(w->bk);
+    d.bv = p(w->bv);
+    d.bo = p(w->bo);
+    d.b1 = p(w->b1);
+    d.b2 = p(w->b2);
+    return d;
+}
+
+const uint16_t* u16(const void* p) { return static_cast<const uint16_t*>(p); }
+uint16_t* u16(void* p) { return static_cast<uint16_t*>(p); }
+
+// Rotary.table in f32 on the host (load time), uploaded.
+int rotary_upload(ming_ctx* ctx, const float* inv_freq, int half, int L, float* cos_dev, float* sin_dev) {
+    std::vector<float> c((size_t)L * half), s((size_t)L * half);
+    for (int l = 0; l < L; l++)
+        for (int i = 0; i < half; i++) {
+            const float f = (float)l * inv_freq[i];
+            c[(size_t)l * half + i] = std::cos(f);
+            s[(size_t)l * half + i] = std::sin(f);
+        }
+    int st;
+    if ((st = hip_check(ctx, hipMemcpyAsync(cos_dev, c.data(), c.size() * 4, hipMemcpyHostToDevice, ctx->stream),
+                        "rotary cos")))
+        return st;
+    if ((st = hip_check(ctx, hipMemcpyAsync(sin_dev, s.data(), s.size() * 4, hipMemcpyHostToDevice, ctx->stream),
+                        "rotary sin")))
+        return st;
+    return hip_check(ctx, hipStreamSynchronize(ctx->stream), "rotary table");
+}
+
+// Per-block workspace of one DiT stack at R rows.
+struct StackBufs {
+    DevBuf rows[2], qkv, att, x1, hh;
+    hipError_t alloc(int R, int D, int F) {
+        hipError_t e = hipSuccess;
+        for (DevBuf* b : {&rows[0], &rows[1], &att, &x1})
+            if (e == hipSuccess) e = b->ensure(sizeof(uint16_t) * (size_t)R * D);
+        if (e == hipSuccess) e = qkv.ensure(sizeof(uint16_t) * (size_t)3 * R * D);
+        if (e == hipSuccess) e = hh.ensure(sizeof(uint16_t) * (size_t)R * F);
+        return e;
+    }
+    void release() {
+        for (DevBuf* b : {&rows[0], &rows[1], &qkv, &att, &x1, &hh}) b->release();
+    }
+};
+
+// The blocks of a stack on rows[0] (B x L rows); returns the buffer holding the output.
+hipError_t run_stack(hipStream_t st, const std::vector<DitBlockDev>& blocks, StackBufs& b, int B, int L,
+                     const float* cos_t, const float* sin_t, uint16_t** out) {
+    int cur = 0;
+    for (const DitBlockDev& w : blocks) {
+        hipError_t e = launch_dit_block(st, w, u16(b.rows[cur].p), B, L, cos_t, sin_t, u16(b.qkv.p), u16(b.att.p),
+                                        u16(b.x1.p), u16(b.hh.p), u16(b.rows[cur ^ 1].p));
+        if (e != hipSuccess) return e;
+        cur ^= 1;
+    }
+    *out = u16(b.rows[cur].p);
+    return hipSuccess;
+}
+
+}  // namespace
+
+struct ming_cfm_model {
+    ming_ctx* ctx = nullptr;
+    ming_dit_cfg cfg{};
+    std::vector<DitBlockDev> blocks;
+    const uint16_t *wx = nullptr, *bx = nullptr, *wc = nullptr, *bc = nullptr, *wf = nullptr, *bf = nullptr,
+                   *final_norm = nullptr;
+    int latent = 0, lm_hidden = 0;
+    uint16_t t[kFlowSteps + 1]{}, dt[kFlowSteps]{}, sq[kFlowSteps]{};
+    DevBuf cos, sin, t_emb, dtd, sqd, zc, ce, xh, y;
+    StackBufs s;
+};
+
+struct ming_agg_model {
+    ming_ctx* ctx = nullptr;
+    ming_dit_cfg cfg{};
+    std::vector<DitBlockDev> blocks;
+    const uint16_t *wx = nullptr, *bx = nullptr, *cls = nullptr, *wf = nullptr, *bf = nullptr,
+                   *final_norm = nullptr;
+    int latent = 0, lm_hidden = 0;
+    DevBuf cos, sin;
+    StackBufs s;
+};
+
+extern "C" {
+
+int ming_rotary_table(ming_ctx* ctx, const float* inv_freq_host, int32_t half, int32_t L, float* cos_dev,
+                      float* sin_dev) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!inv_freq_host || !cos_dev || !sin_dev || half <= 0 || L <= 0)
+        return set_err(ctx, MING_E_ARG, "rotary_table: bad arguments");
+    return rotary_upload(ctx, inv_freq_host, half, L, cos_dev, sin_dev);
+}
+
+int ming_dit_block(ming_ctx* ctx, const ming_dit_cfg* cfg, const ming_dit_block_w* w, const void* x, int32_t B,
+                   int32_t L, const float* cos_dev, const float* sin_dev, ming_dit_out* out) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    int st;
+    if ((st = check_cfg(ctx, cfg)) || (st = check_block(ctx, cfg, w))) return st;
+    if (B <= 0 || L <= 0 || B * L > kMaxRows || L > 8)
+        return set_err(ctx, MING_E_SHAPE, "dit_block: B*L must be in [1, 6] and L <= 8");
+    if (!x || !cos_dev || !sin_dev || !out || !out->qkv || !out->att || !out->x1 || !out->hh || !out->x2)
+        return set_err(ctx, MING_E_ARG, "dit_block: null buffer");
+    const DitBlockDev d = block_dev(cfg, w);
+    return hip_check(ctx,
+                     launch_dit_block(ctx->stream, d, u16(x), B, L, cos_dev, sin_dev, u16(out->qkv), u16(out->att),
+                                      u16(out->x1), u16(out->hh), u16(out->x2)),
+                     "dit_block launch");
+}
+
+int ming_dit_single(ming_ctx* ctx, int32_t which, const ming_dit_cfg* cfg, const ming_dit_block_w* w, const void* x,
+                    const void* in, int32_t B, int32_t L, const float* cos_dev, const float* sin_dev, void* qkv_tmp,
+                    void* out) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    int st;
+    if ((st = check_cfg(ctx, cfg)) || (st = check_block(ctx, cfg, w))) return st;
+    if (which < 0 || which > 3) return set_err(ctx, MING_E_ARG, "dit_single: which must be 0..3");
+    if (B <= 0 || L <= 0 || B * L > kMaxRows || L > 8)
+        return set_err(ctx, MING_E_SHAPE, "dit_single: B*L must be in [1, 6] and L <= 8");
+    if (!x || !out || ((which == 1 || which == 3) && !in) || (which == 0 && (!qkv_tmp || !cos_dev || !sin_dev)))
+        return set_err(ctx, MING_E_ARG, "dit_single: null buffer");
+    const DitBlockDev d = block_dev(cfg, w);
+    return hip_check(ctx,
+                     launch_dit_stage(ctx->stream, which, d, u16(x), u16(in), B, L, cos_dev, sin_dev, u16(qkv_tmp),
+                                      u16(out)),
+                     "dit_single launch");
+}
+
+int ming_cfm_embed(ming_ctx* ctx, const void* y, const ming_linear* x_emb, const void* bx, const void* te,
+                   const void* ce, const void* xh, void* h_out) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!x_emb || !y || !bx || !te || !ce || !xh || !h_out) return set_err(ctx, MING_E_ARG, "cfm_embed: null argument");
+    int st;
+    if ((st = check_bf16(ctx, *x_emb, x_emb->out_features, x_emb->in_features, "x_emb"))) return st;
+    if (x_emb->in_features > 4096 || x_emb->out_features % 8 != 0)
+        return set_err(ctx, MING_E_UNSUPPORTED, "cfm_embed: x_emb shape");
+    return hip_check(ctx,
+                     launch_cfm_embed(ctx->stream, u16(y), u16(x_emb->w), u16(bx), x_emb->out_features,
+                                      x_emb->in_features, u16(te), u16(ce), u16(xh), u16(h_out)),
+                     "cfm_embed launch");
+}
+
+int ming_cfm_final(ming_ctx* ctx, const void* h, int32_t L, const void* norm, const ming_linear* wf, const void* bf,
+                   const void* y, const void* dtt, const void* sq, const void* sde, int32_t step, float cfg,
+                   float shift, void* y_out) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!h || !norm || !wf || !bf || !y || !dtt || !sq || !y_out || (shift != 0.0f && !sde) || L <= 0 || step < 0)
+        return set_err(ctx, MING_E_ARG, "cfm_final: bad arguments");
+    int st;
+    if ((st = check_bf16(ctx, *wf, wf->out_features, wf->in_features, "final"))) return st;
+    if (wf->in_features > 4096) return set_err(ctx, MING_E_UNSUPPORTED, "cfm_final: hidden > 4096");
+    return hip_check(ctx,
+                     launch_cfm_final(ctx->stream, u16(h), L, wf->in_features, u16(norm), 1e-6f, u16(wf->w), u16(bf),
+                                      wf->out_features, u16(y), u16(dtt), u16(sq), u16(sde), step, cfg, shift,
+                                      u16(y_out)),
+                     "cfm_final launch");
+}
+
+// ---- flow head -------------------------------------------------------------------
+
+int ming_cfm_model_create(ming_ctx* ctx, const ming_cfm_w* w, ming_cfm_model** out) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!w || !out || !w->blocks || w->n_blocks <= 0 || !w->inv_freq)
+        return set_err(ctx, MING_E_ARG, "cfm_model_create: bad arguments");
+    *out = nullptr;
+    const ming_dit_cfg* c = &w->cfg;
+    int st;
+    if ((st = check_cfg(ctx, c))) return st;
+    for (int i = 0; i < w->n_blocks; i++)
+        if ((st = check_block(ctx, c, &w->blocks[i]))) return st;
+    const int D = c->hidden, latent = w->x_emb.in_features, H = w->c_emb.in_features;
+    if ((st = check_bf16(ctx, w->x_emb, D, latent, "x_emb")) || (st = check_bf16(ctx, w->c_emb, D, H, "c_emb")) ||
+        (st = check_bf16(ctx, w->t_mlp0, D, 256, "t_mlp0")) || (st = check_bf16(ctx, w->t_mlp2, D, D, "t_mlp2")) ||
+        (st = check_bf16(ctx, w->final, latent, D, "final")))
+        return st;
+    if (H > 4096 || latent > 4096 || latent % 8 != 0)
+        return set_err(ctx, MING_E_UNSUPPORTED, "cfm_model_create: latent/LM hidden sizes");
+    if (!w->bx || !w->bc || !w->bt0 || !w->bt2 || !w->final_norm || !w->bf)
+        return set_err(ctx, MING_E_ARG, "cfm_model_create: null bias or norm");
+    auto* m = new ming_cfm_model;
+    m->ctx = ctx;
+    m->cfg = *c;
+    for (int i = 0; i < w->n_blocks; i++) m->blocks.push_back(block_dev(c, &w->blocks[i]));
+    m->wx = u16(w->x_emb.w);
+    m->bx = u16(w->bx);
+    m->wc = u16(w->c_emb.w);
+    m->bc = u16(w->bc);
+    m->wf = u16(w->final.w);
+    m->bf = u16(w->bf);
+    m->final_norm = u16(w->final_norm);
+    m->latent = latent;
+    m->lm_hidden = H;
+    const int half = c->head_dim / 2, L = 3;
+    hipStream_t s = ctx->stream;
+    hipError_t e = m->cos.ensure(sizeof(float) * L * half);
+    if (e == hipSuccess) e = m->sin.ensure(sizeof(float) * L * half);
+    if (e == hipSuccess) e = m->t_emb.ensure(sizeof(uint16_t) * (size_t)kFlowSteps * 2 * D);
+    if (e == hipSuccess) e = m->dtd.ensure(sizeof(uint16_t) * kFlowSteps);
+    if (e == hipSuccess) e = m->sqd.ensure(sizeof(uint16_t) * kFlowSteps);
+    if (e == hipSuccess) e = m->zc.ensure(sizeof(uint16_t) * 2 * (size_t)H);
+    if (e == hipSuccess) e = m->ce.ensure(sizeof(uint16_t) * 2 * (size_t)D);
+    if (e == hipSuccess) e = m->xh.ensure(sizeof(uint16_t) * (size_t)D);
+    if (e == hipSuccess) e = m->y.ensure(sizeof(uint16_t) * (size_t)latent);
+    if (e == hipSuccess) e = m->s.alloc(2 * L, D, c->ff);
+    if (e == hipSuccess) e = hipMemsetAsync(m->zc.p, 0, m->zc.bytes, s);
+    if (e != hipSuccess) {
+        ming_cfm_model_destroy(m);
+        return hip_check(ctx, e, "cfm_model_create");
+    }
+    if ((st = rotary_upload(ctx, w->inv_freq, half, L, static_cast<float*>(m->cos.p), static_cast<float*>(m->sin.p)))) {
+        ming_cfm_model_destroy(m);
+        return st;
+    }
+    // flowSchedule in bf16 (src/ming_model.zig:1207-1215); flow_dt, flow_sq (:995-1002)
+    {
+        static const float sched[kFlowSteps + 1] = {0, 2, 4, 6, 8, 12, 16, 20, 24, 28, 32};
+        const float c32 = hrb(1.0f / 32.0f), hpi = hrb((float)(3.14159265358979323846 / 2.0));
+        for (int i = 0; i <= kFlowSteps; i++) {
+            const float ti = hrb(c32 * hrb(sched[i]));
+            const float ct = hrb(std::cos(hrb(hpi * ti)));
+            const float sw = hrb(hrb(ct - 1.0f) + ti);
+            m->t[i] = hbf(ti + hrb(-1.0f * sw));
+        }
+        for (int i = 0; i < kFlowSteps; i++) {
+            const float d = hrb(hf(m->t[i + 1]) - hf(m->t[i]));
+            m->dt[i] = hbf(d);
+            m->sq[i] = hbf(std::pow(std::fabs(d), hrb(0.5f)));
+        }
+    }
+    // timestep embeddings (:976-992, :1064-1076): sinusoid rows on the host, MLP on the GPU
+    std::vector<uint16_t> sc((size_t)kFlowSteps * 2 * 256);
+    {
+        const float ef = (float)(std::log(10000.0) / 127.0);
+        float fr[128];
+        for (int k = 0; k < 128; k++) fr[k] = std::exp((float)k * -ef);
+        for (int i = 0; i < kFlowSteps; i++) {
+            const float ts = hrb(hrb(1000.0f) * hf(m->t[i]));
+            for (int r = 0; r < 2; r++)
+                for (int k = 0; k < 128; k++) {
+                    const float a = ts * fr[k];
+                    sc[((size_t)i * 2 + r) * 256 + k] = hbf(std::sin(a));
+                    sc[((size_t)i * 2 + r) * 256 + 128 + k] = hbf(std::cos(a));
+                }
+        }
+    }
+    DevBuf scd, tmp;
+    e = scd.ensure(sizeof(uint16_t) * sc.size());
+    if (e == hipSuccess) e = tmp.ensure(sizeof(uint16_t) * 2 * (size_t)D);
+    if (e == hipSuccess) e = hipMemcpyAsync(scd.p, sc.data(), sizeof(uint16_t) * sc.size(), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(m->dtd.p, m->dt, sizeof(m->dt), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(m->sqd.p, m->sq, sizeof(m->sq), hipMemcpyHostToDevice, s);
+    for (int i = 0; i < kFlowSteps && e == hipSuccess; i++) {
+        e = launch_dit_linear(s, u16(scd.p) + (size_t)i * 2 * 256, 0, 1, 2, nullptr, 0.0f, u16(w->t_mlp0.w), D, 256,
+                              u16(w->bt0), u16(tmp.p), true);
+        if (e == hipSuccess)
+            e = launch_dit_linear(s, u16(tmp.p), 0, 1, 2, nullptr, 0.0f, u16(w->t_mlp2.w), D, D, u16(w->bt2),
+                                  u16(m->t_emb.p) + (size_t)i * 2 * D, false);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    scd.release();
+    tmp.release();
+    if (e != hipSuccess) {
+        ming_cfm_model_destroy(m);
+        return hip_check(ctx, e, "cfm_model_create tables");
+    }
+    *out = m;
+    return MING_OK;
+}
+
+int ming_cfm_model_destroy(ming_cfm_model* m) {
+    if (!m) return MING_E_NOT_INIT;
+    for (DevBuf* b : {&m->cos, &m->sin, &m->t_emb, &m->dtd, &m->sqd, &m->zc, &m->ce, &m->xh, &m->y}) b->release();
+    m->s.release();
+    delete m;
+    return MING_OK;
+}
+
+int ming_cfm_model_tables(ming_cfm_model* m, uint16_t* t, uint16_t* dt, uint16_t* sq, const void** t_emb_dev) {
+    if (!m) return MING_E_NOT_INIT;
+    if (t) std::memcpy(t, m->t, sizeof(m->t));
+    if (dt) std::memcpy(dt, m->dt, sizeof(m->dt));
+    if (sq) std::memcpy(sq, m->sq, sizeof(m->sq));
+    if (t_emb_dev) *t_emb_dev = m->t_emb.p;
+    return MING_OK;
+}
+
+int ming_cfm_sample(ming_ctx* ctx, ming_cfm_model* m, const void* z, const void* hist, const void* noise,
+                    const void* sde, float cfg, float sigma, float temperature, void* latent_out, void* y_steps) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!m) return set_err(ctx, MING_E_NOT_INIT, "cfm_sample: null model");
+    const float shift = sigma * std::sqrt(temperature);
+    if (!z || !hist || !noise || !latent_out || (shift != 0.0f && !sde))
+        return set_err(ctx, MING_E_ARG, "cfm_sample: null buffer");
+    hipStream_t s = ctx->stream;
+    const int D = m->cfg.hidden, H = m->lm_hidden, lat = m->latent, L = 3;
+    const float eps = m->cfg.eps;
+    // once per sample: c_emb([z, 0]) and x_emb(hist) (:1196-1197)
+    hipError_t e = hipMemcpyAsync(m->zc.p, z, sizeof(uint16_t) * H, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess)
+        e = launch_dit_linear(s, u16(m->zc.p), 0, 1, 2, nullptr, eps, m->wc, D, H, m->bc, u16(m->ce.p), false);
+    if (e == hipSuccess)
+        e = launch_dit_linear(s, u16(hist), 0, 1, 1, nullptr, eps, m->wx, D, lat, m->bx, u16(m->xh.p), false);
+    const uint16_t* y = u16(noise);
+    for (int i = 0; i < kFlowSteps && e == hipSuccess; i++) {
+        e = launch_cfm_embed(s, y, m->wx, m->bx, D, lat, u16(m->t_emb.p) + (size_t)i * 2 * D, u16(m->ce.p),
+                             u16(m->xh.p), u16(m->s.rows[0].p));
+        uint16_t* h = nullptr;
+        if (e == hipSuccess)
+            e = run_stack(s, m->blocks, m->s, 2, L, static_cast<const float*>(m->cos.p),
+                          static_cast<const float*>(m->sin.p), &h);
+        if (e == hipSuccess)
+            e = launch_cfm_final(s, h, L, D, m->final_norm, eps, m->wf, m->bf, lat, y, u16(m->dtd.p), u16(m->sqd.p),
+                                 u16(sde), i, cfg, shift, u16(m->y.p));
+        y = u16(m->y.p);
+        if (e == hipSuccess && y_steps)
+            e = hipMemcpyAsync(u16(y_steps) + (size_t)i * lat, m->y.p, sizeof(uint16_t) * lat,
+                               hipMemcpyDeviceToDevice, s);
+    }
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(latent_out, m->y.p, sizeof(uint16_t) * lat, hipMemcpyDeviceToDevice, s);
+    return hip_check(ctx, e, "cfm_sample");
+}
+
+// ---- aggregator ---------------------------------------------------------------------
+
+int ming_agg_model_create(ming_ctx* ctx, const ming_agg_w* w, ming_agg_model** out) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!w || !out || !w->blocks || w->n_blocks <= 0 || !w->inv_freq)
+        return set_err(ctx, MING_E_ARG, "agg_model_create: bad arguments");
+    *out = nullptr;
+    const ming_dit_cfg* c = &w->cfg;
+    int st;
+    if ((st = check_cfg(ctx, c))) return st;
+    for (int i = 0; i < w->n_blocks; i++)
+        if ((st = check_block(ctx, c, &w->blocks[i]))) return st;
+    const int D = c->hidden, latent = w->x_emb.in_features, H = w->final.out_features;
+    if ((st = check_bf16(ctx, w->x_emb, D, latent, "x_emb")) || (st = check_bf16(ctx, w->final, H, D, "final")))
+        return st;
+    if (!w->bx || !w->cls || !w->final_norm || !w->bf) return set_err(ctx, MING_E_ARG, "agg_model_create: null bias");
+    auto* m = new ming_agg_model;
+    m->ctx = ctx;
+    m->cfg = *c;
+    for (int i = 0; i < w->n_blocks; i++) m->blocks.push_back(block_dev(c, &w->blocks[i]));
+    m->wx = u16(w->x_emb.w);
+    m->bx = u16(w->bx);
+    m->cls = u16(w->cls);
+    m->wf = u16(w->final.w);
+    m->bf = u16(w->bf);
+    m->final_norm = u16(w->final_norm);
+    m->latent = latent;
+    m->lm_hidden = H;
+    const int half = c->head_dim / 2, L = 2;
+    hipError_t e = m->cos.ensure(sizeof(float) * L * half);
+    if (e == hipSuccess) e = m->sin.ensure(sizeof(float) * L * half);
+    if (e == hipSuccess) e = m->s.alloc(L, D, c->ff);
+    if (e != hipSuccess) {
+        ming_agg_model_destroy(m);
+        return hip_check(ctx, e, "agg_model_create");
+    }
+    if ((st = rotary_upload(ctx, w->inv_freq, half, L, static_cast<float*>(m->cos.p), static_cast<float*>(m->sin.p)))) {
+        ming_agg_model_destroy(m);
+        return st;
+    }
+    *out = m;
+    return MING_OK;
+}
+
+int ming_agg_model_destroy(ming_agg_model* m) {
+    if (!m) return MING_E_NOT_INIT;
+    m->cos.release();
+    m->sin.release();
+    m->s.release();
+    delete m;
+    return MING_OK;
+}
+
+int ming_aggregate(ming_ctx* ctx, ming_agg_model* m, const void* latent, void* out) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!m) return set_err(ctx, MING_E_NOT_INIT, "aggregate: null model");
+    if (!latent || !out) return set_err(ctx, MING_E_ARG, "aggregate: null buffer");
+    hipStream_t s = ctx->stream;
+    const int D = m->cfg.hidden;
+    // h = [cls, x_emb(latent)] (:1046-1050)
+    hipError_t e = hipMemcpyAsync(m->s.rows[0].p, m->cls, sizeof(uint16_t) * D, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess)
+        e = launch_dit_linear(s, u16(latent), 0, 1, 1, nullptr, 0.0f, m->wx, D, m->latent, m->bx,
+                              u16(m->s.rows[0].p) + D, false);
+    uint16_t* h = nullptr;
+    if (e == hipSuccess)
+        e = run_stack(s, m->blocks, m->s, 1, 2, static_cast<const float*>(m->cos.p),
+                      static_cast<const float*>(m->sin.p), &h);
+    // final(rms(h)) on row 0 (:1051-1052)
+    if (e == hipSuccess)
+        e = launch_dit_linear(s, h, 0, 1, 1, m->final_norm, m->cfg.eps, m->wf, m->lm_hidden, D, m->bf, u16(out),
+                              false);
+    return hip_check(ctx, e, "aggregate");
+}
+
+int ming_stop_prob(ming_ctx* ctx, const ming_linear* head, const void* bias, const void* z, float* p_dev) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!head || !bias || !z || !p_dev) return set_err(ctx, MING_E_ARG, "stop_prob: null argument");
+    int st;
+    if ((st = check_bf16(ctx, *head, 2, head->in_features, "stop_head"))) return st;
+    if (head->in_features > 4096) return set_err(ctx, MING_E_UNSUPPORTED, "stop_prob: hidden > 4096");
+    return hip_check(ctx, launch_stop_prob(ctx->stream, u16(z), u16(head->w), u16(bias), head->in_features, p_dev),
+                     "stop_prob launch");
+}
+
+}  // extern "C"

@@ -78,6 +78,16 @@ struct StepArgs {
     uint64_t* hubtab;         // [kMaxHubs] tagged XCC id of each hub
 };
 
+// One DiT block (fused.Block, src/ming_fused.zig:482-500): bf16 [out, in]
+// linears with biases, two RMSNorm weights; D = hidden, F = feed-forward.
+struct DitBlockDev {
+    int D, F, heads, hd;
+    float eps;
+    const uint16_t *norm1, *norm2;
+    const uint16_t *wq, *wk, *wv, *wo, *w1, *w2;
+    const uint16_t *bq, *bk, *bv, *bo, *b1, *b2;
+};
+
 constexpr int kMaxHubs = 8;
 constexpr int kImgSlots = 5;  // q/k/v, o_proj, gate/up, down, LM head
 

@@ -8,6 +8,7 @@ HF init).  With quant=True every linear is quantized on the GPU to MLX affine
 4-bit / group 64 (ming_quantize); the embedding table doubles as the tied LM
 head (Qwen2-0.5B convention).
 """
+import ctypes
 import math
 from dataclasses import dataclass
 
@@ -198,5 +199,153 @@ def lm_bytes_per_token(spec: LmSpec, ctx_len):
     return spec.weight_bytes_q4() + small + kv_row * ctx_len + kv_row
 
 
-__all__ = ["LmSpec", "QWEN2_05B", "SyntheticLm", "KvCache", "lm_bytes_per_token", "W_AFFINE", "W_BF16",
+# ---- DiT flow head, aggregator and stop head -------------------------------------
+
+
+@dataclass
+class DitSpec:
+    """Shapes of the flow head / aggregator (src/ming_model.zig:37-41, :943-956)."""
+    hidden: int = 1024
+    heads: int = 16
+    head_dim: int = 64
+    ff: int = 4096
+    eps: float = 1e-6
+    cfm_blocks: int = 8
+    agg_blocks: int = 8
+    latent: int = 64
+    lm_hidden: int = 896
+
+    def cfg(self):
+        from . import DitCfg
+
+        return DitCfg(self.hidden, self.heads, self.head_dim, self.ff, self.eps)
+
+    def inv_freq(self):
+        """RotaryEmbedding.inv_freq = 1 / 10000^(2i / head_dim), f32."""
+        i = np.arange(0, self.head_dim, 2, dtype=np.float32)
+        return (1.0 / (np.float32(10000.0) ** (i / np.float32(self.head_dim)))).astype(np.float32)
+
+    def block_params(self):
+        D, F = self.hidden, self.ff
+        return 4 * D * D + 2 * D * F + 5 * D + F
+
+    def cfm_weight_bytes(self):
+        D, H, lat = self.hidden, self.lm_hidden, self.latent
+        return 2 * (self.cfm_blocks * self.block_params() + D * lat + D * H + lat * D + 3 * D + lat)
+
+
+MING_DIT = DitSpec()
+
+_BLOCK_KEYS = (("wq", "attn.to_q"), ("wk", "attn.to_k"), ("wv", "attn.to_v"), ("wo", "attn.to_out.0"),
+               ("w1", "mlp.ff.0.0"), ("w2", "mlp.ff.2"))
+
+
+class SyntheticFlow:
+    """bf16 weights of the flow head ("flowloss.cfm.model"), aggregator
+    ("linear_proj_audio") and stop head under the checkpoint's key names
+    (src/ming_model.zig:941-956, :728-745), random-init: linears and biases
+    bf16(N(0, std)), norm weights 1 + N(0, norm_std).  Host copies (numpy
+    uint16) are kept for the CPU checker; device copies feed the C ABI."""
+
+    def __init__(self, ctx, spec: DitSpec = MING_DIT, seed=0, std=0.02, norm_std=0.0, device="cuda", threads=None,
+                 parts=("cfm", "agg", "stop")):
+        import torch
+
+        from . import AggW, CfmW, DitBlockW
+
+        self.ctx, self.spec, self.device = ctx, spec, device
+        self.hostw, self.dev = {}, {}
+        D, F, lat, H = spec.hidden, spec.ff, spec.latent, spec.lm_hidden
+
+        def put(name, shape, mean=0.0, sd=std):
+            a = synth_normal_bf16(seed, name, int(np.prod(shape)), mean, sd, threads).reshape(shape)
+            self.hostw[name] = a
+            self.dev[name] = torch.from_numpy(a.view(np.int16)).to(device).view(torch.bfloat16)
+
+        def lin(name, N, K, bias=True):
+            put(name + ".weight", (N, K))
+            if bias:
+                put(name + ".bias", (N,))
+
+        def norm(name, n):
+            if norm_std == 0.0:
+                a = np.full(n, 0x3F80, np.uint16)
+                self.hostw[name] = a
+                self.dev[name] = torch.from_numpy(a.view(np.int16)).to(device).view(torch.bfloat16)
+            else:
+                put(name, (n,), 1.0, norm_std)
+
+        def blocks(prefix, n):
+            for i in range(n):
+                b = f"{prefix}.blocks.{i}"
+                norm(f"{b}.norm1.weight", D)
+                norm(f"{b}.norm2.weight", D)
+                for k, key in _BLOCK_KEYS:
+                    N, K = {"w1": (F, D), "w2": (D, F)}.get(k, (D, D))
+                    lin(f"{b}.{key}", N, K)
+
+        self.inv_freq = spec.inv_freq()
+        if "cfm" in parts:
+            C = "flowloss.cfm.model"
+            blocks(C, spec.cfm_blocks)
+            lin(f"{C}.t_embedder.time_mlp.0", D, 256)
+            lin(f"{C}.t_embedder.time_mlp.2", D, D)
+            lin(f"{C}.x_embedder", D, lat)
+            lin(f"{C}.c_embedder.cond_embedder", D, H)
+            norm(f"{C}.final_layer.norm_final.weight", D)
+            lin(f"{C}.final_layer.linear", lat, D)
+            self.cfm_blocks = (DitBlockW * spec.cfm_blocks)(*(self.block_w(C, i) for i in range(spec.cfm_blocks)))
+            self.cfm_w = CfmW(spec.cfg(), spec.cfm_blocks, ctypes.cast(self.cfm_blocks, ctypes.c_void_p),
+                              self.inv_freq.ctypes.data, self.lin_w(f"{C}.x_embedder"),
+                              self.lin_w(f"{C}.c_embedder.cond_embedder"), self.lin_w(f"{C}.t_embedder.time_mlp.0"),
+                              self.lin_w(f"{C}.t_embedder.time_mlp.2"), self.lin_w(f"{C}.final_layer.linear"),
+                              *(self.ptr(f"{C}.{k}") for k in ("x_embedder.bias", "c_embedder.cond_embedder.bias",
+                                                                "t_embedder.time_mlp.0.bias",
+                                                                "t_embedder.time_mlp.2.bias",
+                                                                "final_layer.norm_final.weight",
+                                                                "final_layer.linear.bias")))
+        if "agg" in parts:
+            A = "linear_proj_audio"
+            blocks(A, spec.agg_blocks)
+            lin(f"{A}.x_embedder", D, lat)
+            put(f"{A}.word_embedder.weight", (D,), 0.0, 1.0)
+            norm(f"{A}.final_layer.norm_final.weight", D)
+            lin(f"{A}.final_layer.linear", H, D)
+            self.agg_blocks = (DitBlockW * spec.agg_blocks)(*(self.block_w(A, i) for i in range(spec.agg_blocks)))
+            self.agg_w = AggW(spec.cfg(), spec.agg_blocks, ctypes.cast(self.agg_blocks, ctypes.c_void_p),
+                              self.inv_freq.ctypes.data, self.lin_w(f"{A}.x_embedder"),
+                              self.lin_w(f"{A}.final_layer.linear"),
+                              *(self.ptr(f"{A}.{k}") for k in ("x_embedder.bias", "word_embedder.weight",
+                                                                "final_layer.norm_final.weight",
+                                                                "final_layer.linear.bias")))
+        if "stop" in parts:
+            lin("stop_head", 2, H)
+
+    # ---- C-ABI views ----
+    def ptr(self, name):
+        return self.dev[name].data_ptr()
+
+    def lin_w(self, name):
+        return linear(self.dev[name + ".weight"])
+
+    def block_w(self, prefix, i):
+        from . import DitBlockW
+
+        b = f"{prefix}.blocks.{i}"
+        return DitBlockW(self.ptr(f"{b}.norm1.weight"), self.ptr(f"{b}.norm2.weight"),
+                         *(self.lin_w(f"{b}.{key}") for _, key in _BLOCK_KEYS),
+                         *(self.ptr(f"{b}.{key}.bias") for _, key in _BLOCK_KEYS))
+
+    def cfm_model(self):
+        from . import CfmModel
+
+        return CfmModel(self.ctx, self.cfm_w)
+
+    def agg_model(self):
+        from . import AggModel
+
+        return AggModel(self.ctx, self.agg_w)
+
+
+__all__ = ["DitSpec", "MING_DIT", "SyntheticFlow", "LmSpec", "QWEN2_05B", "SyntheticLm", "KvCache", "lm_bytes_per_token", "W_AFFINE", "W_BF16",
            "Linear", "math"]

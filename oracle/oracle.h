@@ -124,6 +124,95 @@ int or_lm_head(const or_lm_cfg* c, const uint16_t* norm, const or_linear* head, 
 /* Embedding row gather: bf16 table [V,H] or affine-quantized table. */
 void or_embed(const or_linear* table, int id, uint16_t* out);
 
+/* ---- DiT flow head and aggregator ------------------------------------------ */
+typedef struct {
+    int D, heads, head_dim, ff;   /* 1024, 16, 64, 4096 in the reference */
+    float eps;                    /* rms_norm eps, 1e-6 */
+} or_dit_cfg;
+
+/* One DiT block: bf16 [out,in] linears with biases (addmm), two RMSNorms. */
+typedef struct {
+    const uint16_t *norm1, *norm2;
+    or_linear q, k, v, o, ff1, ff2;
+    const uint16_t *bq, *bk, *bv, *bo, *b1, *b2;
+} or_dit_block;
+
+/* Intermediates of one block (optional). */
+typedef struct {
+    uint16_t* qkv;  /* [3][R][D]: rotated q, rotated k, v */
+    uint16_t* att;  /* [R][D] attention output */
+    uint16_t* x1;   /* [R][D] x + out(att) */
+    uint16_t* hh;   /* [R][ff] gelu_approx(ff1(rms(x1))) */
+} or_dit_trace;
+
+/* x_transformers RotaryEmbedding table: cos/sin[l][i] = cos/sin(l * inv_freq[i]) in f32. */
+void or_rotary_table(const float* inv_freq, int half, int L, float* cos_t, float* sin_t);
+/* Interleaved-pair rotary (2i, 2i+1) of every head of the R = B*L rows of x [R][heads*hd]
+ * (row r at position r % L): bf16 * f32 table products in f32, rounded once. */
+void or_rotary(uint16_t* x, int R, int L, int heads, int hd, const float* cos_t, const float* sin_t);
+/* One block on x [B*L][D] -> out [B*L][D]. */
+void or_dit_block_fwd(const or_dit_cfg* c, const or_dit_block* b, const uint16_t* x, int B, int L,
+                      const float* cos_t, const float* sin_t, uint16_t* out, or_dit_trace* tr);
+
+/* EPSS + sway flow schedule, 11 bf16 values. */
+void or_flow_schedule(uint16_t* t);
+/* Step sizes dt[i] = t[i+1] - t[i] and sq[i] = |dt[i]|^0.5, bf16 [10] each. */
+void or_flow_steps(const uint16_t* t, uint16_t* dt, uint16_t* sq);
+/* Timestep sinusoid frequencies exp(-k ln(1e4)/127), f32 [128]. */
+void or_t_freq(float* f);
+/* TimestepEmbedder for scalar t (bf16): out [2][D] (both CFG rows equal). */
+void or_timestep_embed(const or_linear* mlp0, const uint16_t* b0, const or_linear* mlp2, const uint16_t* b2,
+                       const float* t_freq, uint16_t t, uint16_t* out);
+
+typedef struct {
+    or_dit_cfg c;
+    int n_blocks;
+    const or_dit_block* blocks;
+    or_linear x_emb;                 /* latent (64) -> D */
+    const uint16_t* bx;
+    or_linear c_emb;                 /* LM hidden (896) -> D */
+    const uint16_t* bc;
+    const uint16_t* final_norm;      /* [D] */
+    or_linear final;                 /* D -> latent */
+    const uint16_t* bf;
+    const uint16_t* t_emb;           /* [steps][2][D] */
+    const uint16_t* dt;              /* [steps] */
+    const uint16_t* sq;              /* [steps] */
+    const float *cos_t, *sin_t;      /* rotary tables for L = 3 */
+    int steps;
+} or_cfm_model;
+
+/* CFM.sample for one LM step: z [hidden], hist [latent], noise [latent],
+ * sde [steps][latent] -> out [latent]; y_steps [steps][latent] (optional)
+ * receives the latent after every Euler step. */
+void or_cfm_sample(const or_cfm_model* m, const uint16_t* z, const uint16_t* hist, const uint16_t* noise,
+                   const uint16_t* sde, float cfg, float shift_k, uint16_t* out, uint16_t* y_steps);
+/* The 6 DiT input rows [t_emb+c_emb, x_emb(hist), x_emb(y)] x 2 CFG halves for step i. */
+void or_cfm_rows(const or_cfm_model* m, const uint16_t* z, const uint16_t* hist, const uint16_t* y, int step,
+                 uint16_t* rows);
+/* Final norm + linear on the last row of each half, CFG combine and Euler
+ * update for step i: h [2*L][D], y [latent] -> y_out [latent]. */
+void or_cfm_final(const or_cfm_model* m, const uint16_t* h, int L, const uint16_t* y, const uint16_t* sde, int step,
+                  float cfg, float shift_k, uint16_t* y_out);
+
+typedef struct {
+    or_dit_cfg c;
+    int n_blocks;
+    const or_dit_block* blocks;
+    or_linear x_emb;                 /* latent -> D */
+    const uint16_t* bx;
+    const uint16_t* cls;             /* [D] */
+    const uint16_t* final_norm;      /* [D] */
+    or_linear final;                 /* D -> LM hidden */
+    const uint16_t* bf;
+    const float *cos_t, *sin_t;      /* rotary tables for L = 2 */
+} or_agg_model;
+
+/* Aggregator: latent [latent] -> next LM input row [final.N]. */
+void or_aggregate(const or_agg_model* m, const uint16_t* latent, uint16_t* out);
+/* softmax(f32(stop_head(z)))[1]. */
+float or_stop_prob(const or_linear* head, const uint16_t* bias, const uint16_t* z);
+
 /* ---- CPU threads ---------------------------------------------------------- */
 void or_set_threads(int n);
 int or_get_threads(void);

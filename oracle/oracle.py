@@ -40,6 +40,33 @@ class OrLmTrace(ctypes.Structure):
     _fields_ = [("h", c_void_p), ("qkv", c_void_p), ("att", c_void_p), ("x1", c_void_p), ("hh", c_void_p)]
 
 
+class OrDitCfg(ctypes.Structure):
+    _fields_ = [("D", c_int), ("heads", c_int), ("head_dim", c_int), ("ff", c_int), ("eps", c_f32)]
+
+
+class OrDitBlock(ctypes.Structure):
+    _fields_ = [("norm1", c_void_p), ("norm2", c_void_p)] + [
+        (n, OrLinear) for n in ("q", "k", "v", "o", "ff1", "ff2")] + [
+        (n, c_void_p) for n in ("bq", "bk", "bv", "bo", "b1", "b2")]
+
+
+class OrDitTrace(ctypes.Structure):
+    _fields_ = [("qkv", c_void_p), ("att", c_void_p), ("x1", c_void_p), ("hh", c_void_p)]
+
+
+class OrCfmModel(ctypes.Structure):
+    _fields_ = [("c", OrDitCfg), ("n_blocks", c_int), ("blocks", c_void_p), ("x_emb", OrLinear), ("bx", c_void_p),
+                ("c_emb", OrLinear), ("bc", c_void_p), ("final_norm", c_void_p), ("final", OrLinear),
+                ("bf", c_void_p), ("t_emb", c_void_p), ("dt", c_void_p), ("sq", c_void_p), ("cos_t", c_void_p),
+                ("sin_t", c_void_p), ("steps", c_int)]
+
+
+class OrAggModel(ctypes.Structure):
+    _fields_ = [("c", OrDitCfg), ("n_blocks", c_int), ("blocks", c_void_p), ("x_emb", OrLinear), ("bx", c_void_p),
+                ("cls", c_void_p), ("final_norm", c_void_p), ("final", OrLinear), ("bf", c_void_p),
+                ("cos_t", c_void_p), ("sin_t", c_void_p)]
+
+
 _lib = None
 
 
@@ -71,6 +98,21 @@ def lib():
         "or_lm_head": (c_int, [P(OrLmCfg), c_void_p, P(OrLinear), c_void_p, c_void_p, c_void_p, c_void_p,
                                P(c_f32)]),
         "or_embed": (None, [P(OrLinear), c_int, c_void_p]),
+        "or_rotary_table": (None, [c_void_p, c_int, c_int, c_void_p, c_void_p]),
+        "or_rotary": (None, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
+        "or_dit_block_fwd": (None, [P(OrDitCfg), P(OrDitBlock), c_void_p, c_int, c_int, c_void_p, c_void_p,
+                                    c_void_p, P(OrDitTrace)]),
+        "or_flow_schedule": (None, [c_void_p]),
+        "or_flow_steps": (None, [c_void_p, c_void_p, c_void_p]),
+        "or_t_freq": (None, [c_void_p]),
+        "or_timestep_embed": (None, [P(OrLinear), c_void_p, P(OrLinear), c_void_p, c_void_p, ctypes.c_uint16,
+                                     c_void_p]),
+        "or_cfm_rows": (None, [P(OrCfmModel), c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+        "or_cfm_final": (None, [P(OrCfmModel), c_void_p, c_int, c_void_p, c_void_p, c_int, c_f32, c_f32, c_void_p]),
+        "or_cfm_sample": (None, [P(OrCfmModel), c_void_p, c_void_p, c_void_p, c_void_p, c_f32, c_f32, c_void_p,
+                                 c_void_p]),
+        "or_aggregate": (None, [P(OrAggModel), c_void_p, c_void_p]),
+        "or_stop_prob": (c_f32, [P(OrLinear), c_void_p, c_void_p]),
         "or_set_threads": (None, [c_int]),
         "or_get_threads": (c_int, []),
     }
@@ -269,3 +311,141 @@ def set_threads(n):
 
 def get_threads():
     return lib().or_get_threads()
+
+
+# ---- DiT flow head and aggregator ---------------------------------------------------
+
+def dit_cfg(D=1024, heads=16, head_dim=64, ff=4096, eps=1e-6):
+    return OrDitCfg(D, heads, head_dim, ff, eps)
+
+
+class DitBlock:
+    """numpy bf16 weights of one DiT block: dict with norm1, norm2, wq, wk, wv, wo, w1, w2 ([out, in]) and
+    bq, bk, bv, bo, b1, b2."""
+
+    def __init__(self, w):
+        self.a = {k: _c(v, np.uint16) for k, v in w.items()}
+        lin = {n: Linear(self.a[k]) for n, k in (("q", "wq"), ("k", "wk"), ("v", "wv"), ("o", "wo"),
+                                                  ("ff1", "w1"), ("ff2", "w2"))}
+        self.lin = lin
+        self.c = OrDitBlock(_p(self.a["norm1"]), _p(self.a["norm2"]), lin["q"].c, lin["k"].c, lin["v"].c,
+                            lin["o"].c, lin["ff1"].c, lin["ff2"].c,
+                            *(_p(self.a[k]) for k in ("bq", "bk", "bv", "bo", "b1", "b2")))
+
+
+def rotary_table(inv_freq, L):
+    inv = _c(np.asarray(inv_freq, np.float32), np.float32)
+    half = inv.size
+    c = np.empty((L, half), np.float32)
+    s = np.empty((L, half), np.float32)
+    lib().or_rotary_table(_p(inv), half, L, _p(c), _p(s))
+    return c, s
+
+
+def rotary(x, L, heads, hd, cos_t, sin_t):
+    x = np.array(x, dtype=np.uint16, copy=True, order="C")
+    R = x.shape[0]
+    lib().or_rotary(_p(x), R, L, heads, hd, _p(_c(cos_t, np.float32)), _p(_c(sin_t, np.float32)))
+    return x
+
+
+def dit_block_fwd(c, blk, x, B, L, cos_t, sin_t, trace=False):
+    x = _c(x, np.uint16)
+    R, D = B * L, c.D
+    out = np.empty((R, D), np.uint16)
+    tr, arrs = None, {}
+    if trace:
+        arrs = dict(qkv=np.empty((3, R, D), np.uint16), att=np.empty((R, D), np.uint16),
+                    x1=np.empty((R, D), np.uint16), hh=np.empty((R, c.ff), np.uint16))
+        tr = OrDitTrace(*(_p(arrs[k]) for k in ("qkv", "att", "x1", "hh")))
+    lib().or_dit_block_fwd(ctypes.byref(c), ctypes.byref(blk.c), _p(x), B, L, _p(_c(cos_t, np.float32)),
+                           _p(_c(sin_t, np.float32)), _p(out), ctypes.byref(tr) if tr is not None else None)
+    return (out, arrs) if trace else out
+
+
+def flow_schedule():
+    t = np.empty(11, np.uint16)
+    lib().or_flow_schedule(_p(t))
+    dt = np.empty(10, np.uint16)
+    sq = np.empty(10, np.uint16)
+    lib().or_flow_steps(_p(t), _p(dt), _p(sq))
+    return t, dt, sq
+
+
+def t_freq():
+    f = np.empty(128, np.float32)
+    lib().or_t_freq(_p(f))
+    return f
+
+
+def timestep_embed(mlp0, b0, mlp2, b2, t_bf16):
+    D = mlp0.N
+    out = np.empty((2, D), np.uint16)
+    fr = t_freq()
+    lib().or_timestep_embed(ctypes.byref(mlp0.c), _p(_c(b0, np.uint16)), ctypes.byref(mlp2.c), _p(_c(b2, np.uint16)),
+                            _p(fr), int(t_bf16), _p(out))
+    return out
+
+
+class CfmModel:
+    """The flow head for the oracle: blocks (list of DitBlock), x_emb/c_emb/final (Linear) with biases,
+    final_norm, the t_emb table [steps][2][D] and the schedule (dt, sq), rotary tables for L = 3."""
+
+    def __init__(self, c, blocks, x_emb, bx, c_emb, bc, final_norm, final, bf, t_emb, dt, sq, cos_t, sin_t):
+        self.keep = dict(bx=_c(bx, np.uint16), bc=_c(bc, np.uint16), fn=_c(final_norm, np.uint16),
+                         bf=_c(bf, np.uint16), te=_c(t_emb, np.uint16), dt=_c(dt, np.uint16), sq=_c(sq, np.uint16),
+                         cos=_c(cos_t, np.float32), sin=_c(sin_t, np.float32))
+        self.blocks = blocks
+        self.barr = (OrDitBlock * len(blocks))(*(b.c for b in blocks))
+        self.lins = (x_emb, c_emb, final)
+        k = self.keep
+        self.c = OrCfmModel(c, len(blocks), ctypes.cast(self.barr, c_void_p), x_emb.c, _p(k["bx"]), c_emb.c,
+                            _p(k["bc"]), _p(k["fn"]), final.c, _p(k["bf"]), _p(k["te"]), _p(k["dt"]), _p(k["sq"]),
+                            _p(k["cos"]), _p(k["sin"]), int(k["dt"].size))
+        self.latent = final.N
+
+
+def cfm_rows(m, z, hist, y, step):
+    rows = np.empty((6, m.c.c.D), np.uint16)
+    lib().or_cfm_rows(ctypes.byref(m.c), _p(_c(z, np.uint16)), _p(_c(hist, np.uint16)), _p(_c(y, np.uint16)),
+                      int(step), _p(rows))
+    return rows
+
+
+def cfm_final(m, h, L, y, sde, step, cfg, shift):
+    out = np.empty(m.latent, np.uint16)
+    lib().or_cfm_final(ctypes.byref(m.c), _p(_c(h, np.uint16)), L, _p(_c(y, np.uint16)),
+                       _p(None if sde is None else _c(sde, np.uint16)), int(step), float(cfg), float(shift), _p(out))
+    return out
+
+
+def cfm_sample(m, z, hist, noise, sde, cfg, shift):
+    out = np.empty(m.latent, np.uint16)
+    steps = np.empty((m.c.steps, m.latent), np.uint16)
+    lib().or_cfm_sample(ctypes.byref(m.c), _p(_c(z, np.uint16)), _p(_c(hist, np.uint16)), _p(_c(noise, np.uint16)),
+                        _p(None if sde is None else _c(sde, np.uint16)), float(cfg), float(shift), _p(out),
+                        _p(steps))
+    return out, steps
+
+
+class AggModel:
+    def __init__(self, c, blocks, x_emb, bx, cls, final_norm, final, bf, cos_t, sin_t):
+        self.keep = dict(bx=_c(bx, np.uint16), cls=_c(cls, np.uint16), fn=_c(final_norm, np.uint16),
+                         bf=_c(bf, np.uint16), cos=_c(cos_t, np.float32), sin=_c(sin_t, np.float32))
+        self.blocks = blocks
+        self.barr = (OrDitBlock * len(blocks))(*(b.c for b in blocks))
+        self.lins = (x_emb, final)
+        k = self.keep
+        self.c = OrAggModel(c, len(blocks), ctypes.cast(self.barr, c_void_p), x_emb.c, _p(k["bx"]), _p(k["cls"]),
+                            _p(k["fn"]), final.c, _p(k["bf"]), _p(k["cos"]), _p(k["sin"]))
+        self.out_dim = final.N
+
+
+def aggregate(m, latent):
+    out = np.empty(m.out_dim, np.uint16)
+    lib().or_aggregate(ctypes.byref(m.c), _p(_c(latent, np.uint16)), _p(out))
+    return out
+
+
+def stop_prob(head, bias, z):
+    return float(lib().or_stop_prob(ctypes.byref(head.c), _p(_c(bias, np.uint16)), _p(_c(z, np.uint16))))
