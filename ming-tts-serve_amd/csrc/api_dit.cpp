@@ -86,6 +86,13 @@ int check_block(ming_ctx* ctx, const ming_dit_cfg* c, const ming_dit_block_w* w)
     return MING_OK;
 }
 
+// B x L rows fit the kernels: R = B*L <= 6, L <= 8.
+int check_rows(ming_ctx* ctx, int B, int L, const char* what) {
+    if (B <= 0 || L <= 0 || B * L > kMaxRows || L > 8)
+        return set_err(ctx, MING_E_SHAPE, std::string(what) + ": B*L must be in [1, 6] and L <= 8");
+    return MING_OK;
+}
+
 DitBlockDev block_dev(const ming_dit_cfg* c, const ming_dit_block_w* w) {
     auto p = [](const void* v) { return static_cast<const uint16_t*>(v); };
     DitBlockDev d;
@@ -202,9 +209,8 @@ int ming_dit_block(ming_ctx* ctx, const ming_dit_cfg* cfg, const ming_dit_block_
                    int32_t L, const float* cos_dev, const float* sin_dev, ming_dit_out* out) {
     if (!alive(ctx)) return MING_E_NOT_INIT;
     int st;
-    if ((st = check_cfg(ctx, cfg)) || (st = check_block(ctx, cfg, w))) return st;
-    if (B <= 0 || L <= 0 || B * L > kMaxRows || L > 8)
-        return set_err(ctx, MING_E_SHAPE, "dit_block: B*L must be in [1, 6] and L <= 8");
+    if ((st = check_cfg(ctx, cfg)) || (st = check_block(ctx, cfg, w)) || (st = check_rows(ctx, B, L, "dit_block")))
+        return st;
     if (!x || !cos_dev || !sin_dev || !out || !out->qkv || !out->att || !out->x1 || !out->hh || !out->x2)
         return set_err(ctx, MING_E_ARG, "dit_block: null buffer");
     const DitBlockDev d = block_dev(cfg, w);
@@ -221,8 +227,7 @@ int ming_dit_single(ming_ctx* ctx, int32_t which, const ming_dit_cfg* cfg, const
     int st;
     if ((st = check_cfg(ctx, cfg)) || (st = check_block(ctx, cfg, w))) return st;
     if (which < 0 || which > 3) return set_err(ctx, MING_E_ARG, "dit_single: which must be 0..3");
-    if (B <= 0 || L <= 0 || B * L > kMaxRows || L > 8)
-        return set_err(ctx, MING_E_SHAPE, "dit_single: B*L must be in [1, 6] and L <= 8");
+    if ((st = check_rows(ctx, B, L, "dit_single"))) return st;
     if (!x || !out || ((which == 1 || which == 3) && !in) || (which == 0 && (!qkv_tmp || !cos_dev || !sin_dev)))
         return set_err(ctx, MING_E_ARG, "dit_single: null buffer");
     const DitBlockDev d = block_dev(cfg, w);
@@ -274,6 +279,7 @@ int ming_cfm_model_create(ming_ctx* ctx, const ming_cfm_w* w, ming_cfm_model** o
     if ((st = check_cfg(ctx, c))) return st;
     for (int i = 0; i < w->n_blocks; i++)
         if ((st = check_block(ctx, c, &w->blocks[i]))) return st;
+    if ((st = check_rows(ctx, 2, 3, "cfm_model_create"))) return st;
     const int D = c->hidden, latent = w->x_emb.in_features, H = w->c_emb.in_features;
     if ((st = check_bf16(ctx, w->x_emb, D, latent, "x_emb")) || (st = check_bf16(ctx, w->c_emb, D, H, "c_emb")) ||
         (st = check_bf16(ctx, w->t_mlp0, D, 256, "t_mlp0")) || (st = check_bf16(ctx, w->t_mlp2, D, D, "t_mlp2")) ||
@@ -439,6 +445,7 @@ int ming_agg_model_create(ming_ctx* ctx, const ming_agg_w* w, ming_agg_model** o
     if ((st = check_cfg(ctx, c))) return st;
     for (int i = 0; i < w->n_blocks; i++)
         if ((st = check_block(ctx, c, &w->blocks[i]))) return st;
+    if ((st = check_rows(ctx, 1, 2, "agg_model_create"))) return st;
     const int D = c->hidden, latent = w->x_emb.in_features, H = w->final.out_features;
     if ((st = check_bf16(ctx, w->x_emb, D, latent, "x_emb")) || (st = check_bf16(ctx, w->final, H, D, "final")))
         return st;

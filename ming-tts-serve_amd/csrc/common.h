@@ -23,16 +23,15 @@ __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// f32 -> bf16, round to nearest even; NaN stays a quiet NaN.
-__device__ __forceinline__ uint16_t f2bf(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
-}
+// f32 -> bf16, round to nearest even, NaN stays NaN: gfx950's
+// v_cvt_pk_bf16_f32 (one instruction per pair).  It agrees bit for bit with
+// the integer sequence u += 0x7fff + ((u >> 16) & 1), u >>= 16 on all 2^32
+// inputs whose value is not NaN, denormals included.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 __device__ __forceinline__ float rb(float f) { return bf2f(f2bf(f)); }
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
-    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 
 // acc + a.lo*b.lo + a.hi*b.hi with bf16 pairs packed in u32 (v_dot2c_f32_bf16).

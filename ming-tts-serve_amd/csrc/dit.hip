@@ -7,12 +7,18 @@
 // once, attention is f32 with the output rounded once, and every op of the
 // gelu chain and of the CFG/Euler update rounds to bf16.
 //
-// GEMV layout: a workgroup of 4 waves owns 8 output rows (two 32-lane teams
-// per wave, one output row each); the R input rows (R <= 6, K <= 4096) are
-// staged in LDS once per workgroup (normalised there when the stage has an
-// rms_norm); a lane holds K/256 16-byte weight chunks in registers, loaded
-// before the staging so the HBM latency overlaps it; team sums use DPP.
-// Rows past N load the last row again and write nothing.
+// GEMV layout: a workgroup of W waves (W = 2 or 4) owns 2W output rows, one
+// per 32-lane team; a lane holds K/256 16-byte weight chunks in registers.
+// The weight loads go first, then the epilogue's operands (bias, residual,
+// rotary table, CFM inputs), then the R input rows (R <= 6) in one batch of
+// loads -- every load is issued before the first one is used, so the kernel
+// waits for memory once.  The rows are staged in LDS as they are or
+// rms-normalised (the row sums reduced from the registers of the batch).
+// These kernels are latency-bound (a few MB per launch, every workgroup
+// resident at once), so the code keeps the dependent instruction chain of a
+// wave short: native bf16 rounding, one reciprocal square root per row shared
+// by readlane, no loads after the reduction.  Team sums use DPP; rows past N
+// load the last row again and write nothing.
 #include "gemv.h"
 #include "internal.h"
 
@@ -20,9 +26,10 @@ namespace ming {
 
 namespace {
 
-constexpr int kDB = 256;     // threads per workgroup
-constexpr int kDRows = 8;    // output rows per workgroup
-constexpr int kMaxR = 6;     // activation rows
+constexpr int kMaxR = 6;  // activation rows
+// 16-byte LDS vector (the staged rows are 16-byte aligned: K % 8 == 0)
+typedef uint32_t lds_u32x4_t __attribute__((ext_vector_type(4), aligned(16)));
+constexpr int kMaxL = 8;  // positions per sequence (attention)
 
 enum DitEpi {
     E_BIAS = 0,     // out[r][n] = bf16(acc + b)
@@ -35,11 +42,13 @@ enum DitEpi {
     E_STOP = 7,     // softmax of the 2 stop logits (f32), probability of class 1
 };
 
+enum StageMode { M_PLAIN = 0, M_NORM = 1 };
+
 struct DitGemv {
     const uint16_t* x;  // input row r = x + (xrow0 + r * xstride) * K
     int64_t xrow0, xstride;
     int R;
-    const uint16_t* norm;  // rms_norm weight [K] or null
+    const uint16_t* norm;  // M_NORM: rms_norm weight [K]
     float eps;
     const uint16_t* w;  // bf16 [N, K]
     int N, K;
@@ -70,204 +79,339 @@ struct DitGemv {
 
 __device__ __forceinline__ float gelu_chain(float x) {
     const float c0 = rb(0.044715f), c1 = rb(0.7978845608f);
-    const float x3 = rb(powf(x, 3.0f));
+    // x^3 in f64: x*x is exact there and the product rounds once, so the f32
+    // result is x^3 correctly rounded (up to double rounding, which bf16 hides)
+    const float x3 = rb((float)((double)x * (double)x * (double)x));
     const float inner = rb(x + rb(c0 * x3));
     const float th = rb(tanhf(rb(c1 * inner)));
     return rb(rb(0.5f * x) * rb(1.0f + th));
 }
 
-template <int E, bool NORM, int NCH>
-__global__ __launch_bounds__(kDB) void dit_gemv_kernel(DitGemv a) {
+// ---- staging ------------------------------------------------------------------------
+
+// Rows as they are, or rms-normalised: bf16(w * bf16(x * inv)),
+// inv = 1 / sqrt(mean(x^2) + eps) per row.  RC >= R row slots (slots past R
+// repeat row R-1), XCH chunks of 8 per thread per row; the loops carry no
+// branches, so the compiler issues every load, and later every LDS store,
+// back to back.  Threads whose chunk is past the row's end store nothing and
+// add nothing to the sums.
+template <bool NORM, int RC, int XCH, int T>
+__device__ __forceinline__ void stage_rows(const DitGemv& a, uint32_t* xs, float* red, int t) {
+    const int K = a.K, NC = K / 8, K2 = K / 2, R = a.R;
+    uint4 xr[RC][XCH];
+    uint4 gn[XCH];
+#pragma unroll
+    for (int j = 0; j < XCH; j++) {
+        const int c = min(t + T * j, NC - 1);
+        if (NORM) gn[j] = ldg4(a.norm + 8 * c);
+#pragma unroll
+        for (int r = 0; r < RC; r++) xr[r][j] = ldg4(a.x + (a.xrow0 + min(r, R - 1) * a.xstride) * K + 8 * c);
+    }
+    if (!NORM) {
+#pragma unroll
+        for (int j = 0; j < XCH; j++) {
+            const int c = t + T * j;
+            if (c < NC)
+#pragma unroll
+                for (int r = 0; r < RC; r++)
+                    reinterpret_cast<lds_u32x4_t*>(xs)[r * (K2 / 4) + c] = u32x4_t{xr[r][j].x, xr[r][j].y, xr[r][j].z, xr[r][j].w};
+        }
+        return;
+    }
+    float ss[RC];
+#pragma unroll
+    for (int r = 0; r < RC; r++) {
+        ss[r] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < XCH; j++) {
+            const float on = t + T * j < NC ? 1.0f : 0.0f;
+            const uint32_t q[4] = {xr[r][j].x, xr[r][j].y, xr[r][j].z, xr[r][j].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float lo = on * bf_lo(q[e]), hi = on * bf_hi(q[e]);
+                ss[r] += lo * lo;
+                ss[r] += hi * hi;
+            }
+        }
+        ss[r] = team_sum<kWave>(ss[r]);
+    }
+    const int wave = t / kWave, lane = t % kWave;
+    if (lane == 0)
+#pragma unroll
+        for (int r = 0; r < RC; r++) red[wave * kMaxR + r] = ss[r];
+    __syncthreads();
+    // lane r of every wave finishes row r (waves summed in order), then broadcasts it
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < T / kWave; w++) s += red[w * kMaxR + min(lane, RC - 1)];
+    const float my_inv = 1.0f / sqrtf(s / (float)K + a.eps);
+    float inv[RC];
+#pragma unroll
+    for (int r = 0; r < RC; r++) inv[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_inv), r));
+#pragma unroll
+    for (int j = 0; j < XCH; j++) {
+        const int c = t + T * j;
+        const uint32_t g[4] = {gn[j].x, gn[j].y, gn[j].z, gn[j].w};
+        uint4 o[RC];
+#pragma unroll
+        for (int r = 0; r < RC; r++) {
+            const uint32_t q[4] = {xr[r][j].x, xr[r][j].y, xr[r][j].z, xr[r][j].w};
+            uint32_t w4[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                w4[e] = pack_bf2(bf_lo(g[e]) * rb(bf_lo(q[e]) * inv[r]), bf_hi(g[e]) * rb(bf_hi(q[e]) * inv[r]));
+            o[r] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
+        if (c < NC)
+#pragma unroll
+            for (int r = 0; r < RC; r++)
+                reinterpret_cast<lds_u32x4_t*>(xs)[r * (K2 / 4) + c] = u32x4_t{o[r].x, o[r].y, o[r].z, o[r].w};
+    }
+}
+
+// Operands of the epilogue of lane tl (row r = tl, output n), loaded at
+// kernel start so that no load waits at the end.
+struct EpiIn {
+    float b;        // bias
+    float res;      // E_RES: residual
+    float cs, sn;   // E_QKV: rotary
+    float te0, te1, ce0, ce1;  // E_CFMROWS
+    uint16_t xh;
+    float y, dt, sq, sde;      // E_CFM
+};
+
+template <int E>
+__device__ __forceinline__ EpiIn epi_load(const DitGemv& a, int n, int nrow, int which, int r, const uint16_t* Bv) {
+    EpiIn p{};
+    const int rr = min(r, a.R - 1);
+    if (E == E_QKV) {
+        p.b = bf2f(gld(Bv + nrow));
+        const int l = rr % a.L, i = (nrow % a.hd) / 2, half = a.hd / 2;
+        p.cs = gld(a.cos_t + l * half + i);
+        p.sn = gld(a.sin_t + l * half + i);
+    } else {
+        p.b = bf2f(gld(a.bias + n));
+    }
+    if (E == E_RES) p.res = bf2f(gld(a.res + rr * a.ostride + n));
+    if (E == E_CFMROWS) {
+        p.te0 = bf2f(gld(a.te + n));
+        p.te1 = bf2f(gld(a.te + a.N + n));
+        p.ce0 = bf2f(gld(a.ce + n));
+        p.ce1 = bf2f(gld(a.ce + a.N + n));
+        p.xh = gld(a.xh + n);
+    }
+    if (E == E_CFM) {
+        p.y = bf2f(gld(a.y + n));
+        p.dt = bf2f(gld(a.dt + a.step));
+        p.sq = bf2f(gld(a.sq + a.step));
+        p.sde = a.shift != 0.0f ? bf2f(gld(a.sde + (size_t)a.step * a.N + n)) : 0.0f;
+    }
+    return p;
+}
+
+// ---- the GEMV kernel ----------------------------------------------------------------
+
+// W waves, RPW output rows per wave (a team of 64 / RPW lanes per row), NCH
+// 16-byte weight chunks per lane, RC row slots.
+template <int E, int MODE, int NCH, int W, int RC, int RPW>
+__global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
+    constexpr int T = 64 * W, TEAM = kWave / RPW, ROWS = RPW * W, XCH = (NCH * TEAM + T - 1) / T;
+    static_assert(E != E_QKV && E != E_STOP || RPW == 2, "row pairs live in the two halves of a wave");
     extern __shared__ uint32_t xs[];  // [R][K/2] bf16 pairs, natural order
-    __shared__ float red[kDB / kWave][kMaxR];
-    __shared__ float inv_s[kMaxR];
-    const int t = threadIdx.x, wave = t / kWave, lane = t % kWave, team = lane / 32, tl = lane % 32;
+    __shared__ float red[W * kMaxR];
+    static_assert(RC <= kMaxR, "row slots");
+    const int t = threadIdx.x, wave = t / kWave, lane = t % kWave, team = lane / TEAM, tl = lane % TEAM;
     const int K = a.K, R = a.R, NCk = K / 8, K2 = K / 2;
-    const int n = blockIdx.x * kDRows + wave * 2 + team;
+    const int n = blockIdx.x * ROWS + wave * RPW + team;
     const int nn = min(n, a.N - 1);
-    // weight matrix and row of output n (q/k/v: D % 8 == 0 keeps a workgroup in one matrix)
+    // weight matrix and row of output n (q/k/v: D % 8 == 0 keeps a row pair in one matrix)
     const int which = E == E_QKV ? nn / a.D : 0;
     const int nrow = E == E_QKV ? nn % a.D : nn;
-    const uint16_t* W = E == E_QKV ? a.w3[which] : a.w;
-    const uint16_t* Bv = E == E_QKV ? a.b3[which] : a.bias;
-    // weight loads first (lanes past the row's end reload its last chunk)
+    const uint16_t* Wm = E == E_QKV ? (which == 0 ? a.w3[0] : which == 1 ? a.w3[1] : a.w3[2]) : a.w;
+    const uint16_t* Bv = E == E_QKV ? (which == 0 ? a.b3[0] : which == 1 ? a.b3[1] : a.b3[2]) : a.bias;
+    // weight loads first (lanes past the row's end reload its last chunk and
+    // zero it below), then the epilogue's operands, then the rows
     uint4 wr[NCH];
-    const uint16_t* wrow = W + (size_t)nrow * K;
+    const uint16_t* wrow = Wm + (size_t)nrow * K;
 #pragma unroll
-    for (int j = 0; j < NCH; j++) wr[j] = ldg4(wrow + 8 * min(tl + 32 * j, NCk - 1));
-    // stage the R input rows (rms-normalised when NORM)
-    if (NORM) {
-        float ss[kMaxR];
-#pragma unroll
-        for (int r = 0; r < kMaxR; r++) {
-            ss[r] = 0.0f;
-            if (r < R) {
-                const uint16_t* xr = a.x + (a.xrow0 + r * a.xstride) * K;
-                for (int i = t; i < K2; i += kDB) {
-                    const uint32_t v = gld(reinterpret_cast<const uint32_t*>(xr) + i);
-                    const float lo = bf_lo(v), hi = bf_hi(v);
-                    ss[r] += lo * lo;
-                    ss[r] += hi * hi;
-                }
-            }
-            ss[r] = team_sum<kWave>(ss[r]);
-        }
-        if (lane == 0)
-#pragma unroll
-            for (int r = 0; r < kMaxR; r++) red[wave][r] = ss[r];
-        __syncthreads();
-        if (t < kMaxR) {
-            float s = 0.0f;
-            for (int w = 0; w < kDB / kWave; w++) s += red[w][t];
-            inv_s[t] = 1.0f / sqrtf(s / (float)K + a.eps);
-        }
-        __syncthreads();
-        for (int r = 0; r < R; r++) {
-            const uint16_t* xr = a.x + (a.xrow0 + r * a.xstride) * K;
-            const float inv = inv_s[r];
-            for (int i = t; i < K2; i += kDB) {
-                const uint32_t v = gld(reinterpret_cast<const uint32_t*>(xr) + i);
-                const uint32_t wn = gld(reinterpret_cast<const uint32_t*>(a.norm) + i);
-                xs[r * K2 + i] = pack_bf2(bf_lo(wn) * rb(bf_lo(v) * inv), bf_hi(wn) * rb(bf_hi(v) * inv));
-            }
-        }
-    } else {
-        for (int r = 0; r < R; r++) {
-            const uint16_t* xr = a.x + (a.xrow0 + r * a.xstride) * K;
-            for (int i = t; i < K / 8; i += kDB)
-                reinterpret_cast<uint4*>(xs + r * K2)[i] = ldg4(xr + 8 * i);
-        }
-    }
+    for (int j = 0; j < NCH; j++) wr[j] = ldg4(wrow + 8 * min(tl + TEAM * j, NCk - 1));
+    const EpiIn ep = epi_load<E>(a, nn, nrow, which, tl, Bv);
+    stage_rows<MODE == M_NORM, RC, XCH, T>(a, xs, red, t);
     __syncthreads();
-    // dot products of this team's row with the R staged rows
-    float acc[kMaxR];
-#pragma unroll
-    for (int r = 0; r < kMaxR; r++) acc[r] = 0.0f;
+    // dot products of this team's row with the RC staged row slots: no
+    // branches, so all LDS reads issue ahead of the dot chains
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
-        const int c = tl + 32 * j;
-        if (c < NCk) {
+        const uint32_t m = tl + TEAM * j < NCk ? 0xffffffffu : 0u;
+        wr[j].x &= m;
+        wr[j].y &= m;
+        wr[j].z &= m;
+        wr[j].w &= m;
+    }
+    const lds_u32x4_t* xv4 = reinterpret_cast<const lds_u32x4_t*>(xs);
+    float acc[RC];
 #pragma unroll
-            for (int r = 0; r < kMaxR; r++)
-                if (r < R) {
-                    const uint4 xv = reinterpret_cast<const uint4*>(xs + r * K2)[c];
-                    float s = dot2(wr[j].x, xv.x, acc[r]);
-                    s = dot2(wr[j].y, xv.y, s);
-                    s = dot2(wr[j].z, xv.z, s);
-                    acc[r] = dot2(wr[j].w, xv.w, s);
-                }
+    for (int r = 0; r < RC; r++) acc[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+        const int c = min(tl + TEAM * j, NCk - 1);
+#pragma unroll
+        for (int r = 0; r < RC; r++) {
+            const u32x4_t xv = xv4[r * (K2 / 4) + c];
+            float s = dot2(wr[j].x, xv.x, acc[r]);
+            s = dot2(wr[j].y, xv.y, s);
+            s = dot2(wr[j].z, xv.z, s);
+            acc[r] = dot2(wr[j].w, xv.w, s);
         }
     }
 #pragma unroll
-    for (int r = 0; r < kMaxR; r++) acc[r] = team_sum<32>(acc[r]);
+    for (int r = 0; r < RC; r++) acc[r] = team_sum<TEAM>(acc[r]);
     // epilogue: lane tl = r of each team handles row r
     float v = 0.0f;
 #pragma unroll
-    for (int r = 0; r < kMaxR; r++)
+    for (int r = 0; r < RC; r++)
         if (tl == r) v = acc[r];
     const int r = tl;
     if (E == E_QKV) {
-        // the rotary pair (2i, 2i+1) is (team 0, team 1) of this wave: D and 8 are even
-        const float e = r < R ? rb(v + bf2f(gld(Bv + nrow))) : 0.0f;
+        // the rotary pair (2i, 2i+1) is (team 0, team 1) of this wave: D and 2W are even
+        const float e = rb(v + ep.b);
         const float other = __shfl(e, lane ^ 32, kWave);
         if (r >= R || n >= a.N) return;
-        const int col = nrow;
         float o = e;
         if (which < 2) {
-            // four separate f32 products, no fused multiply-add (MLX evaluates mul, then sub/add)
-#pragma clang fp contract(off)
-            const int l = r % a.L, i = (col % a.hd) / 2, half = a.hd / 2;
-            const float cs = gld(a.cos_t + l * half + i), sn = gld(a.sin_t + l * half + i);
+            // four separate f32 products (MLX evaluates mul, then sub/add)
             const float ev = team == 0 ? e : other, od = team == 0 ? other : e;
-            const float p = ev * cs, q = od * sn, s2 = ev * sn, u = od * cs;
+            const float p = ev * ep.cs, q = od * ep.sn, s2 = ev * ep.sn, u = od * ep.cs;
             o = team == 0 ? p - q : s2 + u;
         }
-        gst(a.out + ((size_t)which * R + r) * a.D + col, f2bf(o));
+        gst(a.out + ((size_t)which * R + r) * a.D + nrow, f2bf(o));
         return;
     }
     if (E == E_CFM) {
         // every lane of the team holds both rows' sums: row 0 cond, row 1 uncond
         if (tl != 0 || n >= a.N) return;
-        const float b = bf2f(gld(a.bias + n));
-        const float pc = rb(acc[0] + b), pn = rb(acc[1] + b);
+        const float pc = rb(acc[0] + ep.b), pn = rb(acc[RC > 1 ? 1 : 0] + ep.b);
         const float f0 = rb(pc + rb(rb(pc - pn) * rb(a.cfg)));
-        float y = rb(bf2f(gld(a.y + n)) + rb(bf2f(gld(a.dt + a.step)) * f0));
-        if (a.shift != 0.0f)
-            y = rb(y + rb(rb(rb(a.shift) * bf2f(gld(a.sq + a.step))) * bf2f(gld(a.sde + (size_t)a.step * a.N + n))));
+        float y = rb(ep.y + rb(ep.dt * f0));
+        if (a.shift != 0.0f) y = rb(y + rb(rb(rb(a.shift) * ep.sq) * ep.sde));
         gst(a.y_out + n, f2bf(y));
         return;
     }
     if (E == E_STOP) {
-        const float l1 = __shfl(v, lane ^ 32, kWave);
+        // lane 0 holds logit 0 (bias 0), lane 32 logit 1 (bias 1)
+        const float x = rb(v + ep.b);
+        const float x1 = __shfl(x, lane ^ 32, kWave);
         if (blockIdx.x != 0 || wave != 0 || lane != 0) return;
-        const float x0 = rb(v + bf2f(gld(a.bias))), x1 = rb(l1 + bf2f(gld(a.bias + 1)));
-        const float m = fmaxf(x0, x1), e0 = expf(x0 - m), e1 = expf(x1 - m);
+        const float m = fmaxf(x, x1), e0 = expf(x - m), e1 = expf(x1 - m);
         gst(a.p_out, e1 / (e0 + e1));
         return;
     }
     if (r >= R || n >= a.N) return;
-    const float e = rb(v + bf2f(gld(a.bias + n)));
+    const float e = rb(v + ep.b);
     if (E == E_BIAS) {
         gst(a.out + r * a.ostride + n, f2bf(e));
     } else if (E == E_RES) {
-        gst(a.out + r * a.ostride + n, f2bf(bf2f(gld(a.res + r * a.ostride + n)) + e));
+        gst(a.out + r * a.ostride + n, f2bf(ep.res + e));
     } else if (E == E_GELU) {
         gst(a.out + r * a.ostride + n, f2bf(gelu_chain(e)));
     } else if (E == E_SILU) {
         gst(a.out + r * a.ostride + n, f2bf(e * rb(1.0f / (1.0f + expf(-e)))));
     } else if (E == E_CFMROWS) {
         // rows [t_emb + c_emb, x_emb(hist), x_emb(y)] of both CFG halves
-        const uint16_t xe = f2bf(e), xh = gld(a.xh + n);
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-            gst(a.out + (size_t)(b * 3 + 0) * a.N + n,
-                f2bf(bf2f(gld(a.te + (size_t)b * a.N + n)) + bf2f(gld(a.ce + (size_t)b * a.N + n))));
-            gst(a.out + (size_t)(b * 3 + 1) * a.N + n, xh);
-            gst(a.out + (size_t)(b * 3 + 2) * a.N + n, xe);
-        }
+        const uint16_t xe = f2bf(e);
+        gst(a.out + n, f2bf(ep.te0 + ep.ce0));
+        gst(a.out + (size_t)a.N + n, ep.xh);
+        gst(a.out + (size_t)2 * a.N + n, xe);
+        gst(a.out + (size_t)3 * a.N + n, f2bf(ep.te1 + ep.ce1));
+        gst(a.out + (size_t)4 * a.N + n, ep.xh);
+        gst(a.out + (size_t)5 * a.N + n, xe);
     }
 }
 
 // Attention over the L positions of each sequence, one wave per (sequence,
-// head): lane d owns dimension d; f32 scores with the 1/8 scale on q, f32
-// softmax, output rounded once.
-__global__ __launch_bounds__(kWave) void dit_attn_kernel(const uint16_t* qkv, int R, int L, int D, int heads, int hd,
-                                                         uint16_t* att) {
-    // lanes past head_dim take part in the wave sums with zeros
+// head), lane d owning dimension d (lanes past head_dim add zeros): every
+// q/k/v load is issued first; scores sum_d (q/8) k in f32 (wave sums),
+// p = exp(s - max), l = sum p, o = (sum_j p_j v_j) / l rounded once.
+__global__ __launch_bounds__(kWave) void dit_attn_kernel(const uint16_t* qkv, int R, int L, int D, int heads,
+                                                         int hd, uint16_t* att) {
     const int b = blockIdx.x / heads, h = blockIdx.x % heads, d = threadIdx.x, dd = min(d, hd - 1);
     const bool on = d < hd;
-    const uint16_t* q = qkv;
-    const uint16_t* k = qkv + (size_t)R * D;
-    const uint16_t* v = qkv + (size_t)2 * R * D;
+    const uint16_t* q = qkv + (size_t)(b * L) * D + h * hd + dd;
+    const uint16_t* k = q + (size_t)R * D;
+    const uint16_t* v = q + (size_t)2 * R * D;
+    float qv[kMaxL], kv[kMaxL], vv[kMaxL];
+#pragma unroll
+    for (int i = 0; i < kMaxL; i++)
+        if (i < L) {
+            qv[i] = bf2f(gld(q + (size_t)i * D));
+            kv[i] = bf2f(gld(k + (size_t)i * D));
+            vv[i] = bf2f(gld(v + (size_t)i * D));
+        }
     const float scale = 1.0f / 8.0f;
-    for (int i = 0; i < L; i++) {
-        const float qd = on ? scale * bf2f(gld(q + (size_t)(b * L + i) * D + h * hd + dd)) : 0.0f;
-        float sc[8], m = -INFINITY;
-        for (int j = 0; j < L; j++) {
-            sc[j] = team_sum<kWave>(qd * bf2f(gld(k + (size_t)(b * L + j) * D + h * hd + dd)));
-            m = fmaxf(m, sc[j]);
+#pragma unroll
+    for (int i = 0; i < kMaxL; i++)
+        if (i < L) {
+            const float qd = on ? scale * qv[i] : 0.0f;
+            float sc[kMaxL], m = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < kMaxL; j++)
+                if (j < L) {
+                    sc[j] = team_sum<kWave>(qd * kv[j]);
+                    m = fmaxf(m, sc[j]);
+                }
+            float l = 0.0f, o = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kMaxL; j++)
+                if (j < L) {
+                    const float p = expf(sc[j] - m);
+                    l += p;
+                    o += p * vv[j];
+                }
+            if (on) gst(att + (size_t)(b * L + i) * D + h * hd + d, f2bf(o / l));
         }
-        float l = 0.0f, o = 0.0f;
-        for (int j = 0; j < L; j++) {
-            const float p = expf(sc[j] - m);
-            l += p;
-            o += p * bf2f(gld(v + (size_t)(b * L + j) * D + h * hd + dd));
-        }
-        if (on) gst(att + (size_t)(b * L + i) * D + h * hd + d, f2bf(o / l));
-    }
 }
 
-template <int E, bool NORM>
-hipError_t launch_gemv(hipStream_t st, const DitGemv& a) {
-    const int grid = (a.N + kDRows - 1) / kDRows;
-    const size_t lds = sizeof(uint32_t) * (size_t)a.R * (a.K / 2);
-    if (a.K <= 256)
-        hipLaunchKernelGGL((dit_gemv_kernel<E, NORM, 1>), dim3(grid), dim3(kDB), lds, st, a);
-    else if (a.K <= 1024)
-        hipLaunchKernelGGL((dit_gemv_kernel<E, NORM, 4>), dim3(grid), dim3(kDB), lds, st, a);
+template <int E, int MODE, int W, int RC, int RPW>
+hipError_t launch_wr(hipStream_t st, const DitGemv& a) {
+    constexpr int ROWS = RPW * W, TEAM = kWave / RPW;
+    const int grid = (a.N + ROWS - 1) / ROWS;
+    const size_t lds = sizeof(uint32_t) * (size_t)RC * (a.K / 2);
+    if (a.K <= 8 * TEAM)
+        hipLaunchKernelGGL((dit_gemv_kernel<E, MODE, 1, W, RC, RPW>), dim3(grid), dim3(64 * W), lds, st, a);
+    else if (a.K <= 32 * TEAM)
+        hipLaunchKernelGGL((dit_gemv_kernel<E, MODE, 4, W, RC, RPW>), dim3(grid), dim3(64 * W), lds, st, a);
     else
-        hipLaunchKernelGGL((dit_gemv_kernel<E, NORM, 16>), dim3(grid), dim3(kDB), lds, st, a);
+        hipLaunchKernelGGL((dit_gemv_kernel<E, MODE, 4096 / (8 * TEAM), W, RC, RPW>), dim3(grid), dim3(64 * W),
+                           lds, st, a);
     return hipGetLastError();
+}
+
+// Row slots: 1, 2 or 6 (3..6 rows run in 6 slots).  Long rows (K > 1024) get
+// a whole wave each, shorter ones a half wave.
+template <int E, int MODE, int W>
+hipError_t launch_w(hipStream_t st, const DitGemv& a) {
+    constexpr bool kPairs = E == E_QKV || E == E_STOP;
+    if constexpr (!kPairs) {
+        if (a.K > 1024) {
+            if (a.R == 1) return launch_wr<E, MODE, W, 1, 1>(st, a);
+            if (a.R == 2 || E == E_CFM) return launch_wr<E, MODE, W, 2, 1>(st, a);
+            return launch_wr<E, MODE, W, kMaxR, 1>(st, a);
+        }
+    }
+    if (E == E_CFM) return launch_wr<E, MODE, W, 2, 2>(st, a);
+    if (a.R == 1) return launch_wr<E, MODE, W, 1, 2>(st, a);
+    if (a.R == 2) return launch_wr<E, MODE, W, 2, 2>(st, a);
+    return launch_wr<E, MODE, W, kMaxR, 2>(st, a);
+}
+
+// Four-wave workgroups when that still gives >= 256 of them (one per CU),
+// else two-wave ones: N = 1024 runs as 256 workgroups of 4 rows (long rows:
+// 4 waves of one row each).
+template <int E, int MODE>
+hipError_t launch_gemv(hipStream_t st, const DitGemv& a) {
+    constexpr bool kPairs = E == E_QKV || E == E_STOP;
+    if (!kPairs && a.K > 1024) return launch_w<E, MODE, 4>(st, a);
+    return (a.N + 7) / 8 >= 256 ? launch_w<E, MODE, 4>(st, a) : launch_w<E, MODE, 2>(st, a);
 }
 
 DitGemv gemv_args(const uint16_t* x, int R, const uint16_t* w, int N, int K, const uint16_t* bias, uint16_t* out) {
@@ -315,7 +459,7 @@ hipError_t launch_dit_stage(hipStream_t st, int which, const DitBlockDev& w, con
             a.L = L;
             a.D = D;
             a.hd = w.hd;
-            hipError_t e = launch_gemv<E_QKV, true>(st, a);
+            hipError_t e = launch_gemv<E_QKV, M_NORM>(st, a);
             if (e != hipSuccess) return e;
             hipLaunchKernelGGL(dit_attn_kernel, dim3(B * w.heads), dim3(kWave), 0, st, qkv, R, L, D, w.heads, w.hd,
                                out);
@@ -324,16 +468,16 @@ hipError_t launch_dit_stage(hipStream_t st, int which, const DitBlockDev& w, con
         case 1:
             a = gemv_args(in, R, w.wo, D, D, w.bo, out);
             a.res = x;
-            return launch_gemv<E_RES, false>(st, a);
+            return launch_gemv<E_RES, M_PLAIN>(st, a);
         case 2:
             a = gemv_args(x, R, w.w1, F, D, w.b1, out);
             a.norm = w.norm2;
             a.eps = w.eps;
-            return launch_gemv<E_GELU, true>(st, a);
+            return launch_gemv<E_GELU, M_NORM>(st, a);
         default:
             a = gemv_args(in, R, w.w2, D, F, w.b2, out);
             a.res = x;
-            return launch_gemv<E_RES, false>(st, a);
+            return launch_gemv<E_RES, M_PLAIN>(st, a);
     }
 }
 
@@ -358,8 +502,8 @@ hipError_t launch_dit_linear(hipStream_t st, const uint16_t* x, int64_t xrow0, i
     a.xstride = xstride;
     a.norm = norm;
     a.eps = eps;
-    if (norm) return silu ? launch_gemv<E_SILU, true>(st, a) : launch_gemv<E_BIAS, true>(st, a);
-    return silu ? launch_gemv<E_SILU, false>(st, a) : launch_gemv<E_BIAS, false>(st, a);
+    if (norm) return silu ? launch_gemv<E_SILU, M_NORM>(st, a) : launch_gemv<E_BIAS, M_NORM>(st, a);
+    return silu ? launch_gemv<E_SILU, M_PLAIN>(st, a) : launch_gemv<E_BIAS, M_PLAIN>(st, a);
 }
 
 // fused.embed: rows [2*3][D] = [te + ce, xh, x_emb(y)] per CFG half.
@@ -369,7 +513,7 @@ hipError_t launch_cfm_embed(hipStream_t st, const uint16_t* y, const uint16_t* w
     a.te = te;
     a.ce = ce;
     a.xh = xh;
-    return launch_gemv<E_CFMROWS, false>(st, a);
+    return launch_gemv<E_CFMROWS, M_PLAIN>(st, a);
 }
 
 // fused.final: rms + final linear on rows L-1 and 2L-1 of h, CFG + Euler.
@@ -390,14 +534,14 @@ hipError_t launch_cfm_final(hipStream_t st, const uint16_t* h, int L, int D, con
     a.cfg = cfg;
     a.shift = shift;
     a.y_out = y_out;
-    return launch_gemv<E_CFM, true>(st, a);
+    return launch_gemv<E_CFM, M_NORM>(st, a);
 }
 
 // stopProb: p = softmax(f32(bf16(W z + b)))[1] (W [2][K]).
 hipError_t launch_stop_prob(hipStream_t st, const uint16_t* z, const uint16_t* w, const uint16_t* b, int K, float* p) {
     DitGemv a = gemv_args(z, 1, w, 2, K, b, nullptr);
     a.p_out = p;
-    return launch_gemv<E_STOP, false>(st, a);
+    return launch_gemv<E_STOP, M_PLAIN>(st, a);
 }
 
 }  // namespace ming

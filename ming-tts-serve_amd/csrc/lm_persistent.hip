@@ -471,18 +471,19 @@ __device__ __forceinline__ void st_qkv(const Ctx& c, const LayerDev& Ld, int l) 
 // Unit = (kv head g, split of positions), on the last workers.  The split is
 // walked in tiles of 64 positions: each thread loads one 16 B chunk of K and
 // one of V per tile (the next tile's loads are issued before the current one
-// is computed); scores use 8 lanes per position, the online softmax one wave
-// per head, P.V one thread per (head, dim).
+// is computed; the new row pos replaces its cache row as the tile is stored);
+// scores use 8 lanes per position; then wave h owns q head h: its online
+// softmax runs over lane = position and its P.V over lane = dim, with the
+// running max / sum in registers -- two workgroup barriers per tile.  The
+// last split to arrive merges all splits of the kv head with one batch of
+// loads (lane s holds split s's max and sum, readlane broadcasts weights).
 struct ALds {
     float* q;       // [8][64]
     uint16_t* k;    // [64][64]
     uint16_t* v;    // [64][64]
-    float* p;       // [8][64]
-    float* ml;      // [8][4]: running max, running sum, tile correction
+    float* p;       // [8][64] scores, then probabilities
     uint32_t* kn;   // [32] new k row (bf16 pairs)
     uint32_t* vn;   // [32] new v row
-    float* mw;      // merge: [8][64] split weights
-    float* mlsum;   // merge: [8]
 };
 
 __device__ __forceinline__ ALds alds(uint32_t* lds) {
@@ -491,11 +492,8 @@ __device__ __forceinline__ ALds alds(uint32_t* lds) {
     s.k = reinterpret_cast<uint16_t*>(lds + 512);
     s.v = reinterpret_cast<uint16_t*>(lds + 2560);
     s.p = reinterpret_cast<float*>(lds + 4608);
-    s.ml = reinterpret_cast<float*>(lds + 5120);
-    s.kn = lds + 5152;
+    s.kn = lds + 5152;  // 16-byte aligned
     s.vn = lds + 5184;
-    s.mw = reinterpret_cast<float*>(lds + 5216);
-    s.mlsum = reinterpret_cast<float*>(lds + 5728);
     return s;
 }
 
@@ -574,8 +572,37 @@ __device__ __forceinline__ void attn_recv(const Ctx& c, int l) {
         else
             S.vn[t - hd / 2] = w;
     }
-    if (t < 32) S.ml[t] = (t % 4 == 0) ? -INFINITY : 0.0f;
     stamp(a, slot_in(l, 1));
+}
+
+// Merge of the ns <= NS splits of kv head g (last arriver), wave h = q head h,
+// lane d = dim d: every partial is loaded in one batch (clamped indices).
+template <int NS>
+__device__ __forceinline__ void attn_merge(const Ctx& c, int l, const AttnGeom& q) {
+    const StepArgs& a = c.a;
+    const int grp = a.heads / a.kvh, hd = a.hd, ns = q.ns, g = q.g, h = c.wave, d = c.lane;
+    const size_t sstride = (size_t)grp * (hd + 2);
+    const float* pb = a.part + (size_t)(g * ns) * sstride + (size_t)h * (hd + 2);
+    const int sl = min(d, ns - 1);
+    const float ms = cload(pb + sl * sstride), ls = cload(pb + sl * sstride + 1);
+    float v[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++) v[s] = cload(pb + min(s, ns - 1) * sstride + 2 + d);
+    const float m = d < ns ? ms : -INFINITY;
+    const float M = team_max<kWave>(m);
+    const float w = d < ns ? expf(m - M) : 0.0f;
+    const float lw = team_sum<kWave>(w * (d < ns ? ls : 0.0f));
+    float o = 0.0f;
+#pragma unroll
+    for (int s = 0; s < NS; s++) o += v[s] * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), s));
+    const float val = o / lw;
+    const float nxt = __shfl_down(val, 1, kWave);
+    const int col = (g * grp + h) * hd + d;
+    if ((d & 1) == 0) {
+        const uint32_t wv = pack_bf2(val, nxt);
+        tstore(a.ta + (size_t)l * (a.H / 2) + col / 2, wv, a.epoch);
+        gst(reinterpret_cast<uint32_t*>(a.att + l * a.sx) + col / 2, wv);
+    }
 }
 
 __device__ __forceinline__ void attn_run(const Ctx& c, int l, AttnTile tile) {
@@ -584,18 +611,22 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l, AttnTile tile) {
     const int ns = q.ns, g = q.g, sp = q.sp, j0 = q.j0, j1 = q.j1;
     const int grp = a.heads / a.kvh, hd = a.hd, t = tix();
     const ALds S = alds(c.lds);
-    const int hp = t / 64, d = t % 64;  // P.V: thread owns dim d of head hp
-    float acc = 0.0f;
+    const int h = c.wave, d = c.lane;  // softmax and P.V: wave h = q head h, lane = position / dim
+    float acc = 0.0f, m = -INFINITY, lsum = 0.0f;
     for (int t0 = j0; t0 < j1; t0 += kTile) {
         const int cnt = min(kTile, j1 - t0);
-        lds_sync();
-        const bool ok = attn_tile_valid(c, q, t0);
-        reinterpret_cast<uint4*>(S.k)[t] = ok ? tile.k : make_uint4(0, 0, 0, 0);
-        reinterpret_cast<uint4*>(S.v)[t] = ok ? tile.v : make_uint4(0, 0, 0, 0);
-        lds_sync();
-        if (a.pos >= t0 && a.pos < t0 + cnt && t < hd / 2) {  // new row
-            reinterpret_cast<uint32_t*>(S.k + (a.pos - t0) * hd)[t] = S.kn[t];
-            reinterpret_cast<uint32_t*>(S.v + (a.pos - t0) * hd)[t] = S.vn[t];
+        lds_sync();  // the previous tile (or the q staging) is done with LDS
+        {
+            const int row = t0 + t / 8, ch = t % 8;
+            const bool ok = attn_tile_valid(c, q, t0);
+            uint4 kk = ok ? tile.k : make_uint4(0, 0, 0, 0);
+            uint4 vv = ok ? tile.v : make_uint4(0, 0, 0, 0);
+            if (row == a.pos) {  // the new row, received with q
+                kk = reinterpret_cast<const uint4*>(S.kn)[ch];
+                vv = reinterpret_cast<const uint4*>(S.vn)[ch];
+            }
+            reinterpret_cast<uint4*>(S.k)[t] = kk;
+            reinterpret_cast<uint4*>(S.v)[t] = vv;
         }
         lds_sync();
         if (t0 + kTile < j1) attn_tile_load(c, l, q, t0 + kTile, tile);
@@ -603,8 +634,8 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l, AttnTile tile) {
             const int p = t >> 3, qt = t & 7;
             const uint4 kk = *reinterpret_cast<const uint4*>(S.k + p * hd + qt * 8);
             const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
-            for (int h = 0; h < grp; h++) {
-                const float* qh = S.q + h * hd + qt * 8;
+            for (int hh = 0; hh < grp; hh++) {
+                const float* qh = S.q + hh * hd + qt * 8;
                 float s = 0.0f;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -612,45 +643,36 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l, AttnTile tile) {
                     s += qh[2 * i + 1] * bf_hi(kw[i]);
                 }
                 s = team_sum<8>(s);
-                if (qt == 0) S.p[h * kTile + p] = p < cnt ? s : -INFINITY;
+                if (qt == 0) S.p[hh * kTile + p] = p < cnt ? s : -INFINITY;
             }
         }
         lds_sync();
-        if (c.wave < grp) {  // online softmax, one wave per head, lane = position
-            const int h = c.wave;
-            const float s = S.p[h * kTile + c.lane];
-            const float mt = team_max<kWave>(s);
-            const float mo = S.ml[4 * h], mn = fmaxf(mo, mt);
-            const float e = c.lane < cnt ? expf(s - mn) : 0.0f;
-            S.p[h * kTile + c.lane] = e;
-            const float sum = team_sum<kWave>(e);
-            if (c.lane == 0) {
-                const float corr = expf(mo - mn);  // 0 on the first tile
-                S.ml[4 * h] = mn;
-                S.ml[4 * h + 1] = S.ml[4 * h + 1] * corr + sum;
-                S.ml[4 * h + 2] = corr;
-            }
-        }
-        lds_sync();
-        if (hp < grp) {
-            const float* ph = S.p + hp * kTile;
+        if (h < grp) {
+            float* ph = S.p + h * kTile;
+            const float s = ph[d];
+            const float mn = fmaxf(m, team_max<kWave>(s));
+            const float e = d < cnt ? expf(s - mn) : 0.0f;
+            const float corr = expf(m - mn);  // 0 on the first tile
+            lsum = lsum * corr + team_sum<kWave>(e);
+            m = mn;
+            ph[d] = e;  // read back by the other lanes of this wave only
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
             float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll 8
             for (int p = 0; p < kTile; p += 2) {  // probabilities past cnt are 0
                 s0 += ph[p] * bf2f(S.v[p * hd + d]);
                 s1 += ph[p + 1] * bf2f(S.v[(p + 1) * hd + d]);
             }
-            acc = acc * S.ml[4 * hp + 2] + (s0 + s1);
+            acc = acc * corr + (s0 + s1);
         }
     }
-    lds_sync();
     // partials: device-coherent stores, completed before the arrival
-    if (hp < grp) {
-        float* out = a.part + ((size_t)(g * ns + sp) * grp + hp) * (hd + 2);
+    if (h < grp) {
+        float* out = a.part + ((size_t)(g * ns + sp) * grp + h) * (hd + 2);
         cstore(out + 2 + d, acc);
         if (d == 0) {
-            cstore(out, S.ml[4 * hp]);
-            cstore(out + 1, S.ml[4 * hp + 1]);
+            cstore(out, m);
+            cstore(out + 1, lsum);
         }
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -663,42 +685,13 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l, AttnTile tile) {
         if (old == ns - 1) astore(ctr, 0);
     }
     lds_sync();
-    if (!*last) return;
-    // merge the ns (<= 64) splits of the grp heads of kv head g
-    const float* pbase = a.part + (size_t)(g * ns) * grp * (hd + 2);
-    const size_t sstride = (size_t)grp * (hd + 2);
-    if (c.wave < grp) {
-        const int h = c.wave;
-        const float m = c.lane < ns ? cload(pbase + c.lane * sstride + h * (hd + 2)) : -INFINITY;
-        const float lsum = c.lane < ns ? cload(pbase + c.lane * sstride + h * (hd + 2) + 1) : 0.0f;
-        const float M = team_max<kWave>(m);
-        const float w = c.lane < ns ? expf(m - M) : 0.0f;
-        const float lw = team_sum<kWave>(w * lsum);
-        S.mw[h * 64 + c.lane] = w;
-        if (c.lane == 0) S.mlsum[h] = lw;
-    }
-    lds_sync();
-    if (hp < grp) {
-        constexpr int B = 8;
-        float o = 0.0f;
-        for (int s0 = 0; s0 < ns; s0 += B) {
-            float v[B];
-#pragma unroll
-            for (int i = 0; i < B; i++)
-                v[i] = s0 + i < ns ? cload(pbase + (s0 + i) * sstride + hp * (hd + 2) + 2 + d) : 0.0f;
-#pragma unroll
-            for (int i = 0; i < B; i++)
-                if (s0 + i < ns) o += v[i] * S.mw[hp * 64 + s0 + i];
-        }
-        const float val = o / S.mlsum[hp];
-        const float nxt = __shfl_down(val, 1, kWave);
-        const int col = (g * grp + hp) * hd + d;
-        if ((d & 1) == 0) {
-            const uint32_t w = pack_bf2(val, nxt);
-            tstore(a.ta + (size_t)l * (a.H / 2) + col / 2, w, a.epoch);
-            gst(reinterpret_cast<uint32_t*>(a.att + l * a.sx) + col / 2, w);
-        }
-    }
+    if (!*last || h >= grp) return;
+    if (ns <= 16)
+        attn_merge<16>(c, l, q);
+    else if (ns <= 32)
+        attn_merge<32>(c, l, q);
+    else
+        attn_merge<64>(c, l, q);
 }
 
 // ---- LC: o_proj + residual (unit = row pair, packed on the compute waves) ------
@@ -1000,11 +993,11 @@ __global__ __launch_bounds__(kT) void decode_tagged_kernel(StepArgs args, const 
 }  // namespace
 
 // Positions per attention split on this schedule: a multiple of the 64-row
-// tile, doubled until a kv head has at most 24 splits (each split is one
-// workgroup; the last one to finish merges them).
+// tile, doubled until a kv head has at most 64 splits (each split is one
+// workgroup; the last one to finish merges them, one split per lane).
 int tagged_split_len(int n) {
     int sl = kTile;
-    while ((n + sl - 1) / sl > 24 && sl < 16 * kTile) sl *= 2;
+    while ((n + sl - 1) / sl > 64 && sl < 16 * kTile) sl *= 2;
     return sl;
 }
 
