@@ -333,6 +333,45 @@ int ming_aggregate(ming_ctx* ctx, ming_agg_model* m, const void* latent, void* o
  * softmax(f32(stop_head(z)))[1]; head [2, lm_hidden] bf16 with bias. */
 int ming_stop_prob(ming_ctx* ctx, const ming_linear* head, const void* bias, const void* z, float* p_dev);
 
+/* Sizes of a prepared model (out-pointers may be null). */
+int ming_lm_model_dims(const ming_lm_model* m, int32_t* hidden, int32_t* vocab);
+int ming_cfm_model_dims(const ming_cfm_model* m, int32_t* latent, int32_t* lm_hidden);
+int ming_agg_model_dims(const ming_agg_model* m, int32_t* lm_hidden, int32_t* latent);
+
+/* ---- per-token loop ---------------------------------------------------------
+ * sampleLatents (src/ming_model.zig:1388-1480) on the handles above. */
+
+/* SampleParams (src/ming_model.zig:1365-1373): defaults 1000, 2.0, 0.25, 0.0. */
+typedef struct {
+    int32_t max_steps;
+    float cfg, sigma, temperature;
+} ming_sample_params;
+
+/* Noise replay bank (Noise.replay, src/ming_model.zig:1349-1363): device bf16
+ * [steps][11][latent], row 0 the start noise and rows 1..10 the SDE draws of
+ * each step, filled from the library's counter-based normal stream (seed,
+ * "flow.noise").  MLX's own RNG stream is not reproduced. */
+int ming_noise_bank(ming_ctx* ctx, uint64_t seed, int32_t steps, int32_t latent, void* bank_dev);
+
+/* sampleLatents: embeds [L][hidden] (device bf16) are decoded one position at
+ * a time into kv (appended at kv->len), z = the last row's final-normed hidden;
+ * then for step k < min(max_steps, capacity - len - L): latent_k =
+ * cfmSample(z_k, history, bank[k]) into latents_out[k] (device bf16
+ * [max_steps][latent]); z_{k+1} = LM(aggregate(latent_k)); stop_k =
+ * stopProb(z_k); stop after latent_k when stop_k > 0.5 and k > 3.  history is
+ * prompt_latent (device [latent], optional; zeros when null), then latent_{k-1}.
+ * Pipelined one step ahead: the LM pass for k+1 is queued before stop_k is
+ * read, so on a stop one extra position is appended to kv (the reference
+ * discards its cache; here kv->len ends at len + L + n, or len + L + n - 1
+ * when the step budget ran out).  Returns after the stream drains; *n_steps_out
+ * = latents written; stop_out (host f32 [max_steps], optional) = stop_k;
+ * z_trace (device bf16 [max_steps][hidden], optional) = z_k. */
+int ming_sample_latents(ming_ctx* ctx, ming_lm_model* lm, ming_cfm_model* cfm, ming_agg_model* agg,
+                        const ming_linear* stop_head, const void* stop_bias, const void* embeds, int32_t L,
+                        const void* prompt_latent, ming_kv* kv, const void* noise_bank,
+                        const ming_sample_params* p, void* latents_out, int32_t* n_steps_out, float* stop_out,
+                        void* z_trace);
+
 /* ---- synthetic inputs (host side; benches and tests) -----------------------
  * Counter-based splitmix64 + Box-Muller: element i of stream (seed, name) is
  * a pure function of (seed, fnv1a64(name), i), so any slice can be generated

@@ -17,6 +17,7 @@ Mirrors of the reference interface (sbusso/ming-tts-serve):
   Context.stop_prob     <- stopProb                src/ming_model.zig:1033
   CfmModel.sample       <- cfmSample               src/ming_model.zig:1143
   AggModel.aggregate    <- aggregate               src/ming_model.zig:1154
+  Context.sample_latents <- sampleLatents          src/ming_model.zig:1388
 """
 import ctypes
 import os
@@ -104,6 +105,10 @@ class AggW(ctypes.Structure):
     ] + [(n, c_void_p) for n in ("bx", "cls", "final_norm", "bf")]
 
 
+class SampleParams(ctypes.Structure):
+    _fields_ = [("max_steps", c_i32), ("cfg", c_f32), ("sigma", c_f32), ("temperature", c_f32)]
+
+
 _lib = None
 
 
@@ -166,6 +171,13 @@ def lib():
         "ming_agg_model_destroy": (c_i32, [c_void_p]),
         "ming_aggregate": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p]),
         "ming_stop_prob": (c_i32, [c_void_p, P(Linear), c_void_p, c_void_p, c_void_p]),
+        "ming_lm_model_dims": (c_i32, [c_void_p, P(c_i32), P(c_i32)]),
+        "ming_cfm_model_dims": (c_i32, [c_void_p, P(c_i32), P(c_i32)]),
+        "ming_agg_model_dims": (c_i32, [c_void_p, P(c_i32), P(c_i32)]),
+        "ming_noise_bank": (c_i32, [c_void_p, ctypes.c_uint64, c_i32, c_i32, c_void_p]),
+        "ming_sample_latents": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, P(Linear), c_void_p, c_void_p, c_i32,
+                                        c_void_p, P(Kv), c_void_p, P(SampleParams), c_void_p, P(c_i32), c_void_p,
+                                        c_void_p]),
         "ming_synth_stream": (ctypes.c_uint64, [ctypes.c_uint64, ctypes.c_char_p]),
         "ming_synth_normal_bf16": (None, [ctypes.c_uint64, c_f32, c_f32, c_void_p, ctypes.c_size_t, c_i32]),
         "ming_synth_uniform_i32": (None, [ctypes.c_uint64, c_i32, c_void_p, ctypes.c_size_t]),
@@ -312,6 +324,22 @@ class Context:
 
     def stop_prob(self, head, bias, z, p):
         self.check(self.L.ming_stop_prob(self.h, ctypes.byref(head), ptr(bias), ptr(z), ptr(p)))
+
+
+    # ---- per-token loop ----
+    def noise_bank(self, seed, steps, latent, bank):
+        self.check(self.L.ming_noise_bank(self.h, int(seed), int(steps), int(latent), ptr(bank)))
+
+    def sample_latents(self, lm, cfm, agg, stop_head, stop_bias, embeds, kv, bank, params, latents_out,
+                       prompt_latent=None, z_trace=None):
+        """sampleLatents; returns (n_steps, [stop_k]).  embeds: device bf16 [L, hidden]."""
+        n = c_i32()
+        stops = (c_f32 * int(params.max_steps))()
+        self.check(self.L.ming_sample_latents(self.h, lm.h, cfm.h, agg.h, ctypes.byref(stop_head), ptr(stop_bias),
+                                              ptr(embeds), int(embeds.shape[0]), ptr(prompt_latent),
+                                              ctypes.byref(kv), ptr(bank), ctypes.byref(params), ptr(latents_out),
+                                              ctypes.byref(n), stops, ptr(z_trace)))
+        return n.value, [stops[i] for i in range(n.value)]
 
 
 class CfmModel:

@@ -650,6 +650,13 @@ static int lm_step_impl(ming_ctx* ctx, ming_lm_model* m, const int32_t* token_de
     return MING_OK;
 }
 
+int ming_lm_model_dims(const ming_lm_model* m, int32_t* hidden, int32_t* vocab) {
+    if (!m) return MING_E_NOT_INIT;
+    if (hidden) *hidden = m->cfg.hidden;
+    if (vocab) *vocab = m->cfg.vocab;
+    return MING_OK;
+}
+
 int ming_lm_step(ming_ctx* ctx, ming_lm_model* m, const int32_t* token_dev, const void* x_in, ming_kv* kv,
                  void* hidden_out, float* logits_out, int32_t* argmax_out) {
     if (!alive(ctx)) return MING_E_NOT_INIT;

@@ -387,6 +387,20 @@ int ming_cfm_model_destroy(ming_cfm_model* m) {
     return MING_OK;
 }
 
+int ming_cfm_model_dims(const ming_cfm_model* m, int32_t* latent, int32_t* lm_hidden) {
+    if (!m) return MING_E_NOT_INIT;
+    if (latent) *latent = m->latent;
+    if (lm_hidden) *lm_hidden = m->lm_hidden;
+    return MING_OK;
+}
+
+int ming_agg_model_dims(const ming_agg_model* m, int32_t* lm_hidden, int32_t* latent) {
+    if (!m) return MING_E_NOT_INIT;
+    if (lm_hidden) *lm_hidden = m->lm_hidden;
+    if (latent) *latent = m->latent;
+    return MING_OK;
+}
+
 int ming_cfm_model_tables(ming_cfm_model* m, uint16_t* t, uint16_t* dt, uint16_t* sq, const void** t_emb_dev) {
     if (!m) return MING_E_NOT_INIT;
     if (t) std::memcpy(t, m->t, sizeof(m->t));

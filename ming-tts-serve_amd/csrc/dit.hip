@@ -216,7 +216,7 @@ __device__ __forceinline__ EpiIn epi_load(const DitGemv& a, int n, int nrow, int
 template <int E, int MODE, int NCH, int W, int RC, int RPW>
 __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
     constexpr int T = 64 * W, TEAM = kWave / RPW, ROWS = RPW * W, XCH = (NCH * TEAM + T - 1) / T;
-    static_assert(E != E_QKV && E != E_STOP || RPW == 2, "row pairs live in the two halves of a wave");
+    static_assert((E != E_QKV && E != E_STOP) || RPW == 2, "row pairs live in the two halves of a wave");
     extern __shared__ uint32_t xs[];  // [R][K/2] bf16 pairs, natural order
     __shared__ float red[W * kMaxR];
     static_assert(RC <= kMaxR, "row slots");

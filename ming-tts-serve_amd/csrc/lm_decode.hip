@@ -41,7 +41,7 @@ struct Nch {
     static constexpr int t64 = Q4 ? 3 : 5;
 };
 
-enum Stage { S_EMBED, S_QKV, S_ATTN, S_MERGE, S_O, S_UP, S_DOWN, S_HEAD, S_ARGMAX };
+enum Stage { S_EMBED, S_QKV, S_ATTN, S_MERGE, S_O, S_UP, S_DOWN, S_HEAD, S_ARGMAX, S_FINAL };
 
 __device__ __forceinline__ XStage xstage(uint32_t* lds, int K) { return XStage{lds, reinterpret_cast<float*>(lds + K / 2)}; }
 __device__ __forceinline__ uint16_t* htemp(uint32_t* lds) { return reinterpret_cast<uint16_t*>(lds + kHOff); }
@@ -73,6 +73,7 @@ __host__ __device__ __forceinline__ int units_of(Stage s, int H, int kvh, int hd
         case S_DOWN: return (H + kWpb - 1) / kWpb;
         case S_HEAD: return (V + 2 * kWpb - 1) / (2 * kWpb);
         case S_ARGMAX: return 1;
+        case S_FINAL: return 1;
     }
     return 1;
 }
@@ -591,6 +592,13 @@ __device__ void run_stage(Stage s, const StepArgs& a, const LayerDev& Ld, int l,
         case S_ARGMAX:
             if (bid == 0) argmax_unit(a, lds, nparts);
             break;
+        case S_FINAL:  // final norm only (no head): the hidden output
+            if (bid == 0) {
+                uint16_t* h = htemp(lds);
+                rms_to_lds(a.x + a.n_layers * a.sx, a.final_norm, a.H, a.eps, h, red(lds));
+                for (int i = threadIdx.x; i < a.H; i += blockDim.x) a.hidden[i] = h[i];
+            }
+            break;
     }
 #undef QKV_LOAD
 #undef QKV_COMPUTE
@@ -660,6 +668,7 @@ hipError_t launch_lm_step_kernels(hipStream_t st, const StepArgs& a, const Layer
     if (a.token_in && (e = launch_stage<S_EMBED>(st, a, host_layers[0], 0, 1, 0)) != hipSuccess) return e;
     for (int l = 0; l < a.n_layers; l++)
         if ((e = launch_lm_layer(st, a, host_layers[l], l)) != hipSuccess) return e;
+    if (!a.logits && !a.argmax_out) return launch_stage<S_FINAL>(st, a, host_layers[0], 0, 1, 0);
     const int hg = host_units(S_HEAD, a) < 2048 ? host_units(S_HEAD, a) : 2048;
     if ((e = launch_stage<S_HEAD>(st, a, host_layers[0], 0, hg, 0)) != hipSuccess) return e;
     return launch_stage<S_ARGMAX>(st, a, host_layers[0], 0, 1, hg);

@@ -859,6 +859,11 @@ __device__ __forceinline__ void head_slot_load(const Ctx& c, int p, RowRegs<Nc<Q
 template <int Q4>
 __device__ __forceinline__ void st_head(const Ctx& c) {
     const StepArgs& a = c.a;
+    if (!a.logits && !a.argmax_out) {  // hidden only: hub 0 (or worker 0) writes it, no head
+        if (a.nhubs == 0 && c.w == 0)
+            get_image<Q4>(c, 4 * a.n_layers, 4, a.tx + (size_t)a.n_layers * (a.H / 2), a.H, a.final_norm, a.hidden);
+        return;
+    }
     const int V = a.head.N, nunits = V / 2 + (V & 1);
     const int nw = c.W * kCW, me = c.w * kCW + c.wave - 1;
     HeadW<Q4> W;

@@ -1,0 +1,115 @@
+"""GPU parity of the per-token TTS loop (ming_sample_latents, sampleLatents
+src/ming_model.zig:1388-1480) against the oracle, at the reference widths
+(LM hidden 896, DiT 1024, latent 64) with 2 LM layers and 2 + 2 DiT blocks.
+
+Each step is recomputed on the oracle from the GPU's own inputs (teacher
+forced): z_0 from the prompt prefill, stop_k = stopProb(z_k), latent_k =
+cfmSample(z_k, history_k, noise bank row k), aggregate(latent_k) against the
+GPU kernel's row, and z_{k+1} = LM(that row) with the oracle's own cache.
+Bars: hidden states and aggregator rows 2e-2 + 1e-2 |ref|; the ten-step latent 6e-2 + 2e-2 |ref| (mean |d| <= 2e-2, as the flow head's own
+end-to-end test); stop probabilities 1e-2; the step count follows the stop
+rule (stop after latent_k when stop_k > 0.5 and k > 3) applied to the GPU's
+stop values, and the cache grows by the documented number of positions."""
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from ditkit import oracle_agg, oracle_cfm
+from lmkit import assert_close_bf16, oracle_model, oracle_step
+
+pytestmark = pytest.mark.gpu
+
+
+def mods():
+    return (importlib.import_module("ming-tts-serve_amd"), importlib.import_module("ming-tts-serve_amd.synthetic"))
+
+
+def dev_u16(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda().view(torch.bfloat16)
+
+
+def host_u16(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.fixture(scope="module")
+def models(ctx):
+    ming, S = mods()
+    spec = S.LmSpec(n_layers=2, vocab=256)
+    lm = S.SyntheticLm(ctx, spec, seed=3, quant=True, norm_std=0.1)
+    flow = S.SyntheticFlow(ctx, S.DitSpec(cfm_blocks=2, agg_blocks=2), seed=5, norm_std=0.05)
+    oracle.set_threads(16)
+    return dict(spec=spec, lm=lm, flow=flow, lm_model=lm.model(), cfm=flow.cfm_model(), agg=flow.agg_model(),
+                olm=oracle_model(lm), ocfm=oracle_cfm(flow), oagg=oracle_agg(flow))
+
+
+@pytest.mark.parametrize("case,stop_bias,max_steps", [("stops", (0.0, 20.0), 8), ("runs_out", (20.0, 0.0), 6)])
+def test_sample_latents_matches_oracle(ming, ctx, models, case, stop_bias, max_steps):
+    print(f"[sample_latents] {case} max_steps={max_steps}", flush=True)
+    ming, S = mods()
+    spec, lm, flow = models["spec"], models["lm"], models["flow"]
+    H, lat, L = spec.hidden, flow.spec.latent, 3
+    bias = oracle.to_bf16(np.array(stop_bias, np.float32))
+    bias_d = dev_u16(bias)
+    emb = ming.synth_normal_bf16(71, "loop.embeds", L * H, 0.0, 0.5).reshape(L, H)
+    cache = S.KvCache(spec, L + max_steps + 2)
+    bank = torch.empty((max_steps, 11, lat), dtype=torch.bfloat16, device="cuda")
+    ctx.noise_bank(1234, max_steps, lat, bank)
+    lats = torch.zeros((max_steps, lat), dtype=torch.bfloat16, device="cuda")
+    ztr = torch.zeros((max_steps, H), dtype=torch.bfloat16, device="cuda")
+    params = ming.SampleParams(max_steps, 2.0, 0.25, 0.0)
+    n, stops = ctx.sample_latents(models["lm_model"], models["cfm"], models["agg"], flow.lin_w("stop_head"), bias_d,
+                                  dev_u16(emb), cache.kv, bank, params, lats, z_trace=ztr)
+    g_lat, g_z, g_bank = host_u16(lats), host_u16(ztr), host_u16(bank)
+    # the stop rule on the GPU's own stop values
+    want_n = max_steps
+    for k, sp in enumerate(stops):
+        if sp > 0.5 and k > 3:
+            want_n = k + 1
+            break
+    assert n == want_n, (n, stops)
+    assert n == (5 if case == "stops" else max_steps)
+    assert cache.len == (L + n if n < max_steps or case == "stops" else L + n - 1), cache.len
+    cfg, layers, norm, head = models["olm"]
+    oc, oa = models["ocfm"], models["oagg"]
+    kc = np.zeros((spec.n_layers, spec.kv_heads, L + max_steps + 2, spec.head_dim), np.uint16)
+    vc = np.zeros_like(kc)
+    for i in range(L):
+        _, z_ref, _, _, _ = oracle_step(cfg, layers, norm, head, emb[i], i, kc, vc)
+    assert_close_bf16(g_z[0], z_ref, "z_0 (prefill)")
+    stop_lin = oracle.Linear(flow.hostw["stop_head.weight"])
+    hist = np.zeros(lat, np.uint16)
+    for k in range(n):
+        assert abs(stops[k] - oracle.stop_prob(stop_lin, bias, g_z[k])) <= 1e-2, (k, stops[k])
+        ref, _ = oracle.cfm_sample(oc, g_z[k], hist, g_bank[k, 0], g_bank[k, 1:], 2.0, 0.0)
+        assert_close_bf16(g_lat[k], ref, f"latent {k}", atol=6e-2, rtol=2e-2)
+        assert np.abs(oracle.to_f32(g_lat[k]).astype(np.float64) - oracle.to_f32(ref)).mean() <= 2e-2
+        hist = g_lat[k]
+        if k + 1 < n:
+            # the LM input row the loop used: the same aggregate kernel on the same latent
+            xd = torch.empty(H, dtype=torch.bfloat16, device="cuda")
+            models["agg"].aggregate(dev_u16(g_lat[k]), xd)
+            ctx.sync()
+            xrow = host_u16(xd)
+            assert_close_bf16(xrow, oracle.aggregate(oa, g_lat[k]), f"aggregate {k}")
+            _, z_ref, _, _, _ = oracle_step(cfg, layers, norm, head, xrow, L + k, kc, vc)
+            assert_close_bf16(g_z[k + 1], z_ref, f"z_{k + 1}")
+    assert not np.any(g_lat[n:]), "no latent past the last step"
+
+
+def test_sample_latents_rejects(ming, ctx, models):
+    ming, S = mods()
+    spec, flow = models["spec"], models["flow"]
+    cache = S.KvCache(spec, 3)
+    emb = torch.zeros((3, spec.hidden), dtype=torch.bfloat16, device="cuda")
+    bank = torch.zeros((4, 11, 64), dtype=torch.bfloat16, device="cuda")
+    lats = torch.zeros((4, 64), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ming.MingError) as e:  # prompt fills the cache: no step fits
+        ctx.sample_latents(models["lm_model"], models["cfm"], models["agg"], flow.lin_w("stop_head"),
+                           flow.dev["stop_head.bias"], emb, cache.kv, bank, ming.SampleParams(4, 2.0, 0.25, 0.0),
+                           lats)
+    assert e.value.status == ming.MING_E_CTX_OVER_CAPACITY
+    assert cache.len == 0
