@@ -19,6 +19,16 @@ rocprofv3's FETCH_SIZE/WRITE_SIZE counters measured for this workload,
 scaled by a plain copy's reading (profiles/); null for other workloads.
 `cpu_baseline` times the oracle (the CPU restatement in oracle/, OpenMP over
 output rows) on the host cores on a bounded sample of the same workload.
+
+Two more workloads print a line of the same form (`--workload`):
+  cfm   one flow-head sample per step (cfmSample: 10 CFG Euler steps through
+        8 DiT blocks, hidden 1024, 16 x 64 heads, ff 4096, 6 rows; bf16
+        weights N(0, 0.02)); roofline over the weight bytes of a sample.
+  loop  one token of the TTS loop per step (sampleLatents: flow head,
+        aggregator, a hidden-only 4-bit LM decode step and the stop head),
+        the per-token time being the difference of a K-step and a 1-step run
+        after the same prompt prefill; roofline over the token's weight and
+        KV bytes.
 """
 import argparse
 import importlib
@@ -33,12 +43,15 @@ sys.path.insert(0, os.path.join(ROOT, "oracle"))
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 METRIC = "LM decode tokens/s @bs1 ctx2048 (4-bit) + achieved HBM GB/s % of peak"
+METRIC_CFM = "flow-head samples/s (cfmSample: 10 CFG Euler steps, 8 DiT blocks, hidden 1024, bf16) + achieved GB/s"
+METRIC_LOOP = "TTS tokens/s (sampleLatents step: flow head + aggregator + 4-bit LM decode + stop head) + achieved GB/s"
 HBM_PEAK_GBS = 8000.0
 
 
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--workload", choices=["lm", "cfm", "loop"], default="lm")
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--ctx", type=int, default=2048)
@@ -54,7 +67,10 @@ def main():
         print("bench.py measures one GPU: the decode path runs on a single MI355X "
               "(multi-GPU sharding is described in DESIGN.md, not launched)", file=sys.stderr)
         sys.exit(2)
-    import numpy as np
+    if args.workload == "cfm":
+        return bench_cfm(args)
+    if args.workload == "loop":
+        return bench_loop(args)
     import torch
 
     ming = importlib.import_module("ming-tts-serve_amd")
@@ -180,6 +196,172 @@ def cpu_baseline(ming, S, syn, cache, args):
         "sample": f"{n} decode tokens of the same 24-layer 4-bit model at ctx {args.ctx} "
                   f"({dt:.1f} s, C restatement of the MLX CPU graph, OpenMP over output rows)",
     }
+
+
+# ---- flow head -----------------------------------------------------------------------
+
+def cfm_bytes_per_sample(spec):
+    """bf16 weight bytes one cfmSample reads: per Euler step the blocks, x_emb
+    (for y) and the final layer; once c_emb and x_emb (for the history)."""
+    D, H, lat = spec.hidden, spec.lm_hidden, spec.latent
+    per_step = spec.cfm_blocks * spec.block_params() + D * lat + D + lat * D + lat + D
+    once = D * H + D + D * lat
+    return 2 * (10 * per_step + once)
+
+
+def timed_events(fn, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def base_line(metric, value, unit, args, ms, config, roofline, cpu, data):
+    return {"metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": data, "config": config, "roofline": roofline,
+            "cpu_baseline": cpu}
+
+
+def bench_cfm(args):
+    import numpy as np
+    import torch
+
+    ming = importlib.import_module("ming-tts-serve_amd")
+    S = importlib.import_module("ming-tts-serve_amd.synthetic")
+    spec = S.MING_DIT
+    ctx = ming.Context(0)
+    flow = S.SyntheticFlow(ctx, spec, seed=1, parts=("cfm",))
+    m = flow.cfm_model()
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda().view(torch.bfloat16)
+    host = {k: ming.synth_normal_bf16(s, "bench." + k, n) for k, s, n in
+            (("z", 1, spec.lm_hidden), ("hist", 2, spec.latent), ("noise", 3, spec.latent), ("sde", 4, 10 * spec.latent))}
+    z, hist, noise, sde = (dev(host[k]) for k in ("z", "hist", "noise", "sde"))
+    out = torch.empty(spec.latent, dtype=torch.bfloat16, device="cuda")
+    ms = timed_events(lambda: m.sample(z, hist, noise, sde, 2.0, 0.25, 0.0, out), args.steps, args.warmup)
+    nbytes = cfm_bytes_per_sample(spec)
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        from ditkit import oracle_cfm
+
+        oracle.set_threads(int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1))
+        oc = oracle_cfm(flow)
+        n, t0 = 0, time.time()
+        while True:
+            oracle.cfm_sample(oc, host["z"], host["hist"], host["noise"], host["sde"].reshape(10, -1), 2.0, 0.0)
+            n += 1
+            if time.time() - t0 >= args.cpu_seconds:
+                break
+        dt = time.time() - t0
+        cpu = {"value": round(n / dt, 4), "unit": "samples/s", "cores": oracle.get_threads(), "kind": "port",
+               "sample": f"{n} flow-head samples of the same weights ({dt:.1f} s, C restatement of the MLX graph)"}
+    line = base_line(METRIC_CFM, 1000.0 / ms, "samples/s", args, ms,
+                     {"workload": "flow head of one token: 10 CFG Euler steps through 8 DiT blocks (hidden 1024, "
+                                  "16x64 heads, ff 4096), rows 2 halves x 3 positions", "global_batch": 1, "seq_len": 3},
+                     {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": nbytes,
+                      "launch_ms": round(ms, 5)},
+                     cpu, "synthetic (random-init N(0,0.02) bf16 DiT weights; z, history, noise N(0,1))")
+    print(json.dumps(line), flush=True)
+
+
+# ---- whole per-token loop ------------------------------------------------------------
+
+def bench_loop(args):
+    import numpy as np
+    import torch
+
+    ming = importlib.import_module("ming-tts-serve_amd")
+    S = importlib.import_module("ming-tts-serve_amd.synthetic")
+    lspec, dspec = S.QWEN2_05B, S.MING_DIT
+    ctx = ming.Context(0)
+    lm = S.SyntheticLm(ctx, lspec, seed=0, quant=True)
+    lmm = lm.model()
+    flow = S.SyntheticFlow(ctx, dspec, seed=1)
+    cfm, agg = flow.cfm_model(), flow.agg_model()
+    H, lat, L = lspec.hidden, dspec.latent, 16
+    K = max(2, args.steps)
+    never = torch.tensor([20.0, 0.0], dtype=torch.bfloat16, device="cuda")  # stop bias: the loop runs K steps
+    emb = torch.from_numpy(ming.synth_normal_bf16(5, "bench.embeds", L * H, 0.0, 0.5).view(np.int16).reshape(L, H))
+    emb = emb.cuda().view(torch.bfloat16)
+    bank = torch.empty((K, 11, lat), dtype=torch.bfloat16, device="cuda")
+    ctx.noise_bank(7, K, lat, bank)
+    lats = torch.empty((K, lat), dtype=torch.bfloat16, device="cuda")
+
+    def run(n):
+        cache = S.KvCache(lspec, L + n + 2)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        done, _ = ctx.sample_latents(lmm, cfm, agg, flow.lin_w("stop_head"), never, emb, cache.kv, bank,
+                                     ming.SampleParams(n, 2.0, 0.25, 0.0), lats)
+        return time.perf_counter() - t, done
+
+    for _ in range(max(1, args.warmup // 10)):
+        run(2)
+    t1, _ = run(1)
+    tk, done = run(K)
+    ms = (tk - t1) / (done - 1) * 1e3
+    lm_bytes = S.lm_bytes_per_token(lspec, L + K // 2) - lspec.vocab * lspec.hidden * 0.5625  # no head in the loop
+    nbytes = int(lm_bytes + cfm_bytes_per_sample(dspec) + 2 * (dspec.agg_blocks * dspec.block_params() +
+                 dspec.hidden * lat + dspec.hidden * H + 3 * dspec.hidden + H) + 2 * (2 * H + 2))
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        cpu = loop_cpu_baseline(ming, lm, flow, args)
+    line = base_line(METRIC_LOOP, 1000.0 / ms, "tokens/s", args, ms,
+                     {"workload": f"one sampleLatents step after a {L}-row prompt: flow head (8 blocks x 10 Euler "
+                                  "steps), aggregator (8 blocks), Qwen2-0.5B-shaped 24-layer 4-bit LM decode "
+                                  "(hidden only), stop head", "global_batch": 1, "seq_len": L + K},
+                     {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": nbytes,
+                      "launch_ms": round(ms, 5)},
+                     cpu, "synthetic (random-init N(0,0.02) weights, LM quantized to MLX affine 4-bit/g64; "
+                          "prompt rows N(0,0.25); noise bank N(0,1))")
+    print(json.dumps(line), flush=True)
+
+
+def loop_cpu_baseline(ming, lm, flow, args):
+    """The oracle's per-token work (stop head, flow head, aggregator, LM
+    decode step) on the host cores, for about args.cpu_seconds (>= 1 token)."""
+    import numpy as np
+
+    import oracle
+    from ditkit import oracle_agg, oracle_cfm
+    from lmkit import oracle_model, oracle_step
+
+    oracle.set_threads(int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1))
+    cfg, layers, norm, head = oracle_model(lm)
+    oc, oa = oracle_cfm(flow), oracle_agg(flow)
+    stop = oracle.Linear(flow.hostw["stop_head.weight"])
+    H, lat = lm.spec.hidden, flow.spec.latent
+    kc = np.zeros((lm.spec.n_layers, lm.spec.kv_heads, 64, lm.spec.head_dim), np.uint16)
+    vc = np.zeros_like(kc)
+    z = ming.synth_normal_bf16(9, "bench.z", H)
+    hist = np.zeros(lat, np.uint16)
+    noise = ming.synth_normal_bf16(10, "bench.noise", 11 * lat).reshape(11, lat)
+    n, t0 = 0, time.time()
+    while n < 60:
+        oracle.stop_prob(stop, flow.hostw["stop_head.bias"], z)
+        latent, _ = oracle.cfm_sample(oc, z, hist, noise[0], noise[1:], 2.0, 0.0)
+        x = oracle.aggregate(oa, latent)
+        _, z, _, _, _ = oracle_step(cfg, layers, norm, head, x, n, kc, vc)
+        hist = latent
+        n += 1
+        if time.time() - t0 >= args.cpu_seconds:
+            break
+    dt = time.time() - t0
+    return {"value": round(n / dt, 4), "unit": "tokens/s", "cores": oracle.get_threads(), "kind": "port",
+            "sample": f"{n} TTS tokens of the same models ({dt:.1f} s; the oracle's LM step includes its head)"}
 
 
 if __name__ == "__main__":

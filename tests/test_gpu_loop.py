@@ -6,7 +6,8 @@ Each step is recomputed on the oracle from the GPU's own inputs (teacher
 forced): z_0 from the prompt prefill, stop_k = stopProb(z_k), latent_k =
 cfmSample(z_k, history_k, noise bank row k), aggregate(latent_k) against the
 GPU kernel's row, and z_{k+1} = LM(that row) with the oracle's own cache.
-Bars: hidden states and aggregator rows 2e-2 + 1e-2 |ref|; the ten-step latent 6e-2 + 2e-2 |ref| (mean |d| <= 2e-2, as the flow head's own
+Bars: hidden states and aggregator rows 2e-2 + 1e-2 |ref|; the ten-step
+latent 6e-2 + 2e-2 |ref| (mean |d| <= 2e-2, as the flow head's own
 end-to-end test); stop probabilities 1e-2; the step count follows the stop
 rule (stop after latent_k when stop_k > 0.5 and k > 3) applied to the GPU's
 stop values, and the cache grows by the documented number of positions."""
