@@ -24,6 +24,9 @@ Two more workloads print a line of the same form (`--workload`):
   cfm   one flow-head sample per step (cfmSample: 10 CFG Euler steps through
         8 DiT blocks, hidden 1024, 16 x 64 heads, ff 4096, 6 rows; bf16
         weights N(0, 0.02)); roofline over the weight bytes of a sample.
+  c4    one sample of config 4's adaLN flow head per step (4 blocks, hidden
+        896, 14 x 64 heads, ff 3584, a patch of 4 frames x 64, 10 CFG Euler
+        steps; the modulations of all steps are computed once per sample).
   loop  one token of the TTS loop per step (sampleLatents: flow head,
         aggregator, a hidden-only 4-bit LM decode step and the stop head),
         the per-token time being the difference of a K-step and a 1-step run
@@ -44,6 +47,7 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 METRIC = "LM decode tokens/s @bs1 ctx2048 (4-bit) + achieved HBM GB/s % of peak"
 METRIC_CFM = "flow-head samples/s (cfmSample: 10 CFG Euler steps, 8 DiT blocks, hidden 1024, bf16) + achieved GB/s"
+METRIC_C4 = "adaLN flow-head samples/s (config 4: 4 blocks, hidden 896, 4-frame patch, 10 CFG Euler steps, bf16) + achieved GB/s"
 METRIC_LOOP = "TTS tokens/s (sampleLatents step: flow head + aggregator + 4-bit LM decode + stop head) + achieved GB/s"
 HBM_PEAK_GBS = 8000.0
 
@@ -51,7 +55,7 @@ HBM_PEAK_GBS = 8000.0
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--workload", choices=["lm", "cfm", "loop"], default="lm")
+    p.add_argument("--workload", choices=["lm", "cfm", "c4", "loop"], default="lm")
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--ctx", type=int, default=2048)
@@ -71,6 +75,8 @@ def main():
         return bench_cfm(args)
     if args.workload == "loop":
         return bench_loop(args)
+    if args.workload == "c4":
+        return bench_c4(args)
     import torch
 
     ming = importlib.import_module("ming-tts-serve_amd")
@@ -272,6 +278,53 @@ def bench_cfm(args):
                       "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": nbytes,
                       "launch_ms": round(ms, 5)},
                      cpu, "synthetic (random-init N(0,0.02) bf16 DiT weights; z, history, noise N(0,1))")
+    print(json.dumps(line), flush=True)
+
+
+def bench_c4(args):
+    import numpy as np
+    import torch
+
+    ming = importlib.import_module("ming-tts-serve_amd")
+    S = importlib.import_module("ming-tts-serve_amd.synthetic")
+    spec = S.MING_ADALN
+    ctx = ming.Context(0)
+    syn = S.SyntheticAdaln(ctx, spec, seed=1)
+    m = syn.model()
+    F, lat = spec.frames, spec.latent
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda().view(torch.bfloat16)
+    host = {k: ming.synth_normal_bf16(s, "bench." + k, n) for k, s, n in
+            (("z", 1, spec.lm_hidden), ("noise", 3, F * lat), ("sde", 4, 10 * F * lat))}
+    z, noise, sde = (dev(host[k]) for k in ("z", "noise", "sde"))
+    out = torch.empty((F, lat), dtype=torch.bfloat16, device="cuda")
+    ms = timed_events(lambda: m.sample(z, noise, sde, 2.0, 0.25, 0.0, out), args.steps, args.warmup)
+    nbytes = spec.sample_weight_bytes()
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        from ditkit import oracle_adaln
+
+        oracle.set_threads(int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1))
+        om = oracle_adaln(syn)
+        n, t0 = 0, time.time()
+        while True:
+            oracle.adaln_sample(om, host["z"], host["noise"].reshape(F, lat), host["sde"].reshape(10, F, lat), 2.0,
+                                0.0)
+            n += 1
+            if time.time() - t0 >= args.cpu_seconds:
+                break
+        dt = time.time() - t0
+        cpu = {"value": round(n / dt, 4), "unit": "samples/s", "cores": oracle.get_threads(), "kind": "port",
+               "sample": f"{n} adaLN flow-head samples of the same weights ({dt:.1f} s, C restatement)"}
+    line = base_line(METRIC_C4, 1000.0 / ms, "samples/s", args, ms,
+                     {"workload": "config 4 adaLN flow head: 4 DiT blocks (hidden 896, 14x64 heads, ff 3584) with "
+                                  "adaLN-Zero modulation from silu(t_emb + c_emb(z)), a 4-frame x 64 patch, "
+                                  "10 CFG Euler steps, rows 2 halves x 4 frames", "global_batch": 1, "seq_len": F},
+                     {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": nbytes,
+                      "launch_ms": round(ms, 5)},
+                     cpu, "synthetic (random-init N(0,0.02) bf16 weights; z, noise N(0,1))")
     print(json.dumps(line), flush=True)
 
 

@@ -333,6 +333,56 @@ int ming_aggregate(ming_ctx* ctx, ming_agg_model* m, const void* latent, void* o
  * softmax(f32(stop_head(z)))[1]; head [2, lm_hidden] bf16 with bias. */
 int ming_stop_prob(ming_ctx* ctx, const ming_linear* head, const void* bias, const void* z, float* p_dev);
 
+/* ---- adaLN DiT flow head (config 4) ----------------------------------------
+ * No reference implementation exists (the reference DiT conditions by an
+ * additive row, src/ming_model.zig:1078-1091); this build defines the variant
+ * as the standard adaLN-Zero DiT on the reference block's RMSNorm.  Per CFG half
+ * b (uncond: z = 0) and Euler step s: c = bf16(t_emb[s] + c_emb(z)); per block
+ * mod = bf16(b_ada + W_ada silu(c)) = [shift_a | scale_a | gate_a | shift_m |
+ * scale_m | gate_m] (6 x hidden); modulate(n) = bf16(bf16(n*bf16(1+scale)) +
+ * shift) on each rms_norm output; x1 = bf16(x + bf16(gate_a*out_proj(...))),
+ * x2 = bf16(x1 + bf16(gate_m*ff2(...))).  Rows are the F patch frames
+ * x_emb(y_f) per half (rotary positions 0..F-1); the final layer is
+ * modulate(rms(h)) with [shift | scale] = b_fa + W_fa silu(c), a linear to the
+ * latent and CFG + Euler (+ SDE) per frame.  shift = scale = 0, gate = 1 gives
+ * the reference block exactly. */
+typedef struct {
+    ming_dit_block_w base;
+    ming_linear ada;        /* bf16 [6*hidden, hidden] */
+    const void* bada;       /* bf16 [6*hidden] */
+} ming_adaln_block_w;
+
+/* One adaLN block on x [B, L, hidden] (B <= 2 CFG halves, B*L <= 8) with
+ * mod (device bf16 [B][6*hidden]) and rotary tables [L][head_dim/2]. */
+int ming_adaln_block(ming_ctx* ctx, const ming_dit_cfg* cfg, const ming_adaln_block_w* w, const void* mod,
+                     const void* x, int32_t B, int32_t L, const float* cos_dev, const float* sin_dev,
+                     ming_dit_out* out);
+
+typedef struct {
+    ming_dit_cfg cfg;
+    int32_t n_blocks, frames;                  /* config 4: 4 blocks, 4 frames */
+    const ming_adaln_block_w* blocks;          /* host array [n_blocks] */
+    const float* inv_freq;                     /* host f32 [head_dim/2] */
+    ming_linear x_emb, c_emb, t_mlp0, t_mlp2, final, final_ada;
+    const void *bx, *bc, *bt0, *bt2, *final_norm, *bf, *bfa;
+} ming_adaln_w;
+
+typedef struct ming_adaln_model ming_adaln_model;
+/* Load-time tables (rotary for L = frames, flow schedule, timestep embeddings)
+ * and the workspace of one sample. */
+int ming_adaln_model_create(ming_ctx* ctx, const ming_adaln_w* w, ming_adaln_model** out);
+int ming_adaln_model_destroy(ming_adaln_model* m);
+/* Device tables of the model, the last sample's included: t_emb [10][2][hidden],
+ * silu(c) [10][2][hidden], modulations [n_blocks][10*2][6*hidden], final [10*2][2*hidden]. */
+int ming_adaln_model_tables(ming_adaln_model* m, const void** t_emb_dev, const void** silu_c_dev,
+                            const void** mods_dev, const void** modf_dev);
+/* One flow-head sample of a patch: z [lm_hidden], noise [frames][latent], sde
+ * [10][frames][latent] (device bf16) -> patch_out [frames][latent]; every
+ * modulation of the 10 steps is computed once, up front (its weights are read
+ * once per token); y_steps (optional, [10][frames][latent]) = each step's patch. */
+int ming_adaln_sample(ming_ctx* ctx, ming_adaln_model* m, const void* z, const void* noise, const void* sde,
+                      float cfg, float sigma, float temperature, void* patch_out, void* y_steps);
+
 /* Sizes of a prepared model (out-pointers may be null). */
 int ming_lm_model_dims(const ming_lm_model* m, int32_t* hidden, int32_t* vocab);
 int ming_cfm_model_dims(const ming_cfm_model* m, int32_t* latent, int32_t* lm_hidden);

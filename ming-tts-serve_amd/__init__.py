@@ -105,6 +105,17 @@ class AggW(ctypes.Structure):
     ] + [(n, c_void_p) for n in ("bx", "cls", "final_norm", "bf")]
 
 
+class AdalnBlockW(ctypes.Structure):
+    _fields_ = [("base", DitBlockW), ("ada", Linear), ("bada", c_void_p)]
+
+
+class AdalnW(ctypes.Structure):
+    _fields_ = [("cfg", DitCfg), ("n_blocks", c_i32), ("frames", c_i32), ("blocks", c_void_p),
+                ("inv_freq", c_void_p)] + [
+        (n, Linear) for n in ("x_emb", "c_emb", "t_mlp0", "t_mlp2", "final", "final_ada")
+    ] + [(n, c_void_p) for n in ("bx", "bc", "bt0", "bt2", "final_norm", "bf", "bfa")]
+
+
 class SampleParams(ctypes.Structure):
     _fields_ = [("max_steps", c_i32), ("cfg", c_f32), ("sigma", c_f32), ("temperature", c_f32)]
 
@@ -171,6 +182,13 @@ def lib():
         "ming_agg_model_destroy": (c_i32, [c_void_p]),
         "ming_aggregate": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p]),
         "ming_stop_prob": (c_i32, [c_void_p, P(Linear), c_void_p, c_void_p, c_void_p]),
+        "ming_adaln_block": (c_i32, [c_void_p, P(DitCfg), P(AdalnBlockW), c_void_p, c_void_p, c_i32, c_i32, c_void_p,
+                                     c_void_p, P(DitOut)]),
+        "ming_adaln_model_create": (c_i32, [c_void_p, P(AdalnW), P(c_void_p)]),
+        "ming_adaln_model_destroy": (c_i32, [c_void_p]),
+        "ming_adaln_model_tables": (c_i32, [c_void_p, P(c_void_p), P(c_void_p), P(c_void_p), P(c_void_p)]),
+        "ming_adaln_sample": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_f32, c_f32, c_f32,
+                                      c_void_p, c_void_p]),
         "ming_lm_model_dims": (c_i32, [c_void_p, P(c_i32), P(c_i32)]),
         "ming_cfm_model_dims": (c_i32, [c_void_p, P(c_i32), P(c_i32)]),
         "ming_agg_model_dims": (c_i32, [c_void_p, P(c_i32), P(c_i32)]),
@@ -322,6 +340,10 @@ class Context:
                                          ptr(dt), ptr(sq), ptr(sde), int(step), float(cfg), float(shift),
                                          ptr(y_out)))
 
+    def adaln_block(self, cfg, w, mod, x, B, L, cos, sin, out):
+        self.check(self.L.ming_adaln_block(self.h, ctypes.byref(cfg), ctypes.byref(w), ptr(mod), ptr(x), int(B),
+                                           int(L), ptr(cos), ptr(sin), ctypes.byref(out)))
+
     def stop_prob(self, head, bias, z, p):
         self.check(self.L.ming_stop_prob(self.h, ctypes.byref(head), ptr(bias), ptr(z), ptr(p)))
 
@@ -379,6 +401,37 @@ class CfmModel:
         self.ctx.check(self.ctx.L.ming_cfm_sample(self.ctx.h, self.h, ptr(z), ptr(hist), ptr(noise), ptr(sde),
                                                   float(cfg), float(sigma), float(temperature), ptr(latent_out),
                                                   ptr(y_steps)))
+
+
+class AdalnModel:
+    """ming_adaln_model: the adaLN flow head (config 4)."""
+
+    def __init__(self, ctx, w):
+        self.ctx, self.w = ctx, w
+        h = c_void_p()
+        ctx.check(ctx.L.ming_adaln_model_create(ctx.h, ctypes.byref(w), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.ctx.L.ming_adaln_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tables(self):
+        """Device pointers: t_emb, silu(c), block modulations, final modulations."""
+        ps = [c_void_p() for _ in range(4)]
+        self.ctx.check(self.ctx.L.ming_adaln_model_tables(self.h, *(ctypes.byref(p) for p in ps)))
+        return [p.value for p in ps]
+
+    def sample(self, z, noise, sde, cfg, sigma, temperature, patch_out, y_steps=None):
+        self.ctx.check(self.ctx.L.ming_adaln_sample(self.ctx.h, self.h, ptr(z), ptr(noise), ptr(sde), float(cfg),
+                                                    float(sigma), float(temperature), ptr(patch_out), ptr(y_steps)))
 
 
 class AggModel:

@@ -26,6 +26,16 @@ hipError_t launch_cfm_final(hipStream_t st, const uint16_t* h, int L, int D, con
                             const uint16_t* sq, const uint16_t* sde, int step, float cfg, float shift,
                             uint16_t* y_out);
 hipError_t launch_stop_prob(hipStream_t st, const uint16_t* z, const uint16_t* w, const uint16_t* b, int K, float* p);
+hipError_t launch_adaln_block(hipStream_t st, const DitBlockDev& w, const uint16_t* mod, const uint16_t* x, int B,
+                              int L, const float* cos_t, const float* sin_t, uint16_t* qkv, uint16_t* att, uint16_t* x1,
+                              uint16_t* hh, uint16_t* x2);
+hipError_t launch_adaln_cond(hipStream_t st, const uint16_t* te, const uint16_t* ce, int steps, int D, uint16_t* out);
+hipError_t launch_adaln_rows(hipStream_t st, const uint16_t* y, int F, const uint16_t* wx, const uint16_t* bx, int D,
+                             int latent, uint16_t* rows);
+hipError_t launch_adaln_final(hipStream_t st, const uint16_t* h, int F, int D, const uint16_t* norm, float eps,
+                              const uint16_t* mod, const uint16_t* wf, const uint16_t* bf, int latent, const uint16_t* y,
+                              const uint16_t* dt, const uint16_t* sq, const uint16_t* sde, int step, float cfg,
+                              float shift, uint16_t* y_out);
 }  // namespace ming
 
 using namespace ming;
@@ -170,6 +180,59 @@ hipError_t run_stack(hipStream_t st, const std::vector<DitBlockDev>& blocks, Sta
     return hipSuccess;
 }
 
+// Model.load's flow tables (src/ming_model.zig:976-1004): flowSchedule in
+// bf16 (:1207-1215), flow_dt and flow_sq (:995-1002), and the timestep
+// embeddings (:976-992, :1064-1076) -- sinusoid rows on the host, the MLP on
+// the GPU -- into t_emb [steps][2][D].  Synchronous.
+hipError_t flow_tables(hipStream_t s, const ming_linear& mlp0, const void* b0, const ming_linear& mlp2, const void* b2,
+                       int D, uint16_t* t, uint16_t* dt, uint16_t* sq, uint16_t* dt_dev, uint16_t* sq_dev,
+                       uint16_t* t_emb_dev) {
+    static const float sched[kFlowSteps + 1] = {0, 2, 4, 6, 8, 12, 16, 20, 24, 28, 32};
+    const float c32 = hrb(1.0f / 32.0f), hpi = hrb((float)(3.14159265358979323846 / 2.0));
+    for (int i = 0; i <= kFlowSteps; i++) {
+        const float ti = hrb(c32 * hrb(sched[i]));
+        const float ct = hrb(std::cos(hrb(hpi * ti)));
+        const float sw = hrb(hrb(ct - 1.0f) + ti);
+        t[i] = hbf(ti + hrb(-1.0f * sw));
+    }
+    for (int i = 0; i < kFlowSteps; i++) {
+        const float d = hrb(hf(t[i + 1]) - hf(t[i]));
+        dt[i] = hbf(d);
+        sq[i] = hbf(std::pow(std::fabs(d), hrb(0.5f)));
+    }
+    std::vector<uint16_t> sc((size_t)kFlowSteps * 2 * 256);
+    const float ef = (float)(std::log(10000.0) / 127.0);
+    float fr[128];
+    for (int k = 0; k < 128; k++) fr[k] = std::exp((float)k * -ef);
+    for (int i = 0; i < kFlowSteps; i++) {
+        const float ts = hrb(hrb(1000.0f) * hf(t[i]));
+        for (int r = 0; r < 2; r++)
+            for (int k = 0; k < 128; k++) {
+                const float a = ts * fr[k];
+                sc[((size_t)i * 2 + r) * 256 + k] = hbf(std::sin(a));
+                sc[((size_t)i * 2 + r) * 256 + 128 + k] = hbf(std::cos(a));
+            }
+    }
+    DevBuf scd, tmp;
+    hipError_t e = scd.ensure(sizeof(uint16_t) * sc.size());
+    if (e == hipSuccess) e = tmp.ensure(sizeof(uint16_t) * 2 * (size_t)D);
+    if (e == hipSuccess) e = hipMemcpyAsync(scd.p, sc.data(), sizeof(uint16_t) * sc.size(), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(dt_dev, dt, sizeof(uint16_t) * kFlowSteps, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(sq_dev, sq, sizeof(uint16_t) * kFlowSteps, hipMemcpyHostToDevice, s);
+    for (int i = 0; i < kFlowSteps && e == hipSuccess; i++) {
+        e = launch_dit_linear(s, u16(scd.p) + (size_t)i * 2 * 256, 0, 1, 2, nullptr, 0.0f, u16(mlp0.w), D, 256, u16(b0),
+                              u16(tmp.p), true);
+        if (e == hipSuccess)
+            e = launch_dit_linear(s, u16(tmp.p), 0, 1, 2, nullptr, 0.0f, u16(mlp2.w), D, D, u16(b2),
+                                  t_emb_dev + (size_t)i * 2 * D, false);
+    }
+    const hipError_t es = hipStreamSynchronize(s);  // the host tables above must outlive the copies
+    if (e == hipSuccess) e = es;
+    scd.release();
+    tmp.release();
+    return e;
+}
+
 }  // namespace
 
 struct ming_cfm_model {
@@ -181,6 +244,19 @@ struct ming_cfm_model {
     int latent = 0, lm_hidden = 0;
     uint16_t t[kFlowSteps + 1]{}, dt[kFlowSteps]{}, sq[kFlowSteps]{};
     DevBuf cos, sin, t_emb, dtd, sqd, zc, ce, xh, y;
+    StackBufs s;
+};
+
+struct ming_adaln_model {
+    ming_ctx* ctx = nullptr;
+    ming_dit_cfg cfg{};
+    int frames = 0, latent = 0, lm_hidden = 0;
+    std::vector<DitBlockDev> blocks;
+    std::vector<const uint16_t*> ada, bada;
+    const uint16_t *wx = nullptr, *bx = nullptr, *wc = nullptr, *bc = nullptr, *wf = nullptr, *bf = nullptr,
+                   *final_norm = nullptr, *wfa = nullptr, *bfa = nullptr;
+    uint16_t t[kFlowSteps + 1]{}, dt[kFlowSteps]{}, sq[kFlowSteps]{};
+    DevBuf cos, sin, t_emb, dtd, sqd, zc, ce, silu_c, mods, modf, y;
     StackBufs s;
 };
 
@@ -323,54 +399,8 @@ int ming_cfm_model_create(ming_ctx* ctx, const ming_cfm_w* w, ming_cfm_model** o
         ming_cfm_model_destroy(m);
         return st;
     }
-    // flowSchedule in bf16 (src/ming_model.zig:1207-1215); flow_dt, flow_sq (:995-1002)
-    {
-        static const float sched[kFlowSteps + 1] = {0, 2, 4, 6, 8, 12, 16, 20, 24, 28, 32};
-        const float c32 = hrb(1.0f / 32.0f), hpi = hrb((float)(3.14159265358979323846 / 2.0));
-        for (int i = 0; i <= kFlowSteps; i++) {
-            const float ti = hrb(c32 * hrb(sched[i]));
-            const float ct = hrb(std::cos(hrb(hpi * ti)));
-            const float sw = hrb(hrb(ct - 1.0f) + ti);
-            m->t[i] = hbf(ti + hrb(-1.0f * sw));
-        }
-        for (int i = 0; i < kFlowSteps; i++) {
-            const float d = hrb(hf(m->t[i + 1]) - hf(m->t[i]));
-            m->dt[i] = hbf(d);
-            m->sq[i] = hbf(std::pow(std::fabs(d), hrb(0.5f)));
-        }
-    }
-    // timestep embeddings (:976-992, :1064-1076): sinusoid rows on the host, MLP on the GPU
-    std::vector<uint16_t> sc((size_t)kFlowSteps * 2 * 256);
-    {
-        const float ef = (float)(std::log(10000.0) / 127.0);
-        float fr[128];
-        for (int k = 0; k < 128; k++) fr[k] = std::exp((float)k * -ef);
-        for (int i = 0; i < kFlowSteps; i++) {
-            const float ts = hrb(hrb(1000.0f) * hf(m->t[i]));
-            for (int r = 0; r < 2; r++)
-                for (int k = 0; k < 128; k++) {
-                    const float a = ts * fr[k];
-                    sc[((size_t)i * 2 + r) * 256 + k] = hbf(std::sin(a));
-                    sc[((size_t)i * 2 + r) * 256 + 128 + k] = hbf(std::cos(a));
-                }
-        }
-    }
-    DevBuf scd, tmp;
-    e = scd.ensure(sizeof(uint16_t) * sc.size());
-    if (e == hipSuccess) e = tmp.ensure(sizeof(uint16_t) * 2 * (size_t)D);
-    if (e == hipSuccess) e = hipMemcpyAsync(scd.p, sc.data(), sizeof(uint16_t) * sc.size(), hipMemcpyHostToDevice, s);
-    if (e == hipSuccess) e = hipMemcpyAsync(m->dtd.p, m->dt, sizeof(m->dt), hipMemcpyHostToDevice, s);
-    if (e == hipSuccess) e = hipMemcpyAsync(m->sqd.p, m->sq, sizeof(m->sq), hipMemcpyHostToDevice, s);
-    for (int i = 0; i < kFlowSteps && e == hipSuccess; i++) {
-        e = launch_dit_linear(s, u16(scd.p) + (size_t)i * 2 * 256, 0, 1, 2, nullptr, 0.0f, u16(w->t_mlp0.w), D, 256,
-                              u16(w->bt0), u16(tmp.p), true);
-        if (e == hipSuccess)
-            e = launch_dit_linear(s, u16(tmp.p), 0, 1, 2, nullptr, 0.0f, u16(w->t_mlp2.w), D, D, u16(w->bt2),
-                                  u16(m->t_emb.p) + (size_t)i * 2 * D, false);
-    }
-    if (e == hipSuccess) e = hipStreamSynchronize(s);
-    scd.release();
-    tmp.release();
+    e = flow_tables(s, w->t_mlp0, w->bt0, w->t_mlp2, w->bt2, D, m->t, m->dt, m->sq, u16(m->dtd.p), u16(m->sqd.p),
+                    u16(m->t_emb.p));
     if (e != hipSuccess) {
         ming_cfm_model_destroy(m);
         return hip_check(ctx, e, "cfm_model_create tables");
@@ -531,6 +561,179 @@ int ming_stop_prob(ming_ctx* ctx, const ming_linear* head, const void* bias, con
     if (head->in_features > 4096) return set_err(ctx, MING_E_UNSUPPORTED, "stop_prob: hidden > 4096");
     return hip_check(ctx, launch_stop_prob(ctx->stream, u16(z), u16(head->w), u16(bias), head->in_features, p_dev),
                      "stop_prob launch");
+}
+
+}  // extern "C"
+
+// ---- adaLN flow head (config 4) ---------------------------------------------------------
+
+namespace {
+
+int check_adaln_block(ming_ctx* ctx, const ming_dit_cfg* c, const ming_adaln_block_w* w) {
+    if (!w) return set_err(ctx, MING_E_ARG, "adaln: null block");
+    int st;
+    if ((st = check_block(ctx, c, &w->base)) || (st = check_bf16(ctx, w->ada, 6 * c->hidden, c->hidden, "ada")))
+        return st;
+    if (!w->bada) return set_err(ctx, MING_E_ARG, "adaln: null ada bias");
+    return MING_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ming_adaln_block(ming_ctx* ctx, const ming_dit_cfg* cfg, const ming_adaln_block_w* w, const void* mod,
+                     const void* x, int32_t B, int32_t L, const float* cos_dev, const float* sin_dev,
+                     ming_dit_out* out) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    int st;
+    if ((st = check_cfg(ctx, cfg)) || (st = check_adaln_block(ctx, cfg, w))) return st;
+    if (B <= 0 || B > 2 || L <= 0 || B * L > 8 || L > 8)
+        return set_err(ctx, MING_E_SHAPE, "adaln_block: B must be 1 or 2, B*L <= 8, L <= 8");
+    if (!x || !mod || !cos_dev || !sin_dev || !out || !out->qkv || !out->att || !out->x1 || !out->hh || !out->x2)
+        return set_err(ctx, MING_E_ARG, "adaln_block: null buffer");
+    const DitBlockDev d = block_dev(cfg, &w->base);
+    return hip_check(ctx,
+                     launch_adaln_block(ctx->stream, d, u16(mod), u16(x), B, L, cos_dev, sin_dev, u16(out->qkv),
+                                        u16(out->att), u16(out->x1), u16(out->hh), u16(out->x2)),
+                     "adaln_block launch");
+}
+
+int ming_adaln_model_create(ming_ctx* ctx, const ming_adaln_w* w, ming_adaln_model** out) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!w || !out || !w->blocks || w->n_blocks <= 0 || !w->inv_freq)
+        return set_err(ctx, MING_E_ARG, "adaln_model_create: bad arguments");
+    *out = nullptr;
+    const ming_dit_cfg* c = &w->cfg;
+    int st;
+    if ((st = check_cfg(ctx, c))) return st;
+    for (int i = 0; i < w->n_blocks; i++)
+        if ((st = check_adaln_block(ctx, c, &w->blocks[i]))) return st;
+    const int D = c->hidden, latent = w->x_emb.in_features, H = w->c_emb.in_features, F = w->frames;
+    if (F <= 0 || 2 * F > 8) return set_err(ctx, MING_E_SHAPE, "adaln_model_create: frames must be in [1, 4]");
+    if ((st = check_bf16(ctx, w->x_emb, D, latent, "x_emb")) || (st = check_bf16(ctx, w->c_emb, D, H, "c_emb")) ||
+        (st = check_bf16(ctx, w->t_mlp0, D, 256, "t_mlp0")) || (st = check_bf16(ctx, w->t_mlp2, D, D, "t_mlp2")) ||
+        (st = check_bf16(ctx, w->final, latent, D, "final")) ||
+        (st = check_bf16(ctx, w->final_ada, 2 * D, D, "final_ada")))
+        return st;
+    if (H > 4096 || latent > 4096 || latent % 8 != 0)
+        return set_err(ctx, MING_E_UNSUPPORTED, "adaln_model_create: latent/LM hidden sizes");
+    if (!w->bx || !w->bc || !w->bt0 || !w->bt2 || !w->final_norm || !w->bf || !w->bfa)
+        return set_err(ctx, MING_E_ARG, "adaln_model_create: null bias or norm");
+    auto* m = new ming_adaln_model;
+    m->ctx = ctx;
+    m->cfg = *c;
+    m->frames = F;
+    m->latent = latent;
+    m->lm_hidden = H;
+    for (int i = 0; i < w->n_blocks; i++) {
+        m->blocks.push_back(block_dev(c, &w->blocks[i].base));
+        m->ada.push_back(u16(w->blocks[i].ada.w));
+        m->bada.push_back(u16(w->blocks[i].bada));
+    }
+    m->wx = u16(w->x_emb.w);
+    m->bx = u16(w->bx);
+    m->wc = u16(w->c_emb.w);
+    m->bc = u16(w->bc);
+    m->wf = u16(w->final.w);
+    m->bf = u16(w->bf);
+    m->final_norm = u16(w->final_norm);
+    m->wfa = u16(w->final_ada.w);
+    m->bfa = u16(w->bfa);
+    const int half = c->head_dim / 2, rows = 2 * kFlowSteps;
+    hipStream_t s = ctx->stream;
+    hipError_t e = m->cos.ensure(sizeof(float) * F * half);
+    if (e == hipSuccess) e = m->sin.ensure(sizeof(float) * F * half);
+    if (e == hipSuccess) e = m->t_emb.ensure(sizeof(uint16_t) * (size_t)kFlowSteps * 2 * D);
+    if (e == hipSuccess) e = m->dtd.ensure(sizeof(uint16_t) * kFlowSteps);
+    if (e == hipSuccess) e = m->sqd.ensure(sizeof(uint16_t) * kFlowSteps);
+    if (e == hipSuccess) e = m->zc.ensure(sizeof(uint16_t) * 2 * (size_t)H);
+    if (e == hipSuccess) e = m->ce.ensure(sizeof(uint16_t) * 2 * (size_t)D);
+    if (e == hipSuccess) e = m->silu_c.ensure(sizeof(uint16_t) * (size_t)rows * D);
+    if (e == hipSuccess) e = m->mods.ensure(sizeof(uint16_t) * (size_t)w->n_blocks * rows * 6 * D);
+    if (e == hipSuccess) e = m->modf.ensure(sizeof(uint16_t) * (size_t)rows * 2 * D);
+    if (e == hipSuccess) e = m->y.ensure(sizeof(uint16_t) * (size_t)F * latent);
+    if (e == hipSuccess) e = m->s.alloc(2 * F, D, c->ff);
+    if (e == hipSuccess) e = hipMemsetAsync(m->zc.p, 0, m->zc.bytes, s);
+    if (e == hipSuccess)
+        e = flow_tables(s, w->t_mlp0, w->bt0, w->t_mlp2, w->bt2, D, m->t, m->dt, m->sq, u16(m->dtd.p), u16(m->sqd.p),
+                        u16(m->t_emb.p));
+    if (e != hipSuccess) {
+        ming_adaln_model_destroy(m);
+        return hip_check(ctx, e, "adaln_model_create");
+    }
+    if ((st = rotary_upload(ctx, w->inv_freq, half, F, static_cast<float*>(m->cos.p), static_cast<float*>(m->sin.p)))) {
+        ming_adaln_model_destroy(m);
+        return st;
+    }
+    *out = m;
+    return MING_OK;
+}
+
+int ming_adaln_model_destroy(ming_adaln_model* m) {
+    if (!m) return MING_E_NOT_INIT;
+    for (DevBuf* b : {&m->cos, &m->sin, &m->t_emb, &m->dtd, &m->sqd, &m->zc, &m->ce, &m->silu_c, &m->mods, &m->modf,
+                      &m->y})
+        b->release();
+    m->s.release();
+    delete m;
+    return MING_OK;
+}
+
+int ming_adaln_model_tables(ming_adaln_model* m, const void** t_emb_dev, const void** silu_c_dev, const void** mods_dev,
+                            const void** modf_dev) {
+    if (!m) return MING_E_NOT_INIT;
+    if (t_emb_dev) *t_emb_dev = m->t_emb.p;
+    if (silu_c_dev) *silu_c_dev = m->silu_c.p;
+    if (mods_dev) *mods_dev = m->mods.p;
+    if (modf_dev) *modf_dev = m->modf.p;
+    return MING_OK;
+}
+
+int ming_adaln_sample(ming_ctx* ctx, ming_adaln_model* m, const void* z, const void* noise, const void* sde, float cfg,
+                      float sigma, float temperature, void* patch_out, void* y_steps) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!m) return set_err(ctx, MING_E_NOT_INIT, "adaln_sample: null model");
+    const float shift = sigma * std::sqrt(temperature);
+    if (!z || !noise || !patch_out || (shift != 0.0f && !sde))
+        return set_err(ctx, MING_E_ARG, "adaln_sample: null buffer");
+    hipStream_t s = ctx->stream;
+    const int D = m->cfg.hidden, H = m->lm_hidden, lat = m->latent, F = m->frames, rows = 2 * kFlowSteps;
+    const size_t patch = (size_t)F * lat;
+    const float eps = m->cfg.eps;
+    // once per token: c_emb([z, 0]), silu(t_emb[s] + c_emb) of every step, and every modulation
+    hipError_t e = hipMemcpyAsync(m->zc.p, z, sizeof(uint16_t) * H, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess)
+        e = launch_dit_linear(s, u16(m->zc.p), 0, 1, 2, nullptr, eps, m->wc, D, H, m->bc, u16(m->ce.p), false);
+    if (e == hipSuccess) e = launch_adaln_cond(s, u16(m->t_emb.p), u16(m->ce.p), kFlowSteps, D, u16(m->silu_c.p));
+    for (size_t k = 0; k < m->blocks.size() && e == hipSuccess; k++)
+        e = launch_dit_linear(s, u16(m->silu_c.p), 0, 1, rows, nullptr, eps, m->ada[k], 6 * D, D, m->bada[k],
+                              u16(m->mods.p) + k * rows * 6 * D, false);
+    if (e == hipSuccess)
+        e = launch_dit_linear(s, u16(m->silu_c.p), 0, 1, rows, nullptr, eps, m->wfa, 2 * D, D, m->bfa, u16(m->modf.p),
+                              false);
+    if (e == hipSuccess) e = hipMemcpyAsync(m->y.p, noise, sizeof(uint16_t) * patch, hipMemcpyDeviceToDevice, s);
+    uint16_t* y = u16(m->y.p);
+    for (int i = 0; i < kFlowSteps && e == hipSuccess; i++) {
+        e = launch_adaln_rows(s, y, F, m->wx, m->bx, D, lat, u16(m->s.rows[0].p));
+        int cur = 0;
+        for (size_t k = 0; k < m->blocks.size() && e == hipSuccess; k++) {
+            const uint16_t* mk = u16(m->mods.p) + (k * rows + 2 * (size_t)i) * 6 * D;
+            e = launch_adaln_block(s, m->blocks[k], mk, u16(m->s.rows[cur].p), 2, F, static_cast<const float*>(m->cos.p),
+                                   static_cast<const float*>(m->sin.p), u16(m->s.qkv.p), u16(m->s.att.p),
+                                   u16(m->s.x1.p), u16(m->s.hh.p), u16(m->s.rows[cur ^ 1].p));
+            cur ^= 1;
+        }
+        if (e == hipSuccess)
+            e = launch_adaln_final(s, u16(m->s.rows[cur].p), F, D, m->final_norm, eps,
+                                   u16(m->modf.p) + (size_t)2 * i * 2 * D, m->wf, m->bf, lat, y, u16(m->dtd.p),
+                                   u16(m->sqd.p), u16(sde), i, cfg, shift, y);
+        if (e == hipSuccess && y_steps)
+            e = hipMemcpyAsync(u16(y_steps) + (size_t)i * patch, y, sizeof(uint16_t) * patch, hipMemcpyDeviceToDevice,
+                               s);
+    }
+    if (e == hipSuccess) e = hipMemcpyAsync(patch_out, y, sizeof(uint16_t) * patch, hipMemcpyDeviceToDevice, s);
+    return hip_check(ctx, e, "adaln_sample");
 }
 
 }  // extern "C"

@@ -26,7 +26,8 @@ namespace ming {
 
 namespace {
 
-constexpr int kMaxR = 6;  // activation rows
+constexpr int kMaxR = 6;       // activation rows of a reference-shape block (2 x 3)
+constexpr int kMaxSlots = 20;  // row slots of the widest launch (adaLN modulations: 10 steps x 2 halves)
 // 16-byte LDS vector (the staged rows are 16-byte aligned: K % 8 == 0)
 typedef uint32_t lds_u32x4_t __attribute__((ext_vector_type(4), aligned(16)));
 constexpr int kMaxL = 8;  // positions per sequence (attention)
@@ -40,9 +41,12 @@ enum DitEpi {
     E_CFMROWS = 5,  // x_emb(y) column n into the 6 CFM input rows (+ t_emb + c_emb, x_emb(hist))
     E_CFM = 6,      // CFG combine + Euler update of latent channel n (rows: cond, uncond)
     E_STOP = 7,     // softmax of the 2 stop logits (f32), probability of class 1
+    E_GATE = 8,     // out[r][n] = bf16(res + bf16(gate * bf16(acc + b))), adaLN gated residual
+    E_CFMF = 9,     // CFG + Euler of frame f = lane: rows f (cond) and F + f (uncond)
+    E_PATCH = 10,   // x_emb of frame r into rows r and R + r (both CFG halves)
 };
 
-enum StageMode { M_PLAIN = 0, M_NORM = 1 };
+enum StageMode { M_PLAIN = 0, M_NORM = 1, M_ADANORM = 2 };  // M_ADANORM: rms_norm, then modulate
 
 struct DitGemv {
     const uint16_t* x;  // input row r = x + (xrow0 + r * xstride) * K
@@ -55,7 +59,12 @@ struct DitGemv {
     const uint16_t* bias;  // [N]
     uint16_t* out;         // out[r * ostride + n] (layouts per epilogue)
     int64_t ostride;
-    const uint16_t* res;   // E_RES: res[r * ostride + n]
+    const uint16_t* res;   // E_RES, E_GATE: res[r * ostride + n]
+    // adaLN: modulation vectors of the CFG half of row r = mod + (r / rph) * mstride + {soff, coff, goff} * K|N
+    const uint16_t* mod;
+    int64_t mstride;
+    int rph, soff, coff, goff;
+    int F;                 // E_CFMF: frames per half
     // E_QKV: rows [0, D) of wq, then wk, then wv (N = 3*D)
     const uint16_t* w3[3];
     const uint16_t* b3[3];
@@ -95,17 +104,27 @@ __device__ __forceinline__ float gelu_chain(float x) {
 // branches, so the compiler issues every load, and later every LDS store,
 // back to back.  Threads whose chunk is past the row's end store nothing and
 // add nothing to the sums.
-template <bool NORM, int RC, int XCH, int T>
+template <int MODE, int RC, int XCH, int T>
 __device__ __forceinline__ void stage_rows(const DitGemv& a, uint32_t* xs, float* red, int t) {
+    constexpr bool NORM = MODE != M_PLAIN, ADA = MODE == M_ADANORM;
     const int K = a.K, NC = K / 8, K2 = K / 2, R = a.R;
     uint4 xr[RC][XCH];
     uint4 gn[XCH];
+    uint4 msh[2][XCH], msc[2][XCH];  // adaLN shift / scale chunks of the (at most 2) CFG halves
+    const int nh = ADA ? (R + a.rph - 1) / a.rph : 1;
 #pragma unroll
     for (int j = 0; j < XCH; j++) {
         const int c = min(t + T * j, NC - 1);
         if (NORM) gn[j] = ldg4(a.norm + 8 * c);
 #pragma unroll
         for (int r = 0; r < RC; r++) xr[r][j] = ldg4(a.x + (a.xrow0 + min(r, R - 1) * a.xstride) * K + 8 * c);
+        if (ADA)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint16_t* mh = a.mod + min(h, nh - 1) * a.mstride;
+                msh[h][j] = ldg4(mh + (size_t)a.soff * K + 8 * c);
+                msc[h][j] = ldg4(mh + (size_t)a.coff * K + 8 * c);
+            }
     }
     if (!NORM) {
 #pragma unroll
@@ -138,12 +157,12 @@ __device__ __forceinline__ void stage_rows(const DitGemv& a, uint32_t* xs, float
     const int wave = t / kWave, lane = t % kWave;
     if (lane == 0)
 #pragma unroll
-        for (int r = 0; r < RC; r++) red[wave * kMaxR + r] = ss[r];
+        for (int r = 0; r < RC; r++) red[wave * kMaxSlots + r] = ss[r];
     __syncthreads();
     // lane r of every wave finishes row r (waves summed in order), then broadcasts it
     float s = 0.0f;
 #pragma unroll
-    for (int w = 0; w < T / kWave; w++) s += red[w * kMaxR + min(lane, RC - 1)];
+    for (int w = 0; w < T / kWave; w++) s += red[w * kMaxSlots + min(lane, RC - 1)];
     const float my_inv = 1.0f / sqrtf(s / (float)K + a.eps);
     float inv[RC];
 #pragma unroll
@@ -157,9 +176,23 @@ __device__ __forceinline__ void stage_rows(const DitGemv& a, uint32_t* xs, float
         for (int r = 0; r < RC; r++) {
             const uint32_t q[4] = {xr[r][j].x, xr[r][j].y, xr[r][j].z, xr[r][j].w};
             uint32_t w4[4];
+            if (ADA) {
+                // modulate(n) = bf16(bf16(n * bf16(1 + scale)) + shift), half of the row's slot
+                const bool h1 = min(r, R - 1) / a.rph != 0;
+                const uint4 s4 = h1 ? msh[1][j] : msh[0][j], c4 = h1 ? msc[1][j] : msc[0][j];
+                const uint32_t sh[4] = {s4.x, s4.y, s4.z, s4.w}, sc[4] = {c4.x, c4.y, c4.z, c4.w};
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                w4[e] = pack_bf2(bf_lo(g[e]) * rb(bf_lo(q[e]) * inv[r]), bf_hi(g[e]) * rb(bf_hi(q[e]) * inv[r]));
+                for (int e = 0; e < 4; e++) {
+                    const float nl = rb(bf_lo(g[e]) * rb(bf_lo(q[e]) * inv[r]));
+                    const float nh2 = rb(bf_hi(g[e]) * rb(bf_hi(q[e]) * inv[r]));
+                    const float vl = rb(nl * rb(1.0f + bf_lo(sc[e]))), vh = rb(nh2 * rb(1.0f + bf_hi(sc[e])));
+                    w4[e] = pack_bf2(vl + bf_lo(sh[e]), vh + bf_hi(sh[e]));
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    w4[e] = pack_bf2(bf_lo(g[e]) * rb(bf_lo(q[e]) * inv[r]), bf_hi(g[e]) * rb(bf_hi(q[e]) * inv[r]));
+            }
             o[r] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
         }
         if (c < NC)
@@ -173,7 +206,8 @@ __device__ __forceinline__ void stage_rows(const DitGemv& a, uint32_t* xs, float
 // kernel start so that no load waits at the end.
 struct EpiIn {
     float b;        // bias
-    float res;      // E_RES: residual
+    float res;      // E_RES, E_GATE: residual
+    float gate;     // E_GATE
     float cs, sn;   // E_QKV: rotary
     float te0, te1, ce0, ce1;  // E_CFMROWS
     uint16_t xh;
@@ -192,7 +226,15 @@ __device__ __forceinline__ EpiIn epi_load(const DitGemv& a, int n, int nrow, int
     } else {
         p.b = bf2f(gld(a.bias + n));
     }
-    if (E == E_RES) p.res = bf2f(gld(a.res + rr * a.ostride + n));
+    if (E == E_RES || E == E_GATE) p.res = bf2f(gld(a.res + rr * a.ostride + n));
+    if (E == E_GATE) p.gate = bf2f(gld(a.mod + (rr / a.rph) * a.mstride + (size_t)a.goff * a.N + n));
+    if (E == E_CFMF) {
+        const int f = min(r, a.F - 1);
+        p.y = bf2f(gld(a.y + (size_t)f * a.N + n));
+        p.dt = bf2f(gld(a.dt + a.step));
+        p.sq = bf2f(gld(a.sq + a.step));
+        p.sde = a.shift != 0.0f ? bf2f(gld(a.sde + ((size_t)a.step * a.F + f) * a.N + n)) : 0.0f;
+    }
     if (E == E_CFMROWS) {
         p.te0 = bf2f(gld(a.te + n));
         p.te1 = bf2f(gld(a.te + a.N + n));
@@ -216,10 +258,10 @@ __device__ __forceinline__ EpiIn epi_load(const DitGemv& a, int n, int nrow, int
 template <int E, int MODE, int NCH, int W, int RC, int RPW>
 __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
     constexpr int T = 64 * W, TEAM = kWave / RPW, ROWS = RPW * W, XCH = (NCH * TEAM + T - 1) / T;
-    static_assert((E != E_QKV && E != E_STOP) || RPW == 2, "row pairs live in the two halves of a wave");
+    static_assert((E != E_QKV && E != E_STOP && E != E_CFMF) || RPW == 2, "per-row lanes live in a half wave");
     extern __shared__ uint32_t xs[];  // [R][K/2] bf16 pairs, natural order
-    __shared__ float red[W * kMaxR];
-    static_assert(RC <= kMaxR, "row slots");
+    __shared__ float red[W * kMaxSlots];
+    static_assert(RC <= kMaxSlots, "row slots");
     const int t = threadIdx.x, wave = t / kWave, lane = t % kWave, team = lane / TEAM, tl = lane % TEAM;
     const int K = a.K, R = a.R, NCk = K / 8, K2 = K / 2;
     const int n = blockIdx.x * ROWS + wave * RPW + team;
@@ -236,7 +278,7 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
 #pragma unroll
     for (int j = 0; j < NCH; j++) wr[j] = ldg4(wrow + 8 * min(tl + TEAM * j, NCk - 1));
     const EpiIn ep = epi_load<E>(a, nn, nrow, which, tl, Bv);
-    stage_rows<MODE == M_NORM, RC, XCH, T>(a, xs, red, t);
+    stage_rows<MODE, RC, XCH, T>(a, xs, red, t);
     __syncthreads();
     // dot products of this team's row with the RC staged row slots: no
     // branches, so all LDS reads issue ahead of the dot chains
@@ -297,6 +339,22 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
         gst(a.y_out + n, f2bf(y));
         return;
     }
+    if (E == E_CFMF) {
+        // lane tl < F: frame tl, rows tl (cond) and F + tl (uncond)
+        float vc = 0.0f, vu = 0.0f;
+#pragma unroll
+        for (int q = 0; q < RC; q++) {
+            if (tl == q) vc = acc[q];
+            if (tl + a.F == q) vu = acc[q];
+        }
+        if (tl >= a.F || n >= a.N) return;
+        const float pc = rb(vc + ep.b), pn = rb(vu + ep.b);
+        const float f0 = rb(pc + rb(rb(pc - pn) * rb(a.cfg)));
+        float y = rb(ep.y + rb(ep.dt * f0));
+        if (a.shift != 0.0f) y = rb(y + rb(rb(rb(a.shift) * ep.sq) * ep.sde));
+        gst(a.y_out + (size_t)tl * a.N + n, f2bf(y));
+        return;
+    }
     if (E == E_STOP) {
         // lane 0 holds logit 0 (bias 0), lane 32 logit 1 (bias 1)
         const float x = rb(v + ep.b);
@@ -312,6 +370,12 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
         gst(a.out + r * a.ostride + n, f2bf(e));
     } else if (E == E_RES) {
         gst(a.out + r * a.ostride + n, f2bf(ep.res + e));
+    } else if (E == E_GATE) {
+        gst(a.out + r * a.ostride + n, f2bf(ep.res + rb(ep.gate * e)));
+    } else if (E == E_PATCH) {
+        const uint16_t xe = f2bf(e);
+        gst(a.out + (size_t)r * a.N + n, xe);
+        gst(a.out + (size_t)(R + r) * a.N + n, xe);
     } else if (E == E_GELU) {
         gst(a.out + r * a.ostride + n, f2bf(gelu_chain(e)));
     } else if (E == E_SILU) {
@@ -326,6 +390,17 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
         gst(a.out + (size_t)4 * a.N + n, ep.xh);
         gst(a.out + (size_t)5 * a.N + n, xe);
     }
+}
+
+// adaLN conditions of every Euler step and CFG half: out [steps][2][D] =
+// silu(bf16(te[s][b] + ce[b])) with each op rounded (silu = x * sigmoid(x)).
+__global__ __launch_bounds__(256) void adaln_cond_kernel(const uint16_t* te, const uint16_t* ce, int steps, int D,
+                                                         uint16_t* out) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= steps * 2 * D) return;
+    const float v = rb(bf2f(gld(te + i)) + bf2f(gld(ce + i % (2 * D))));
+    const float sg = rb(1.0f / (1.0f + expf(-v)));
+    gst(out + i, f2bf(v * sg));
 }
 
 // Attention over the L positions of each sequence, one wave per (sequence,
@@ -386,22 +461,32 @@ hipError_t launch_wr(hipStream_t st, const DitGemv& a) {
     return hipGetLastError();
 }
 
-// Row slots: 1, 2 or 6 (3..6 rows run in 6 slots).  Long rows (K > 1024) get
-// a whole wave each, shorter ones a half wave.
+// Row slots.  Reference-shape stages: 1, 2 or 6 (3..6 rows run in 6 slots);
+// adaLN stages: 2 or 8; the modulation GEMV (bias epilogue, plain rows) also
+// 20.  Only the sets a stage uses are compiled.
+template <int E, int MODE, int W, int RPW>
+hipError_t launch_rc(hipStream_t st, const DitGemv& a) {
+    constexpr bool kAda = MODE == M_ADANORM || E == E_GATE || E == E_CFMF || E == E_PATCH;
+    if constexpr (kAda) {
+        if (a.R <= 2) return launch_wr<E, MODE, W, 2, RPW>(st, a);
+        return launch_wr<E, MODE, W, 8, RPW>(st, a);
+    } else {
+        if (E == E_CFM) return launch_wr<E, MODE, W, 2, RPW>(st, a);
+        if (a.R == 1) return launch_wr<E, MODE, W, 1, RPW>(st, a);
+        if (a.R == 2) return launch_wr<E, MODE, W, 2, RPW>(st, a);
+        if constexpr (E == E_BIAS && MODE == M_PLAIN)
+            if (a.R > kMaxR) return launch_wr<E, MODE, W, kMaxSlots, RPW>(st, a);
+        return launch_wr<E, MODE, W, kMaxR, RPW>(st, a);
+    }
+}
+
+// Long rows (K > 1024) get a whole wave each, shorter ones a half wave.
 template <int E, int MODE, int W>
 hipError_t launch_w(hipStream_t st, const DitGemv& a) {
-    constexpr bool kPairs = E == E_QKV || E == E_STOP;
-    if constexpr (!kPairs) {
-        if (a.K > 1024) {
-            if (a.R == 1) return launch_wr<E, MODE, W, 1, 1>(st, a);
-            if (a.R == 2 || E == E_CFM) return launch_wr<E, MODE, W, 2, 1>(st, a);
-            return launch_wr<E, MODE, W, kMaxR, 1>(st, a);
-        }
-    }
-    if (E == E_CFM) return launch_wr<E, MODE, W, 2, 2>(st, a);
-    if (a.R == 1) return launch_wr<E, MODE, W, 1, 2>(st, a);
-    if (a.R == 2) return launch_wr<E, MODE, W, 2, 2>(st, a);
-    return launch_wr<E, MODE, W, kMaxR, 2>(st, a);
+    constexpr bool kPairs = E == E_QKV || E == E_STOP || E == E_CFMF;
+    if constexpr (!kPairs)
+        if (a.K > 1024) return launch_rc<E, MODE, W, 1>(st, a);
+    return launch_rc<E, MODE, W, 2>(st, a);
 }
 
 // Four-wave workgroups when that still gives >= 256 of them (one per CU),
@@ -409,7 +494,7 @@ hipError_t launch_w(hipStream_t st, const DitGemv& a) {
 // 4 waves of one row each).
 template <int E, int MODE>
 hipError_t launch_gemv(hipStream_t st, const DitGemv& a) {
-    constexpr bool kPairs = E == E_QKV || E == E_STOP;
+    constexpr bool kPairs = E == E_QKV || E == E_STOP || E == E_CFMF;
     if (!kPairs && a.K > 1024) return launch_w<E, MODE, 4>(st, a);
     return (a.N + 7) / 8 >= 256 ? launch_w<E, MODE, 4>(st, a) : launch_w<E, MODE, 2>(st, a);
 }
@@ -535,6 +620,125 @@ hipError_t launch_cfm_final(hipStream_t st, const uint16_t* h, int L, int D, con
     a.shift = shift;
     a.y_out = y_out;
     return launch_gemv<E_CFM, M_NORM>(st, a);
+}
+
+// ---- adaLN flow head (config 4) -----------------------------------------------------
+
+// One stage of an adaLN block on x [R][D] (R = B*L, half b = rows [bL, bL + L)),
+// mod [B][6D] = [shift_a, scale_a, gate_a, shift_m, scale_m, gate_m] per half:
+//   0  modulate(rms1(x)) -> q/k/v + rotary -> qkv, attention -> out
+//   1  out = bf16(x + bf16(gate_a * out_proj(in)))
+//   2  out = gelu(ff1(modulate(rms2(x))))
+//   3  out = bf16(x + bf16(gate_m * ff2(in)))
+hipError_t launch_adaln_stage(hipStream_t st, int which, const DitBlockDev& w, const uint16_t* mod, const uint16_t* x,
+                              const uint16_t* in, int B, int L, const float* cos_t, const float* sin_t, uint16_t* qkv,
+                              uint16_t* out) {
+    const int R = B * L, D = w.D, F = w.F;
+    DitGemv a;
+    switch (which) {
+        case 0:
+            a = gemv_args(x, R, nullptr, 3 * D, D, nullptr, qkv);
+            a.w3[0] = w.wq;
+            a.w3[1] = w.wk;
+            a.w3[2] = w.wv;
+            a.b3[0] = w.bq;
+            a.b3[1] = w.bk;
+            a.b3[2] = w.bv;
+            a.norm = w.norm1;
+            a.eps = w.eps;
+            a.cos_t = cos_t;
+            a.sin_t = sin_t;
+            a.L = L;
+            a.D = D;
+            a.hd = w.hd;
+            a.soff = 0;
+            a.coff = 1;
+            break;
+        case 1:
+            a = gemv_args(in, R, w.wo, D, D, w.bo, out);
+            a.res = x;
+            a.goff = 2;
+            break;
+        case 2:
+            a = gemv_args(x, R, w.w1, F, D, w.b1, out);
+            a.norm = w.norm2;
+            a.eps = w.eps;
+            a.soff = 3;
+            a.coff = 4;
+            break;
+        default:
+            a = gemv_args(in, R, w.w2, D, F, w.b2, out);
+            a.res = x;
+            a.goff = 5;
+            break;
+    }
+    a.mod = mod;
+    a.mstride = 6 * (int64_t)D;
+    a.rph = L;
+    switch (which) {
+        case 0: {
+            hipError_t e = launch_gemv<E_QKV, M_ADANORM>(st, a);
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL(dit_attn_kernel, dim3(B * w.heads), dim3(kWave), 0, st, qkv, R, L, D, w.heads, w.hd,
+                               out);
+            return hipGetLastError();
+        }
+        case 1:
+            return launch_gemv<E_GATE, M_PLAIN>(st, a);
+        case 2:
+            return launch_gemv<E_GELU, M_ADANORM>(st, a);
+        default:
+            return launch_gemv<E_GATE, M_PLAIN>(st, a);
+    }
+}
+
+hipError_t launch_adaln_block(hipStream_t st, const DitBlockDev& w, const uint16_t* mod, const uint16_t* x, int B,
+                              int L, const float* cos_t, const float* sin_t, uint16_t* qkv, uint16_t* att, uint16_t* x1,
+                              uint16_t* hh, uint16_t* x2) {
+    hipError_t e;
+    if ((e = launch_adaln_stage(st, 0, w, mod, x, nullptr, B, L, cos_t, sin_t, qkv, att)) != hipSuccess) return e;
+    if ((e = launch_adaln_stage(st, 1, w, mod, x, att, B, L, cos_t, sin_t, qkv, x1)) != hipSuccess) return e;
+    if ((e = launch_adaln_stage(st, 2, w, mod, x1, nullptr, B, L, cos_t, sin_t, qkv, hh)) != hipSuccess) return e;
+    return launch_adaln_stage(st, 3, w, mod, x1, hh, B, L, cos_t, sin_t, qkv, x2);
+}
+
+hipError_t launch_adaln_cond(hipStream_t st, const uint16_t* te, const uint16_t* ce, int steps, int D, uint16_t* out) {
+    const int n = steps * 2 * D;
+    hipLaunchKernelGGL(adaln_cond_kernel, dim3((n + 255) / 256), dim3(256), 0, st, te, ce, steps, D, out);
+    return hipGetLastError();
+}
+
+// Input rows of a patch: rows [2][F][D] = x_emb(y_f) for both halves; y [F][latent].
+hipError_t launch_adaln_rows(hipStream_t st, const uint16_t* y, int F, const uint16_t* wx, const uint16_t* bx, int D,
+                             int latent, uint16_t* rows) {
+    DitGemv a = gemv_args(y, F, wx, D, latent, bx, rows);
+    return launch_gemv<E_PATCH, M_PLAIN>(st, a);
+}
+
+// Final adaLN layer on h [2F][D]: modulate(rms(h)) with mod [2][2D] = [shift | scale]
+// per half, linear to the latent, CFG + Euler (+ SDE) per frame: y [F][latent] -> y_out.
+hipError_t launch_adaln_final(hipStream_t st, const uint16_t* h, int F, int D, const uint16_t* norm, float eps,
+                              const uint16_t* mod, const uint16_t* wf, const uint16_t* bf, int latent, const uint16_t* y,
+                              const uint16_t* dt, const uint16_t* sq, const uint16_t* sde, int step, float cfg,
+                              float shift, uint16_t* y_out) {
+    DitGemv a = gemv_args(h, 2 * F, wf, latent, D, bf, nullptr);
+    a.norm = norm;
+    a.eps = eps;
+    a.mod = mod;
+    a.mstride = 2 * (int64_t)D;
+    a.rph = F;
+    a.soff = 0;
+    a.coff = 1;
+    a.F = F;
+    a.y = y;
+    a.dt = dt;
+    a.sq = sq;
+    a.sde = sde;
+    a.step = step;
+    a.cfg = cfg;
+    a.shift = shift;
+    a.y_out = y_out;
+    return launch_gemv<E_CFMF, M_ADANORM>(st, a);
 }
 
 // stopProb: p = softmax(f32(bf16(W z + b)))[1] (W [2][K]).

@@ -347,5 +347,125 @@ class SyntheticFlow:
         return AggModel(self.ctx, self.agg_w)
 
 
-__all__ = ["DitSpec", "MING_DIT", "SyntheticFlow", "LmSpec", "QWEN2_05B", "SyntheticLm", "KvCache", "lm_bytes_per_token", "W_AFFINE", "W_BF16",
+@dataclass
+class AdalnSpec(DitSpec):
+    """Config 4's adaLN flow head: 4 blocks, hidden 896, 14 heads x 64, ff 4 x 896,
+    a patch of 4 frames x 64 (no reference shape; DiT-style adaLN-Zero)."""
+    hidden: int = 896
+    heads: int = 14
+    ff: int = 3584
+    cfm_blocks: int = 4
+    frames: int = 4
+
+    def ada_params(self):
+        return 6 * self.hidden * self.hidden + 6 * self.hidden
+
+    def sample_weight_bytes(self):
+        """bf16 bytes one sample reads: the modulation linears once, then per Euler
+        step the blocks, x_emb and the final linear; c_emb once."""
+        D, H, lat = self.hidden, self.lm_hidden, self.latent
+        once = self.cfm_blocks * self.ada_params() + 2 * D * D + 2 * D + D * H + D
+        per_step = self.cfm_blocks * self.block_params() + D * lat + D + lat * D + lat + D
+        return 2 * (once + 10 * per_step)
+
+
+MING_ADALN = AdalnSpec()
+
+
+class SyntheticAdaln:
+    """bf16 weights of config 4's adaLN flow head (DiT-style key names under
+    "adaln": blocks.{i}.{attn,mlp,norm*,adaLN_modulation.1}, t_embedder,
+    x_embedder, c_embedder, final_layer.{norm_final, linear, adaLN_modulation.1}),
+    random-init N(0, std); norms 1 + N(0, norm_std).  ada_std scales the
+    modulation linears (0 with bias_pattern "zero" gives shift = scale = 0,
+    gate = 1: the reference block)."""
+
+    def __init__(self, ctx, spec: AdalnSpec = MING_ADALN, seed=0, std=0.02, norm_std=0.0, ada_std=None,
+                 zero_modulation=False, device="cuda", threads=None):
+        import torch
+
+        from . import AdalnBlockW, AdalnW
+
+        self.ctx, self.spec, self.device = ctx, spec, device
+        self.hostw, self.dev = {}, {}
+        D, F, lat, H = spec.hidden, spec.ff, spec.latent, spec.lm_hidden
+        ada_std = std if ada_std is None else ada_std
+
+        def store(name, a):
+            self.hostw[name] = a
+            self.dev[name] = torch.from_numpy(a.view(np.int16)).to(device).view(torch.bfloat16)
+
+        def put(name, shape, mean=0.0, sd=std):
+            store(name, synth_normal_bf16(seed, name, int(np.prod(shape)), mean, sd, threads).reshape(shape))
+
+        def lin(name, N, K, bias=True, sd=std):
+            put(name + ".weight", (N, K), 0.0, sd)
+            if bias:
+                put(name + ".bias", (N,), 0.0, sd)
+
+        def norm(name, n):
+            if norm_std == 0.0:
+                store(name, np.full(n, 0x3F80, np.uint16))
+            else:
+                put(name, (n,), 1.0, norm_std)
+
+        def zero_ada(name, chunks, gates):
+            store(name + ".weight", np.zeros((chunks * D, D), np.uint16))
+            b = np.zeros(chunks * D, np.uint16)
+            for g in gates:
+                b[g * D:(g + 1) * D] = 0x3F80  # 1.0
+            store(name + ".bias", b)
+
+        A = "adaln"
+        for i in range(spec.cfm_blocks):
+            b = f"{A}.blocks.{i}"
+            norm(f"{b}.norm1.weight", D)
+            norm(f"{b}.norm2.weight", D)
+            for k, key in _BLOCK_KEYS:
+                N, K = {"w1": (F, D), "w2": (D, F)}.get(k, (D, D))
+                lin(f"{b}.{key}", N, K)
+            if zero_modulation:
+                zero_ada(f"{b}.adaLN_modulation.1", 6, (2, 5))
+            else:
+                lin(f"{b}.adaLN_modulation.1", 6 * D, D, sd=ada_std)
+        lin(f"{A}.t_embedder.time_mlp.0", D, 256)
+        lin(f"{A}.t_embedder.time_mlp.2", D, D)
+        lin(f"{A}.x_embedder", D, lat)
+        lin(f"{A}.c_embedder", D, H)
+        norm(f"{A}.final_layer.norm_final.weight", D)
+        lin(f"{A}.final_layer.linear", lat, D)
+        if zero_modulation:
+            zero_ada(f"{A}.final_layer.adaLN_modulation.1", 2, ())
+        else:
+            lin(f"{A}.final_layer.adaLN_modulation.1", 2 * D, D, sd=ada_std)
+        self.inv_freq = spec.inv_freq()
+        self.blocks = (AdalnBlockW * spec.cfm_blocks)(*(self.block_w(i) for i in range(spec.cfm_blocks)))
+        lw = lambda n: linear(self.dev[n + ".weight"])
+        pt = lambda n: self.dev[n].data_ptr()
+        self.w = AdalnW(spec.cfg(), spec.cfm_blocks, spec.frames, ctypes.cast(self.blocks, ctypes.c_void_p),
+                        self.inv_freq.ctypes.data, lw(f"{A}.x_embedder"), lw(f"{A}.c_embedder"),
+                        lw(f"{A}.t_embedder.time_mlp.0"), lw(f"{A}.t_embedder.time_mlp.2"),
+                        lw(f"{A}.final_layer.linear"), lw(f"{A}.final_layer.adaLN_modulation.1"),
+                        pt(f"{A}.x_embedder.bias"), pt(f"{A}.c_embedder.bias"), pt(f"{A}.t_embedder.time_mlp.0.bias"),
+                        pt(f"{A}.t_embedder.time_mlp.2.bias"), pt(f"{A}.final_layer.norm_final.weight"),
+                        pt(f"{A}.final_layer.linear.bias"), pt(f"{A}.final_layer.adaLN_modulation.1.bias"))
+
+    def block_w(self, i):
+        from . import AdalnBlockW, DitBlockW
+
+        b = f"adaln.blocks.{i}"
+        p = lambda n: self.dev[n].data_ptr()
+        base = DitBlockW(p(f"{b}.norm1.weight"), p(f"{b}.norm2.weight"),
+                         *(linear(self.dev[f"{b}.{key}.weight"]) for _, key in _BLOCK_KEYS),
+                         *(p(f"{b}.{key}.bias") for _, key in _BLOCK_KEYS))
+        return AdalnBlockW(base, linear(self.dev[f"{b}.adaLN_modulation.1.weight"]),
+                           p(f"{b}.adaLN_modulation.1.bias"))
+
+    def model(self):
+        from . import AdalnModel
+
+        return AdalnModel(self.ctx, self.w)
+
+
+__all__ = ["AdalnSpec", "MING_ADALN", "SyntheticAdaln", "DitSpec", "MING_DIT", "SyntheticFlow", "LmSpec", "QWEN2_05B", "SyntheticLm", "KvCache", "lm_bytes_per_token", "W_AFFINE", "W_BF16",
            "Linear", "math"]

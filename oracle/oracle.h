@@ -213,6 +213,60 @@ void or_aggregate(const or_agg_model* m, const uint16_t* latent, uint16_t* out);
 /* softmax(f32(stop_head(z)))[1]. */
 float or_stop_prob(const or_linear* head, const uint16_t* bias, const uint16_t* z);
 
+/* ---- adaLN DiT flow head (config 4) -----------------------------------------
+ * No reference implementation exists; this build defines it as the standard
+ * adaLN-Zero DiT (Peebles & Xie) on the reference block's RMSNorm.  Per CFG half
+ * b (uncond: z = 0) and Euler step s: c = bf16(t_emb[s] + c_emb(z)); silu(c)
+ * with each op rounded; per block mod = bf16(addmm(b_ada, silu(c), W_ada^T)) =
+ * [shift_a | scale_a | gate_a | shift_m | scale_m | gate_m] (6 x D);
+ * modulate(n) = bf16(bf16(n * bf16(1 + scale)) + shift) on the rms_norm output;
+ * x1 = bf16(x + bf16(gate_a * out_proj(...))), x2 likewise with gate_m.  The
+ * sequence is the F patch frames x_emb(y_f) per half (rotary positions 0..F-1);
+ * the final layer is modulate(rms(h)) with [shift | scale] = addmm(b_fa,
+ * silu(c), W_fa^T), a linear to the latent, and CFG + Euler (+ SDE) per frame.
+ * With shift = scale = 0 and gate = 1 a block is the reference block. */
+void or_adaln_block_fwd(const or_dit_cfg* c, const or_dit_block* b, const uint16_t* mod, const uint16_t* x, int B,
+                        int L, const float* cos_t, const float* sin_t, uint16_t* out, or_dit_trace* tr);
+
+typedef struct {
+    or_dit_block blk;
+    or_linear ada;                   /* D -> 6D */
+    const uint16_t* bada;
+} or_adaln_block;
+
+typedef struct {
+    or_dit_cfg c;
+    int n_blocks;
+    const or_adaln_block* blocks;
+    or_linear x_emb;                 /* latent -> D */
+    const uint16_t* bx;
+    or_linear c_emb;                 /* LM hidden -> D */
+    const uint16_t* bc;
+    const uint16_t* final_norm;      /* [D] */
+    or_linear final;                 /* D -> latent */
+    const uint16_t* bf;
+    or_linear final_ada;             /* D -> 2D */
+    const uint16_t* bfa;
+    const uint16_t* t_emb;           /* [steps][2][D] */
+    const uint16_t* dt;              /* [steps] */
+    const uint16_t* sq;              /* [steps] */
+    const float *cos_t, *sin_t;      /* rotary tables for L = frames */
+    int steps, frames;
+} or_adaln_model;
+
+/* silu(c) rows [steps][2][D] for LM hidden z. */
+void or_adaln_cond(const or_adaln_model* m, const uint16_t* z, uint16_t* silu_c);
+/* Modulations of every step and half: mods [n_blocks][steps*2][6D], modf [steps*2][2D]. */
+void or_adaln_mods(const or_adaln_model* m, const uint16_t* silu_c, uint16_t* mods, uint16_t* modf);
+/* Input rows [2][F][D] = x_emb(y_f) for both halves; y [F][latent]. */
+void or_adaln_rows(const or_adaln_model* m, const uint16_t* y, uint16_t* rows);
+/* Final adaLN layer on h [2F][D] with modf_step [2][2D], CFG + Euler of step: y [F][latent] -> y_out. */
+void or_adaln_final(const or_adaln_model* m, const uint16_t* h, const uint16_t* modf_step, const uint16_t* y,
+                    const uint16_t* sde, int step, float cfg, float shift_k, uint16_t* y_out);
+/* The whole sample: noise [F][latent], sde [steps][F][latent] -> out [F][latent]. */
+void or_adaln_sample(const or_adaln_model* m, const uint16_t* z, const uint16_t* noise, const uint16_t* sde,
+                     float cfg, float shift_k, uint16_t* out, uint16_t* y_steps);
+
 /* ---- CPU threads ---------------------------------------------------------- */
 void or_set_threads(int n);
 int or_get_threads(void);

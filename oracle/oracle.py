@@ -61,6 +61,18 @@ class OrCfmModel(ctypes.Structure):
                 ("sin_t", c_void_p), ("steps", c_int)]
 
 
+class OrAdalnBlock(ctypes.Structure):
+    _fields_ = [("blk", OrDitBlock), ("ada", OrLinear), ("bada", c_void_p)]
+
+
+class OrAdalnModel(ctypes.Structure):
+    _fields_ = [("c", OrDitCfg), ("n_blocks", c_int), ("blocks", c_void_p), ("x_emb", OrLinear), ("bx", c_void_p),
+                ("c_emb", OrLinear), ("bc", c_void_p), ("final_norm", c_void_p), ("final", OrLinear),
+                ("bf", c_void_p), ("final_ada", OrLinear), ("bfa", c_void_p), ("t_emb", c_void_p),
+                ("dt", c_void_p), ("sq", c_void_p), ("cos_t", c_void_p), ("sin_t", c_void_p), ("steps", c_int),
+                ("frames", c_int)]
+
+
 class OrAggModel(ctypes.Structure):
     _fields_ = [("c", OrDitCfg), ("n_blocks", c_int), ("blocks", c_void_p), ("x_emb", OrLinear), ("bx", c_void_p),
                 ("cls", c_void_p), ("final_norm", c_void_p), ("final", OrLinear), ("bf", c_void_p),
@@ -113,6 +125,15 @@ def lib():
                                  c_void_p]),
         "or_aggregate": (None, [P(OrAggModel), c_void_p, c_void_p]),
         "or_stop_prob": (c_f32, [P(OrLinear), c_void_p, c_void_p]),
+        "or_adaln_block_fwd": (None, [P(OrDitCfg), P(OrDitBlock), c_void_p, c_void_p, c_int, c_int, c_void_p,
+                                      c_void_p, c_void_p, P(OrDitTrace)]),
+        "or_adaln_cond": (None, [P(OrAdalnModel), c_void_p, c_void_p]),
+        "or_adaln_mods": (None, [P(OrAdalnModel), c_void_p, c_void_p, c_void_p]),
+        "or_adaln_rows": (None, [P(OrAdalnModel), c_void_p, c_void_p]),
+        "or_adaln_final": (None, [P(OrAdalnModel), c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_f32, c_f32,
+                                  c_void_p]),
+        "or_adaln_sample": (None, [P(OrAdalnModel), c_void_p, c_void_p, c_void_p, c_f32, c_f32, c_void_p,
+                                   c_void_p]),
         "or_set_threads": (None, [c_int]),
         "or_get_threads": (c_int, []),
     }
@@ -449,3 +470,78 @@ def aggregate(m, latent):
 
 def stop_prob(head, bias, z):
     return float(lib().or_stop_prob(ctypes.byref(head.c), _p(_c(bias, np.uint16)), _p(_c(z, np.uint16))))
+
+
+# ---- adaLN flow head (config 4) ---------------------------------------------------------
+
+def adaln_block_fwd(c, blk, mod, x, B, L, cos_t, sin_t, trace=False):
+    """blk: DitBlock; mod [B][6D] bf16 modulation (shift_a, scale_a, gate_a, shift_m, scale_m, gate_m)."""
+    x = _c(x, np.uint16)
+    R, D = B * L, c.D
+    out = np.empty((R, D), np.uint16)
+    tr, arrs = None, {}
+    if trace:
+        arrs = dict(qkv=np.empty((3, R, D), np.uint16), att=np.empty((R, D), np.uint16),
+                    x1=np.empty((R, D), np.uint16), hh=np.empty((R, c.ff), np.uint16))
+        tr = OrDitTrace(*(_p(arrs[k]) for k in ("qkv", "att", "x1", "hh")))
+    lib().or_adaln_block_fwd(ctypes.byref(c), ctypes.byref(blk.c), _p(_c(mod, np.uint16)), _p(x), B, L,
+                             _p(_c(cos_t, np.float32)), _p(_c(sin_t, np.float32)), _p(out),
+                             ctypes.byref(tr) if tr is not None else None)
+    return (out, arrs) if trace else out
+
+
+class AdalnModel:
+    """The adaLN flow head for the oracle: blocks (list of (DitBlock, ada Linear, bada)), embedders, final
+    layer with its adaLN linear, t_emb [steps][2][D], schedule, rotary tables for L = frames."""
+
+    def __init__(self, c, blocks, x_emb, bx, c_emb, bc, final_norm, final, bf, final_ada, bfa, t_emb, dt, sq,
+                 cos_t, sin_t, frames):
+        self.keep = dict(bx=_c(bx, np.uint16), bc=_c(bc, np.uint16), fn=_c(final_norm, np.uint16),
+                         bf=_c(bf, np.uint16), bfa=_c(bfa, np.uint16), te=_c(t_emb, np.uint16),
+                         dt=_c(dt, np.uint16), sq=_c(sq, np.uint16), cos=_c(cos_t, np.float32),
+                         sin=_c(sin_t, np.float32), bada=[_c(b[2], np.uint16) for b in blocks])
+        self.blocks = blocks
+        self.barr = (OrAdalnBlock * len(blocks))(*(OrAdalnBlock(b[0].c, b[1].c, _p(self.keep["bada"][i]))
+                                                  for i, b in enumerate(blocks)))
+        self.lins = (x_emb, c_emb, final, final_ada)
+        k = self.keep
+        self.c = OrAdalnModel(c, len(blocks), ctypes.cast(self.barr, c_void_p), x_emb.c, _p(k["bx"]), c_emb.c,
+                              _p(k["bc"]), _p(k["fn"]), final.c, _p(k["bf"]), final_ada.c, _p(k["bfa"]), _p(k["te"]),
+                              _p(k["dt"]), _p(k["sq"]), _p(k["cos"]), _p(k["sin"]), int(k["dt"].size), int(frames))
+        self.frames, self.latent, self.D = int(frames), final.N, c.D
+
+
+def adaln_cond(m, z):
+    out = np.empty((m.c.steps, 2, m.D), np.uint16)
+    lib().or_adaln_cond(ctypes.byref(m.c), _p(_c(z, np.uint16)), _p(out))
+    return out
+
+
+def adaln_mods(m, silu_c):
+    rows = 2 * m.c.steps
+    mods = np.empty((len(m.blocks), rows, 6 * m.D), np.uint16)
+    modf = np.empty((rows, 2 * m.D), np.uint16)
+    lib().or_adaln_mods(ctypes.byref(m.c), _p(_c(silu_c, np.uint16)), _p(mods), _p(modf))
+    return mods, modf
+
+
+def adaln_rows(m, y):
+    rows = np.empty((2 * m.frames, m.D), np.uint16)
+    lib().or_adaln_rows(ctypes.byref(m.c), _p(_c(y, np.uint16)), _p(rows))
+    return rows
+
+
+def adaln_final(m, h, modf_step, y, sde, step, cfg, shift):
+    out = np.empty((m.frames, m.latent), np.uint16)
+    lib().or_adaln_final(ctypes.byref(m.c), _p(_c(h, np.uint16)), _p(_c(modf_step, np.uint16)), _p(_c(y, np.uint16)),
+                         _p(None if sde is None else _c(sde, np.uint16)), int(step), float(cfg), float(shift), _p(out))
+    return out
+
+
+def adaln_sample(m, z, noise, sde, cfg, shift):
+    out = np.empty((m.frames, m.latent), np.uint16)
+    steps = np.empty((m.c.steps, m.frames, m.latent), np.uint16)
+    lib().or_adaln_sample(ctypes.byref(m.c), _p(_c(z, np.uint16)), _p(_c(noise, np.uint16)),
+                          _p(None if sde is None else _c(sde, np.uint16)), float(cfg), float(shift), _p(out),
+                          _p(steps))
+    return out, steps

@@ -82,8 +82,35 @@ static void sdpa_small(const uint16_t* q, const uint16_t* k, const uint16_t* v, 
             }
 }
 
-void or_dit_block_fwd(const or_dit_cfg* c, const or_dit_block* b, const uint16_t* x, int B, int L,
-                      const float* cos_t, const float* sin_t, uint16_t* out, or_dit_trace* tr) {
+/* adaLN modulation of rows h [R][D] in place: half = r / L selects mod + half * 6D;
+ * h = bf16(bf16(h * bf16(1 + scale)) + shift), each op a materialised bf16 array. */
+static void modulate(uint16_t* h, int R, int L, int D, const uint16_t* mod, int mstride, int soff, int coff) {
+    for (int r = 0; r < R; r++) {
+        const uint16_t* sh = mod + (size_t)(r / L) * mstride + (size_t)soff * D;
+        const uint16_t* sc = mod + (size_t)(r / L) * mstride + (size_t)coff * D;
+        for (int i = 0; i < D; i++) {
+            const float t1 = or_rb(1.0f + or_f32(sc[i]));
+            const float v = or_rb(or_f32(h[(size_t)r * D + i]) * t1);
+            h[(size_t)r * D + i] = or_bf16(v + or_f32(sh[i]));
+        }
+    }
+}
+
+/* Gated residual: out = bf16(x + bf16(gate * a)), gate from the row's half. */
+static void gated_add(const uint16_t* x, const uint16_t* a, int R, int L, int D, const uint16_t* mod, int mstride,
+                      int goff, uint16_t* out) {
+    for (int r = 0; r < R; r++) {
+        const uint16_t* g = mod + (size_t)(r / L) * mstride + (size_t)goff * D;
+        for (int i = 0; i < D; i++) {
+            const size_t k = (size_t)r * D + i;
+            out[k] = or_bf16(or_f32(x[k]) + or_rb(or_f32(g[i]) * or_f32(a[k])));
+        }
+    }
+}
+
+/* One block; mod (optional) [B][6D] = per half [shift_a, scale_a, gate_a, shift_m, scale_m, gate_m]. */
+static void block_fwd(const or_dit_cfg* c, const or_dit_block* b, const uint16_t* mod, const uint16_t* x, int B,
+                      int L, const float* cos_t, const float* sin_t, uint16_t* out, or_dit_trace* tr) {
     const int R = B * L, D = c->D, F = c->ff;
     uint16_t* h = malloc(sizeof(uint16_t) * (size_t)R * D);
     uint16_t* qkv = malloc(sizeof(uint16_t) * (size_t)3 * R * D);
@@ -93,6 +120,7 @@ void or_dit_block_fwd(const or_dit_cfg* c, const or_dit_block* b, const uint16_t
     uint16_t* f1 = malloc(sizeof(uint16_t) * (size_t)R * F);
     uint16_t* hh = malloc(sizeof(uint16_t) * (size_t)R * F);
     or_rms_norm(x, b->norm1, R, D, c->eps, h);
+    if (mod) modulate(h, R, L, D, mod, 6 * D, 0, 1);
     or_linear_fwd(&b->q, h, R, b->bq, qkv);
     or_linear_fwd(&b->k, h, R, b->bk, qkv + (size_t)R * D);
     or_linear_fwd(&b->v, h, R, b->bv, qkv + (size_t)2 * R * D);
@@ -100,12 +128,19 @@ void or_dit_block_fwd(const or_dit_cfg* c, const or_dit_block* b, const uint16_t
     or_rotary(qkv + (size_t)R * D, R, L, c->heads, c->head_dim, cos_t, sin_t);
     sdpa_small(qkv, qkv + (size_t)R * D, qkv + (size_t)2 * R * D, B, L, c->heads, c->head_dim, 1.0f / 8.0f, att);
     or_linear_fwd(&b->o, att, R, b->bo, t1);
-    or_add(x, t1, (int64_t)R * D, x1);
+    if (mod)
+        gated_add(x, t1, R, L, D, mod, 6 * D, 2, x1);
+    else
+        or_add(x, t1, (int64_t)R * D, x1);
     or_rms_norm(x1, b->norm2, R, D, c->eps, h);
+    if (mod) modulate(h, R, L, D, mod, 6 * D, 3, 4);
     or_linear_fwd(&b->ff1, h, R, b->b1, f1);
     or_gelu_approx(f1, (int64_t)R * F, hh);
     or_linear_fwd(&b->ff2, hh, R, b->b2, t1);
-    or_add(x1, t1, (int64_t)R * D, out);
+    if (mod)
+        gated_add(x1, t1, R, L, D, mod, 6 * D, 5, out);
+    else
+        or_add(x1, t1, (int64_t)R * D, out);
     if (tr) {
         if (tr->qkv) memcpy(tr->qkv, qkv, sizeof(uint16_t) * (size_t)3 * R * D);
         if (tr->att) memcpy(tr->att, att, sizeof(uint16_t) * (size_t)R * D);
@@ -119,6 +154,16 @@ void or_dit_block_fwd(const or_dit_cfg* c, const or_dit_block* b, const uint16_t
     free(x1);
     free(f1);
     free(hh);
+}
+
+void or_dit_block_fwd(const or_dit_cfg* c, const or_dit_block* b, const uint16_t* x, int B, int L,
+                      const float* cos_t, const float* sin_t, uint16_t* out, or_dit_trace* tr) {
+    block_fwd(c, b, NULL, x, B, L, cos_t, sin_t, out, tr);
+}
+
+void or_adaln_block_fwd(const or_dit_cfg* c, const or_dit_block* b, const uint16_t* mod, const uint16_t* x, int B,
+                        int L, const float* cos_t, const float* sin_t, uint16_t* out, or_dit_trace* tr) {
+    block_fwd(c, b, mod, x, B, L, cos_t, sin_t, out, tr);
 }
 
 /* flowSchedule (:1207-1215) in bf16: t = (1/32) * sched; t = t + (-1) * (cos(pi/2 * t) - 1 + t). */
@@ -277,4 +322,101 @@ float or_stop_prob(const or_linear* head, const uint16_t* bias, const uint16_t* 
     const float mx = fmaxf(l0, l1);
     const float e0 = expf(l0 - mx), e1 = expf(l1 - mx);
     return e1 / (e0 + e1);
+}
+
+/* ---- adaLN flow head (config 4; the build's definition, see oracle.h) ---------------- */
+
+static void silu_rows(const uint16_t* c, int64_t n, uint16_t* out) {
+    for (int64_t i = 0; i < n; i++) {  /* silu: x * sigmoid(x), each op rounded (as the timestep MLP) */
+        const float v = or_f32(c[i]);
+        const float sg = or_rb(1.0f / (1.0f + expf(-v)));
+        out[i] = or_bf16(v * sg);
+    }
+}
+
+void or_adaln_cond(const or_adaln_model* m, const uint16_t* z, uint16_t* silu_c) {
+    const int D = m->c.D;
+    const int64_t H = m->c_emb.K;
+    uint16_t* zc = calloc((size_t)2 * H, sizeof(uint16_t));
+    uint16_t* ce = malloc(sizeof(uint16_t) * 2 * D);
+    uint16_t* cc = malloc(sizeof(uint16_t) * 2 * D);
+    memcpy(zc, z, sizeof(uint16_t) * H);  /* [z, zeros] */
+    or_linear_fwd(&m->c_emb, zc, 2, m->bc, ce);
+    for (int s = 0; s < m->steps; s++) {
+        or_add(m->t_emb + (size_t)s * 2 * D, ce, 2 * D, cc);
+        silu_rows(cc, 2 * D, silu_c + (size_t)s * 2 * D);
+    }
+    free(zc);
+    free(ce);
+    free(cc);
+}
+
+void or_adaln_mods(const or_adaln_model* m, const uint16_t* silu_c, uint16_t* mods, uint16_t* modf) {
+    const int D = m->c.D, rows = 2 * m->steps;
+    for (int k = 0; k < m->n_blocks; k++)
+        or_linear_fwd(&m->blocks[k].ada, silu_c, rows, m->blocks[k].bada, mods + (size_t)k * rows * 6 * D);
+    or_linear_fwd(&m->final_ada, silu_c, rows, m->bfa, modf);
+}
+
+void or_adaln_rows(const or_adaln_model* m, const uint16_t* y, uint16_t* rows) {
+    const int D = m->c.D, F = m->frames;
+    or_linear_fwd(&m->x_emb, y, F, m->bx, rows);
+    memcpy(rows + (size_t)F * D, rows, sizeof(uint16_t) * (size_t)F * D);
+}
+
+void or_adaln_final(const or_adaln_model* m, const uint16_t* h, const uint16_t* modf_step, const uint16_t* y,
+                    const uint16_t* sde, int step, float cfg, float shift_k, uint16_t* y_out) {
+    const int D = m->c.D, F = m->frames, R = 2 * F;
+    const int64_t n = m->final.N;
+    uint16_t* hn = malloc(sizeof(uint16_t) * (size_t)R * D);
+    uint16_t* o = malloc(sizeof(uint16_t) * (size_t)R * n);
+    or_rms_norm(h, m->final_norm, R, D, m->c.eps, hn);
+    modulate(hn, R, F, D, modf_step, 2 * D, 0, 1);
+    or_linear_fwd(&m->final, hn, R, m->bf, o);
+    const float cf = or_rb(cfg), dt = or_f32(m->dt[step]), sq = or_f32(m->sq[step]), sk = or_rb(shift_k);
+    for (int f = 0; f < F; f++)
+        for (int64_t i = 0; i < n; i++) {
+            const float pc = or_f32(o[(size_t)f * n + i]), pu = or_f32(o[(size_t)(F + f) * n + i]);
+            const float f0 = or_rb(pc + or_rb(or_rb(pc - pu) * cf));
+            float v = or_rb(or_f32(y[(size_t)f * n + i]) + or_rb(dt * f0));
+            if (shift_k != 0.0f)
+                v = or_rb(v + or_rb(or_rb(sk * sq) * or_f32(sde[((size_t)step * F + f) * n + i])));
+            y_out[(size_t)f * n + i] = or_bf16(v);
+        }
+    free(hn);
+    free(o);
+}
+
+void or_adaln_sample(const or_adaln_model* m, const uint16_t* z, const uint16_t* noise, const uint16_t* sde,
+                     float cfg, float shift_k, uint16_t* out, uint16_t* y_steps) {
+    const int D = m->c.D, F = m->frames, R = 2 * F, rows = 2 * m->steps;
+    const int64_t n = (int64_t)F * m->final.N;
+    uint16_t* silu_c = malloc(sizeof(uint16_t) * (size_t)rows * D);
+    uint16_t* mods = malloc(sizeof(uint16_t) * (size_t)m->n_blocks * rows * 6 * D);
+    uint16_t* modf = malloc(sizeof(uint16_t) * (size_t)rows * 2 * D);
+    uint16_t* y = malloc(sizeof(uint16_t) * n);
+    uint16_t* a = malloc(sizeof(uint16_t) * (size_t)R * D);
+    uint16_t* b2 = malloc(sizeof(uint16_t) * (size_t)R * D);
+    or_adaln_cond(m, z, silu_c);
+    or_adaln_mods(m, silu_c, mods, modf);
+    memcpy(y, noise, sizeof(uint16_t) * n);
+    for (int i = 0; i < m->steps; i++) {
+        or_adaln_rows(m, y, a);
+        for (int k = 0; k < m->n_blocks; k++) {
+            const uint16_t* mk = mods + ((size_t)k * rows + 2 * i) * 6 * D;
+            or_adaln_block_fwd(&m->c, &m->blocks[k].blk, mk, a, 2, F, m->cos_t, m->sin_t, b2, NULL);
+            uint16_t* t = a;
+            a = b2;
+            b2 = t;
+        }
+        or_adaln_final(m, a, modf + (size_t)2 * i * 2 * D, y, sde, i, cfg, shift_k, y);
+        if (y_steps) memcpy(y_steps + (size_t)i * n, y, sizeof(uint16_t) * n);
+    }
+    memcpy(out, y, sizeof(uint16_t) * n);
+    free(silu_c);
+    free(mods);
+    free(modf);
+    free(y);
+    free(a);
+    free(b2);
 }

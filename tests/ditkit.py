@@ -54,3 +54,24 @@ def oracle_agg(syn):
                            h[f"{AGG}.word_embedder.weight"], h[f"{AGG}.final_layer.norm_final.weight"],
                            olin(syn, f"{AGG}.final_layer.linear"), h[f"{AGG}.final_layer.linear.bias"], cos_t,
                            sin_t)
+
+
+ADA = "adaln"
+
+
+def oracle_adaln(syn):
+    """Config 4's adaLN flow head on the oracle, with its own t_emb / dt / sq."""
+    spec, h = syn.spec, syn.hostw
+    c = ocfg(spec)
+    blocks = [(oblock(syn, ADA, i), olin(syn, f"{ADA}.blocks.{i}.adaLN_modulation.1"),
+               h[f"{ADA}.blocks.{i}.adaLN_modulation.1.bias"]) for i in range(spec.cfm_blocks)]
+    t, dt, sq = oracle.flow_schedule()
+    m0, m2 = olin(syn, f"{ADA}.t_embedder.time_mlp.0"), olin(syn, f"{ADA}.t_embedder.time_mlp.2")
+    te = np.stack([oracle.timestep_embed(m0, h[f"{ADA}.t_embedder.time_mlp.0.bias"], m2,
+                                         h[f"{ADA}.t_embedder.time_mlp.2.bias"], t[i]) for i in range(10)])
+    cos_t, sin_t = oracle.rotary_table(spec.inv_freq(), spec.frames)
+    return oracle.AdalnModel(c, blocks, olin(syn, f"{ADA}.x_embedder"), h[f"{ADA}.x_embedder.bias"],
+                             olin(syn, f"{ADA}.c_embedder"), h[f"{ADA}.c_embedder.bias"],
+                             h[f"{ADA}.final_layer.norm_final.weight"], olin(syn, f"{ADA}.final_layer.linear"),
+                             h[f"{ADA}.final_layer.linear.bias"], olin(syn, f"{ADA}.final_layer.adaLN_modulation.1"),
+                             h[f"{ADA}.final_layer.adaLN_modulation.1.bias"], te, dt, sq, cos_t, sin_t, spec.frames)

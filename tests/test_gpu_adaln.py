@@ -1,0 +1,173 @@
+"""GPU parity of config 4's adaLN flow head (ming_adaln_block,
+ming_adaln_model_create / ming_adaln_sample) against the oracle.
+
+The variant has no reference implementation; its definition (adaLN-Zero DiT
+on the reference block's RMSNorm, modulations from silu(t_emb + c_emb(z)))
+is stated in include/ming_hip.h and restated in oracle/oracle_dit.c.  Bars:
+block stages and outputs, conditions, modulations and each Euler step's
+patch within 2e-2 + 1e-2 |ref| (bf16); the free-running ten-step patch within
+6e-2 + 2e-2 |ref| and a mean |d| of 2e-2 (as the reference flow head); with
+shift = scale = 0 and gate = 1 the GPU adaLN block reproduces the GPU
+reference block bit for bit."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from ditkit import ADA, oblock, ocfg, oracle_adaln
+from lmkit import assert_close_bf16
+
+pytestmark = pytest.mark.gpu
+
+C4 = dict(hidden=896, heads=14, head_dim=64, ff=3584)
+
+
+def syn_mod():
+    import importlib
+
+    return importlib.import_module("ming-tts-serve_amd.synthetic")
+
+
+def dev_u16(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda().view(torch.bfloat16)
+
+
+def host_u16(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def bf16_empty(*shape):
+    return torch.empty(shape, dtype=torch.bfloat16, device="cuda")
+
+
+def rotary(ctx, spec, L):
+    cos = torch.empty((L, spec.head_dim // 2), dtype=torch.float32, device="cuda")
+    sin = torch.empty_like(cos)
+    ctx.rotary_table(spec.inv_freq(), L, cos, sin)
+    return cos, sin
+
+
+def block_out(R, D, F):
+    out = dict(qkv=bf16_empty(3, R, D), att=bf16_empty(R, D), x1=bf16_empty(R, D), hh=bf16_empty(R, F),
+               x2=bf16_empty(R, D))
+    return out
+
+
+@pytest.mark.parametrize("shape,B,L", [(C4, 2, 4), (C4, 1, 4), (dict(hidden=128, heads=2, head_dim=64, ff=256), 2, 3)])
+def test_adaln_block_matches_oracle(ming, ctx, shape, B, L):
+    print(f"[adaln_block] {shape} B={B} L={L}", flush=True)
+    S = syn_mod()
+    spec = S.AdalnSpec(**shape, cfm_blocks=1, frames=L)
+    syn = S.SyntheticAdaln(ctx, spec, seed=23, norm_std=0.1)
+    R, D = B * L, spec.hidden
+    x = ming.synth_normal_bf16(24, "adaln.x", R * D).reshape(R, D)
+    mod = ming.synth_normal_bf16(25, "adaln.mod", B * 6 * D, 0.0, 0.3).reshape(B, 6 * D)
+    cos, sin = rotary(ctx, spec, L)
+    ct, st = oracle.rotary_table(spec.inv_freq(), L)
+    out = block_out(R, D, spec.ff)
+    ctx.adaln_block(spec.cfg(), syn.blocks[0], dev_u16(mod), dev_u16(x), B, L, cos, sin,
+                    ming.DitOut(*(out[k].data_ptr() for k in ("qkv", "att", "x1", "hh", "x2"))))
+    ctx.sync()
+    ref, tr = oracle.adaln_block_fwd(ocfg(spec), oblock(syn, ADA, 0), mod, x, B, L, ct, st, trace=True)
+    assert_close_bf16(host_u16(out["qkv"]), tr["qkv"], "q|k|v (modulated, rotated)")
+    assert_close_bf16(host_u16(out["att"]), tr["att"], "attention")
+    assert_close_bf16(host_u16(out["x1"]), tr["x1"], "x + gate_a * out_proj")
+    assert_close_bf16(host_u16(out["hh"]), tr["hh"], "gelu(ff1(modulated))")
+    assert_close_bf16(host_u16(out["x2"]), ref, "block output")
+
+
+def test_adaln_zero_modulation_equals_reference_block(ming, ctx):
+    S = syn_mod()
+    spec = S.AdalnSpec(**C4, cfm_blocks=1, frames=3)
+    syn = S.SyntheticAdaln(ctx, spec, seed=26, norm_std=0.1)
+    B, L, D = 2, 3, spec.hidden
+    R = B * L
+    x = dev_u16(ming.synth_normal_bf16(27, "adaln.x0", R * D).reshape(R, D))
+    zmod = np.zeros((B, 6 * D), np.uint16)
+    zmod[:, 2 * D:3 * D] = 0x3F80
+    zmod[:, 5 * D:] = 0x3F80
+    cos, sin = rotary(ctx, spec, L)
+    a, r = block_out(R, D, spec.ff), block_out(R, D, spec.ff)
+    keys = ("qkv", "att", "x1", "hh", "x2")
+    ctx.adaln_block(spec.cfg(), syn.blocks[0], dev_u16(zmod), x, B, L, cos, sin,
+                    ming.DitOut(*(a[k].data_ptr() for k in keys)))
+    ctx.dit_block(spec.cfg(), syn.blocks[0].base, x, B, L, cos, sin, ming.DitOut(*(r[k].data_ptr() for k in keys)))
+    ctx.sync()
+    for k in keys:
+        assert torch.equal(a[k].float(), r[k].float()), k
+
+
+def read_dev(ming, ctx, ptr, shape):
+    out = np.empty(shape, np.uint16)
+    ctx.check(ming.lib().ming_memcpy_dtoh(ctx.h, out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(ptr),
+                                          out.nbytes))
+    return out
+
+
+@pytest.fixture(scope="module")
+def c4(ming, ctx):
+    S = syn_mod()
+    syn = S.SyntheticAdaln(ctx, S.MING_ADALN, seed=31, norm_std=0.05, ada_std=0.02)
+    oracle.set_threads(16)
+    return syn, syn.model(), oracle_adaln(syn)
+
+
+@pytest.mark.parametrize("sigma,temperature", [(0.25, 0.0), (0.25, 1.0)])
+def test_adaln_sample_matches_oracle(ming, ctx, c4, sigma, temperature):
+    print(f"[adaln_sample] sigma={sigma} temperature={temperature}", flush=True)
+    syn, m, om = c4
+    spec = syn.spec
+    D, F, lat = spec.hidden, spec.frames, spec.latent
+    z = ming.synth_normal_bf16(41, "c4.z", spec.lm_hidden)
+    noise = ming.synth_normal_bf16(42, "c4.noise", F * lat).reshape(F, lat)
+    sde = ming.synth_normal_bf16(43, "c4.sde", 10 * F * lat).reshape(10, F, lat)
+    out = bf16_empty(F, lat)
+    steps = bf16_empty(10, F, lat)
+    m.sample(dev_u16(z), dev_u16(noise), dev_u16(sde), 2.0, sigma, temperature, out, steps)
+    ctx.sync()
+    g = host_u16(steps)
+    assert np.array_equal(host_u16(out), g[9])
+    shift = float(np.float32(sigma) * np.sqrt(np.float32(temperature)))
+    # the once-per-token tables: conditions and modulations
+    te_p, sc_p, mods_p, modf_p = m.tables()
+    assert_close_bf16(read_dev(ming, ctx, te_p, (10, 2, D)), om.keep["te"], "timestep embeddings")
+    g_sc = read_dev(ming, ctx, sc_p, (10, 2, D))
+    assert_close_bf16(g_sc, oracle.adaln_cond(om, z), "silu(t_emb + c_emb)")
+    g_mods = read_dev(ming, ctx, mods_p, (spec.cfm_blocks, 20, 6 * D))
+    g_modf = read_dev(ming, ctx, modf_p, (20, 2 * D))
+    r_mods, r_modf = oracle.adaln_mods(om, g_sc)  # teacher forced on the GPU's conditions
+    assert_close_bf16(g_mods, r_mods, "block modulations")
+    assert_close_bf16(g_modf, r_modf, "final modulations")
+    # every Euler step from the GPU's previous patch and the GPU's modulations
+    c = ocfg(spec)
+    for i in range(10):
+        y_in = noise if i == 0 else g[i - 1]
+        h = oracle.adaln_rows(om, y_in)
+        for k, blk in enumerate(om.blocks):
+            h = oracle.adaln_block_fwd(c, blk[0], g_mods[k, 2 * i:2 * i + 2], h, 2, F, om.keep["cos"], om.keep["sin"])
+        ref = oracle.adaln_final(om, h, g_modf[2 * i:2 * i + 2], y_in, sde, i, 2.0, shift)
+        assert_close_bf16(g[i], ref, f"Euler step {i} (teacher forced)")
+    ref_out, _ = oracle.adaln_sample(om, z, noise, sde, 2.0, shift)
+    assert_close_bf16(g[9], ref_out, "patch (end to end)", atol=6e-2, rtol=2e-2)
+    assert np.abs(oracle.to_f32(g[9]).astype(np.float64) - oracle.to_f32(ref_out)).mean() <= 2e-2
+
+
+def test_adaln_rejects(ming, ctx):
+    S = syn_mod()
+    spec = S.AdalnSpec(hidden=128, heads=2, head_dim=64, ff=256, cfm_blocks=1, frames=3)
+    syn = S.SyntheticAdaln(ctx, spec, seed=1)
+    cos, sin = rotary(ctx, spec, 3)
+    out = block_out(9, 128, 256)
+    o = ming.DitOut(*(out[k].data_ptr() for k in ("qkv", "att", "x1", "hh", "x2")))
+    mod = bf16_empty(3, 6 * 128)
+    x = bf16_empty(9, 128)
+    with pytest.raises(ming.MingError) as e:  # three halves
+        ctx.adaln_block(spec.cfg(), syn.blocks[0], mod, x, 3, 3, cos, sin, o)
+    assert e.value.status == ming.MING_E_SHAPE
+    w = ming.AdalnW.from_buffer_copy(syn.w)
+    w.frames = 5  # 2 x 5 rows > 8
+    with pytest.raises(ming.MingError) as e:
+        ming.AdalnModel(ctx, w)
+    assert e.value.status == ming.MING_E_SHAPE

@@ -17,7 +17,7 @@ import pytest
 import torch
 
 import oracle
-from ditkit import AGG, CFM, oblock, ocfg, olin, oracle_agg, oracle_cfm
+from ditkit import ADA, AGG, CFM, oblock, ocfg, olin, oracle_adaln, oracle_agg, oracle_cfm
 
 S = importlib.import_module("ming-tts-serve_amd.synthetic")
 
@@ -258,3 +258,111 @@ def test_stop_prob_closed_forms(small):
         lg = f64(small.hostw["stop_head.weight"]) @ f64(z) + torch.from_numpy(bb)
         want = float(torch.softmax(lg, 0)[1])
         assert abs(oracle.stop_prob(head, bias, z) - want) < 1e-2
+
+
+# ---- adaLN flow head (config 4; the build's own definition) -----------------------------
+
+@pytest.fixture(scope="module")
+def ada_small():
+    spec = S.AdalnSpec(hidden=128, heads=2, head_dim=64, ff=256, cfm_blocks=2, frames=3)
+    return S.SyntheticAdaln(None, spec, seed=17, std=0.1, norm_std=0.1, ada_std=0.05, device="cpu")
+
+
+def zero_mod(B, D):
+    m = np.zeros((B, 6 * D), np.uint16)
+    m[:, 2 * D:3 * D] = 0x3F80
+    m[:, 5 * D:6 * D] = 0x3F80
+    return m
+
+
+def test_adaln_zero_modulation_is_the_reference_block(ada_small):
+    sp = ada_small.spec
+    x = bf16_bits(torch.from_numpy(np.random.default_rng(2).normal(0, 1, (6, sp.hidden)).astype(np.float32)))
+    c, s = oracle.rotary_table(sp.inv_freq(), 3)
+    blk = oblock(ada_small, ADA, 0)
+    ref, tr = oracle.dit_block_fwd(ocfg(sp), blk, x, 2, 3, c, s, trace=True)
+    got, tg = oracle.adaln_block_fwd(ocfg(sp), blk, zero_mod(2, sp.hidden), x, 2, 3, c, s, trace=True)
+    assert np.array_equal(oracle.to_f32(got), oracle.to_f32(ref))
+    for k in ("qkv", "att", "x1", "hh"):
+        assert np.array_equal(oracle.to_f32(tg[k]), oracle.to_f32(tr[k])), k
+
+
+def test_adaln_block_vs_f64(ada_small):
+    sp = ada_small.spec
+    B, L, D = 2, 3, sp.hidden
+    rng = np.random.default_rng(4)
+    x = bf16_bits(torch.from_numpy(rng.normal(0, 1, (B * L, D)).astype(np.float32)))
+    mod = bf16_bits(torch.from_numpy(rng.normal(0, 0.3, (B, 6 * D)).astype(np.float32)))
+    c, s = oracle.rotary_table(sp.inv_freq(), L)
+    out, tr = oracle.adaln_block_fwd(ocfg(sp), oblock(ada_small, ADA, 0), mod, x, B, L, c, s, trace=True)
+    h, b = ada_small.hostw, f"{ADA}.blocks.0"
+    lin = lambda k, v: v @ f64(h[f"{b}.{k}.weight"]).T + f64(h[f"{b}.{k}.bias"])
+    md = f64(mod).reshape(B, 6, D)
+    per_row = lambda j: md[:, j, :].repeat_interleave(L, 0)  # [B*L][D]
+    modulate = lambda n, j: n * (1 + per_row(j + 1)) + per_row(j)
+    # each stage from the oracle's previous stage (teacher forced)
+    xf = f64(x)
+    n1 = modulate(rms64(xf, f64(h[f"{b}.norm1.weight"]), sp.eps), 0)
+    q = rotate64(lin("attn.to_q", n1), L, sp.heads, sp.head_dim, sp.inv_freq())
+    close(tr["qkv"][0], q.numpy(), "q (modulated, rotated)")
+    close(tr["qkv"][2], lin("attn.to_v", n1).numpy(), "v (modulated)")
+    x1 = xf + per_row(2) * lin("attn.to_out.0", f64(tr["att"]))
+    close(tr["x1"], x1.numpy(), "x + gate_a * out_proj")
+    f = lin("mlp.ff.0.0", modulate(rms64(f64(tr["x1"]), f64(h[f"{b}.norm2.weight"]), sp.eps), 3))
+    hh = 0.5 * f * (1 + torch.tanh(math.sqrt(2 / math.pi) * (f + 0.044715 * f ** 3)))
+    close(tr["hh"], hh.numpy(), "gelu(ff1(modulated))")
+    want = f64(tr["x1"]) + per_row(5) * lin("mlp.ff.2", f64(tr["hh"]))
+    close(out, want.numpy(), "block output")
+
+
+def test_adaln_cond_mods_and_final_vs_f64(ada_small):
+    sp, h = ada_small.spec, ada_small.hostw
+    om = oracle_adaln(ada_small)
+    D = sp.hidden
+    z = bf16_bits(torch.from_numpy(np.random.default_rng(6).normal(0, 1, sp.lm_hidden).astype(np.float32)))
+    sc = oracle.adaln_cond(om, z)
+    ce = torch.stack([f64(z), torch.zeros(sp.lm_hidden, dtype=torch.float64)]) @ \
+        f64(h[f"{ADA}.c_embedder.weight"]).T + f64(h[f"{ADA}.c_embedder.bias"])
+    te = f64(om.keep["te"])
+    cc = te + ce[None]
+    close(sc, (cc * torch.sigmoid(cc)).numpy(), "silu(t_emb + c_emb)")
+    mods, modf = oracle.adaln_mods(om, sc)
+    w0 = f"{ADA}.blocks.1.adaLN_modulation.1"
+    want = f64(sc).reshape(20, D) @ f64(h[w0 + ".weight"]).T + f64(h[w0 + ".bias"])
+    close(mods[1], want.numpy(), "block 1 modulations")
+    # final layer: rows [2F][D], modulation of step 7
+    F, step = sp.frames, 7
+    rng = np.random.default_rng(8)
+    hrow = bf16_bits(torch.from_numpy(rng.normal(0, 1, (2 * F, D)).astype(np.float32)))
+    y = bf16_bits(torch.from_numpy(rng.normal(0, 1, (F, 64)).astype(np.float32)))
+    sde = bf16_bits(torch.from_numpy(rng.normal(0, 1, (10, F, 64)).astype(np.float32)))
+    got = oracle.adaln_final(om, hrow, modf[2 * step:2 * step + 2], y, sde, step, 2.0, 0.5)
+    mf = f64(modf[2 * step:2 * step + 2]).reshape(2, 2, D)
+    n = rms64(f64(hrow), f64(h[f"{ADA}.final_layer.norm_final.weight"]), sp.eps)
+    half = torch.arange(2 * F) // F
+    hm = n * (1 + mf[half, 1]) + mf[half, 0]
+    o = hm @ f64(h[f"{ADA}.final_layer.linear.weight"]).T + f64(h[f"{ADA}.final_layer.linear.bias"])
+    pc, pu = o[:F], o[F:]
+    want = f64(y) + f64(om.keep["dt"])[step] * (pc + (pc - pu) * 2.0) + 0.5 * f64(om.keep["sq"])[step] * f64(sde[step])
+    close(got, want.numpy(), "final adaLN layer + CFG + Euler (per frame)")
+
+
+def test_adaln_zero_velocity_closed_form(ada_small):
+    """Final linear 0: the velocity of every frame is the final bias b, so
+    y_10 = noise + (t_10 - t_0) b + shift * sum_i sq_i sde_i per frame."""
+    om0 = oracle_adaln(ada_small)
+    h, sp = ada_small.hostw, ada_small.spec
+    k = om0.keep
+    zero = oracle.Linear(np.zeros_like(h[f"{ADA}.final_layer.linear.weight"]))
+    om = oracle.AdalnModel(ocfg(sp), om0.blocks, olin(ada_small, f"{ADA}.x_embedder"), k["bx"],
+                           olin(ada_small, f"{ADA}.c_embedder"), k["bc"], k["fn"], zero, k["bf"],
+                           olin(ada_small, f"{ADA}.final_layer.adaLN_modulation.1"), k["bfa"], k["te"], k["dt"],
+                           k["sq"], k["cos"], k["sin"], sp.frames)
+    rng = np.random.default_rng(10)
+    mk = lambda *shape: bf16_bits(torch.from_numpy(rng.normal(0, 1, shape).astype(np.float32)))
+    z, noise, sde = mk(sp.lm_hidden), mk(sp.frames, 64), mk(10, sp.frames, 64)
+    for shift in (0.0, 0.5):
+        out, steps = oracle.adaln_sample(om, z, noise, sde, 2.0, shift)
+        want = f64(noise) + f64(k["bf"])[None] + shift * (f64(k["sq"])[:, None, None] * f64(sde)).sum(0)
+        close(out, want.numpy(), f"adaLN zero-velocity sample shift {shift}", atol=3e-2)
+        assert np.array_equal(out, steps[9])
