@@ -108,6 +108,16 @@ int ming_qgemv_f32(ming_ctx* ctx, const ming_tensor* x, const ming_tensor* w, co
                    const ming_tensor* biases, float global_scale, int32_t group_size, int32_t bits,
                    ming_tensor* y);
 
+/* Y [M, N] = global_scale * (X W^T) for M = 1..64 activation rows (X bf16
+ * [M, K]); y bf16 (rounded once) or f32 (the accumulators).  The batched
+ * shape of the same call (mlx_quantized_matmul with M > 1, src/mlx.zig:279),
+ * as a server batching M sequences' decode steps issues it: matrix-core
+ * GEMM, the weight bytes read once for all M rows.  Same accumulation as
+ * ming_qgemv per group of 64; the sum order over groups differs, so results
+ * agree with ming_qgemv within f32 rounding, not bit for bit. */
+int ming_qgemm(ming_ctx* ctx, const ming_tensor* x, const ming_tensor* w, const ming_tensor* scales,
+               const ming_tensor* biases, float global_scale, int32_t group_size, int32_t bits, ming_tensor* y);
+
 /* out bf16 [N, K] = bf16(global_scale * (s*q + b)).  Mirrors mlx_dequantize
  * (src/mlx.zig:288). */
 int ming_dequantize(ming_ctx* ctx, const ming_tensor* w, const ming_tensor* scales, const ming_tensor* biases,

@@ -248,6 +248,7 @@ int ming_ctx_destroy(ming_ctx* ctx) {
     if (!alive(ctx)) return MING_E_NOT_INIT;
     (void)hipStreamSynchronize(ctx->stream);
     ctx->part.release();
+    ctx->qstage.release();
     if (ctx->dev_flags) (void)hipFree(ctx->dev_flags);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     ctx->alive = false;
@@ -367,6 +368,45 @@ int ming_qgemv(ming_ctx* ctx, const ming_tensor* x, const ming_tensor* w, const 
 int ming_qgemv_f32(ming_ctx* ctx, const ming_tensor* x, const ming_tensor* w, const ming_tensor* s,
                    const ming_tensor* b, float g, int32_t gs, int32_t bits, ming_tensor* y) {
     return qgemv_impl(ctx, x, w, s, b, g, gs, bits, y, true);
+}
+
+// Batched rows (mlx_quantized_matmul with M > 1, src/mlx.zig:279-282): MFMA GEMM over
+// activations staged once per call into the context's staging buffer.
+static int qgemm_impl(ming_ctx* ctx, const ming_tensor* x, const ming_tensor* w, const ming_tensor* s,
+                      const ming_tensor* b, float g, int32_t gs, int32_t bits, ming_tensor* y) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    int64_t N, K;
+    int st = check_affine(ctx, w, s, b, gs, bits, N, K);
+    if (st) return st;
+    int64_t xm, xk, ym, yn;
+    if (!as_2d(x, xm, xk) || !as_2d(y, ym, yn)) return set_err(ctx, MING_E_SHAPE, "qgemm: x/y must be 1-D or 2-D");
+    if (x->dtype != MING_DT_BF16) return set_err(ctx, MING_E_SHAPE, "qgemm: x must be bf16");
+    if (y->dtype != MING_DT_F32 && y->dtype != MING_DT_BF16) return set_err(ctx, MING_E_SHAPE, "qgemm: y must be bf16 or f32");
+    if (xk != K || ym != xm || yn != N)
+        return set_err(ctx, MING_E_SHAPE, "qgemm: x " + shape_str(x) + " / y " + shape_str(y) +
+                                              " do not match w [" + std::to_string(N) + "," + std::to_string(K) + "]");
+    if (xm < 1 || xm > 64) return set_err(ctx, MING_E_UNSUPPORTED, "qgemm: 1..64 activation rows");
+    if (N > INT32_MAX / 64 || K > 65536) return set_err(ctx, MING_E_UNSUPPORTED, "qgemm: N or K too large");
+    const int M = (int)xm, Mp = (M + 15) / 16 * 16;
+    const size_t xs_bytes = (size_t)Mp * K * 2, need = xs_bytes + (size_t)Mp * (K / 64) * sizeof(float);
+    if ((st = hip_check(ctx, ctx->qstage.ensure(need), "hipMalloc(qgemm staging)"))) return st;
+    uint4* xs = static_cast<uint4*>(ctx->qstage.p);
+    float* xsum = reinterpret_cast<float*>(static_cast<char*>(ctx->qstage.p) + xs_bytes);
+    if ((st = hip_check(ctx, launch_qgemm_stage(ctx->stream, static_cast<const uint16_t*>(x->data), M, (int)K, xs, xsum),
+                        "qgemm staging launch")))
+        return st;
+    const bool f32 = y->dtype == MING_DT_F32;
+    return hip_check(ctx,
+                     launch_qgemm(ctx->stream, xs, xsum, M, (int)N, (int)K, static_cast<const uint32_t*>(w->data),
+                                  static_cast<const uint16_t*>(s->data), static_cast<const uint16_t*>(b->data), g,
+                                  f32 ? nullptr : static_cast<uint16_t*>(y->data),
+                                  f32 ? static_cast<float*>(y->data) : nullptr),
+                     "qgemm launch");
+}
+
+int ming_qgemm(ming_ctx* ctx, const ming_tensor* x, const ming_tensor* w, const ming_tensor* s, const ming_tensor* b,
+               float g, int32_t gs, int32_t bits, ming_tensor* y) {
+    return qgemm_impl(ctx, x, w, s, b, g, gs, bits, y);
 }
 
 int ming_dequantize(ming_ctx* ctx, const ming_tensor* w, const ming_tensor* s, const ming_tensor* b, int32_t gs,

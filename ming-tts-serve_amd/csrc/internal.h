@@ -39,6 +39,7 @@ struct ming_ctx {
     size_t max_lds = 0;
     bool alive = false;
     ming::DevBuf part;                // attention partials of ming_lm_layer
+    ming::DevBuf qstage;              // staged activations of ming_qgemm
     bool timeout_seen = false;        // ming_sync saw the device error flag
 };
 
@@ -54,5 +55,10 @@ hipError_t launch_dequantize(hipStream_t st, const uint32_t* w, const uint16_t* 
                              int64_t K, float gscale, uint16_t* out);
 hipError_t launch_quantize(hipStream_t st, const uint16_t* w, int64_t N, int64_t K, uint32_t* wq, uint16_t* s,
                            uint16_t* b);
+// Batched 4-bit GEMM on MFMA: stage X [M][K] (K % 64 == 0) into xs [Mp][K/8] and
+// xsum [Mp][K/64] (Mp = M rounded up to 16), then Y = g * X W^T for M <= 64.
+hipError_t launch_qgemm_stage(hipStream_t st, const uint16_t* x, int M, int K, uint4* xs, float* xsum);
+hipError_t launch_qgemm(hipStream_t st, const uint4* xs, const float* xsum, int M, int N, int K, const uint32_t* w,
+                        const uint16_t* s, const uint16_t* b, float gscale, uint16_t* y, float* yf);
 
 }  // namespace ming
