@@ -237,6 +237,54 @@ int ming_lm_model_trace(ming_lm_model* m, void* x, void* x1, void* att, void* qk
  * tokens_dev[1..n] receive the argmaxes.  No host synchronisation inside. */
 int ming_lm_generate(ming_ctx* ctx, ming_lm_model* m, ming_kv* kv, int32_t n_steps, int32_t* tokens_dev);
 
+/* ---- Multi-request decode over a paged KV cache ------------------------------
+ * No counterpart in the reference: its service decodes one request at a
+ * time with a contiguous cache per request (src/ming_service.zig:11-14,
+ * :175-206).  Here n_seq sequences advance one token per call; each linear is
+ * one 4-bit GEMM over the n_seq rows on the matrix cores (ming_qgemm's
+ * arithmetic) and attention reads each sequence's pages.  Per sequence the
+ * result is the batch-1 step's (ming_lm_step) within f32 summation order.
+ *
+ * Paged cache: pages of 64 positions, one page id per 64 positions of a
+ * sequence for all layers and kv heads; head_dim 64.
+ *   k: bf16 [n_layers][n_pages][kv_heads][64 positions][head_dim]
+ *   v: bf16 [n_layers][n_pages][kv_heads][head_dim][64 positions]
+ *      (each V page stored transposed). */
+typedef struct {
+    void* k;
+    void* v;
+    int32_t n_layers, kv_heads, head_dim, page_size, n_pages;
+} ming_kv_pages;
+
+/* Workspace for up to max_seqs (<= 64) sequences of up to max_ctx positions
+ * on a prepared model (4-bit linears; head_dim 64; hidden and inter
+ * multiples of 64).  Holds every layer's activations of the last step. */
+typedef struct ming_lm_batch ming_lm_batch;
+int ming_lm_batch_create(ming_ctx* ctx, ming_lm_model* m, int32_t max_seqs, int32_t max_ctx, ming_lm_batch** out);
+int ming_lm_batch_destroy(ming_lm_batch* b);
+
+/* One decode step of n_seq sequences.  Input rows: the embeddings of
+ * tokens_dev (device i32 [n_seq]) or x_in (device bf16 [n_seq][hidden]).
+ * page_table_dev: device i32 [n_seq][pages_per_seq], the pages of sequence i
+ * in position order (pages_per_seq * 64 <= max_ctx); pos_dev: device i32
+ * [n_seq], the position of each sequence's new row (its cached length); the
+ * step writes the new k/v rows there and adds 1 to every pos_dev entry.
+ * Outputs (each optional, device): hidden_out bf16 [n_seq][hidden]
+ * (final-normed), logits_out f32 [n_seq][vocab], argmax_out i32 [n_seq]
+ * (lowest index on ties).  A position at or past pages_per_seq * 64, or a
+ * page id outside [0, n_pages), is reported by the next ming_sync as
+ * MING_E_CTX_OVER_CAPACITY (that sequence's append and attention are skipped). */
+int ming_lm_batch_step(ming_lm_batch* b, int32_t n_seq, const int32_t* tokens_dev, const void* x_in,
+                       const ming_kv_pages* kv, const int32_t* page_table_dev, int32_t pages_per_seq, int32_t* pos_dev,
+                       void* hidden_out, float* logits_out, int32_t* argmax_out);
+
+/* Per-layer activations of the last ming_lm_batch_step (n_seq rows each), as
+ * ming_lm_model_trace lays them out with a sequence axis after the layer
+ * axis: x [n_layers + 1][n_seq][hidden], x1 and att [n_layers][n_seq][hidden],
+ * qkv [n_layers][n_seq][hidden + 2*kv_heads*head_dim], hh [n_layers][n_seq]
+ * [inter].  Device buffers; NULL skips one. */
+int ming_lm_batch_trace(ming_lm_batch* b, void* x, void* x1, void* att, void* qkv, void* hh);
+
 /* ---- DiT flow head and aggregator ------------------------------------------
  * The reference's fused DiT path (src/ming_fused.zig:482-573) and its
  * callers DitStack.forward (src/ming_model.zig:770-797), cfmSample (:1143),

@@ -75,6 +75,14 @@ class Kv(ctypes.Structure):
     ]
 
 
+class KvPages(ctypes.Structure):
+    """ming_kv_pages: paged cache of 64-position pages (V pages transposed)."""
+    _fields_ = [
+        ("k", c_void_p), ("v", c_void_p), ("n_layers", c_i32), ("kv_heads", c_i32), ("head_dim", c_i32),
+        ("page_size", c_i32), ("n_pages", c_i32),
+    ]
+
+
 class LmOut(ctypes.Structure):
     _fields_ = [("qkv", c_void_p), ("o", c_void_p), ("x1", c_void_p), ("hh", c_void_p), ("x2", c_void_p)]
 
@@ -166,6 +174,11 @@ def lib():
         "ming_lm_step": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, P(Kv), c_void_p, c_void_p, c_void_p]),
         "ming_lm_generate": (c_i32, [c_void_p, c_void_p, P(Kv), c_i32, c_void_p]),
         "ming_lm_model_trace": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+        "ming_lm_batch_create": (c_i32, [c_void_p, c_void_p, c_i32, c_i32, P(c_void_p)]),
+        "ming_lm_batch_destroy": (c_i32, [c_void_p]),
+        "ming_lm_batch_step": (c_i32, [c_void_p, c_i32, c_void_p, c_void_p, P(KvPages), c_void_p, c_i32, c_void_p,
+                                       c_void_p, c_void_p, c_void_p]),
+        "ming_lm_batch_trace": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
         "ming_rotary_table": (c_i32, [c_void_p, c_void_p, c_i32, c_i32, c_void_p, c_void_p]),
         "ming_dit_block": (c_i32, [c_void_p, P(DitCfg), P(DitBlockW), c_void_p, c_i32, c_i32, c_void_p, c_void_p,
                                    P(DitOut)]),
@@ -512,6 +525,52 @@ class LmModel:
 
     def generate(self, kv, n_steps, tokens):
         self.ctx.check(self.ctx.L.ming_lm_generate(self.ctx.h, self.h, ctypes.byref(kv), int(n_steps), ptr(tokens)))
+
+
+class LmBatch:
+    """ming_lm_batch: workspace of the multi-request decode step of an LmModel."""
+
+    def __init__(self, model, max_seqs, max_ctx):
+        self.ctx = model.ctx
+        self.model = model
+        self.max_seqs = int(max_seqs)
+        h = c_void_p()
+        self.ctx.check(self.ctx.L.ming_lm_batch_create(self.ctx.h, model.h, int(max_seqs), int(max_ctx),
+                                                       ctypes.byref(h)))
+        self.h = h
+        self.n = 0
+
+    def close(self):
+        if self.h:
+            self.ctx.L.ming_lm_batch_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def step(self, pages, table, pos, tokens=None, x_in=None, hidden=None, logits=None, argmax=None):
+        """One step of n = len(pos) sequences; table: device i32 [n][pages_per_seq]."""
+        n, pps = int(table.shape[0]), int(table.shape[1])
+        self.ctx.check(self.ctx.L.ming_lm_batch_step(self.h, n, ptr(tokens), ptr(x_in), ctypes.byref(pages.kv),
+                                                     ptr(table), pps, ptr(pos), ptr(hidden), ptr(logits),
+                                                     ptr(argmax)))
+        self.n = n
+
+    def trace(self):
+        """dict of per-layer activations [layer][seq][...] of the last step (device bf16)."""
+        torch = _torch()
+        c, n = self.model.cfg, self.n
+        H, L, nq = c.hidden, c.n_layers, c.hidden + 2 * c.kv_heads * c.head_dim
+        t = dict(x=torch.empty((L + 1, n, H), dtype=torch.bfloat16, device="cuda"),
+                 x1=torch.empty((L, n, H), dtype=torch.bfloat16, device="cuda"),
+                 att=torch.empty((L, n, H), dtype=torch.bfloat16, device="cuda"),
+                 qkv=torch.empty((L, n, nq), dtype=torch.bfloat16, device="cuda"),
+                 hh=torch.empty((L, n, c.inter), dtype=torch.bfloat16, device="cuda"))
+        self.ctx.check(self.ctx.L.ming_lm_batch_trace(self.h, *(ptr(t[k]) for k in ("x", "x1", "att", "qkv", "hh"))))
+        return t
 
 
 # ---- synthetic inputs ---------------------------------------------------------

@@ -215,6 +215,16 @@ int layer_scratch(ming_ctx* ctx, DevBuf& part, size_t floats) {
 
 }  // namespace
 
+bool ming::lm_model_view(const ming_lm_model* m, LmView& v) {
+    if (!m || !m->ctx) return false;
+    v.cfg = m->cfg;
+    v.layers = m->layers.data();
+    v.head = m->head;
+    v.embed = m->embed;
+    v.final_norm = m->final_norm;
+    return true;
+}
+
 extern "C" {
 
 // ---- context ------------------------------------------------------------------
@@ -281,6 +291,14 @@ int ming_sync(ming_ctx* ctx) {
         (void)hipMemset(ctx->dev_flags, 0, sizeof(int32_t));
         ctx->timeout_seen = true;
         return set_err(ctx, MING_E_TIMEOUT, "a device-side wait exceeded its spin limit");
+    }
+    // [1]: a batched step met a position or page id outside its paged cache
+    st = hip_check(ctx, hipMemcpy(&flag, ctx->dev_flags + 1, sizeof(flag), hipMemcpyDeviceToHost), "read error flag");
+    if (st) return st;
+    if (flag) {
+        (void)hipMemset(ctx->dev_flags + 1, 0, sizeof(int32_t));
+        return set_err(ctx, MING_E_CTX_OVER_CAPACITY,
+                       "a batched step met a position or page id outside its paged cache (append and attention skipped)");
     }
     return MING_OK;
 }
@@ -390,18 +408,26 @@ static int qgemm_impl(ming_ctx* ctx, const ming_tensor* x, const ming_tensor* w,
     const int M = (int)xm, Mp = (M + 15) / 16 * 16;
     const size_t xs_bytes = (size_t)Mp * K * 2, need = xs_bytes + (size_t)Mp * (K / 64) * sizeof(float);
     if ((st = hip_check(ctx, ctx->qstage.ensure(need), "hipMalloc(qgemm staging)"))) return st;
-    uint4* xs = static_cast<uint4*>(ctx->qstage.p);
+    void* xs = ctx->qstage.p;
     float* xsum = reinterpret_cast<float*>(static_cast<char*>(ctx->qstage.p) + xs_bytes);
-    if ((st = hip_check(ctx, launch_qgemm_stage(ctx->stream, static_cast<const uint16_t*>(x->data), M, (int)K, xs, xsum),
+    if ((st = hip_check(ctx,
+                        launch_stage(ctx->stream, static_cast<const uint16_t*>(x->data), (int)K, M, (int)K, nullptr,
+                                     0.0f, xs, xsum, nullptr, nullptr),
                         "qgemm staging launch")))
         return st;
     const bool f32 = y->dtype == MING_DT_F32;
-    return hip_check(ctx,
-                     launch_qgemm(ctx->stream, xs, xsum, M, (int)N, (int)K, static_cast<const uint32_t*>(w->data),
-                                  static_cast<const uint16_t*>(s->data), static_cast<const uint16_t*>(b->data), g,
-                                  f32 ? nullptr : static_cast<uint16_t*>(y->data),
-                                  f32 ? static_cast<float*>(y->data) : nullptr),
-                     "qgemm launch");
+    QgemmArgs a{};
+    a.xs = xs;
+    a.xsum = xsum;
+    a.M = M;
+    a.K = (int)K;
+    a.nseg = 1;
+    a.seg[0] = QSeg{static_cast<const uint32_t*>(w->data), static_cast<const uint16_t*>(s->data),
+                    static_cast<const uint16_t*>(b->data), nullptr, (int)N, 0, g};
+    a.y = f32 ? nullptr : static_cast<uint16_t*>(y->data);
+    a.yf = f32 ? static_cast<float*>(y->data) : nullptr;
+    a.ldy = (int)N;
+    return hip_check(ctx, launch_qgemm_epi(ctx->stream, a, QE_PLAIN), "qgemm launch");
 }
 
 int ming_qgemm(ming_ctx* ctx, const ming_tensor* x, const ming_tensor* w, const ming_tensor* s, const ming_tensor* b,

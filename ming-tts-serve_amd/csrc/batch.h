@@ -1,0 +1,81 @@
+// Argument blocks of the batched (multi-sequence) decode kernels, shared by the
+// host glue and the kernels (no device code).
+#pragma once
+
+#include <stdint.h>
+
+namespace ming {
+
+// Epilogues of the batched 4-bit GEMM.
+enum QEpi : int {
+    QE_PLAIN = 0,   // y = bf16(g acc) and/or yf = g acc
+    QE_RES = 1,     // y = bf16(res + bf16(g acc))
+    QE_SWIGLU = 2,  // two segments (gate, up) of one width: y = swiglu(bf16(g acc_gate), bf16(g acc_up))
+    QE_QKV = 3,     // three segments (q, k, v): + bias, rope on q/k, k/v rows appended to the pages
+};
+
+// One weight matrix of a GEMM call (a call may concatenate up to three along N).
+struct QSeg {
+    const uint32_t* w;      // u32 [N][K/8]
+    const uint16_t* s;      // bf16 [N][K/64]
+    const uint16_t* b;      // bf16 [N][K/64]
+    const uint16_t* bias;   // QE_QKV: bf16 [N]
+    int N, col0;            // output columns [col0, col0 + N)
+    float gscale;
+};
+
+// Where QE_QKV puts each sequence's new k/v row.  Pages hold 64 positions of
+// one layer and kv head: K [n_pages][kvh][64][64] row-major, V [n_pages][kvh]
+// [64 dims][64 positions] (transposed, so that attention reads 8 positions of
+// one dim as 16 contiguous bytes).
+struct QPaged {
+    uint16_t* kp;           // this layer's K pages
+    uint16_t* vp;           // this layer's V pages
+    const int32_t* table;   // [n_seq][pages_per_seq] page ids
+    const int32_t* pos;     // [n_seq] position of the new row
+    const float* rope_cs;   // f32 [max_ctx][32][2]: (cos, sin) of pos * inv_freq[i]
+    int32_t* flags;         // [1] set to 1 on a position or page id out of range
+    int pages_per_seq, n_pages, kvh, max_ctx;
+};
+
+struct QgemmArgs {
+    const void* xs;         // uint4 [Mp][K/8]: staged activations (pair order)
+    const float* xsum;      // [Mp][K/64]
+    int M, K;
+    QSeg seg[3];
+    int nseg;
+    int blocks[3];          // workgroups of each segment
+    uint16_t* y;            // bf16 [M][ldy]
+    float* yf;              // f32 [M][ldy] (QE_PLAIN)
+    int ldy;
+    const uint16_t* res;    // QE_RES: bf16 [M][ldres]
+    int ldres;
+    QPaged pg;
+};
+
+// Paged decode attention of n_seq sequences: one workgroup per (sequence,
+// kv head, split of 4 pages); one wave per page.
+struct PagedAttnArgs {
+    const uint16_t* qkv;    // bf16 [n_seq][ldq]: roped q at column 0
+    int ldq;
+    const uint16_t* kp;
+    const uint16_t* vp;
+    const int32_t* table;
+    const int32_t* pos;
+    int32_t* flags;
+    float* part;            // f32 [n_seq][kvh][max_splits][grp][68]: o[64], m, l
+    int pages_per_seq, n_pages, kvh, grp, max_splits;
+    float scale;            // 1/sqrt(head_dim)
+};
+
+// Merge of the splits into attention rows, staged for the o projection.
+struct MergeArgs {
+    const float* part;
+    const int32_t* pos;
+    int n_seq, heads, kvh, grp, max_splits;
+    uint16_t* att;          // bf16 [n_seq][heads * 64]
+    void* xs;               // uint4 [Mp][heads * 8]
+    float* xsum;            // [Mp][heads]
+};
+
+}  // namespace ming

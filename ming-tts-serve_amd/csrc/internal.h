@@ -6,6 +6,8 @@
 #include <string>
 
 #include "../../include/ming_hip.h"
+#include "args.h"
+#include "batch.h"
 
 namespace ming {
 // Device memory owned by a context or model; grows on demand.
@@ -55,10 +57,27 @@ hipError_t launch_dequantize(hipStream_t st, const uint32_t* w, const uint16_t* 
                              int64_t K, float gscale, uint16_t* out);
 hipError_t launch_quantize(hipStream_t st, const uint16_t* w, int64_t N, int64_t K, uint32_t* wq, uint16_t* s,
                            uint16_t* b);
-// Batched 4-bit GEMM on MFMA: stage X [M][K] (K % 64 == 0) into xs [Mp][K/8] and
-// xsum [Mp][K/64] (Mp = M rounded up to 16), then Y = g * X W^T for M <= 64.
-hipError_t launch_qgemm_stage(hipStream_t st, const uint16_t* x, int M, int K, uint4* xs, float* xsum);
-hipError_t launch_qgemm(hipStream_t st, const uint4* xs, const float* xsum, int M, int N, int K, const uint32_t* w,
-                        const uint16_t* s, const uint16_t* b, float gscale, uint16_t* y, float* yf);
+// ---- batched decode (qgemm.hip, batch.hip) ----
+// Batched 4-bit GEMM on MFMA over activations staged by launch_stage; a.blocks
+// is filled by the launcher.  epi is a QEpi.
+hipError_t launch_qgemm_epi(hipStream_t st, QgemmArgs a, int epi);
+// Rows [0, Mp) of x [M][ldx] (Mp = M rounded up to 16; rows >= M zero) staged
+// as uint4 xs [Mp][K/8] + f32 xsum [Mp][K/64]; norm_w non-null: rms first.
+hipError_t launch_stage(hipStream_t st, const uint16_t* x, int ldx, int M, int K, const uint16_t* norm_w, float eps,
+                        void* xs, float* xsum, uint16_t* hout, int32_t* pos_inc);
+hipError_t launch_embed_rows(hipStream_t st, const LinearDev& E, const int32_t* tokens, int n, uint16_t* x);
+hipError_t launch_rope_table(hipStream_t st, float* cs, int max_ctx, int half, float log2_theta);
+hipError_t launch_paged_attn(hipStream_t st, const PagedAttnArgs& a, int n_seq);
+hipError_t launch_merge_stage(hipStream_t st, const MergeArgs& a);
+hipError_t launch_argmax_rows(hipStream_t st, const float* logits, int n, int V, int32_t* out);
+
+// Read-only view of a prepared decode stack (for the batched step).
+struct LmView {
+    ming_lm_cfg cfg;
+    const LayerDev* layers;   // host array [n_layers]
+    LinearDev head, embed;
+    const uint16_t* final_norm;
+};
+bool lm_model_view(const ming_lm_model* m, LmView& v);
 
 }  // namespace ming

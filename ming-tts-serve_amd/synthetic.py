@@ -14,7 +14,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import (Context, Kv, Linear, LmCfg, LmLayerW, LmModel, W_AFFINE, W_BF16, linear, synth_normal_bf16)
+from . import (Context, Kv, KvPages, Linear, LmCfg, LmLayerW, LmModel, W_AFFINE, W_BF16, linear, synth_normal_bf16)
 
 
 @dataclass
@@ -187,6 +187,87 @@ class KvCache:
 
         return (self.k.view(torch.int16).cpu().numpy().view(np.uint16),
                 self.v.view(torch.int16).cpu().numpy().view(np.uint16))
+
+
+class PagedKv:
+    """Paged bf16 KV cache of n_seq sequences on the device (ming_kv_pages):
+    pages of 64 positions, K [n_layers][n_pages][kv_heads][64][head_dim], V
+    [n_layers][n_pages][kv_heads][head_dim][64] (each page transposed).  Each
+    sequence owns pages_per_seq pages, drawn from a seeded permutation of the
+    pool so that consecutive positions do not sit in consecutive pages."""
+
+    def __init__(self, spec: LmSpec, n_seq, pages_per_seq, spare=0, seed=0, device="cuda"):
+        import torch
+
+        self.spec, self.n_seq, self.pps = spec, int(n_seq), int(pages_per_seq)
+        self.n_pages = self.n_seq * self.pps + int(spare)
+        L, kvh, hd = spec.n_layers, spec.kv_heads, spec.head_dim
+        self.k = torch.zeros((L, self.n_pages, kvh, 64, hd), dtype=torch.bfloat16, device=device)
+        self.v = torch.zeros((L, self.n_pages, kvh, hd, 64), dtype=torch.bfloat16, device=device)
+        perm = np.random.default_rng(seed).permutation(self.n_pages)[: self.n_seq * self.pps]
+        self.set_table(perm.reshape(self.n_seq, self.pps))
+        self.pos = torch.zeros(self.n_seq, dtype=torch.int32, device=device)
+        self.kv = KvPages(self.k.data_ptr(), self.v.data_ptr(), L, kvh, hd, 64, self.n_pages)
+
+    def set_table(self, table):
+        import torch
+
+        self.table_host = np.ascontiguousarray(table, dtype=np.int32)
+        self.table = torch.from_numpy(self.table_host).to(self.k.device)
+
+    def set_seq(self, i, kc, vc):
+        """Rows [0, n) of sequence i from contiguous host u16 [L][kvh][n][hd]; pos[i] = n."""
+        import torch
+
+        L, kvh, n, hd = kc.shape
+        for p in range((n + 63) // 64):
+            m = min(64, n - 64 * p)
+            bk = np.zeros((L, kvh, 64, hd), np.uint16)
+            bv = np.zeros((L, kvh, 64, hd), np.uint16)
+            bk[:, :, :m] = kc[:, :, 64 * p:64 * p + m]
+            bv[:, :, :m] = vc[:, :, 64 * p:64 * p + m]
+            pid = int(self.table_host[i, p])
+            self.k[:, pid] = torch.from_numpy(bk.view(np.int16)).to(self.k.device).view(torch.bfloat16)
+            self.v[:, pid] = torch.from_numpy(np.ascontiguousarray(bv.transpose(0, 1, 3, 2)).view(np.int16)).to(
+                self.k.device).view(torch.bfloat16)
+        self.pos[i] = n
+
+    def fill_random(self, lens, seed=0, std=1.0):
+        """Sequence i gets lens[i] rows ~ bf16(N(0, std)) in every layer/head;
+        returns the host copies [(kc, vc)] in the contiguous layout."""
+        L, kvh, hd = self.spec.n_layers, self.spec.kv_heads, self.spec.head_dim
+        host = []
+        for i, n in enumerate(lens):
+            kc = synth_normal_bf16(seed, f"pkv.k.{i}", L * kvh * n * hd, 0.0, std).reshape(L, kvh, n, hd)
+            vc = synth_normal_bf16(seed, f"pkv.v.{i}", L * kvh * n * hd, 0.0, std).reshape(L, kvh, n, hd)
+            self.set_seq(i, kc, vc)
+            host.append((kc, vc))
+        return host
+
+    def fill_device(self, lens, seed=0):
+        """Every page ~ bf16(N(0,1)) from a seeded device generator (benchmark
+        contents); pos = lens."""
+        import torch
+
+        g = torch.Generator(device=self.k.device)
+        g.manual_seed(int(seed))
+        self.k.normal_(generator=g)
+        self.v.normal_(generator=g)
+        self.pos.copy_(torch.tensor(lens, dtype=torch.int32))
+
+    def gather(self, i, n):
+        """Rows [0, n) of sequence i as contiguous host u16 [L][kvh][n][hd] (k, v)."""
+        import torch
+
+        pages = [int(p) for p in self.table_host[i, : (n + 63) // 64]]
+        idx = torch.tensor(pages, dtype=torch.long, device=self.k.device)
+        k = self.k.index_select(1, idx).permute(0, 2, 1, 3, 4)  # [L][kvh][np][64][hd]
+        v = self.v.index_select(1, idx).permute(0, 2, 1, 4, 3)
+        L, kvh = k.shape[0], k.shape[1]
+        k = k.reshape(L, kvh, -1, k.shape[-1])[:, :, :n]
+        v = v.reshape(L, kvh, -1, v.shape[-1])[:, :, :n]
+        return (k.contiguous().view(torch.int16).cpu().numpy().view(np.uint16),
+                v.contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
 
 
 def lm_bytes_per_token(spec: LmSpec, ctx_len):
