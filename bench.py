@@ -32,6 +32,12 @@ Two more workloads print a line of the same form (`--workload`):
         the per-token time being the difference of a K-step and a 1-step run
         after the same prompt prefill; roofline over the token's weight and
         KV bytes.
+  server  config 5's multi-request decode: --seqs sequences (16 or 64) with
+        contexts drawn uniform in [128, 4096] (seed 0) over a paged bf16 KV
+        cache advance one token per step (each fed its own argmax) through
+        the batched 4-bit step (MFMA GEMMs, paged attention); value is
+        tokens/s over all sequences; roofline over the step's weight bytes
+        plus every sequence's KV read and append.
 """
 import argparse
 import importlib
@@ -55,7 +61,8 @@ HBM_PEAK_GBS = 8000.0
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--workload", choices=["lm", "cfm", "c4", "loop"], default="lm")
+    p.add_argument("--workload", choices=["lm", "cfm", "c4", "loop", "server"], default="lm")
+    p.add_argument("--seqs", type=int, default=64, help="server workload: concurrent sequences")
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--ctx", type=int, default=2048)
@@ -77,6 +84,8 @@ def main():
         return bench_loop(args)
     if args.workload == "c4":
         return bench_c4(args)
+    if args.workload == "server":
+        return bench_server(args)
     import torch
 
     ming = importlib.import_module("ming-tts-serve_amd")
@@ -202,6 +211,85 @@ def cpu_baseline(ming, S, syn, cache, args):
         "sample": f"{n} decode tokens of the same 24-layer 4-bit model at ctx {args.ctx} "
                   f"({dt:.1f} s, C restatement of the MLX CPU graph, OpenMP over output rows)",
     }
+
+
+# ---- multi-request decode ------------------------------------------------------------
+
+METRIC_SERVER = ("multi-request decode tokens/s (config 5: 4-bit LM, paged bf16 KV, ragged ctx 128..4096) "
+                 "+ achieved HBM GB/s")
+
+
+def bench_server(args):
+    import numpy as np
+    import torch
+
+    ming = importlib.import_module("ming-tts-serve_amd")
+    S = importlib.import_module("ming-tts-serve_amd.synthetic")
+    spec = S.QWEN2_05B
+    n = args.seqs
+    ctx = ming.Context(0)
+    t0 = time.time()
+    syn = S.SyntheticLm(ctx, spec, seed=0, quant=True)
+    m = syn.model()
+    lens = [int(v) for v in np.random.default_rng(0).integers(128, 4096 + 1, n)]
+    pps = (max(lens) + args.warmup + args.steps + 1 + 63) // 64
+    batch = ming.LmBatch(m, n, pps * 64)
+    pk = S.PagedKv(spec, n, pps, seed=0)
+    pk.fill_device(lens, seed=1)
+    tok = torch.tensor([int(t) for t in ming.synth_uniform_i32(0, "server.tok", n, spec.vocab)], dtype=torch.int32,
+                       device="cuda")
+    torch.cuda.synchronize()
+    print(f"[bench] server setup {time.time() - t0:.1f}s ({n} sequences, {pps} pages each)", file=sys.stderr,
+          flush=True)
+
+    def step():
+        batch.step(pk, pk.table, pk.pos, tokens=tok, argmax=tok)
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    start = [p + args.warmup for p in lens]
+    ms = timed_events(step, args.steps, 0)
+    ctx.sync()
+    assert pk.pos.cpu().tolist() == [p + args.steps for p in start]
+    kv_row = spec.n_layers * 2 * spec.kvd * 2
+    fixed = S.lm_bytes_per_token(spec, 0) - kv_row
+    mean_ctx = float(np.mean(start)) + (args.steps - 1) / 2.0
+    nbytes = int(fixed + n * (mean_ctx + 1) * kv_row)
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        from lmkit import oracle_model, oracle_step
+
+        oracle.set_threads(int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1))
+        cfg, layers, norm, head = oracle_model(syn)
+        done, t1, i = 0, time.time(), 0
+        while True:  # sequences in turn, each at its own context, one token each
+            pos = int(pk.pos[i].item())
+            kc, vc = pk.gather(i, pos)
+            kcc = np.zeros(kc.shape[:2] + (pos + 1, kc.shape[3]), np.uint16)
+            vcc = np.zeros_like(kcc)
+            kcc[:, :, :pos], vcc[:, :, :pos] = kc, vc
+            oracle_step(cfg, layers, norm, head, oracle.embed(head, int(tok[i].item())), pos, kcc, vcc)
+            done += 1
+            i = (i + 1) % n
+            if time.time() - t1 >= args.cpu_seconds:
+                break
+        dt = time.time() - t1
+        cpu = {"value": round(done / dt, 3), "unit": "tokens/s", "cores": oracle.get_threads(), "kind": "port",
+               "sample": f"{done} decode tokens of sequences 0..{min(done, n) - 1} at their own contexts "
+                         f"({dt:.1f} s, C restatement of the batch-1 graph, one sequence at a time)"}
+    line = base_line(METRIC_SERVER, n * 1000.0 / ms, "tokens/s", args, ms,
+                     {"workload": f"{n} concurrent sequences, one decode token each per step, contexts uniform in "
+                                  f"[128, 4096] (seed 0, mean {mean_ctx:.0f}) advancing during the run; Qwen2-0.5B "
+                                  f"-shaped 24-layer 4-bit LM, paged bf16 KV (64-position pages), greedy argmax",
+                      "global_batch": n, "seq_len": int(round(mean_ctx))},
+                     {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": nbytes,
+                      "launch_ms": round(ms, 5)},
+                     cpu, "synthetic (random-init N(0,0.02) weights quantized to MLX affine 4-bit/g64; KV N(0,1))")
+    print(json.dumps(line), flush=True)
 
 
 # ---- flow head -----------------------------------------------------------------------

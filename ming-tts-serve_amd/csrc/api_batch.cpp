@@ -20,7 +20,7 @@ struct ming_lm_batch {
     int H = 0, kvd = 0, nq = 0, I = 0, V = 0, L = 0;
     // every layer's activations, [layer][max_seqs][width]
     DevBuf x, x1, qkv, att, hh;
-    DevBuf xs, xsum, part, logits, hid, amax, rope;
+    DevBuf xs, xsum, part, pmax, pidx, hid, rope;
 };
 
 namespace {
@@ -78,9 +78,10 @@ int ming_lm_batch_create(ming_ctx* ctx, ming_lm_model* m, int32_t max_seqs, int3
     grab(b->hh, L * S * b->I * 2);
     grab(b->xs, Mp * kmax * 2);
     grab(b->xsum, Mp * (kmax / 64) * 4);
-    grab(b->logits, S * b->V * 4);
+    const size_t nblk = ((size_t)b->V + 63) / 64;  // column blocks of the head GEMM
+    grab(b->pmax, S * nblk * 4);
+    grab(b->pidx, S * nblk * 4);
     grab(b->hid, S * b->H * 2);
-    grab(b->amax, S * 4);
     grab(b->rope, (size_t)max_ctx * 32 * 2 * 4);
     const int max_splits = (max_ctx / 64 + 3) / 4;
     grab(b->part, S * c.kv_heads * max_splits * (c.heads / c.kv_heads) * 68 * 4);
@@ -98,8 +99,8 @@ int ming_lm_batch_create(ming_ctx* ctx, ming_lm_model* m, int32_t max_seqs, int3
 int ming_lm_batch_destroy(ming_lm_batch* b) {
     if (!b) return MING_OK;
     if (b->ctx && b->ctx->stream) (void)hipStreamSynchronize(b->ctx->stream);
-    for (DevBuf* d : {&b->x, &b->x1, &b->qkv, &b->att, &b->hh, &b->xs, &b->xsum, &b->part, &b->logits, &b->hid,
-                      &b->amax, &b->rope})
+    for (DevBuf* d : {&b->x, &b->x1, &b->qkv, &b->att, &b->hh, &b->xs, &b->xsum, &b->part, &b->pmax, &b->pidx,
+                      &b->hid, &b->rope})
         d->release();
     delete b;
     return MING_OK;
@@ -199,7 +200,8 @@ int ming_lm_batch_step(ming_lm_batch* b, int32_t n_seq, const int32_t* tokens_de
         pa.scale = 0.125f;  // 1/sqrt(64)
         e = launch_paged_attn(st, pa, n_seq);
         if (e != hipSuccess) break;
-        MergeArgs ma{pa.part, pos_dev, n_seq, c.heads, c.kv_heads, grp, max_splits, att, b->xs.p, xsum};
+        MergeArgs ma{pa.part, pos_dev, n_seq, c.heads, c.kv_heads, grp, max_splits, att, b->xs.p, xsum,
+                     (n_seq + 15) / 16 * 16};
         e = launch_merge_stage(st, ma);
         if (e != hipSuccess) break;
         const LinearDev* ol[1] = {&Ld.o};
@@ -221,10 +223,24 @@ int ming_lm_batch_step(ming_lm_batch* b, int32_t n_seq, const int32_t* tokens_de
                          hout, pos_dev);
     }
     if (e == hipSuccess && (logits_out || argmax_out)) {
-        float* lg = logits_out ? logits_out : static_cast<float*>(b->logits.p);
-        const LinearDev* hl[1] = {&b->view.head};
-        e = gemm(hl, 1, nullptr, QE_PLAIN, nullptr, b->V, nullptr, lg, nullptr);
-        if (e == hipSuccess && argmax_out) e = launch_argmax_rows(st, lg, n_seq, b->V, argmax_out);
+        // the head GEMM writes the f32 logits when asked and per-row argmax partials of each column block
+        QgemmArgs a{};
+        a.xs = b->xs.p;
+        a.xsum = xsum;
+        a.M = n_seq;
+        a.K = H;
+        a.nseg = 1;
+        const LinearDev& hd = b->view.head;
+        a.seg[0] = QSeg{hd.w, hd.s, hd.b, nullptr, hd.N, 0, hd.gscale};
+        a.yf = logits_out;
+        a.ldy = b->V;
+        if (argmax_out) {
+            a.pmax = static_cast<float*>(b->pmax.p);
+            a.pidx = static_cast<int32_t*>(b->pidx.p);
+        }
+        e = launch_qgemm_epi(st, a, QE_PLAIN);
+        if (e == hipSuccess && argmax_out)
+            e = launch_argmax_partials(st, a.pmax, a.pidx, (b->V + 63) / 64, n_seq, argmax_out);
     }
     if (e != hipSuccess) return hip_check(ctx, e, "lm_batch_step launch");
     b->last_n = n_seq;

@@ -39,8 +39,8 @@ struct QPaged {
 };
 
 struct QgemmArgs {
-    const void* xs;         // uint4 [Mp][K/8]: staged activations (pair order)
-    const float* xsum;      // [Mp][K/64]
+    const void* xs;         // uint4 [K/64][Mp][8]: staged activations (pair order, group-major)
+    const float* xsum;      // [K/64][Mp]
     int M, K;
     QSeg seg[3];
     int nseg;
@@ -51,6 +51,9 @@ struct QgemmArgs {
     const uint16_t* res;    // QE_RES: bf16 [M][ldres]
     int ldres;
     QPaged pg;
+    float* pmax;            // wide QE_PLAIN: per-row argmax partials [M][nblk] (max, index)
+    int32_t* pidx;
+    int nblk;               // set by the launcher
 };
 
 // Paged decode attention of n_seq sequences: one workgroup per (sequence,
@@ -74,8 +77,9 @@ struct MergeArgs {
     const int32_t* pos;
     int n_seq, heads, kvh, grp, max_splits;
     uint16_t* att;          // bf16 [n_seq][heads * 64]
-    void* xs;               // uint4 [Mp][heads * 8]
-    float* xsum;            // [Mp][heads]
+    void* xs;               // uint4 [heads][Mp][8]
+    float* xsum;            // [heads][Mp]
+    int Mp;                 // n_seq rounded up to 16
 };
 
 }  // namespace ming

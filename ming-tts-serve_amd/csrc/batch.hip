@@ -34,11 +34,12 @@ __global__ __launch_bounds__(256) void stage_kernel(const uint16_t* __restrict__
                                                     float* __restrict__ xsum, uint16_t* __restrict__ hout,
                                                     int32_t* __restrict__ pos_inc) {
     __shared__ float red[4];
-    const int m = blockIdx.x, tid = threadIdx.x, KW8 = K / 8, G = K / 64;
-    uint4* xr = xs + (size_t)m * KW8;
+    const int m = blockIdx.x, Mp = gridDim.x, tid = threadIdx.x, KW8 = K / 8, G = K / 64;
+    // group-major: word wi = 8 g + w of row m at xs[(g Mp + m) 8 + w], its group sum at xsum[g Mp + m]
+    auto xw = [&](int wi) { return xs + ((size_t)(wi / 8) * Mp + m) * 8 + wi % 8; };
     if (m >= M) {
-        for (int wi = tid; wi < KW8; wi += 256) gst(xr + wi, make_uint4(0, 0, 0, 0));
-        for (int g = tid; g < G; g += 256) gst(xsum + (size_t)m * G + g, 0.0f);
+        for (int wi = tid; wi < KW8; wi += 256) gst(xw(wi), make_uint4(0, 0, 0, 0));
+        for (int g = tid; g < G; g += 256) gst(xsum + (size_t)g * Mp + m, 0.0f);
         return;
     }
     const uint16_t* row = x + (size_t)m * ldx;
@@ -71,7 +72,7 @@ __global__ __launch_bounds__(256) void stage_kernel(const uint16_t* __restrict__
             v = make_uint4(o[0], o[1], o[2], o[3]);
         }
         if (hout) gst(reinterpret_cast<uint4*>(hout + (size_t)m * K) + wi, v);
-        gst(xr + wi, pair_order(v));
+        gst(xw(wi), pair_order(v));
         const uint32_t e[4] = {v.x, v.y, v.z, v.w};
         float s = 0.0f;
 #pragma unroll
@@ -79,7 +80,7 @@ __global__ __launch_bounds__(256) void stage_kernel(const uint16_t* __restrict__
         s += __shfl_xor(s, 1);
         s += __shfl_xor(s, 2);
         s += __shfl_xor(s, 4);
-        if (tid % 8 == 0) gst(xsum + (size_t)m * G + wi / 8, s);
+        if (tid % 8 == 0) gst(xsum + (size_t)(wi / 8) * Mp + m, s);
     }
     if (pos_inc && tid == 0) gst(pos_inc + m, gld(pos_inc + m) + 1);
 }
@@ -315,50 +316,11 @@ __global__ __launch_bounds__(256) void merge_stage_kernel(MergeArgs a) {
     gst(a.att + (size_t)b * H + h * 64 + lane, (uint16_t)hb);
     const uint32_t word = hb | (__shfl_down(hb, 4) << 16);  // lanes with lane % 8 < 4
     const uint32_t w1 = __shfl_down(word, 1), w2 = __shfl_down(word, 2), w3 = __shfl_down(word, 3);
+    // the head's 64 dims are group h of the o projection's K (group-major staging)
     if (lane % 8 == 0)
-        gst(static_cast<uint4*>(a.xs) + (size_t)b * (H / 8) + h * 8 + lane / 8, make_uint4(word, w1, w2, w3));
+        gst(static_cast<uint4*>(a.xs) + ((size_t)h * a.Mp + b) * 8 + lane / 8, make_uint4(word, w1, w2, w3));
     const float sum = team_sum<kWave>(bf2f((uint16_t)hb));
-    if (lane == 0) gst(a.xsum + (size_t)b * a.heads + h, sum);
-}
-
-// ---- greedy argmax per row (lowest index on ties) --------------------------------------
-__global__ __launch_bounds__(256) void argmax_rows_kernel(const float* __restrict__ logits, int V,
-                                                          int32_t* __restrict__ out) {
-    __shared__ float bv[4];
-    __shared__ int bi[4];
-    const float* row = logits + (size_t)blockIdx.x * V;
-    float best = -INFINITY;
-    int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < V; i += 256) {
-        const float v = gld(row + i);
-        if (v > best) {
-            best = v;
-            idx = i;
-        }
-    }
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-        const float ov = __shfl_xor(best, d);
-        const int oi = __shfl_xor(idx, d);
-        if (ov > best || (ov == best && oi < idx)) {
-            best = ov;
-            idx = oi;
-        }
-    }
-    const int wave = threadIdx.x / kWave;
-    if (threadIdx.x % kWave == 0) {
-        bv[wave] = best;
-        bi[wave] = idx;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; w++)
-            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) {
-                best = bv[w];
-                idx = bi[w];
-            }
-        gst(out + blockIdx.x, idx == 0x7fffffff ? 0 : idx);
-    }
+    if (lane == 0) gst(a.xsum + (size_t)h * a.Mp + b, sum);
 }
 
 }  // namespace
@@ -394,11 +356,6 @@ hipError_t launch_paged_attn(hipStream_t st, const PagedAttnArgs& a, int n_seq) 
 hipError_t launch_merge_stage(hipStream_t st, const MergeArgs& a) {
     const int items = a.n_seq * a.heads;
     hipLaunchKernelGGL(merge_stage_kernel, dim3((items + 3) / 4), dim3(256), 0, st, a);
-    return hipGetLastError();
-}
-
-hipError_t launch_argmax_rows(hipStream_t st, const float* logits, int n, int V, int32_t* out) {
-    hipLaunchKernelGGL(argmax_rows_kernel, dim3(n), dim3(256), 0, st, logits, V, out);
     return hipGetLastError();
 }
 

@@ -61,15 +61,19 @@ hipError_t launch_quantize(hipStream_t st, const uint16_t* w, int64_t N, int64_t
 // Batched 4-bit GEMM on MFMA over activations staged by launch_stage; a.blocks
 // is filled by the launcher.  epi is a QEpi.
 hipError_t launch_qgemm_epi(hipStream_t st, QgemmArgs a, int epi);
+// Per-row argmax of n rows from the wide GEMM's partials [n][nblk]
+// (nblk = ceil(N / 64) column blocks).
+hipError_t launch_argmax_partials(hipStream_t st, const float* pmax, const int32_t* pidx, int nblk, int n,
+                                  int32_t* out);
 // Rows [0, Mp) of x [M][ldx] (Mp = M rounded up to 16; rows >= M zero) staged
-// as uint4 xs [Mp][K/8] + f32 xsum [Mp][K/64]; norm_w non-null: rms first.
+// group-major as uint4 xs [K/64][Mp][8] + f32 xsum [K/64][Mp]; norm_w
+// non-null: rms first.
 hipError_t launch_stage(hipStream_t st, const uint16_t* x, int ldx, int M, int K, const uint16_t* norm_w, float eps,
                         void* xs, float* xsum, uint16_t* hout, int32_t* pos_inc);
 hipError_t launch_embed_rows(hipStream_t st, const LinearDev& E, const int32_t* tokens, int n, uint16_t* x);
 hipError_t launch_rope_table(hipStream_t st, float* cs, int max_ctx, int half, float log2_theta);
 hipError_t launch_paged_attn(hipStream_t st, const PagedAttnArgs& a, int n_seq);
 hipError_t launch_merge_stage(hipStream_t st, const MergeArgs& a);
-hipError_t launch_argmax_rows(hipStream_t st, const float* logits, int n, int V, int32_t* out);
 
 // Read-only view of a prepared decode stack (for the batched step).
 struct LmView {

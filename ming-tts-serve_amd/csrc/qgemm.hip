@@ -19,11 +19,13 @@
 // (8 words) lane l takes words 2j and 2j+1 (j = l / 16), one per MFMA, so each
 // MFMA's 32 k lie in one group and a lane loads 8 contiguous bytes per row.
 //
-// Workgroup: KW waves split the groups of K; each wave accumulates MT x 16
-// rows by NW x 16 columns, keeping the next group's loads in flight while the
-// current group's MFMAs run; the waves' partial sums are added through LDS and
-// the first wave applies the epilogue (QEpi).  One call may concatenate up to
-// three matrices along N (q/k/v; gate/up), each a run of workgroups.
+// Workgroup (column block x, row-tile group y): KW waves split the groups of
+// K; each wave accumulates MT x 16 rows by NW x 16 columns, with two groups'
+// loads in flight while one group's MFMAs run; the waves' partial sums are
+// added through LDS and every wave applies the epilogue (QEpi) to its share of
+// the rows.  One call may concatenate up to three matrices along N (q/k/v;
+// gate/up), each a run of workgroups.  Staged activations are group-major:
+// xs [K/64][Mp][8] 16-byte words, xsum [K/64][Mp] (Mp = M rounded up to 16).
 #include "batch.h"
 #include "common.h"
 #include "internal.h"
@@ -41,11 +43,18 @@ __device__ __forceinline__ uint2 ldg2(const void* p) {
     return make_uint2(v.x, v.y);
 }
 
+// A value the compiler must keep in a register: with the nibble mask and the
+// magic constant in registers, each pair is one v_and_or_b32 (gfx9 VOP3 takes
+// no literal operands, so with literals it would be an AND and an OR).
+__device__ __forceinline__ uint32_t in_reg(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 // bf16 pairs (128 + q_i, 128 + q_{i+4}) of one packed word, as the 8-value B operand.
-__device__ __forceinline__ bf16x8_t unpack_b(uint32_t w) {
-    return __builtin_bit_cast(bf16x8_t, u32x4_t{(w & 0x000f000fu) | kQ4Magic, ((w >> 4) & 0x000f000fu) | kQ4Magic,
-                                                ((w >> 8) & 0x000f000fu) | kQ4Magic,
-                                                ((w >> 12) & 0x000f000fu) | kQ4Magic});
+__device__ __forceinline__ bf16x8_t unpack_b(uint32_t w, uint32_t mask, uint32_t magic) {
+    return __builtin_bit_cast(bf16x8_t, u32x4_t{(w & mask) | magic, ((w >> 4) & mask) | magic,
+                                                ((w >> 8) & mask) | magic, ((w >> 12) & mask) | magic});
 }
 
 __device__ __forceinline__ bf16x8_t as_a(uint4 v) { return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w}); }
@@ -59,52 +68,76 @@ template <int MT, int NW>
 struct GroupIn {
     uint2 wq[NW];       // words 2j, 2j+1 of the group, weight row of tile t
     float sc[NW], bi[NW];
-    uint4 xa[MT][2];    // A operand words 2j, 2j+1 of row 16mt + c
-    float xsv[MT][4];   // group sums of rows 16mt + 4j + r
+    uint4 xa[MT][2];    // A operand words 2j, 2j+1 of row 16 mt + c
+    float4 xsv[MT];     // group sums of rows 16 mt + 4j + r, r = 0..3
 };
 
+// Per-lane 32-bit byte offsets from the uniform bases: the loads then take a
+// scalar base plus a 32-bit vector offset, with no per-load 64-bit arithmetic.
 template <int MT, int NW>
-struct Rows {
-    const uint32_t* w[NW];
-    const uint16_t* s[NW];
-    const uint16_t* b[NW];
+struct Offs {
+    uint32_t w[NW];     // row n_t * K/2 + 8j
+    uint32_t s[NW];     // row n_t * G * 2
+    uint32_t x;         // ((16 mt0 + c) * 8 + 2j) * 16     (+ g * Mp * 128 + 2048 mt)
+    uint32_t xs;        // (16 mt0 + 4j) * 4                  (+ g * Mp * 4 + 64 mt)
 };
 
-template <int MT, int NW>
-__device__ __forceinline__ void group_load(const QgemmArgs& a, const Rows<MT, NW>& R, int g, int c, int j,
-                                           GroupIn<MT, NW>& in) {
-    const int G = a.K / 64, KW8 = a.K / 8;
-    const uint4* xs = static_cast<const uint4*>(a.xs);
-#pragma unroll
-    for (int t = 0; t < NW; t++) {
-        in.wq[t] = ldg2(R.w[t] + 8 * g + 2 * j);
-        in.sc[t] = bf2f(gld(R.s[t] + g));
-        in.bi[t] = bf2f(gld(R.b[t] + g));
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-        const uint4* xp = xs + (size_t)(16 * mt + c) * KW8 + 8 * g + 2 * j;
-        in.xa[mt][0] = ldg4(xp);
-        in.xa[mt][1] = ldg4(xp + 1);
-#pragma unroll
-        for (int r = 0; r < 4; r++) in.xsv[mt][r] = gld(a.xsum + (size_t)(16 * mt + 4 * j + r) * G + g);
-    }
+template <class T>
+__device__ __forceinline__ const T* at(const T* base, uint32_t byte_off) {
+    return reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + byte_off);
 }
 
 template <int MT, int NW>
-__device__ __forceinline__ void group_mma(const GroupIn<MT, NW>& in, f32x4_t (&acc)[MT][NW]) {
+__device__ __forceinline__ void group_load(const QgemmArgs& a, const uint32_t* const (&wb)[NW],
+                                           const uint16_t* const (&sb)[NW], const uint16_t* const (&bb)[NW],
+                                           const Offs<MT, NW>& o, int Mp, int g, GroupIn<MT, NW>& in) {
+    const uint4* xs = static_cast<const uint4*>(a.xs);
 #pragma unroll
     for (int t = 0; t < NW; t++) {
-        const bf16x8_t b0 = unpack_b(in.wq[t].x), b1 = unpack_b(in.wq[t].y);
-        const float s = in.sc[t], off = in.bi[t] - 128.0f * in.sc[t];
+        in.wq[t] = ldg2(at(wb[t], o.w[t] + 32u * g));
+        in.sc[t] = bf2f(gld(at(sb[t], o.s[t] + 2u * g)));
+        in.bi[t] = bf2f(gld(at(bb[t], o.s[t] + 2u * g)));
+    }
+    const uint32_t xg = o.x + (uint32_t)g * Mp * 128u, sg = o.xs + (uint32_t)g * Mp * 4u;
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        in.xa[mt][0] = ldg4(at(xs, xg + 2048u * mt));
+        in.xa[mt][1] = ldg4(at(xs, xg + 2048u * mt + 16u));
+        const uint4 v = ldg4(at(a.xsum, sg + 64u * mt));
+        in.xsv[mt] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+    }
+}
+
+// acc += s * sum_k (128 + q_k) x_k + (b - 128 s) * sum_k x_k for one group.  The
+// MFMAs of tile t + 1 are issued before tile t is folded, so the fold's VALU
+// work covers the matrix core's latency.
+template <int MT, int NW>
+__device__ __forceinline__ void group_mma(const GroupIn<MT, NW>& in, f32x4_t (&acc)[MT][NW], uint32_t mask,
+                                          uint32_t magic) {
+    f32x4_t ag[2][MT];
+    auto issue = [&](int t, f32x4_t (&dst)[MT]) {
+        const bf16x8_t b0 = unpack_b(in.wq[t].x, mask, magic), b1 = unpack_b(in.wq[t].y, mask, magic);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+            dst[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_a(in.xa[mt][0]), b0, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+            dst[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_a(in.xa[mt][1]), b1, dst[mt], 0, 0, 0);
+    };
+    auto fold = [&](int t, const f32x4_t (&src)[MT]) {
+        const float s = in.sc[t], off = fmaf(-128.0f, in.sc[t], in.bi[t]);
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
-            f32x4_t ag = {0.0f, 0.0f, 0.0f, 0.0f};
-            ag = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_a(in.xa[mt][0]), b0, ag, 0, 0, 0);
-            ag = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_a(in.xa[mt][1]), b1, ag, 0, 0, 0);
+            const float xv[4] = {in.xsv[mt].x, in.xsv[mt].y, in.xsv[mt].z, in.xsv[mt].w};
 #pragma unroll
-            for (int r = 0; r < 4; r++) acc[mt][t][r] += s * ag[r] + off * in.xsv[mt][r];
+            for (int r = 0; r < 4; r++) acc[mt][t][r] = fmaf(off, xv[r], fmaf(s, src[mt][r], acc[mt][t][r]));
         }
+    };
+    issue(0, ag[0]);
+#pragma unroll
+    for (int t = 0; t < NW; t++) {
+        if (t + 1 < NW) issue(t + 1, ag[(t + 1) & 1]);
+        fold(t, ag[t & 1]);
     }
 }
 
@@ -150,10 +183,44 @@ __device__ __forceinline__ void qkv_row(const QgemmArgs& a, const QSeg& S, int s
     }
 }
 
-template <int MT, int NW, int KW, int EPI>
-__global__ __launch_bounds__(64 * KW) void qgemm_kernel(QgemmArgs a) {
-    extern __shared__ float red[];  // [KW - 1][MT][NW][4][64]
+// Per-row argmax of the workgroup's columns (lowest index on ties): lanes of
+// one j hold one row; v[t] is column n0 + 16t + c.
+template <int NW>
+__device__ __forceinline__ void row_argmax(const QgemmArgs& a, int n0, int c, int m, const float (&v)[NW], int N) {
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+#pragma unroll
+    for (int t = 0; t < NW; t++) {
+        const int n = n0 + 16 * t + c;
+        if (n < N && v[t] > best) {
+            best = v[t];
+            idx = n;
+        }
+    }
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) {
+        const float ov = __shfl_xor(best, d);
+        const int oi = __shfl_xor(idx, d);
+        if (ov > best || (ov == best && oi < idx)) {
+            best = ov;
+            idx = oi;
+        }
+    }
+    if (c == 0) {
+        const int blk = n0 / (16 * NW);
+        gst(a.pmax + (size_t)m * a.nblk + blk, best);
+        gst(a.pidx + (size_t)m * a.nblk + blk, idx);
+    }
+}
+
+// KW = blockDim.x / 64 waves (<= KWMAX) split the K/64 groups; each wave takes
+// its groups either through a three-deep register ring (GPW = 0) or in chunks
+// of GPW whose loads are all issued before the chunk's MFMAs.
+template <int MT, int NW, int GPW, int KWMAX, int EPI>
+__global__ __launch_bounds__(64 * KWMAX) void qgemm_kernel(QgemmArgs a) {
+    extern __shared__ float red[];  // [KW][MT * 4][NW][64]
     constexpr int TPS = EPI == QE_SWIGLU ? NW / 2 : NW;  // column tiles per segment and workgroup
+    const int KW = blockDim.x / kWave;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, c = lane % 16, j = lane / 16;
     int blk = blockIdx.x, si = 0;
     if (EPI != QE_SWIGLU && a.nseg > 1 && blk >= a.blocks[0]) {
@@ -165,61 +232,90 @@ __global__ __launch_bounds__(64 * KW) void qgemm_kernel(QgemmArgs a) {
         }
     }
     const int n0 = blk * 16 * TPS;
-    const int G = a.K / 64, KW8 = a.K / 8;
-    Rows<MT, NW> R;
+    const int G = a.K / 64, KW8 = a.K / 8, MTT = (a.M + 15) / 16, Mp = 16 * MTT;
+    const int mt0 = blockIdx.y * MT;  // the launcher picks MT dividing MTT
+    const uint32_t* wb[NW];
+    const uint16_t* sb[NW];
+    const uint16_t* bb[NW];
+    Offs<MT, NW> o;
 #pragma unroll
     for (int t = 0; t < NW; t++) {
         const QSeg& S = pick(a, EPI == QE_SWIGLU ? (t < TPS ? 0 : 1) : si);
         const int n = min(n0 + 16 * (t % TPS) + c, S.N - 1);
-        R.w[t] = S.w + (size_t)n * KW8;
-        R.s[t] = S.s + (size_t)n * G;
-        R.b[t] = S.b + (size_t)n * G;
+        wb[t] = S.w;
+        sb[t] = S.s;
+        bb[t] = S.b;
+        o.w[t] = (uint32_t)n * KW8 * 4u + 8u * j;
+        o.s[t] = (uint32_t)n * G * 2u;
     }
+    o.x = ((uint32_t)(16 * mt0 + c) * 8u + 2u * j) * 16u;
+    o.xs = (uint32_t)(16 * mt0 + 4 * j) * 4u;
     const int gper = (G + KW - 1) / KW, g0 = wave * gper, g1 = min(G, g0 + gper);
     f32x4_t acc[MT][NW];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
         for (int t = 0; t < NW; t++) acc[mt][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    if (g0 < g1) {
-        GroupIn<MT, NW> cur, nxt;
-        group_load<MT, NW>(a, R, g0, c, j, cur);
-        for (int g = g0; g < g1; g++) {
-            if (g + 1 < g1) group_load<MT, NW>(a, R, g + 1, c, j, nxt);
-            group_mma<MT, NW>(cur, acc);
-            if (g + 1 < g1) cur = nxt;
+    const uint32_t mask = in_reg(0x000f000fu), magic = in_reg(kQ4Magic);
+    if constexpr (GPW == 0) {
+        // a ring of three groups in registers: two groups' loads in flight while one computes
+        if (g0 < g1) {
+            GroupIn<MT, NW> b0, b1, b2;
+            group_load<MT, NW>(a, wb, sb, bb, o, Mp, g0, b0);
+            if (g0 + 1 < g1) group_load<MT, NW>(a, wb, sb, bb, o, Mp, g0 + 1, b1);
+            for (int g = g0; g < g1; g += 3) {
+                if (g + 2 < g1) group_load<MT, NW>(a, wb, sb, bb, o, Mp, g + 2, b2);
+                group_mma<MT, NW>(b0, acc, mask, magic);
+                if (g + 1 >= g1) break;
+                if (g + 3 < g1) group_load<MT, NW>(a, wb, sb, bb, o, Mp, g + 3, b0);
+                group_mma<MT, NW>(b1, acc, mask, magic);
+                if (g + 2 >= g1) break;
+                if (g + 4 < g1) group_load<MT, NW>(a, wb, sb, bb, o, Mp, g + 4, b1);
+                group_mma<MT, NW>(b2, acc, mask, magic);
+            }
+        }
+    } else {
+        // chunks of GPW groups whose loads are all issued before the chunk's MFMAs
+        for (int gb = g0; gb < g1; gb += GPW) {
+            GroupIn<MT, NW> in[GPW];
+#pragma unroll
+            for (int u = 0; u < GPW; u++)
+                if (gb + u < g1) group_load<MT, NW>(a, wb, sb, bb, o, Mp, gb + u, in[u]);
+#pragma unroll
+            for (int u = 0; u < GPW; u++)
+                if (gb + u < g1) group_mma<MT, NW>(in[u], acc, mask, magic);
         }
     }
-    if (KW > 1) {
-        if (wave > 0)
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                for (int t = 0; t < NW; t++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        red[((((wave - 1) * MT + mt) * NW + t) * 4 + r) * kWave + lane] = acc[mt][t][r];
-        __syncthreads();
-        if (wave > 0) return;
+    // the waves' partial sums through LDS; wave w then owns the row slots u = mt * 4 + r with u % KW == w
+    if (KWMAX > 1) {
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-            for (int t = 0; t < NW; t++)
+            for (int r = 0; r < 4; r++)
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    for (int w = 1; w < KW; w++) acc[mt][t][r] += red[((((w - 1) * MT + mt) * NW + t) * 4 + r) * kWave + lane];
+                for (int t = 0; t < NW; t++) red[(((wave * MT + mt) * 4 + r) * NW + t) * kWave + lane] = acc[mt][t][r];
+        __syncthreads();
     }
     const QSeg& S = pick(a, si);
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const int m = 16 * mt + 4 * j + r;
+            if ((mt * 4 + r) % KW != wave) continue;
+            const int m = 16 * (mt0 + mt) + 4 * j + r;
             if (m >= a.M) continue;
-            if constexpr (EPI == QE_QKV) {
-                float v[NW];
+            float v[NW];
 #pragma unroll
-                for (int t = 0; t < NW; t++) v[t] = acc[mt][t][r];
+            for (int t = 0; t < NW; t++) {
+                if (KWMAX > 1) {
+                    float sum = 0.0f;
+                    for (int w = 0; w < KW; w++) sum += red[(((w * MT + mt) * 4 + r) * NW + t) * kWave + lane];
+                    v[t] = sum;
+                } else {
+                    v[t] = acc[mt][t][r];
+                }
+            }
+            if constexpr (EPI == QE_QKV) {
                 qkv_row<MT, NW>(a, S, si, n0, c, m, v);
             } else if constexpr (EPI == QE_SWIGLU) {
                 const float gg = a.seg[0].gscale, gu = a.seg[1].gscale;
@@ -227,52 +323,58 @@ __global__ __launch_bounds__(64 * KW) void qgemm_kernel(QgemmArgs a) {
                 for (int t = 0; t < TPS; t++) {
                     const int n = n0 + 16 * t + c;
                     if (n >= S.N) continue;
-                    const float gv = rb(acc[mt][t][r] * gg), u = rb(acc[mt][t + TPS][r] * gu);
+                    const float gv = rb(v[t] * gg), u = rb(v[t + TPS] * gu);
                     const float sg = rb(1.0f / (1.0f + expf(-gv)));
                     gst(a.y + (size_t)m * a.ldy + n, f2bf(rb(gv * sg) * u));
                 }
             } else {
 #pragma unroll
                 for (int t = 0; t < NW; t++) {
+                    v[t] *= S.gscale;
                     const int n = n0 + 16 * t + c;
                     if (n >= S.N) continue;
-                    const float v = acc[mt][t][r] * S.gscale;
-                    const size_t o = (size_t)m * a.ldy + S.col0 + n;
+                    const size_t off = (size_t)m * a.ldy + S.col0 + n;
                     if constexpr (EPI == QE_RES) {
-                        gst(a.y + o, f2bf(bf2f(gld(a.res + (size_t)m * a.ldres + S.col0 + n)) + rb(v)));
+                        gst(a.y + off, f2bf(bf2f(gld(a.res + (size_t)m * a.ldres + S.col0 + n)) + rb(v[t])));
                     } else {
-                        if (a.y) gst(a.y + o, f2bf(v));
-                        if (a.yf) gst(a.yf + o, v);
+                        if (a.y) gst(a.y + off, f2bf(v[t]));
+                        if (a.yf) gst(a.yf + off, v[t]);
                     }
                 }
+                if constexpr (EPI == QE_PLAIN)
+                    if (a.pmax) row_argmax<NW>(a, n0, c, m, v, S.N);
             }
         }
 }
 
-template <int MT, int NW, int KW, int EPI>
+template <int MT, int NW, int GPW, int KWMAX, int EPI>
 hipError_t launch_k(hipStream_t st, const QgemmArgs& a) {
     const int grid = a.blocks[0] + (a.nseg > 1 ? a.blocks[1] : 0) + (a.nseg > 2 ? a.blocks[2] : 0);
-    const size_t lds = sizeof(float) * (size_t)(KW - 1) * MT * NW * 4 * kWave;
-    hipLaunchKernelGGL((qgemm_kernel<MT, NW, KW, EPI>), dim3(grid), dim3(64 * KW), lds, st, a);
+    const int mtt = (a.M + 15) / 16, gy = mtt / MT;
+    const int G = a.K / 64, kw = GPW == 0 ? KWMAX : min(KWMAX, (G + GPW - 1) / GPW);
+    const size_t lds = KWMAX > 1 ? sizeof(float) * (size_t)kw * MT * 4 * NW * kWave : 0;
+    hipLaunchKernelGGL((qgemm_kernel<MT, NW, GPW, KWMAX, EPI>), dim3(grid, gy), dim3(64 * kw), lds, st, a);
     return hipGetLastError();
 }
 
-template <int NW, int EPI>
+// row tiles per workgroup: 2 when MTMAX allows and the row-tile count is even, else 1
+template <int NW, int GPW, int KWMAX, int EPI, int MTMAX>
 hipError_t launch_mt(hipStream_t st, const QgemmArgs& a) {
-    switch ((a.M + 15) / 16) {
-        case 1: return launch_k<1, NW, 4, EPI>(st, a);
-        case 2: return launch_k<2, NW, 4, EPI>(st, a);
-        case 3: return launch_k<3, NW, 4, EPI>(st, a);
-        case 4: return launch_k<4, NW, 4, EPI>(st, a);
-        default: return hipErrorInvalidValue;
-    }
+    const int mtt = (a.M + 15) / 16;
+    if constexpr (MTMAX >= 2)
+        if (mtt % 2 == 0) return launch_k<2, NW, GPW, KWMAX, EPI>(st, a);
+    return launch_k<1, NW, GPW, KWMAX, EPI>(st, a);
 }
 
 }  // namespace
 
-// a.blocks is filled here: wide matrices (plain epilogue, N >= 16384) take 4
-// column tiles per wave, narrow ones 1 so that they still spread over the CUs;
-// q/k/v take one head (4 tiles) per workgroup, gate/up 2 + 2 tiles.
+// a.blocks is filled here.  Shapes: the LM head 4 column tiles x 2 row tiles
+// per wave, one wave per workgroup streaming all of K through the register
+// ring; gate/up 2 + 2 column tiles x 2 row tiles, two waves splitting K; q/k/v
+// one head (4 tiles) x 1 row tile, K in chunks of 2 groups over up to 8
+// waves; the narrow o/down projections 1 x 1, K in chunks of 5 groups over up
+// to 16 waves, so that they still spread over the CUs.  (Four row tiles per
+// wave would keep the accumulators in AGPRs.)
 hipError_t launch_qgemm_epi(hipStream_t st, QgemmArgs a, int epi) {
     if (a.M < 1 || a.M > 64 || a.K % 64 || a.nseg < 1 || a.nseg > 3) return hipErrorInvalidValue;
     auto set_blocks = [&a](int cols) {
@@ -280,29 +382,80 @@ hipError_t launch_qgemm_epi(hipStream_t st, QgemmArgs a, int epi) {
     };
     switch (epi) {
         case QE_PLAIN:
-            if (a.nseg == 1 && a.seg[0].N >= 16384) {
+            if (a.nseg == 1 && (a.seg[0].N >= 16384 || a.pmax)) {  // argmax partials: blocks of 64 columns
                 set_blocks(64);
-                return launch_mt<4, QE_PLAIN>(st, a);
+                a.nblk = a.blocks[0];
+                return launch_mt<4, 0, 1, QE_PLAIN, 2>(st, a);
             }
+            if (a.pmax) return hipErrorInvalidValue;
             set_blocks(16);
-            return launch_mt<1, QE_PLAIN>(st, a);
+            return launch_mt<1, 5, 16, QE_PLAIN, 1>(st, a);
         case QE_RES:
             set_blocks(16);
-            return launch_mt<1, QE_RES>(st, a);
+            return launch_mt<1, 5, 16, QE_RES, 1>(st, a);
         case QE_SWIGLU:
             if (a.nseg != 2 || a.seg[0].N != a.seg[1].N) return hipErrorInvalidValue;
             set_blocks(32);
             a.blocks[1] = 0;
-            return launch_mt<4, QE_SWIGLU>(st, a);
+            return launch_mt<4, 0, 2, QE_SWIGLU, 2>(st, a);
         case QE_QKV:
             if (a.nseg != 3) return hipErrorInvalidValue;
             for (int i = 0; i < 3; i++)
                 if (a.seg[i].N % 64) return hipErrorInvalidValue;
             set_blocks(64);
-            return launch_mt<4, QE_QKV>(st, a);
+            return launch_mt<4, 2, 8, QE_QKV, 1>(st, a);
         default:
             return hipErrorInvalidValue;
     }
+}
+
+// Final argmax over the head GEMM's per-workgroup partials: one workgroup per row.
+__global__ __launch_bounds__(256) void argmax_partials_kernel(const float* __restrict__ pmax,
+                                                              const int32_t* __restrict__ pidx, int nblk,
+                                                              int32_t* __restrict__ out) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    const float* pm = pmax + (size_t)blockIdx.x * nblk;
+    const int32_t* pi = pidx + (size_t)blockIdx.x * nblk;
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < nblk; i += 256) {
+        const float v = gld(pm + i);
+        const int k = gld(pi + i);
+        if (v > best || (v == best && k < idx)) {
+            best = v;
+            idx = k;
+        }
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        const float ov = __shfl_xor(best, d);
+        const int oi = __shfl_xor(idx, d);
+        if (ov > best || (ov == best && oi < idx)) {
+            best = ov;
+            idx = oi;
+        }
+    }
+    const int wave = threadIdx.x / kWave;
+    if (threadIdx.x % kWave == 0) {
+        bv[wave] = best;
+        bi[wave] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++)
+            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) {
+                best = bv[w];
+                idx = bi[w];
+            }
+        gst(out + blockIdx.x, idx == 0x7fffffff ? 0 : idx);
+    }
+}
+
+hipError_t launch_argmax_partials(hipStream_t st, const float* pmax, const int32_t* pidx, int nblk, int n,
+                                  int32_t* out) {
+    hipLaunchKernelGGL(argmax_partials_kernel, dim3(n), dim3(256), 0, st, pmax, pidx, nblk, out);
+    return hipGetLastError();
 }
 
 }  // namespace ming
