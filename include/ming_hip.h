@@ -278,6 +278,22 @@ int ming_lm_batch_step(ming_lm_batch* b, int32_t n_seq, const int32_t* tokens_de
                        const ming_kv_pages* kv, const int32_t* page_table_dev, int32_t pages_per_seq, int32_t* pos_dev,
                        void* hidden_out, float* logits_out, int32_t* argmax_out);
 
+/* Multi-token prefill of one sequence (QStack prefill over the prompt,
+ * src/ming_model.zig:576-614: every layer over L rows with causal attention):
+ * rows [0, L) -- the embeddings of tokens_dev (i32 [L]) or x_in (bf16
+ * [L][hidden]) -- at positions pos0 .. pos0 + L - 1 of the sequence whose
+ * pages are page_table_dev (i32 [pages_per_seq]).  Row i attends to
+ * positions <= pos0 + i; the k/v rows of every position are written into the
+ * pages.  Runs as ceil(L / max_seqs) batched steps in which the rows are
+ * sequences sharing one page table, so each row's result equals a one-row
+ * ming_lm_batch_step at that position bit for bit.  Outputs (optional,
+ * device): hidden_out bf16 [L][hidden], logits_out f32 [L][vocab],
+ * argmax_out i32 [L].  pos0 + L > pages_per_seq * 64 returns
+ * MING_E_CTX_OVER_CAPACITY before anything is launched. */
+int ming_lm_prefill(ming_lm_batch* b, int32_t L, const int32_t* tokens_dev, const void* x_in, const ming_kv_pages* kv,
+                    const int32_t* page_table_dev, int32_t pages_per_seq, int32_t pos0, void* hidden_out,
+                    float* logits_out, int32_t* argmax_out);
+
 /* Per-layer activations of the last ming_lm_batch_step (n_seq rows each), as
  * ming_lm_model_trace lays them out with a sequence axis after the layer
  * axis: x [n_layers + 1][n_seq][hidden], x1 and att [n_layers][n_seq][hidden],

@@ -179,6 +179,8 @@ def lib():
         "ming_lm_batch_step": (c_i32, [c_void_p, c_i32, c_void_p, c_void_p, P(KvPages), c_void_p, c_i32, c_void_p,
                                        c_void_p, c_void_p, c_void_p]),
         "ming_lm_batch_trace": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+        "ming_lm_prefill": (c_i32, [c_void_p, c_i32, c_void_p, c_void_p, P(KvPages), c_void_p, c_i32, c_i32,
+                                    c_void_p, c_void_p, c_void_p]),
         "ming_rotary_table": (c_i32, [c_void_p, c_void_p, c_i32, c_i32, c_void_p, c_void_p]),
         "ming_dit_block": (c_i32, [c_void_p, P(DitCfg), P(DitBlockW), c_void_p, c_i32, c_i32, c_void_p, c_void_p,
                                    P(DitOut)]),
@@ -558,6 +560,15 @@ class LmBatch:
                                                      ptr(table), pps, ptr(pos), ptr(hidden), ptr(logits),
                                                      ptr(argmax)))
         self.n = n
+
+    def prefill(self, pages, table_row, pos0, tokens=None, x_in=None, hidden=None, logits=None, argmax=None, L=None):
+        """Causal prefill of one sequence: rows at positions pos0.. over its pages
+        (table_row: device i32 [pages_per_seq])."""
+        n = int(L if L is not None else (tokens.shape[0] if tokens is not None else x_in.shape[0]))
+        self.ctx.check(self.ctx.L.ming_lm_prefill(self.h, n, ptr(tokens), ptr(x_in), ctypes.byref(pages.kv),
+                                                  ptr(table_row), int(table_row.shape[-1]), int(pos0), ptr(hidden),
+                                                  ptr(logits), ptr(argmax)))
+        self.n = min(n, self.max_seqs) if n <= self.max_seqs else n - (n - 1) // self.max_seqs * self.max_seqs
 
     def trace(self):
         """dict of per-layer activations [layer][seq][...] of the last step (device bf16)."""

@@ -21,6 +21,7 @@ struct ming_lm_batch {
     // every layer's activations, [layer][max_seqs][width]
     DevBuf x, x1, qkv, att, hh;
     DevBuf xs, xsum, part, pmax, pidx, hid, rope;
+    DevBuf prows, ppos;  // prefill: page-table rows and positions of one chunk
 };
 
 namespace {
@@ -82,6 +83,8 @@ int ming_lm_batch_create(ming_ctx* ctx, ming_lm_model* m, int32_t max_seqs, int3
     grab(b->pmax, S * nblk * 4);
     grab(b->pidx, S * nblk * 4);
     grab(b->hid, S * b->H * 2);
+    grab(b->prows, S * (size_t)(max_ctx / 64) * 4);
+    grab(b->ppos, S * 4);
     grab(b->rope, (size_t)max_ctx * 32 * 2 * 4);
     const int max_splits = (max_ctx / 64 + 3) / 4;
     grab(b->part, S * c.kv_heads * max_splits * (c.heads / c.kv_heads) * 68 * 4);
@@ -100,7 +103,7 @@ int ming_lm_batch_destroy(ming_lm_batch* b) {
     if (!b) return MING_OK;
     if (b->ctx && b->ctx->stream) (void)hipStreamSynchronize(b->ctx->stream);
     for (DevBuf* d : {&b->x, &b->x1, &b->qkv, &b->att, &b->hh, &b->xs, &b->xsum, &b->part, &b->pmax, &b->pidx,
-                      &b->hid, &b->rope})
+                      &b->hid, &b->rope, &b->prows, &b->ppos})
         d->release();
     delete b;
     return MING_OK;
@@ -244,6 +247,36 @@ int ming_lm_batch_step(ming_lm_batch* b, int32_t n_seq, const int32_t* tokens_de
     }
     if (e != hipSuccess) return hip_check(ctx, e, "lm_batch_step launch");
     b->last_n = n_seq;
+    return MING_OK;
+}
+
+int ming_lm_prefill(ming_lm_batch* b, int32_t L, const int32_t* tokens_dev, const void* x_in, const ming_kv_pages* kv,
+                    const int32_t* page_table_dev, int32_t pages_per_seq, int32_t pos0, void* hidden_out,
+                    float* logits_out, int32_t* argmax_out) {
+    if (!b || !alive(b->ctx)) return MING_E_NOT_INIT;
+    ming_ctx* ctx = b->ctx;
+    if (L < 1) return set_err(ctx, MING_E_ARG, "lm_prefill: L < 1");
+    if (!tokens_dev && !x_in) return set_err(ctx, MING_E_ARG, "lm_prefill: need tokens_dev or x_in");
+    if (!page_table_dev) return set_err(ctx, MING_E_ARG, "lm_prefill: null page table");
+    if (pages_per_seq < 1 || (int64_t)pages_per_seq * 64 > b->max_ctx)
+        return set_err(ctx, MING_E_CTX_OVER_CAPACITY, "lm_prefill: pages_per_seq * 64 exceeds max_ctx");
+    if (pos0 < 0 || (int64_t)pos0 + L > (int64_t)pages_per_seq * 64)
+        return set_err(ctx, MING_E_CTX_OVER_CAPACITY, "lm_prefill: pos0 + L exceeds the sequence's pages");
+    int32_t* rows = static_cast<int32_t*>(b->prows.p);
+    int32_t* pos = static_cast<int32_t*>(b->ppos.p);
+    const size_t H = (size_t)b->H, V = (size_t)b->V;
+    for (int start = 0; start < L; start += b->max_seqs) {
+        const int n = L - start < b->max_seqs ? L - start : b->max_seqs;
+        int st = hip_check(ctx, launch_prefill_rows(ctx->stream, page_table_dev, pages_per_seq, n, pos0 + start, rows, pos),
+                           "lm_prefill rows");
+        if (st) return st;
+        st = ming_lm_batch_step(
+            b, n, tokens_dev ? tokens_dev + start : nullptr,
+            x_in ? static_cast<const uint16_t*>(x_in) + (size_t)start * H : nullptr, kv, rows, pages_per_seq, pos,
+            hidden_out ? static_cast<uint16_t*>(hidden_out) + (size_t)start * H : nullptr,
+            logits_out ? logits_out + (size_t)start * V : nullptr, argmax_out ? argmax_out + start : nullptr);
+        if (st) return st;
+    }
     return MING_OK;
 }
 

@@ -323,6 +323,16 @@ __global__ __launch_bounds__(256) void merge_stage_kernel(MergeArgs a) {
     if (lane == 0) gst(a.xsum + (size_t)h * a.Mp + b, sum);
 }
 
+// ---- prefill rows: n virtual sequences over one sequence's pages ----------------------
+// Row i of the chunk is position p0 + i of the same sequence: its page-table
+// row is the sequence's table and its position p0 + i.
+__global__ __launch_bounds__(256) void prefill_rows_kernel(const int32_t* __restrict__ table, int pps, int n, int p0,
+                                                           int32_t* __restrict__ rows, int32_t* __restrict__ pos) {
+    const int k = blockIdx.x * 256 + threadIdx.x;
+    if (k < n * pps) gst(rows + k, gld(table + k % pps));
+    if (k < n) gst(pos + k, p0 + k);
+}
+
 }  // namespace
 
 hipError_t launch_stage(hipStream_t st, const uint16_t* x, int ldx, int M, int K, const uint16_t* norm_w, float eps,
@@ -350,6 +360,13 @@ hipError_t launch_rope_table(hipStream_t st, float* cs, int max_ctx, int half, f
 
 hipError_t launch_paged_attn(hipStream_t st, const PagedAttnArgs& a, int n_seq) {
     hipLaunchKernelGGL(paged_attn_kernel, dim3(a.max_splits, a.kvh, n_seq), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_rows(hipStream_t st, const int32_t* table, int pps, int n, int p0, int32_t* rows,
+                               int32_t* pos) {
+    const int k = n * pps > n ? n * pps : n;
+    hipLaunchKernelGGL(prefill_rows_kernel, dim3((k + 255) / 256), dim3(256), 0, st, table, pps, n, p0, rows, pos);
     return hipGetLastError();
 }
 

@@ -74,6 +74,9 @@ hipError_t launch_embed_rows(hipStream_t st, const LinearDev& E, const int32_t* 
 hipError_t launch_rope_table(hipStream_t st, float* cs, int max_ctx, int half, float log2_theta);
 hipError_t launch_paged_attn(hipStream_t st, const PagedAttnArgs& a, int n_seq);
 hipError_t launch_merge_stage(hipStream_t st, const MergeArgs& a);
+// rows [n][pps] = n copies of table [pps]; pos [n] = p0, p0 + 1, ...
+hipError_t launch_prefill_rows(hipStream_t st, const int32_t* table, int pps, int n, int p0, int32_t* rows,
+                               int32_t* pos);
 
 // Read-only view of a prepared decode stack (for the batched step).
 struct LmView {

@@ -227,3 +227,79 @@ def test_batch_qwen_shape_matches_oracle(ming, ctx, qwen):
     seqs = [int(order[0]), int(order[5]), int(order[10]), int(order[-1])]
     worst = check_teacher_forced(ming, b, pk, orc, host, lens, tokens, hid, lg, am, "qwen", seqs=seqs)
     print(f"[batch] qwen shape worst layer max|d| {worst:.3e}", flush=True)
+
+
+# ---- multi-token prefill (rows of one sequence as sequences sharing its pages) ----
+
+def one_row_table(pk):
+    return pk.table[0].contiguous()
+
+
+def test_prefill_equals_single_row_steps(ming, ctx, small):
+    """70 prompt rows after 10 cached ones (a 64-row chunk and a 6-row chunk):
+    hidden rows, logits, ids and the cache equal 70 one-row steps bit for bit."""
+    S, spec, syn, m, b, orc = small
+    L, pos0 = 70, 10
+    toks = ming.synth_uniform_i32(31, "prefill.tok", L, spec.vocab)
+    tok = torch.tensor([int(t) for t in toks], dtype=torch.int32, device="cuda")
+    outs = []
+    for mode in ("prefill", "steps"):
+        pk = S.PagedKv(spec, 1, 2, spare=5, seed=3)
+        pk.fill_random([pos0], seed=32)
+        hid = torch.empty((L, spec.hidden), dtype=torch.bfloat16, device="cuda")
+        lg = torch.empty((L, spec.vocab), dtype=torch.float32, device="cuda")
+        am = torch.empty(L, dtype=torch.int32, device="cuda")
+        if mode == "prefill":
+            b.prefill(pk, one_row_table(pk), pos0, tokens=tok, hidden=hid, logits=lg, argmax=am)
+        else:
+            pos = torch.empty(1, dtype=torch.int32, device="cuda")
+            for i in range(L):
+                pos.fill_(pos0 + i)
+                b.step(pk, pk.table, pos, tokens=tok[i:i + 1], hidden=hid[i:i + 1], logits=lg[i:i + 1],
+                       argmax=am[i:i + 1])
+        ctx.sync()
+        outs.append((hid, lg, am, pk.gather(0, pos0 + L)))
+    (h0, l0, a0, (k0, v0)), (h1, l1, a1, (k1, v1)) = outs
+    assert torch.equal(h0, h1) and torch.equal(l0, l1) and torch.equal(a0, a1)
+    assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
+
+
+def test_prefill_matches_oracle(ming, ctx, small):
+    """20 prompt rows from position 0: every layer of every row against the
+    oracle on the GPU's own layer input and the rows the GPU cached before it."""
+    S, spec, syn, m, b, orc = small
+    cfg, layers, norm, head = orc
+    L = 20
+    pk = S.PagedKv(spec, 1, 1, spare=2, seed=5)
+    x = ming.synth_normal_bf16(33, "prefill.x", L * spec.hidden).reshape(L, spec.hidden)
+    hid = torch.empty((L, spec.hidden), dtype=torch.bfloat16, device="cuda")
+    b.prefill(pk, one_row_table(pk), 0, x_in=torch.from_numpy(x.view(np.int16)).cuda().view(torch.bfloat16),
+              hidden=hid)
+    ctx.sync()
+    tr = {k: host_u16(v) for k, v in b.trace().items()}
+    gk, gv = pk.gather(0, L)
+    assert np.array_equal(tr["x"][0], x)
+    for i in range(L):
+        for l, lay in enumerate(layers):
+            k_l = np.zeros((cfg.kv_heads, i + 1, cfg.head_dim), np.uint16)
+            v_l = np.zeros_like(k_l)
+            k_l[:, :i] = gk[l, :, :i]
+            v_l[:, :i] = gv[l, :, :i]
+            x2, t = oracle.lm_layer_step(cfg, lay, tr["x"][l, i], i, k_l, v_l, trace=True)
+            w = f"prefill row {i} layer {l}"
+            assert_close_bf16(tr["qkv"][l, i], t["qkv"], w + " q|k|v")
+            assert_close_bf16(tr["att"][l, i], t["att"], w + " attention (causal)")
+            assert_close_bf16(tr["x"][l + 1, i], x2, w + " output")
+            assert_close_bf16(gk[l, :, i], k_l[:, i], w + " cached k")
+            assert_close_bf16(gv[l, :, i], v_l[:, i], w + " cached v")
+        _, rhid, _, _, _ = oracle.lm_head(cfg, norm, head, tr["x"][-1, i])
+        assert_close_bf16(host_u16(hid[i]), rhid, f"prefill row {i} hidden")
+
+
+def test_prefill_capacity_error(ming, ctx, small):
+    S, spec, syn, m, b, orc = small
+    pk = S.PagedKv(spec, 1, 1, seed=6)
+    tok = torch.zeros(10, dtype=torch.int32, device="cuda")
+    with pytest.raises(ming.MingError) as e:
+        b.prefill(pk, one_row_table(pk), 60, tokens=tok)  # 60 + 10 > 64
+    assert e.value.status == ming.MING_E_CTX_OVER_CAPACITY
