@@ -38,6 +38,10 @@ Two more workloads print a line of the same form (`--workload`):
         the batched 4-bit step (MFMA GEMMs, paged attention); value is
         tokens/s over all sequences; roofline over the step's weight bytes
         plus every sequence's KV read and append.
+  prefill one 512-token prompt per step through ming_lm_prefill (8 batched
+        chunks of 64 rows over a paged cache, causal); value is prompt
+        tokens/s; roofline over the weights once per chunk plus the causal
+        KV reads and appends.
 """
 import argparse
 import importlib
@@ -61,8 +65,9 @@ HBM_PEAK_GBS = 8000.0
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--workload", choices=["lm", "cfm", "c4", "loop", "server"], default="lm")
+    p.add_argument("--workload", choices=["lm", "cfm", "c4", "loop", "server", "prefill"], default="lm")
     p.add_argument("--seqs", type=int, default=64, help="server workload: concurrent sequences")
+    p.add_argument("--prompt", type=int, default=512, help="prefill workload: prompt tokens")
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--ctx", type=int, default=2048)
@@ -86,6 +91,8 @@ def main():
         return bench_c4(args)
     if args.workload == "server":
         return bench_server(args)
+    if args.workload == "prefill":
+        return bench_prefill(args)
     import torch
 
     ming = importlib.import_module("ming-tts-serve_amd")
@@ -289,6 +296,63 @@ def bench_server(args):
                       "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": nbytes,
                       "launch_ms": round(ms, 5)},
                      cpu, "synthetic (random-init N(0,0.02) weights quantized to MLX affine 4-bit/g64; KV N(0,1))")
+    print(json.dumps(line), flush=True)
+
+
+METRIC_PREFILL = "prompt prefill tokens/s (4-bit LM, causal, paged bf16 KV) + achieved HBM GB/s"
+
+
+def bench_prefill(args):
+    import numpy as np
+    import torch
+
+    ming = importlib.import_module("ming-tts-serve_amd")
+    S = importlib.import_module("ming-tts-serve_amd.synthetic")
+    spec = S.QWEN2_05B
+    L = args.prompt
+    ctx = ming.Context(0)
+    syn = S.SyntheticLm(ctx, spec, seed=0, quant=True)
+    m = syn.model()
+    pps = (L + 63) // 64
+    batch = ming.LmBatch(m, 64, pps * 64)
+    pk = S.PagedKv(spec, 1, pps, seed=0)
+    ids = ming.synth_uniform_i32(0, "prefill.prompt", L, spec.vocab)
+    tok = torch.tensor([int(t) for t in ids], dtype=torch.int32, device="cuda")
+    hid = torch.empty((L, spec.hidden), dtype=torch.bfloat16, device="cuda")
+    row = pk.table[0].contiguous()
+    ms = timed_events(lambda: batch.prefill(pk, row, 0, tokens=tok, hidden=hid), args.steps, args.warmup)
+    ctx.sync()
+    kv_row = spec.n_layers * 2 * spec.kvd * 2
+    chunks = (L + 63) // 64
+    nbytes = int(chunks * (S.lm_bytes_per_token(spec, 0) - kv_row) + kv_row * (L * (L + 1) // 2 + L))
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        from lmkit import oracle_model, oracle_step
+
+        oracle.set_threads(int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1))
+        cfg, layers, norm, head = oracle_model(syn)
+        kc = np.zeros((spec.n_layers, spec.kv_heads, L, spec.head_dim), np.uint16)
+        vc = np.zeros_like(kc)
+        done, t1 = 0, time.time()
+        while done < L:  # the oracle prefills row by row (its cache grows like the reference's)
+            oracle_step(cfg, layers, norm, head, oracle.embed(head, int(ids[done])), done, kc, vc)
+            done += 1
+            if time.time() - t1 >= args.cpu_seconds:
+                break
+        dt = time.time() - t1
+        cpu = {"value": round(done / dt, 3), "unit": "tokens/s", "cores": oracle.get_threads(), "kind": "port",
+               "sample": f"the first {done} rows of the same prompt, one position at a time ({dt:.1f} s, "
+                         f"C restatement of the layer graph)"}
+    line = base_line(METRIC_PREFILL, L * 1000.0 / ms, "tokens/s", args, ms,
+                     {"workload": f"one {L}-token prompt (uniform ids, seed 0) from position 0 through the 24-layer "
+                                  f"4-bit Qwen2-0.5B-shaped LM, causal, paged bf16 KV, {chunks} chunks of <= 64 rows",
+                      "global_batch": 1, "seq_len": L},
+                     {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": nbytes,
+                      "launch_ms": round(ms, 5)},
+                     cpu, "synthetic (random-init N(0,0.02) weights quantized to MLX affine 4-bit/g64)")
     print(json.dumps(line), flush=True)
 
 
