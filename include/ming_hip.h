@@ -46,7 +46,12 @@ enum ming_status {
     MING_E_TIMEOUT = 7              /* a device-side wait exceeded its spin limit */
 };
 
-enum ming_dtype { MING_DT_BF16 = 1, MING_DT_F32 = 2, MING_DT_U32 = 3, MING_DT_I32 = 4 };
+enum ming_dtype {
+    MING_DT_BF16 = 1, MING_DT_F32 = 2, MING_DT_U32 = 3, MING_DT_I32 = 4,
+    /* storage dtypes a checkpoint may hold (no compute entry point takes them) */
+    MING_DT_F16 = 5, MING_DT_I64 = 6, MING_DT_U8 = 7, MING_DT_F64 = 8, MING_DT_I8 = 9, MING_DT_BOOL = 10,
+    MING_DT_I16 = 11, MING_DT_U16 = 12, MING_DT_U64 = 13
+};
 
 /* Replaces mlx_array (src/mlx.zig) on the hot path: a borrowed device view. */
 typedef struct {
@@ -505,6 +510,62 @@ uint64_t ming_synth_stream(uint64_t seed, const char* name);
 void ming_synth_normal_bf16(uint64_t stream, float mean, float std, uint16_t* out, size_t n, int threads);
 /* uniform integers in [0, hi) */
 void ming_synth_uniform_i32(uint64_t stream, int32_t hi, int32_t* out, size_t n);
+
+/* ---- Checkpoint loading ------------------------------------------------------
+ * Tensors.load (src/ming_model.zig:316-350) reads `model.safetensors` through
+ * mlx_load_safetensors; here the container is read natively.  A safetensors
+ * file is an 8-byte little-endian header length, a JSON header {name:
+ * {dtype, shape, data_offsets}} and the data block. */
+
+/* Host-only index of a safetensors file (no device work): open parses and
+ * validates the header (offsets inside the file, sizes matching dtype and
+ * shape, unique names); `err` (optional) receives a message on failure.
+ * Entry i: name, dtype (enum ming_dtype), ndim <= 8, shape[8], absolute file
+ * offset and byte size.  ming_st_find returns an entry index or -1. */
+typedef struct ming_st ming_st;
+int ming_st_open(const char* path, ming_st** out, char* err, size_t err_cap);
+int ming_st_close(ming_st* st);
+int32_t ming_st_count(const ming_st* st);
+int ming_st_entry(const ming_st* st, int32_t i, const char** name, int32_t* dtype, int32_t* ndim, int64_t* shape,
+                  uint64_t* offset, uint64_t* nbytes);
+int32_t ming_st_find(const ming_st* st, const char* name);
+
+/* Device copies of a checkpoint's tensors (those whose names start with one
+ * of `prefixes`; all when n_prefixes is 0), uploaded through pinned staging
+ * buffers on the context's stream; the call returns after the upload.  The
+ * handle owns the memory; models built from it borrow it, so it must outlive
+ * them.  ming_weights_get fills a borrowed view (ndim > 4 folds into the
+ * last kept dimension). */
+typedef struct ming_weights ming_weights;
+int ming_weights_load(ming_ctx* ctx, const char* path, const char* const* prefixes, int32_t n_prefixes,
+                      ming_weights** out);
+int ming_weights_destroy(ming_weights* w);
+int ming_weights_get(const ming_weights* w, const char* name, ming_tensor* out);
+
+/* The linear `name` [out_features, in_features] (Tensors.lin,
+ * src/ming_model.zig:456-466): an MLX 4-bit triplet (`name.weight` u32
+ * [out, in/8], `name.scales` and `name.biases` bf16 [out, in/64]) when the
+ * checkpoint holds one, else the bf16 `name.weight` -- quantized to MLX
+ * affine 4-bit / group 64 on the GPU when quantize != 0 (ming_quantize's
+ * arithmetic; the copy is owned by the weights handle). */
+int ming_weights_linear(ming_weights* w, const char* name, int32_t out_features, int32_t in_features,
+                        int32_t quantize, ming_linear* out);
+
+/* The decode stack of a Ming checkpoint: QStack.load("model.model", 24)
+ * (src/ming_model.zig:544-560) with the embedding and tied head
+ * `model.model.embed_tokens`, norms, q/k/v biases; the shape comes from cfg
+ * and is checked against every tensor.  Linears as ming_weights_linear. */
+int ming_lm_model_from_weights(ming_ctx* ctx, ming_weights* w, const ming_lm_cfg* cfg, int32_t quantize,
+                               ming_lm_model** out);
+
+/* The flow head (`flowloss.cfm.model`: DitStack.load + embedders + final
+ * layer, src/ming_model.zig:941-950, with `rotary_embed.inv_freq` f32) and
+ * the aggregator (`linear_proj_audio`, :951-956) of a checkpoint; bf16
+ * linears (the fused DiT path's format). */
+int ming_cfm_model_from_weights(ming_ctx* ctx, ming_weights* w, const ming_dit_cfg* cfg, int32_t n_blocks,
+                                int32_t lm_hidden, int32_t latent, ming_cfm_model** out);
+int ming_agg_model_from_weights(ming_ctx* ctx, ming_weights* w, const ming_dit_cfg* cfg, int32_t n_blocks,
+                                int32_t lm_hidden, int32_t latent, ming_agg_model** out);
 
 #ifdef __cplusplus
 }

@@ -179,6 +179,19 @@ def lib():
         "ming_lm_batch_step": (c_i32, [c_void_p, c_i32, c_void_p, c_void_p, P(KvPages), c_void_p, c_i32, c_void_p,
                                        c_void_p, c_void_p, c_void_p]),
         "ming_lm_batch_trace": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+        "ming_st_open": (c_i32, [ctypes.c_char_p, P(c_void_p), ctypes.c_char_p, ctypes.c_size_t]),
+        "ming_st_close": (c_i32, [c_void_p]),
+        "ming_st_count": (c_i32, [c_void_p]),
+        "ming_st_entry": (c_i32, [c_void_p, c_i32, P(ctypes.c_char_p), P(c_i32), P(c_i32), P(ctypes.c_int64),
+                                  P(ctypes.c_uint64), P(ctypes.c_uint64)]),
+        "ming_st_find": (c_i32, [c_void_p, ctypes.c_char_p]),
+        "ming_weights_load": (c_i32, [c_void_p, ctypes.c_char_p, c_void_p, c_i32, P(c_void_p)]),
+        "ming_weights_destroy": (c_i32, [c_void_p]),
+        "ming_weights_get": (c_i32, [c_void_p, ctypes.c_char_p, P(Tensor)]),
+        "ming_weights_linear": (c_i32, [c_void_p, ctypes.c_char_p, c_i32, c_i32, c_i32, P(Linear)]),
+        "ming_lm_model_from_weights": (c_i32, [c_void_p, c_void_p, P(LmCfg), c_i32, P(c_void_p)]),
+        "ming_cfm_model_from_weights": (c_i32, [c_void_p, c_void_p, P(DitCfg), c_i32, c_i32, c_i32, P(c_void_p)]),
+        "ming_agg_model_from_weights": (c_i32, [c_void_p, c_void_p, P(DitCfg), c_i32, c_i32, c_i32, P(c_void_p)]),
         "ming_lm_prefill": (c_i32, [c_void_p, c_i32, c_void_p, c_void_p, P(KvPages), c_void_p, c_i32, c_i32,
                                     c_void_p, c_void_p, c_void_p]),
         "ming_rotary_table": (c_i32, [c_void_p, c_void_p, c_i32, c_i32, c_void_p, c_void_p]),
@@ -257,7 +270,10 @@ def tensor(t, dtype=None):
 
 
 def ptr(t):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    """Device address of a torch tensor (or an address given as an int)."""
+    if t is None:
+        return None
+    return ctypes.c_void_p(t if isinstance(t, int) else t.data_ptr())
 
 
 def linear(w, scales=None, biases=None, global_scale=1.0, out_features=None, in_features=None):
@@ -389,6 +405,13 @@ class Context:
 class CfmModel:
     """ming_cfm_model: the flow head's load-time tables plus one sample's workspace."""
 
+    @classmethod
+    def wrap(cls, ctx, h, keep=None):
+        """A model created by another entry point (the *_from_weights loaders)."""
+        m = cls.__new__(cls)
+        m.ctx, m.w, m.h = ctx, keep, h
+        return m
+
     def __init__(self, ctx, w):
         self.ctx, self.w = ctx, w  # w: CfmW (its blocks array and inv_freq must stay alive)
         h = c_void_p()
@@ -459,6 +482,13 @@ class AdalnModel:
 class AggModel:
     """ming_agg_model: the aggregator's rotary table and workspace."""
 
+    @classmethod
+    def wrap(cls, ctx, h, keep=None):
+        """A model created by another entry point (the *_from_weights loaders)."""
+        m = cls.__new__(cls)
+        m.ctx, m.w, m.h = ctx, keep, h
+        return m
+
     def __init__(self, ctx, w):
         self.ctx, self.w = ctx, w
         h = c_void_p()
@@ -482,6 +512,13 @@ class AggModel:
 
 class LmModel:
     """ming_lm_model: prepared decode stack (QStack.fuse)."""
+
+    @classmethod
+    def wrap(cls, ctx, cfg, h):
+        """A model created by another entry point (ming_lm_model_from_weights)."""
+        m = cls.__new__(cls)
+        m.ctx, m.cfg, m.h = ctx, cfg, h
+        return m
 
     def __init__(self, ctx, cfg, layers, final_norm, head, embed):
         self.ctx = ctx
@@ -582,6 +619,89 @@ class LmBatch:
                  hh=torch.empty((L, n, c.inter), dtype=torch.bfloat16, device="cuda"))
         self.ctx.check(self.ctx.L.ming_lm_batch_trace(self.h, *(ptr(t[k]) for k in ("x", "x1", "att", "qkv", "hh"))))
         return t
+
+
+# ---- checkpoints ----------------------------------------------------------------
+
+DTYPE_NAMES = {1: "BF16", 2: "F32", 3: "U32", 4: "I32", 5: "F16", 6: "I64", 7: "U8", 8: "F64", 9: "I8", 10: "BOOL",
+               11: "I16", 12: "U16", 13: "U64"}
+
+
+def st_index(path):
+    """ming_st_*: the parsed header of a safetensors file as a list of dicts
+    (name, dtype name, shape, absolute offset, nbytes); MingError on a bad file."""
+    L = lib()
+    h = c_void_p()
+    err = ctypes.create_string_buffer(512)
+    st = L.ming_st_open(str(path).encode(), ctypes.byref(h), err, len(err))
+    if st:
+        raise MingError(st, err.value.decode(errors="replace"))
+    try:
+        out = []
+        for i in range(L.ming_st_count(h)):
+            name, dt, nd = ctypes.c_char_p(), c_i32(), c_i32()
+            shape = (ctypes.c_int64 * 8)()
+            off, nb = ctypes.c_uint64(), ctypes.c_uint64()
+            L.ming_st_entry(h, i, ctypes.byref(name), ctypes.byref(dt), ctypes.byref(nd), shape, ctypes.byref(off),
+                            ctypes.byref(nb))
+            out.append(dict(name=name.value.decode(), dtype=DTYPE_NAMES.get(dt.value, "?"),
+                            shape=[shape[k] for k in range(nd.value)], offset=off.value, nbytes=nb.value))
+        return out
+    finally:
+        L.ming_st_close(h)
+
+
+class Weights:
+    """ming_weights: a checkpoint's tensors on the device (Tensors.load)."""
+
+    def __init__(self, ctx, path, prefixes=None):
+        self.ctx = ctx
+        h = c_void_p()
+        pre = [p.encode() for p in (prefixes or [])]
+        arr = (ctypes.c_char_p * max(1, len(pre)))(*pre)
+        ctx.check(ctx.L.ming_weights_load(ctx.h, str(path).encode(), arr if pre else None, len(pre), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.ctx.L.ming_weights_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def get(self, name):
+        t = Tensor()
+        if self.ctx.L.ming_weights_get(self.h, name.encode(), ctypes.byref(t)):
+            raise KeyError(name)
+        return t
+
+    def linear(self, name, out_features, in_features, quantize=False):
+        w = Linear()
+        self.ctx.check(self.ctx.L.ming_weights_linear(self.h, name.encode(), int(out_features), int(in_features),
+                                                      int(quantize), ctypes.byref(w)))
+        return w
+
+    def lm_model(self, cfg, quantize=True):
+        h = c_void_p()
+        self.ctx.check(self.ctx.L.ming_lm_model_from_weights(self.ctx.h, self.h, ctypes.byref(cfg), int(quantize),
+                                                             ctypes.byref(h)))
+        return LmModel.wrap(self.ctx, cfg, h)
+
+    def cfm_model(self, cfg, n_blocks, lm_hidden, latent):
+        h = c_void_p()
+        self.ctx.check(self.ctx.L.ming_cfm_model_from_weights(self.ctx.h, self.h, ctypes.byref(cfg), int(n_blocks),
+                                                              int(lm_hidden), int(latent), ctypes.byref(h)))
+        return CfmModel.wrap(self.ctx, h, keep=self)
+
+    def agg_model(self, cfg, n_blocks, lm_hidden, latent):
+        h = c_void_p()
+        self.ctx.check(self.ctx.L.ming_agg_model_from_weights(self.ctx.h, self.h, ctypes.byref(cfg), int(n_blocks),
+                                                              int(lm_hidden), int(latent), ctypes.byref(h)))
+        return AggModel.wrap(self.ctx, h, keep=self)
 
 
 # ---- synthetic inputs ---------------------------------------------------------

@@ -1,0 +1,674 @@
+// Checkpoint loading: the safetensors container (Tensors.load,
+// src/ming_model.zig:316-350) read natively, its tensors uploaded to the
+// device, and the decode stack / flow head / aggregator built from them under
+// the reference's key map (QStack.load :544-560, DitStack.load :728-742,
+// Model.load :935-956).  Linears come either from an MLX 4-bit triplet
+// (`<name>.weight` u32 [out, in/8], `.scales`, `.biases` bf16 [out, in/64]) or
+// from a bf16 `<name>.weight` [out, in], optionally quantized to 4-bit on the
+// GPU at load time.
+//
+// Container: 8-byte little-endian header length n, n bytes of JSON
+// {"name": {"dtype": "BF16", "shape": [..], "data_offsets": [begin, end]},
+//  "__metadata__": {...}}, then the data block (offsets relative to it).
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "args.h"
+#include "internal.h"
+
+using namespace ming;
+
+namespace {
+
+constexpr uint64_t kMaxHeader = 100ull << 20;  // the format's own header limit
+
+int dtype_of(const std::string& s, int& size) {
+    struct D {
+        const char* n;
+        int dt, sz;
+    };
+    static const D tab[] = {{"BF16", MING_DT_BF16, 2}, {"F32", MING_DT_F32, 4}, {"U32", MING_DT_U32, 4},
+                            {"I32", MING_DT_I32, 4},   {"F16", MING_DT_F16, 2}, {"I64", MING_DT_I64, 8},
+                            {"U8", MING_DT_U8, 1},     {"F64", MING_DT_F64, 8}, {"I8", MING_DT_I8, 1},
+                            {"BOOL", MING_DT_BOOL, 1}, {"I16", MING_DT_I16, 2}, {"U16", MING_DT_U16, 2},
+                            {"U64", MING_DT_U64, 8}};
+    for (const D& d : tab)
+        if (s == d.n) {
+            size = d.sz;
+            return d.dt;
+        }
+    size = 0;
+    return 0;
+}
+
+// A minimal JSON reader for the header: objects, arrays, strings, integers.
+struct Json {
+    const char* p;
+    const char* e;
+    std::string err;
+
+    bool fail(const char* what) {
+        if (err.empty()) err = what;
+        return false;
+    }
+    void ws() {
+        while (p < e && (*p == ' ' || *p == '\t' || *p == '\n' || *p == '\r')) p++;
+    }
+    bool lit(char c) {
+        ws();
+        if (p < e && *p == c) {
+            p++;
+            return true;
+        }
+        return false;
+    }
+    bool str(std::string& out) {
+        ws();
+        if (p >= e || *p != '"') return fail("expected a string");
+        p++;
+        out.clear();
+        while (p < e && *p != '"') {
+            char c = *p++;
+            if (c == '\\') {
+                if (p >= e) return fail("bad escape");
+                const char x = *p++;
+                switch (x) {
+                    case '"': c = '"'; break;
+                    case '\\': c = '\\'; break;
+                    case '/': c = '/'; break;
+                    case 'b': c = '\b'; break;
+                    case 'f': c = '\f'; break;
+                    case 'n': c = '\n'; break;
+                    case 'r': c = '\r'; break;
+                    case 't': c = '\t'; break;
+                    case 'u': {
+                        if (e - p < 4) return fail("bad \\u escape");
+                        unsigned v = 0;
+                        for (int i = 0; i < 4; i++) {
+                            const char h = *p++;
+                            v = v * 16 + (h >= '0' && h <= '9' ? h - '0'
+                                          : (h | 32) >= 'a' && (h | 32) <= 'f' ? (h | 32) - 'a' + 10
+                                                                                 : 99u);
+                            if (v > 0xffff) return fail("bad \\u escape");
+                        }
+                        if (v > 0x7f) return fail("non-ASCII \\u escape in a name");
+                        c = (char)v;
+                        break;
+                    }
+                    default:
+                        return fail("bad escape");
+                }
+            }
+            out.push_back(c);
+        }
+        if (p >= e) return fail("unterminated string");
+        p++;
+        return true;
+    }
+    bool integer(int64_t& v) {
+        ws();
+        bool neg = false;
+        if (p < e && *p == '-') {
+            neg = true;
+            p++;
+        }
+        if (p >= e || *p < '0' || *p > '9') return fail("expected an integer");
+        uint64_t u = 0;
+        while (p < e && *p >= '0' && *p <= '9') {
+            if (u > (UINT64_MAX - 9) / 10) return fail("integer overflow");
+            u = u * 10 + (uint64_t)(*p++ - '0');
+        }
+        if (u > (uint64_t)INT64_MAX) return fail("integer overflow");
+        v = neg ? -(int64_t)u : (int64_t)u;
+        return true;
+    }
+    // skip any value (metadata)
+    bool skip(int depth = 0) {
+        ws();
+        if (depth > 32) return fail("nesting too deep");
+        if (p >= e) return fail("truncated");
+        if (*p == '"') {
+            std::string s;
+            return str(s);
+        }
+        if (*p == '{' || *p == '[') {
+            const char close = *p == '{' ? '}' : ']';
+            const bool obj = *p == '{';
+            p++;
+            if (lit(close)) return true;
+            do {
+                if (obj) {
+                    std::string k;
+                    if (!str(k) || !lit(':')) return fail("bad object");
+                }
+                if (!skip(depth + 1)) return false;
+            } while (lit(','));
+            return lit(close) || fail("bad container");
+        }
+        while (p < e && *p != ',' && *p != '}' && *p != ']' && *p != ' ' && *p != '\n') p++;  // number/true/false/null
+        return true;
+    }
+    bool int_array(std::vector<int64_t>& out) {
+        out.clear();
+        if (!lit('[')) return fail("expected an array");
+        if (lit(']')) return true;
+        do {
+            int64_t v;
+            if (!integer(v)) return false;
+            out.push_back(v);
+        } while (lit(','));
+        return lit(']') || fail("bad array");
+    }
+};
+
+}  // namespace
+
+struct ming_st {
+    std::string path;
+    uint64_t data_off = 0, file_size = 0;
+    struct Entry {
+        std::string name;
+        int32_t dtype = 0, ndim = 0;
+        int64_t shape[8] = {0};
+        uint64_t begin = 0, end = 0;
+    };
+    std::vector<Entry> entries;
+    std::unordered_map<std::string, size_t> index;
+};
+
+namespace {
+
+void put_err(char* err, size_t cap, const std::string& msg) {
+    if (err && cap) {
+        std::snprintf(err, cap, "%s", msg.c_str());
+    }
+}
+
+int st_parse(const char* path, ming_st& st, std::string& err) {
+    FILE* f = std::fopen(path, "rb");
+    if (!f) {
+        err = std::string("cannot open ") + path;
+        return MING_E_ARG;
+    }
+    std::fseek(f, 0, SEEK_END);
+    const long long fsz = ftello(f);
+    std::fseek(f, 0, SEEK_SET);
+    unsigned char hb[8];
+    if (fsz < 8 || std::fread(hb, 1, 8, f) != 8) {
+        std::fclose(f);
+        err = "file too short for a safetensors header";
+        return MING_E_SHAPE;
+    }
+    uint64_t n = 0;
+    for (int i = 7; i >= 0; i--) n = (n << 8) | hb[i];
+    if (n > kMaxHeader || n + 8 > (uint64_t)fsz) {
+        std::fclose(f);
+        err = "header length out of range";
+        return MING_E_SHAPE;
+    }
+    std::string js(n, '\0');
+    if (n && std::fread(&js[0], 1, n, f) != n) {
+        std::fclose(f);
+        err = "truncated header";
+        return MING_E_SHAPE;
+    }
+    std::fclose(f);
+    st.path = path;
+    st.data_off = 8 + n;
+    st.file_size = (uint64_t)fsz;
+    const uint64_t dlen = st.file_size - st.data_off;
+    Json j{js.data(), js.data() + js.size(), {}};
+    if (!j.lit('{')) {
+        err = "header is not a JSON object";
+        return MING_E_SHAPE;
+    }
+    if (!j.lit('}')) {
+        do {
+            ming_st::Entry en;
+            if (!j.str(en.name) || !j.lit(':')) break;
+            if (en.name == "__metadata__") {
+                if (!j.skip()) break;
+                continue;
+            }
+            if (!j.lit('{')) {
+                j.fail("tensor entry is not an object");
+                break;
+            }
+            bool have_dt = false, have_shape = false, have_off = false;
+            std::string dts;
+            std::vector<int64_t> shape, offs;
+            if (!j.lit('}')) {
+                do {
+                    std::string k;
+                    if (!j.str(k) || !j.lit(':')) break;
+                    if (k == "dtype") {
+                        have_dt = j.str(dts);
+                    } else if (k == "shape") {
+                        have_shape = j.int_array(shape);
+                    } else if (k == "data_offsets") {
+                        have_off = j.int_array(offs);
+                    } else if (!j.skip()) {
+                        break;
+                    }
+                } while (j.lit(','));
+                if (!j.lit('}')) j.fail("bad tensor entry");
+            }
+            if (!j.err.empty()) break;
+            if (!have_dt || !have_shape || !have_off || offs.size() != 2) {
+                j.fail("tensor entry lacks dtype, shape or data_offsets");
+                break;
+            }
+            int size = 0;
+            en.dtype = dtype_of(dts, size);
+            if (!en.dtype) {
+                j.fail("unknown dtype");
+                break;
+            }
+            if (shape.size() > 8) {
+                j.fail("more than 8 dimensions");
+                break;
+            }
+            uint64_t count = 1;
+            for (size_t i = 0; i < shape.size(); i++) {
+                if (shape[i] < 0 || (shape[i] && count > UINT64_MAX / (uint64_t)shape[i])) {
+                    j.fail("bad shape");
+                    break;
+                }
+                count *= (uint64_t)shape[i];
+                en.shape[i] = shape[i];
+            }
+            if (!j.err.empty()) break;
+            en.ndim = (int32_t)shape.size();
+            if (offs[0] < 0 || offs[1] < offs[0] || (uint64_t)offs[1] > dlen) {
+                j.fail("data_offsets outside the data block");
+                break;
+            }
+            en.begin = (uint64_t)offs[0];
+            en.end = (uint64_t)offs[1];
+            if (count > UINT64_MAX / (uint64_t)size || en.end - en.begin != count * (uint64_t)size) {
+                j.fail("data_offsets do not match dtype and shape");
+                break;
+            }
+            if (st.index.count(en.name)) {
+                j.fail("duplicate tensor name");
+                break;
+            }
+            st.index[en.name] = st.entries.size();
+            st.entries.push_back(std::move(en));
+        } while (j.lit(','));
+        if (j.err.empty() && !j.lit('}')) j.fail("bad header object");
+    }
+    if (!j.err.empty()) {
+        err = "safetensors header: " + j.err;
+        return MING_E_SHAPE;
+    }
+    return MING_OK;
+}
+
+}  // namespace
+
+// ---- device weights -------------------------------------------------------------
+
+struct ming_weights {
+    ming_ctx* ctx = nullptr;
+    void* base = nullptr;  // one allocation for every uploaded tensor
+    std::unordered_map<std::string, ming_tensor> map;
+    std::vector<void*> extra;  // derived buffers (4-bit copies made at load time)
+    std::vector<ming_dit_block_w> cfm_blocks, agg_blocks;
+    std::vector<float> cfm_inv_freq, agg_inv_freq;
+};
+
+namespace {
+
+bool alive(const ming_ctx* c) { return c && c->alive; }
+
+const ming_tensor* wget(const ming_weights* w, const std::string& k) {
+    auto it = w->map.find(k);
+    return it == w->map.end() ? nullptr : &it->second;
+}
+
+// The linear `name` ([out, in]): an MLX 4-bit triplet if present, else bf16
+// (quantized on the GPU when q4 is set; the copy is owned by w).
+int make_linear(ming_weights* w, const std::string& name, bool q4, int64_t N, int64_t K, ming_linear& L) {
+    ming_ctx* ctx = w->ctx;
+    const ming_tensor* t = wget(w, name + ".weight");
+    if (!t) return set_err(ctx, MING_E_ARG, "missing weight " + name + ".weight");
+    std::memset(&L, 0, sizeof(L));
+    L.out_features = (int32_t)N;
+    L.in_features = (int32_t)K;
+    const ming_tensor* s = wget(w, name + ".scales");
+    const ming_tensor* b = wget(w, name + ".biases");
+    if (s || b) {
+        if (!s || !b || t->dtype != MING_DT_U32 || s->dtype != MING_DT_BF16 || b->dtype != MING_DT_BF16 ||
+            t->ndim != 2 || t->shape[0] != N || t->shape[1] != K / 8 || s->ndim != 2 || s->shape[0] != N ||
+            s->shape[1] != K / 64 || b->ndim != 2 || b->shape[0] != N || b->shape[1] != K / 64)
+            return set_err(ctx, MING_E_SHAPE, name + ": MLX 4-bit triplet must be u32 [out, in/8] + bf16 [out, in/64] x2");
+        L.kind = MING_W_AFFINE;
+        L.group_size = 64;
+        L.bits = 4;
+        L.global_scale = 1.0f;
+        L.w = t->data;
+        L.scales = s->data;
+        L.biases = b->data;
+        return MING_OK;
+    }
+    if (t->dtype != MING_DT_BF16 || t->ndim != 2 || t->shape[0] != N || t->shape[1] != K)
+        return set_err(ctx, MING_E_SHAPE, name + ".weight must be bf16 [" + std::to_string(N) + ", " +
+                                              std::to_string(K) + "]");
+    if (!q4) {
+        L.kind = MING_W_BF16;
+        L.w = t->data;
+        return MING_OK;
+    }
+    if (K % 64) return set_err(ctx, MING_E_SHAPE, name + ": in_features % 64 != 0, cannot quantize");
+    void* buf = nullptr;
+    const size_t wq = (size_t)N * K / 2, sb = (size_t)N * (K / 64) * 2;
+    int st = hip_check(ctx, hipMalloc(&buf, wq + 2 * sb), "hipMalloc(4-bit copy)");
+    if (st) return st;
+    w->extra.push_back(buf);
+    uint32_t* q = static_cast<uint32_t*>(buf);
+    uint16_t* sc = reinterpret_cast<uint16_t*>(static_cast<char*>(buf) + wq);
+    uint16_t* bi = reinterpret_cast<uint16_t*>(static_cast<char*>(buf) + wq + sb);
+    st = hip_check(ctx, launch_quantize(ctx->stream, static_cast<const uint16_t*>(t->data), N, K, q, sc, bi),
+                   "quantize at load");
+    if (st) return st;
+    L.kind = MING_W_AFFINE;
+    L.group_size = 64;
+    L.bits = 4;
+    L.global_scale = 1.0f;
+    L.w = q;
+    L.scales = sc;
+    L.biases = bi;
+    return MING_OK;
+}
+
+int vec(ming_weights* w, const std::string& name, int64_t n, const void*& out, int dtype = MING_DT_BF16) {
+    const ming_tensor* t = wget(w, name);
+    if (!t) return set_err(w->ctx, MING_E_ARG, "missing weight " + name);
+    int64_t cnt = 1;
+    for (int i = 0; i < t->ndim; i++) cnt *= t->shape[i];
+    if (t->dtype != dtype || cnt != n)
+        return set_err(w->ctx, MING_E_SHAPE, name + ": expected " + std::to_string(n) + " values of the stated dtype");
+    out = t->data;
+    return MING_OK;
+}
+
+int dit_blocks(ming_weights* w, const std::string& prefix, const ming_dit_cfg& c, int n,
+               std::vector<ming_dit_block_w>& out, std::vector<float>& inv_freq) {
+    out.assign(n, ming_dit_block_w{});
+    const int64_t D = c.hidden, F = c.ff;
+    static const char* keys[6] = {"attn.to_q", "attn.to_k", "attn.to_v", "attn.to_out.0", "mlp.ff.0.0", "mlp.ff.2"};
+    for (int i = 0; i < n; i++) {
+        const std::string b = prefix + ".blocks." + std::to_string(i) + ".";
+        ming_dit_block_w& B = out[i];
+        ming_linear* L[6] = {&B.wq, &B.wk, &B.wv, &B.wo, &B.w1, &B.w2};
+        const void** bias[6] = {&B.bq, &B.bk, &B.bv, &B.bo, &B.b1, &B.b2};
+        int st;
+        if ((st = vec(w, b + "norm1.weight", D, B.norm1)) || (st = vec(w, b + "norm2.weight", D, B.norm2))) return st;
+        for (int k = 0; k < 6; k++) {
+            const int64_t N = k == 4 ? F : D, K = k == 5 ? F : D;
+            if ((st = make_linear(w, b + keys[k], false, N, K, *L[k])) || (st = vec(w, b + keys[k] + ".bias", N, *bias[k])))
+                return st;
+        }
+    }
+    const ming_tensor* t = wget(w, prefix + ".rotary_embed.inv_freq");
+    if (!t || t->dtype != MING_DT_F32 || t->ndim != 1 || t->shape[0] != c.head_dim / 2)
+        return set_err(w->ctx, MING_E_ARG, "missing or malformed " + prefix + ".rotary_embed.inv_freq (f32 [head_dim/2])");
+    inv_freq.resize(c.head_dim / 2);
+    return hip_check(w->ctx, hipMemcpy(inv_freq.data(), t->data, inv_freq.size() * 4, hipMemcpyDeviceToHost),
+                     "read inv_freq");
+}
+
+}  // namespace
+
+extern "C" {
+
+int ming_st_open(const char* path, ming_st** out, char* err, size_t err_cap) {
+    if (!path || !out) return MING_E_ARG;
+    *out = nullptr;
+    auto* st = new ming_st();
+    std::string e;
+    const int s = st_parse(path, *st, e);
+    if (s) {
+        put_err(err, err_cap, e);
+        delete st;
+        return s;
+    }
+    *out = st;
+    return MING_OK;
+}
+
+int ming_st_close(ming_st* st) {
+    delete st;
+    return MING_OK;
+}
+
+int32_t ming_st_count(const ming_st* st) { return st ? (int32_t)st->entries.size() : 0; }
+
+int ming_st_entry(const ming_st* st, int32_t i, const char** name, int32_t* dtype, int32_t* ndim, int64_t* shape,
+                  uint64_t* offset, uint64_t* nbytes) {
+    if (!st || i < 0 || i >= (int32_t)st->entries.size()) return MING_E_ARG;
+    const ming_st::Entry& e = st->entries[i];
+    if (name) *name = e.name.c_str();
+    if (dtype) *dtype = e.dtype;
+    if (ndim) *ndim = e.ndim;
+    if (shape)
+        for (int k = 0; k < 8; k++) shape[k] = k < e.ndim ? e.shape[k] : 0;
+    if (offset) *offset = st->data_off + e.begin;
+    if (nbytes) *nbytes = e.end - e.begin;
+    return MING_OK;
+}
+
+int32_t ming_st_find(const ming_st* st, const char* name) {
+    if (!st || !name) return -1;
+    auto it = st->index.find(name);
+    return it == st->index.end() ? -1 : (int32_t)it->second;
+}
+
+int ming_weights_load(ming_ctx* ctx, const char* path, const char* const* prefixes, int32_t n_prefixes,
+                      ming_weights** out) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!path || !out || n_prefixes < 0 || (n_prefixes > 0 && !prefixes))
+        return set_err(ctx, MING_E_ARG, "weights_load: bad arguments");
+    *out = nullptr;
+    ming_st st;
+    std::string e;
+    int s = st_parse(path, st, e);
+    if (s) return set_err(ctx, s, e);
+    auto wanted = [&](const std::string& n) {
+        if (n_prefixes == 0) return true;
+        for (int i = 0; i < n_prefixes; i++)
+            if (prefixes[i] && n.compare(0, std::strlen(prefixes[i]), prefixes[i]) == 0) return true;
+        return false;
+    };
+    // layout: every selected tensor at a 256-byte aligned offset of one allocation
+    std::vector<size_t> sel, dev_off;
+    size_t total = 0;
+    for (size_t i = 0; i < st.entries.size(); i++)
+        if (wanted(st.entries[i].name)) {
+            sel.push_back(i);
+            dev_off.push_back(total);
+            total += (st.entries[i].end - st.entries[i].begin + 255) / 256 * 256;
+        }
+    auto* w = new ming_weights();
+    w->ctx = ctx;
+    if (total && (s = hip_check(ctx, hipMalloc(&w->base, total), "hipMalloc(weights)"))) {
+        delete w;
+        return s;
+    }
+    FILE* f = std::fopen(path, "rb");
+    if (!f) {
+        ming_weights_destroy(w);
+        return set_err(ctx, MING_E_ARG, std::string("cannot open ") + path);
+    }
+    // two pinned staging buffers: the copy of one overlaps the read of the other
+    constexpr size_t kChunk = 32u << 20;
+    void* stage[2] = {nullptr, nullptr};
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    hipError_t he = hipSuccess;
+    for (int i = 0; i < 2 && he == hipSuccess; i++) {
+        he = hipHostMalloc(&stage[i], kChunk, hipHostMallocDefault);
+        if (he == hipSuccess) he = hipEventCreateWithFlags(&ev[i], hipEventDisableTiming);
+    }
+    int buf = 0;
+    bool used[2] = {false, false};
+    for (size_t k = 0; k < sel.size() && he == hipSuccess && !s; k++) {
+        const ming_st::Entry& en = st.entries[sel[k]];
+        const uint64_t nb = en.end - en.begin;
+        if (fseeko(f, (off_t)(st.data_off + en.begin), SEEK_SET) != 0) {
+            s = set_err(ctx, MING_E_ARG, "seek failed in " + std::string(path));
+            break;
+        }
+        for (uint64_t done = 0; done < nb && he == hipSuccess;) {
+            const size_t n = (size_t)(nb - done < kChunk ? nb - done : kChunk);
+            if (used[buf]) he = hipEventSynchronize(ev[buf]);
+            if (he != hipSuccess) break;
+            if (std::fread(stage[buf], 1, n, f) != n) {
+                s = set_err(ctx, MING_E_ARG, "short read of " + en.name);
+                break;
+            }
+            he = hipMemcpyAsync(static_cast<char*>(w->base) + dev_off[k] + done, stage[buf], n, hipMemcpyHostToDevice,
+                                ctx->stream);
+            if (he == hipSuccess) he = hipEventRecord(ev[buf], ctx->stream);
+            used[buf] = true;
+            buf ^= 1;
+            done += n;
+        }
+        if (s || he != hipSuccess) break;
+        ming_tensor t{};
+        t.data = static_cast<char*>(w->base) + dev_off[k];
+        t.dtype = en.dtype;
+        t.ndim = en.ndim < 4 ? en.ndim : 4;
+        for (int d = 0; d < t.ndim; d++) t.shape[d] = en.shape[d];
+        if (en.ndim > 4)  // fold trailing dimensions into the last one kept
+            for (int d = 4; d < en.ndim; d++) t.shape[3] *= en.shape[d];
+        w->map[en.name] = t;
+    }
+    std::fclose(f);
+    const hipError_t hs = hipStreamSynchronize(ctx->stream);
+    if (he == hipSuccess) he = hs;
+    for (int i = 0; i < 2; i++) {
+        if (ev[i]) (void)hipEventDestroy(ev[i]);
+        if (stage[i]) (void)hipHostFree(stage[i]);
+    }
+    if (!s && he != hipSuccess) s = hip_check(ctx, he, "weights upload");
+    if (s) {
+        ming_weights_destroy(w);
+        return s;
+    }
+    *out = w;
+    return MING_OK;
+}
+
+int ming_weights_destroy(ming_weights* w) {
+    if (!w) return MING_OK;
+    if (w->ctx && w->ctx->stream) (void)hipStreamSynchronize(w->ctx->stream);
+    for (void* p : w->extra) (void)hipFree(p);
+    if (w->base) (void)hipFree(w->base);
+    delete w;
+    return MING_OK;
+}
+
+int ming_weights_get(const ming_weights* w, const char* name, ming_tensor* out) {
+    if (!w || !name || !out) return MING_E_ARG;
+    const ming_tensor* t = wget(w, name);
+    if (!t) return MING_E_ARG;
+    *out = *t;
+    return MING_OK;
+}
+
+int ming_weights_linear(ming_weights* w, const char* name, int32_t out_features, int32_t in_features,
+                        int32_t quantize, ming_linear* out) {
+    if (!w || !alive(w->ctx)) return MING_E_NOT_INIT;
+    if (!name || !out) return set_err(w->ctx, MING_E_ARG, "weights_linear: bad arguments");
+    return make_linear(w, name, quantize != 0, out_features, in_features, *out);
+}
+
+int ming_lm_model_from_weights(ming_ctx* ctx, ming_weights* w, const ming_lm_cfg* cfg, int32_t quantize,
+                               ming_lm_model** out) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!w || !cfg || !out) return set_err(ctx, MING_E_ARG, "lm_model_from_weights: bad arguments");
+    const std::string P = "model.model";
+    const int64_t H = cfg->hidden, kvd = (int64_t)cfg->kv_heads * cfg->head_dim, I = cfg->inter;
+    std::vector<ming_lm_layer_w> layers(cfg->n_layers);
+    int st;
+    for (int i = 0; i < cfg->n_layers; i++) {
+        const std::string L = P + ".layers." + std::to_string(i) + ".";
+        ming_lm_layer_w& l = layers[i];
+        if ((st = vec(w, L + "input_layernorm.weight", H, l.ln1)) ||
+            (st = vec(w, L + "post_attention_layernorm.weight", H, l.ln2)) ||
+            (st = make_linear(w, L + "self_attn.q_proj", quantize, H, H, l.wq)) ||
+            (st = make_linear(w, L + "self_attn.k_proj", quantize, kvd, H, l.wk)) ||
+            (st = make_linear(w, L + "self_attn.v_proj", quantize, kvd, H, l.wv)) ||
+            (st = make_linear(w, L + "self_attn.o_proj", quantize, H, H, l.wo)) ||
+            (st = make_linear(w, L + "mlp.gate_proj", quantize, I, H, l.wg)) ||
+            (st = make_linear(w, L + "mlp.up_proj", quantize, I, H, l.wu)) ||
+            (st = make_linear(w, L + "mlp.down_proj", quantize, H, I, l.wd)) ||
+            (st = vec(w, L + "self_attn.q_proj.bias", H, l.bq)) || (st = vec(w, L + "self_attn.k_proj.bias", kvd, l.bk)) ||
+            (st = vec(w, L + "self_attn.v_proj.bias", kvd, l.bv)))
+            return st;
+    }
+    if (wget(w, P + ".layers." + std::to_string(cfg->n_layers) + ".input_layernorm.weight"))
+        return set_err(ctx, MING_E_SHAPE, "lm_model_from_weights: the checkpoint has more layers than cfg->n_layers");
+    ming_linear emb;
+    const void* norm = nullptr;
+    if ((st = make_linear(w, P + ".embed_tokens", quantize, cfg->vocab, H, emb)) || (st = vec(w, P + ".norm.weight", H, norm)))
+        return st;
+    if ((st = hip_check(ctx, hipStreamSynchronize(ctx->stream), "quantize at load"))) return st;
+    // tied head (lm_head = embed_tokens, as the reference's QStack decode)
+    return ming_lm_model_create(ctx, cfg, layers.data(), norm, &emb, &emb, out);
+}
+
+int ming_cfm_model_from_weights(ming_ctx* ctx, ming_weights* w, const ming_dit_cfg* cfg, int32_t n_blocks,
+                                int32_t lm_hidden, int32_t latent, ming_cfm_model** out) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!w || !cfg || !out || n_blocks < 1) return set_err(ctx, MING_E_ARG, "cfm_model_from_weights: bad arguments");
+    const std::string C = "flowloss.cfm.model";
+    int st;
+    if ((st = dit_blocks(w, C, *cfg, n_blocks, w->cfm_blocks, w->cfm_inv_freq))) return st;
+    ming_cfm_w cw{};
+    cw.cfg = *cfg;
+    cw.n_blocks = n_blocks;
+    cw.blocks = w->cfm_blocks.data();
+    cw.inv_freq = w->cfm_inv_freq.data();
+    const int64_t D = cfg->hidden;
+    if ((st = make_linear(w, C + ".x_embedder", false, D, latent, cw.x_emb)) ||
+        (st = make_linear(w, C + ".c_embedder.cond_embedder", false, D, lm_hidden, cw.c_emb)) ||
+        (st = make_linear(w, C + ".t_embedder.time_mlp.0", false, D, 256, cw.t_mlp0)) ||
+        (st = make_linear(w, C + ".t_embedder.time_mlp.2", false, D, D, cw.t_mlp2)) ||
+        (st = make_linear(w, C + ".final_layer.linear", false, latent, D, cw.final)) ||
+        (st = vec(w, C + ".x_embedder.bias", D, cw.bx)) || (st = vec(w, C + ".c_embedder.cond_embedder.bias", D, cw.bc)) ||
+        (st = vec(w, C + ".t_embedder.time_mlp.0.bias", D, cw.bt0)) ||
+        (st = vec(w, C + ".t_embedder.time_mlp.2.bias", D, cw.bt2)) ||
+        (st = vec(w, C + ".final_layer.norm_final.weight", D, cw.final_norm)) ||
+        (st = vec(w, C + ".final_layer.linear.bias", latent, cw.bf)))
+        return st;
+    return ming_cfm_model_create(ctx, &cw, out);
+}
+
+int ming_agg_model_from_weights(ming_ctx* ctx, ming_weights* w, const ming_dit_cfg* cfg, int32_t n_blocks,
+                                int32_t lm_hidden, int32_t latent, ming_agg_model** out) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!w || !cfg || !out || n_blocks < 1) return set_err(ctx, MING_E_ARG, "agg_model_from_weights: bad arguments");
+    const std::string A = "linear_proj_audio";
+    int st;
+    if ((st = dit_blocks(w, A, *cfg, n_blocks, w->agg_blocks, w->agg_inv_freq))) return st;
+    ming_agg_w aw{};
+    aw.cfg = *cfg;
+    aw.n_blocks = n_blocks;
+    aw.blocks = w->agg_blocks.data();
+    aw.inv_freq = w->agg_inv_freq.data();
+    const int64_t D = cfg->hidden;
+    if ((st = make_linear(w, A + ".x_embedder", false, D, latent, aw.x_emb)) ||
+        (st = make_linear(w, A + ".final_layer.linear", false, lm_hidden, D, aw.final)) ||
+        (st = vec(w, A + ".x_embedder.bias", D, aw.bx)) || (st = vec(w, A + ".word_embedder.weight", D, aw.cls)) ||
+        (st = vec(w, A + ".final_layer.norm_final.weight", D, aw.final_norm)) ||
+        (st = vec(w, A + ".final_layer.linear.bias", lm_hidden, aw.bf)))
+        return st;
+    return ming_agg_model_create(ctx, &aw, out);
+}
+
+}  // extern "C"
