@@ -401,6 +401,20 @@ int ming_cfm_model_tables(ming_cfm_model* m, uint16_t* t, uint16_t* dt, uint16_t
 int ming_cfm_sample(ming_ctx* ctx, ming_cfm_model* m, const void* z, const void* hist, const void* noise,
                     const void* sde, float cfg, float sigma, float temperature, void* latent_out, void* y_steps);
 
+/* cfmSample for n sequences at once (1 <= n <= 64), as a server batching
+ * requests runs the flow head once per step (no reference counterpart: the
+ * reference samples one request at a time).  Per sequence b the same
+ * arithmetic as ming_cfm_sample on row b of each input: z [n][lm_hidden],
+ * hist / noise [n][latent], sde [n][steps][latent] (may be NULL when
+ * sigma * sqrt(temperature) == 0) -> latents_out [n][latent]; y_steps
+ * (optional) [n][steps][latent].  Every DiT linear runs as one matrix-core
+ * GEMM over the 6 n rows, so results agree with n ming_cfm_sample calls within
+ * f32 summation order, not bit for bit.  hidden, ff, lm_hidden and latent
+ * must be multiples of 64. */
+int ming_cfm_sample_batch(ming_ctx* ctx, ming_cfm_model* m, int32_t n, const void* z, const void* hist,
+                          const void* noise, const void* sde, float cfg, float sigma, float temperature,
+                          void* latents_out, void* y_steps);
+
 /* Aggregator precomputation (rotary table for L = 2) and workspace. */
 int ming_agg_model_create(ming_ctx* ctx, const ming_agg_w* w, ming_agg_model** out);
 int ming_agg_model_destroy(ming_agg_model* m);

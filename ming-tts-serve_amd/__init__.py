@@ -203,6 +203,8 @@ def lib():
         "ming_cfm_final": (c_i32, [c_void_p, c_void_p, c_i32, c_void_p, P(Linear), c_void_p, c_void_p, c_void_p,
                                    c_void_p, c_void_p, c_i32, c_f32, c_f32, c_void_p]),
         "ming_cfm_model_create": (c_i32, [c_void_p, P(CfmW), P(c_void_p)]),
+        "ming_cfm_sample_batch": (c_i32, [c_void_p, c_void_p, c_i32, c_void_p, c_void_p, c_void_p, c_void_p, c_f32, c_f32,
+                                          c_f32, c_void_p, c_void_p]),
         "ming_cfm_model_destroy": (c_i32, [c_void_p]),
         "ming_cfm_model_tables": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, P(c_void_p)]),
         "ming_cfm_sample": (c_i32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_f32, c_f32, c_f32,
@@ -441,6 +443,12 @@ class CfmModel:
                                                         dt.ctypes.data_as(c_void_p), sq.ctypes.data_as(c_void_p),
                                                         ctypes.byref(te)))
         return t, dt, sq, te.value
+
+    def sample_batch(self, n, z, hist, noise, sde, cfg, sigma, temperature, latents_out, y_steps=None):
+        """ming_cfm_sample_batch: n sequences' flow head in one pass."""
+        self.ctx.check(self.ctx.L.ming_cfm_sample_batch(self.ctx.h, self.h, int(n), ptr(z), ptr(hist), ptr(noise),
+                                                        ptr(sde), float(cfg), float(sigma), float(temperature),
+                                                        ptr(latents_out), ptr(y_steps)))
 
     def sample(self, z, hist, noise, sde, cfg, sigma, temperature, latent_out, y_steps=None):
         self.ctx.check(self.ctx.L.ming_cfm_sample(self.ctx.h, self.h, ptr(z), ptr(hist), ptr(noise), ptr(sde),

@@ -245,6 +245,8 @@ struct ming_cfm_model {
     uint16_t t[kFlowSteps + 1]{}, dt[kFlowSteps]{}, sq[kFlowSteps]{};
     DevBuf cos, sin, t_emb, dtd, sqd, zc, ce, xh, y;
     StackBufs s;
+    // ming_cfm_sample_batch workspace (grown on demand): n sequences, 6 n rows
+    DevBuf bce, bxh, bxe, brows[2], bhn, bqkv, batt, bx1, bhh, by[2], bhf;
 };
 
 struct ming_adaln_model {
@@ -411,7 +413,10 @@ int ming_cfm_model_create(ming_ctx* ctx, const ming_cfm_w* w, ming_cfm_model** o
 
 int ming_cfm_model_destroy(ming_cfm_model* m) {
     if (!m) return MING_E_NOT_INIT;
-    for (DevBuf* b : {&m->cos, &m->sin, &m->t_emb, &m->dtd, &m->sqd, &m->zc, &m->ce, &m->xh, &m->y}) b->release();
+    for (DevBuf* b : {&m->cos, &m->sin, &m->t_emb, &m->dtd, &m->sqd, &m->zc, &m->ce, &m->xh, &m->y, &m->bce, &m->bxh,
+                      &m->bxe, &m->brows[0], &m->brows[1], &m->bhn, &m->bqkv, &m->batt, &m->bx1, &m->bhh, &m->by[0],
+                      &m->by[1], &m->bhf})
+        b->release();
     m->s.release();
     delete m;
     return MING_OK;
@@ -475,6 +480,71 @@ int ming_cfm_sample(ming_ctx* ctx, ming_cfm_model* m, const void* z, const void*
     if (e == hipSuccess)
         e = hipMemcpyAsync(latent_out, m->y.p, sizeof(uint16_t) * lat, hipMemcpyDeviceToDevice, s);
     return hip_check(ctx, e, "cfm_sample");
+}
+
+// cfmSample of n sequences in one pass (the flow head of a batched server
+// step): the rows of every sequence go through each DiT linear as one GEMM.
+int ming_cfm_sample_batch(ming_ctx* ctx, ming_cfm_model* m, int32_t n, const void* z, const void* hist,
+                          const void* noise, const void* sde, float cfg, float sigma, float temperature,
+                          void* latents_out, void* y_steps) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!m) return set_err(ctx, MING_E_NOT_INIT, "cfm_sample_batch: null model");
+    const float shift = sigma * std::sqrt(temperature);
+    if (n < 1 || n > 64) return set_err(ctx, MING_E_UNSUPPORTED, "cfm_sample_batch: 1..64 sequences");
+    if (!z || !hist || !noise || !latents_out || (shift != 0.0f && !sde))
+        return set_err(ctx, MING_E_ARG, "cfm_sample_batch: null buffer");
+    const int D = m->cfg.hidden, F = m->cfg.ff, H = m->lm_hidden, lat = m->latent, L = 3, R = 6 * n;
+    if (D % 64 || F % 64 || H % 64 || lat % 64 || m->cfg.head_dim % 2)
+        return set_err(ctx, MING_E_UNSUPPORTED, "cfm_sample_batch: hidden, ff, lm_hidden and latent must be multiples of 64");
+    hipStream_t s = ctx->stream;
+    const size_t b2 = sizeof(uint16_t);
+    hipError_t e = hipSuccess;
+    auto grow = [&](DevBuf& d, size_t bytes) {
+        if (e == hipSuccess) e = d.ensure(bytes);
+    };
+    grow(m->bce, (size_t)n * D * b2);
+    grow(m->bxh, (size_t)n * D * b2);
+    grow(m->bxe, (size_t)n * D * b2);
+    grow(m->brows[0], (size_t)R * D * b2);
+    grow(m->brows[1], (size_t)R * D * b2);
+    grow(m->bhn, (size_t)R * D * b2);
+    grow(m->bqkv, (size_t)3 * R * D * b2);
+    grow(m->batt, (size_t)R * D * b2);
+    grow(m->bx1, (size_t)R * D * b2);
+    grow(m->bhh, (size_t)R * F * b2);
+    grow(m->by[0], (size_t)n * lat * b2);
+    grow(m->by[1], (size_t)n * lat * b2);
+    grow(m->bhf, (size_t)2 * n * D * b2);
+    if (e != hipSuccess) return hip_check(ctx, e, "cfm_sample_batch workspace");
+    const float eps = m->cfg.eps;
+    // once per sample: c_emb(z) (the unconditional half is c_emb(0) = bias) and x_emb(hist) (:1196-1197)
+    e = launch_dit_linear_gemm(s, u16(z), n, m->wc, D, H, m->bc, u16(m->bce.p));
+    if (e == hipSuccess) e = launch_dit_linear_gemm(s, u16(hist), n, m->wx, D, lat, m->bx, u16(m->bxh.p));
+    const uint16_t* y = u16(noise);
+    int yi = 0;
+    for (int i = 0; i < kFlowSteps && e == hipSuccess; i++) {
+        e = launch_dit_linear_gemm(s, y, n, m->wx, D, lat, m->bx, u16(m->bxe.p));
+        if (e == hipSuccess)
+            e = launch_cfm_rows_batch(s, u16(m->t_emb.p) + (size_t)i * 2 * D, u16(m->bce.p), m->bc, u16(m->bxh.p),
+                                      u16(m->bxe.p), n, D, u16(m->brows[0].p));
+        int cur = 0;
+        for (size_t bl = 0; bl < m->blocks.size() && e == hipSuccess; bl++) {
+            e = launch_dit_block_gemm(s, m->blocks[bl], u16(m->brows[cur].p), R, L,
+                                      static_cast<const float*>(m->cos.p), static_cast<const float*>(m->sin.p),
+                                      u16(m->bhn.p), u16(m->bqkv.p), u16(m->batt.p), u16(m->bx1.p), u16(m->bhh.p),
+                                      u16(m->brows[cur ^ 1].p));
+            cur ^= 1;
+        }
+        if (e == hipSuccess)
+            e = launch_cfm_final_batch(s, u16(m->brows[cur].p), n, L, D, m->final_norm, eps, m->wf, m->bf, lat, y,
+                                       u16(m->dtd.p), u16(m->sqd.p), u16(sde), i, kFlowSteps, cfg, shift,
+                                       u16(m->bhf.p), u16(m->by[yi].p), u16(y_steps));
+        y = u16(m->by[yi].p);
+        yi ^= 1;
+    }
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(latents_out, y, (size_t)n * lat * b2, hipMemcpyDeviceToDevice, s);
+    return hip_check(ctx, e, "cfm_sample_batch");
 }
 
 // ---- aggregator ---------------------------------------------------------------------

@@ -566,6 +566,13 @@ hipError_t launch_dit_stage(hipStream_t st, int which, const DitBlockDev& w, con
     }
 }
 
+// Attention of B sequences of L rows on qkv [3][B L][D] (one wave per (sequence, head)).
+hipError_t launch_dit_attn(hipStream_t st, const uint16_t* qkv, int B, int L, int D, int heads, int hd, uint16_t* att) {
+    if (L > kMaxL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(dit_attn_kernel, dim3(B * heads), dim3(kWave), 0, st, qkv, B * L, L, D, heads, hd, att);
+    return hipGetLastError();
+}
+
 // One DiT block: the four stages in order.
 hipError_t launch_dit_block(hipStream_t st, const DitBlockDev& w, const uint16_t* x, int B, int L,
                             const float* cos_t, const float* sin_t, uint16_t* qkv, uint16_t* att, uint16_t* x1,

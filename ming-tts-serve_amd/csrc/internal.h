@@ -78,6 +78,20 @@ hipError_t launch_merge_stage(hipStream_t st, const MergeArgs& a);
 hipError_t launch_prefill_rows(hipStream_t st, const int32_t* table, int pps, int n, int p0, int32_t* rows,
                                int32_t* pos);
 
+// ---- flow head over many sequences (dit.hip, dit_batch.hip) ----
+hipError_t launch_dit_attn(hipStream_t st, const uint16_t* qkv, int B, int L, int D, int heads, int hd, uint16_t* att);
+hipError_t launch_dit_block_gemm(hipStream_t st, const DitBlockDev& w, const uint16_t* x, int R, int L,
+                                 const float* cos_t, const float* sin_t, uint16_t* hn, uint16_t* qkv, uint16_t* att,
+                                 uint16_t* x1, uint16_t* hh, uint16_t* out);
+hipError_t launch_dit_linear_gemm(hipStream_t st, const uint16_t* x, int R, const uint16_t* w, int N, int K,
+                                  const uint16_t* b, uint16_t* out);
+hipError_t launch_cfm_rows_batch(hipStream_t st, const uint16_t* te, const uint16_t* ce, const uint16_t* bc,
+                                 const uint16_t* xh, const uint16_t* xe, int n, int D, uint16_t* rows);
+hipError_t launch_cfm_final_batch(hipStream_t st, const uint16_t* h, int n, int L, int D, const uint16_t* norm,
+                                  float eps, const uint16_t* wf, const uint16_t* bf, int latent, const uint16_t* y,
+                                  const uint16_t* dt, const uint16_t* sq, const uint16_t* sde, int step, int steps,
+                                  float cfg, float shift, uint16_t* hn, uint16_t* y_out, uint16_t* y_steps);
+
 // Read-only view of a prepared decode stack (for the batched step).
 struct LmView {
     ming_lm_cfg cfg;

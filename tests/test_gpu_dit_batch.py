@@ -1,0 +1,101 @@
+"""GPU parity of the flow head over many sequences (ming_cfm_sample_batch:
+cfmSample, src/ming_model.zig:1143-1151, :1161-1203, for n sequences in one
+pass, every DiT linear one bf16 matrix-core GEMM over the 6 n rows) against
+the oracle, at the reference shape (8 blocks, hidden 1024, 16 x 64 heads,
+ff 4096).
+
+Bars (those of the single-sequence flow head): every Euler step of every
+sequence, teacher forced on the GPU's own previous latent, within
+2e-2 + 1e-2 |ref|; the free-running ten-step latent within 6e-2 + 2e-2 |ref|
+and a mean |d| of 2e-2; each sequence equal to a one-sequence batch call
+(bit for bit: the GEMMs' per-row arithmetic does not depend on n)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from ditkit import ocfg, oracle_cfm
+from lmkit import assert_close_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def syn_mod():
+    import importlib
+
+    return importlib.import_module("ming-tts-serve_amd.synthetic")
+
+
+def dev_u16(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda().view(torch.bfloat16)
+
+
+def host_u16(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.fixture(scope="module")
+def flowb(ming, ctx):
+    S = syn_mod()
+    syn = S.SyntheticFlow(ctx, S.MING_DIT, seed=61, norm_std=0.05, parts=("cfm",))
+    oracle.set_threads(16)
+    return syn, syn.cfm_model(), oracle_cfm(syn)
+
+
+def inputs(ming, spec, n, tag):
+    z = ming.synth_normal_bf16(71, f"{tag}.z", n * spec.lm_hidden).reshape(n, spec.lm_hidden)
+    hist = ming.synth_normal_bf16(72, f"{tag}.hist", n * spec.latent).reshape(n, spec.latent)
+    noise = ming.synth_normal_bf16(73, f"{tag}.noise", n * spec.latent).reshape(n, spec.latent)
+    sde = ming.synth_normal_bf16(74, f"{tag}.sde", n * 10 * spec.latent).reshape(n, 10, spec.latent)
+    return z, hist, noise, sde
+
+
+@pytest.mark.parametrize("n,cfg,sigma,temperature", [(5, 2.0, 0.25, 1.0), (16, 2.0, 0.0, 0.0)])
+def test_cfm_batch_matches_oracle(ming, ctx, flowb, n, cfg, sigma, temperature):
+    print(f"[cfm_batch] n={n} cfg={cfg} sigma={sigma} temperature={temperature}", flush=True)
+    syn, m, oc = flowb
+    spec = syn.spec
+    z, hist, noise, sde = inputs(ming, spec, n, f"b{n}")
+    out = torch.empty((n, spec.latent), dtype=torch.bfloat16, device="cuda")
+    steps = torch.empty((n, 10, spec.latent), dtype=torch.bfloat16, device="cuda")
+    m.sample_batch(n, dev_u16(z), dev_u16(hist), dev_u16(noise), dev_u16(sde), cfg, sigma, temperature, out, steps)
+    ctx.sync()
+    g = host_u16(steps)
+    assert np.array_equal(host_u16(out), g[:, 9])
+    shift = float(np.float32(sigma) * np.sqrt(np.float32(temperature)))
+    c = ocfg(spec)
+    check = range(n) if n <= 5 else (0, n // 2, n - 1)
+    for b in check:
+        for i in range(10):
+            y_in = noise[b] if i == 0 else g[b, i - 1]
+            h = oracle.cfm_rows(oc, z[b], hist[b], y_in, i)
+            for blk in oc.blocks:
+                h = oracle.dit_block_fwd(c, blk, h, 2, 3, oc.keep["cos"], oc.keep["sin"])
+            ref = oracle.cfm_final(oc, h, 3, y_in, sde[b], i, cfg, shift)
+            assert_close_bf16(g[b, i], ref, f"sequence {b} Euler step {i} (teacher forced)")
+        ref_out, _ = oracle.cfm_sample(oc, z[b], hist[b], noise[b], sde[b], cfg, shift)
+        assert_close_bf16(g[b, 9], ref_out, f"sequence {b} latent (end to end)", atol=6e-2, rtol=2e-2)
+        assert np.abs(oracle.to_f32(g[b, 9]).astype(np.float64) - oracle.to_f32(ref_out)).mean() <= 2e-2
+
+
+def test_cfm_batch_rows_independent_of_n(ming, ctx, flowb):
+    syn, m, oc = flowb
+    spec = syn.spec
+    n = 20
+    z, hist, noise, sde = (dev_u16(a) for a in inputs(ming, spec, n, "ind"))
+    out = torch.empty((n, spec.latent), dtype=torch.bfloat16, device="cuda")
+    m.sample_batch(n, z, hist, noise, sde, 2.0, 0.25, 1.0, out)
+    one = torch.empty((1, spec.latent), dtype=torch.bfloat16, device="cuda")
+    for b in (0, 7, 19):
+        m.sample_batch(1, z[b:b + 1], hist[b:b + 1], noise[b:b + 1], sde[b:b + 1], 2.0, 0.25, 1.0, one)
+        ctx.sync()
+        assert torch.equal(one[0], out[b]), b
+
+
+def test_cfm_batch_rejects(ming, ctx, flowb):
+    syn, m, oc = flowb
+    spec = syn.spec
+    buf = torch.empty((65, spec.latent), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ming.MingError) as e:
+        m.sample_batch(65, buf, buf, buf, buf, 2.0, 0.0, 0.0, buf)
+    assert e.value.status == ming.MING_E_UNSUPPORTED
