@@ -35,9 +35,13 @@ Two more workloads print a line of the same form (`--workload`):
   server  config 5's multi-request decode: --seqs sequences (16 or 64) with
         contexts drawn uniform in [128, 4096] (seed 0) over a paged bf16 KV
         cache advance one token per step (each fed its own argmax) through
-        the batched 4-bit step (MFMA GEMMs, paged attention); value is
-        tokens/s over all sequences; roofline over the step's weight bytes
-        plus every sequence's KV read and append.
+        the batched 4-bit step (MFMA GEMMs, paged attention), and the DiT
+        flow head samples every sequence's latent from its hidden state
+        (ming_cfm_sample_batch: 10 CFG Euler steps through 8 blocks, bf16;
+        --lm-only leaves it out); value is tokens/s over all sequences;
+        roofline over the step's weight bytes (4-bit LM once, the flow head's
+        bf16 weights once per Euler step) plus every sequence's KV read and
+        append.
   prefill one 512-token prompt per step through ming_lm_prefill (8 batched
         chunks of 64 rows over a paged cache, causal); value is prompt
         tokens/s; roofline over the weights once per chunk plus the causal
@@ -67,6 +71,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--workload", choices=["lm", "cfm", "c4", "loop", "server", "prefill"], default="lm")
     p.add_argument("--seqs", type=int, default=64, help="server workload: concurrent sequences")
+    p.add_argument("--lm-only", action="store_true", help="server workload: no DiT head")
     p.add_argument("--prompt", type=int, default=512, help="prefill workload: prompt tokens")
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
@@ -245,12 +250,27 @@ def bench_server(args):
     pk.fill_device(lens, seed=1)
     tok = torch.tensor([int(t) for t in ming.synth_uniform_i32(0, "server.tok", n, spec.vocab)], dtype=torch.int32,
                        device="cuda")
+    dit = not args.lm_only
+    if dit:
+        dspec = S.MING_DIT
+        flow = S.SyntheticFlow(ctx, dspec, seed=1, parts=("cfm",))
+        cfm = flow.cfm_model()
+        dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda().view(torch.bfloat16)
+        hid = torch.empty((n, spec.hidden), dtype=torch.bfloat16, device="cuda")
+        hist = dev(ming.synth_normal_bf16(2, "server.hist", n * dspec.latent)).reshape(n, dspec.latent)
+        noise = dev(ming.synth_normal_bf16(3, "server.noise", n * dspec.latent)).reshape(n, dspec.latent)
+        sde = dev(ming.synth_normal_bf16(4, "server.sde", n * 10 * dspec.latent)).reshape(n, 10, dspec.latent)
+        lat = torch.empty((n, dspec.latent), dtype=torch.bfloat16, device="cuda")
     torch.cuda.synchronize()
     print(f"[bench] server setup {time.time() - t0:.1f}s ({n} sequences, {pps} pages each)", file=sys.stderr,
           flush=True)
 
     def step():
-        batch.step(pk, pk.table, pk.pos, tokens=tok, argmax=tok)
+        if dit:  # the flow head samples each sequence's latent from its hidden state
+            batch.step(pk, pk.table, pk.pos, tokens=tok, hidden=hid, argmax=tok)
+            cfm.sample_batch(n, hid, hist, noise, sde, 2.0, 0.25, 1.0, lat)
+        else:
+            batch.step(pk, pk.table, pk.pos, tokens=tok, argmax=tok)
 
     for _ in range(args.warmup):
         step()
@@ -263,6 +283,8 @@ def bench_server(args):
     fixed = S.lm_bytes_per_token(spec, 0) - kv_row
     mean_ctx = float(np.mean(start)) + (args.steps - 1) / 2.0
     nbytes = int(fixed + n * (mean_ctx + 1) * kv_row)
+    if dit:
+        nbytes += cfm_bytes_per_sample(S.MING_DIT)
     achieved = nbytes / (ms * 1e-3) / 1e9
     cpu = None
     if not args.no_cpu:
@@ -290,7 +312,9 @@ def bench_server(args):
     line = base_line(METRIC_SERVER, n * 1000.0 / ms, "tokens/s", args, ms,
                      {"workload": f"{n} concurrent sequences, one decode token each per step, contexts uniform in "
                                   f"[128, 4096] (seed 0, mean {mean_ctx:.0f}) advancing during the run; Qwen2-0.5B "
-                                  f"-shaped 24-layer 4-bit LM, paged bf16 KV (64-position pages), greedy argmax",
+                                  f"-shaped 24-layer 4-bit LM, paged bf16 KV (64-position pages), greedy argmax" +
+                                  ("; DiT flow head per token (10 CFG Euler steps, 8 blocks, hidden 1024, bf16) on "
+                                   "every sequence's hidden state" if dit else "; LM only"),
                       "global_batch": n, "seq_len": int(round(mean_ctx))},
                      {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                       "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": nbytes,

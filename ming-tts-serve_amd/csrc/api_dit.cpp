@@ -246,7 +246,7 @@ struct ming_cfm_model {
     DevBuf cos, sin, t_emb, dtd, sqd, zc, ce, xh, y;
     StackBufs s;
     // ming_cfm_sample_batch workspace (grown on demand): n sequences, 6 n rows
-    DevBuf bce, bxh, bxe, brows[2], bhn, bqkv, batt, bx1, bhh, by[2], bhf;
+    DevBuf bce, bxh, bxe, brows[2], bhn, bqkv, batt, bx1, bhh, by[2], bhf, bpart;
 };
 
 struct ming_adaln_model {
@@ -415,7 +415,7 @@ int ming_cfm_model_destroy(ming_cfm_model* m) {
     if (!m) return MING_E_NOT_INIT;
     for (DevBuf* b : {&m->cos, &m->sin, &m->t_emb, &m->dtd, &m->sqd, &m->zc, &m->ce, &m->xh, &m->y, &m->bce, &m->bxh,
                       &m->bxe, &m->brows[0], &m->brows[1], &m->bhn, &m->bqkv, &m->batt, &m->bx1, &m->bhh, &m->by[0],
-                      &m->by[1], &m->bhf})
+                      &m->by[1], &m->bhf, &m->bpart})
         b->release();
     m->s.release();
     delete m;
@@ -515,6 +515,7 @@ int ming_cfm_sample_batch(ming_ctx* ctx, ming_cfm_model* m, int32_t n, const voi
     grow(m->by[0], (size_t)n * lat * b2);
     grow(m->by[1], (size_t)n * lat * b2);
     grow(m->bhf, (size_t)2 * n * D * b2);
+    grow(m->bpart, (size_t)4 * R * D * sizeof(float));
     if (e != hipSuccess) return hip_check(ctx, e, "cfm_sample_batch workspace");
     const float eps = m->cfg.eps;
     // once per sample: c_emb(z) (the unconditional half is c_emb(0) = bias) and x_emb(hist) (:1196-1197)
@@ -532,7 +533,7 @@ int ming_cfm_sample_batch(ming_ctx* ctx, ming_cfm_model* m, int32_t n, const voi
             e = launch_dit_block_gemm(s, m->blocks[bl], u16(m->brows[cur].p), R, L,
                                       static_cast<const float*>(m->cos.p), static_cast<const float*>(m->sin.p),
                                       u16(m->bhn.p), u16(m->bqkv.p), u16(m->batt.p), u16(m->bx1.p), u16(m->bhh.p),
-                                      u16(m->brows[cur ^ 1].p));
+                                      u16(m->brows[cur ^ 1].p), static_cast<float*>(m->bpart.p));
             cur ^= 1;
         }
         if (e == hipSuccess)

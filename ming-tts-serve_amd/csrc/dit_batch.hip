@@ -9,10 +9,9 @@
 // GEMM: Y [R][N] = X [R][K] W^T, bf16 in, f32 accumulate.  MFMA 16x16x32 bf16
 // lane layout (gfx950): A lane l = row l % 16, k-block l / 16 (8 values); B
 // lane l = column l % 16, same k-block; C[r] = (row 4 (l / 16) + r, column
-// l % 16).  A rows and W rows are both K-contiguous, so each lane loads 16
-// contiguous bytes per operand per MFMA.  Workgroup (column block x, row-tile
-// group y): KW <= 4 waves split K; a wave holds MT row tiles x NW column tiles;
-// two groups of 64 k in flight while one computes; partial sums meet in LDS.
+// l % 16).  A rows and W rows are both K-contiguous: the workgroup stages
+// 64-k slices of both through LDS (dgemm_kernel below) and each lane reads
+// its 16-byte fragments from there.
 #include "args.h"
 #include "common.h"
 #include "internal.h"
@@ -43,6 +42,10 @@ struct DGemm {
     float cfg, shift;
     uint16_t* y_out;       // [n][N]
     uint16_t* y_steps;     // optional [n][steps][N]
+    // split K: grid z = ks slices of K / ks; f32 partials [ks][R][N] (bias and
+    // epilogue applied by dreduce_kernel)
+    float* part;
+    int ks;
 };
 
 __device__ __forceinline__ bf16x8_t as8(uint4 v) { return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w}); }
@@ -55,111 +58,139 @@ __device__ __forceinline__ float gelu_chain_b(float x) {
     return rb(rb(0.5f * x) * rb(1.0f + th));
 }
 
-template <int MT, int NW>
-struct DIn {
-    uint4 a[MT][2], b[NW][2];
+// LDS-tiled GEMM: workgroup tile BM rows x 64 columns, K staged 64 at a time
+// through two LDS buffers (rows padded to 72 values: the 16 rows a fragment
+// read touches fall in distinct banks).  256 threads load each stage
+// cooperatively (16 bytes each, coalesced) while the previous stage's MFMAs
+// run; wave w owns rows 32 (w / 2) .. + 32 and columns 32 (w % 2) .. + 32 of
+// a 64-row tile (BM = 64), or rows 0 .. 32 and columns 16 w .. + 16 (BM = 32).
+constexpr int kBN = 64, kBK = 64, kPad = 72;
+
+template <int BM>
+struct DTile {
+    static constexpr int NT = BM == 64 ? 2 : 1;       // 16-column tiles per wave
+    static constexpr int AL = BM * kBK / 8 / 256;    // A chunks (16 B) per thread per stage
+    static constexpr int BL = kBN * kBK / 8 / 256;   // B chunks per thread per stage
 };
 
-template <int MT, int NW>
-__device__ __forceinline__ void dload(const uint16_t* const (&xr)[MT], const uint16_t* const (&wr)[NW], int g,
-                                      DIn<MT, NW>& in) {
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-        in.a[mt][0] = ldg4(xr[mt] + 64 * g);
-        in.a[mt][1] = ldg4(xr[mt] + 64 * g + 32);
-    }
-#pragma unroll
-    for (int t = 0; t < NW; t++) {
-        in.b[t][0] = ldg4(wr[t] + 64 * g);
-        in.b[t][1] = ldg4(wr[t] + 64 * g + 32);
-    }
-}
-
-template <int MT, int NW>
-__device__ __forceinline__ void dmma(const DIn<MT, NW>& in, f32x4_t (&acc)[MT][NW]) {
-#pragma unroll
-    for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int t = 0; t < NW; t++)
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-                acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as8(in.a[mt][h]), as8(in.b[t][h]), acc[mt][t], 0, 0, 0);
-}
-
-template <int MT, int NW, int E>
+template <int BM, int E>
 __global__ __launch_bounds__(256) void dgemm_kernel(DGemm a) {
-    extern __shared__ float red[];  // [KW][MT * 4][NW][64]
-    const int KW = blockDim.x / kWave;
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, c = lane % 16, j = lane / 16;
-    const int NS = E == DE_QKV ? a.N / 3 : a.N;  // columns per segment
-    const int n0 = blockIdx.x * 16 * NW, si = E == DE_QKV ? n0 / NS : 0, ns0 = n0 - si * NS;
+    using T = DTile<BM>;
+    constexpr int NT = T::NT;
+    __shared__ __align__(16) uint16_t As[2][BM * kPad];
+    __shared__ __align__(16) uint16_t Bs[2][kBN * kPad];
+    const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave, c = lane % 16, j = lane / 16;
+    const int NS = E == DE_QKV ? a.N / 3 : a.N;  // columns per segment (a tile never straddles two)
+    const int n0 = blockIdx.x * kBN, si = E == DE_QKV ? n0 / NS : 0, ns0 = n0 - si * NS;
     const uint16_t* W = si == 0 ? a.w[0] : (si == 1 ? a.w[1] : a.w[2]);
     const uint16_t* B = si == 0 ? a.b[0] : (si == 1 ? a.b[1] : a.b[2]);
-    const int MTT = (a.R + 15) / 16, mt0 = blockIdx.y * MT, G = a.K / 64;
-    const uint16_t* xr[MT];
-    const uint16_t* wr[NW];
+    const int m0 = blockIdx.y * BM, S = a.K / kBK / a.ks, s0 = blockIdx.z * S;
+    const int wm = BM == 64 ? wave / 2 : 0, wn = BM == 64 ? wave % 2 : wave;
+    // this thread's global chunks: chunk q -> (row q / 8, k 8 (q % 8))
+    const uint16_t* ag[T::AL];
+    const uint16_t* bg[T::BL];
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-        const int r = min(16 * min(mt0 + mt, MTT - 1) + c, a.R - 1);
-        xr[mt] = a.x + (size_t)r * a.ldx + 8 * j;
+    for (int i = 0; i < T::AL; i++) {
+        const int q = tid + 256 * i, r = min(m0 + q / 8, a.R - 1);
+        ag[i] = a.x + (size_t)r * a.ldx + 8 * (q % 8);
     }
 #pragma unroll
-    for (int t = 0; t < NW; t++) {
-        const int n = min(ns0 + 16 * t + c, NS - 1);
-        wr[t] = W + (size_t)n * a.K + 8 * j;
+    for (int i = 0; i < T::BL; i++) {
+        const int q = tid + 256 * i, n = min(ns0 + q / 8, NS - 1);
+        bg[i] = W + (size_t)n * a.K + 8 * (q % 8);
     }
-    const int gper = (G + KW - 1) / KW, g0 = wave * gper, g1 = min(G, g0 + gper);
-    f32x4_t acc[MT][NW];
+    // two register sets: the stage about to be stored to LDS and the one after it, in flight
+    uint4 ar[2][T::AL], br[2][T::BL];
+    auto gload = [&](int s, int set) {
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++)
+        for (int i = 0; i < T::AL; i++) ar[set][i] = ldg4(ag[i] + kBK * (s0 + s));
 #pragma unroll
-        for (int t = 0; t < NW; t++) acc[mt][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    if (g0 < g1) {
-        DIn<MT, NW> b0, b1, b2;
-        dload<MT, NW>(xr, wr, g0, b0);
-        if (g0 + 1 < g1) dload<MT, NW>(xr, wr, g0 + 1, b1);
-        for (int g = g0; g < g1; g += 3) {
-            if (g + 2 < g1) dload<MT, NW>(xr, wr, g + 2, b2);
-            dmma<MT, NW>(b0, acc);
-            if (g + 1 >= g1) break;
-            if (g + 3 < g1) dload<MT, NW>(xr, wr, g + 3, b0);
-            dmma<MT, NW>(b1, acc);
-            if (g + 2 >= g1) break;
-            if (g + 4 < g1) dload<MT, NW>(xr, wr, g + 4, b1);
-            dmma<MT, NW>(b2, acc);
+        for (int i = 0; i < T::BL; i++) br[set][i] = ldg4(bg[i] + kBK * (s0 + s));
+    };
+    auto lstore = [&](int buf, int set) {
+#pragma unroll
+        for (int i = 0; i < T::AL; i++) {
+            const int q = tid + 256 * i;
+            *reinterpret_cast<uint4*>(&As[buf][(q / 8) * kPad + 8 * (q % 8)]) = ar[set][i];
         }
-    }
-    if (KW > 1) {
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++)
+        for (int i = 0; i < T::BL; i++) {
+            const int q = tid + 256 * i;
+            *reinterpret_cast<uint4*>(&Bs[buf][(q / 8) * kPad + 8 * (q % 8)]) = br[set][i];
+        }
+    };
+    f32x4_t acc[2][NT];
 #pragma unroll
-            for (int r = 0; r < 4; r++)
+    for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-                for (int t = 0; t < NW; t++) red[(((wave * MT + mt) * 4 + r) * NW + t) * kWave + lane] = acc[mt][t][r];
+        for (int t = 0; t < NT; t++) acc[mt][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute = [&](int buf) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            uint4 af[2], bfr[NT];
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+                af[mt] = *reinterpret_cast<const uint4*>(&As[buf][(32 * wm + 16 * mt + c) * kPad + 32 * ks + 8 * j]);
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+                bfr[t] = *reinterpret_cast<const uint4*>(
+                    &Bs[buf][((BM == 64 ? 32 : 16) * wn + 16 * t + c) * kPad + 32 * ks + 8 * j]);
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                for (int t = 0; t < NT; t++)
+                    acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as8(af[mt]), as8(bfr[t]), acc[mt][t], 0, 0, 0);
+        }
+    };
+    // stages in pairs so that every register-set and LDS-buffer index is a constant:
+    // stage s computes from buffer s & 1 while stage s + 1 waits in set (s + 1) & 1
+    // and stage s + 2 loads into set s & 1
+    gload(0, 0);
+    if (S > 1) gload(1, 1);
+    lstore(0, 0);
+    __syncthreads();
+    for (int s = 0; s < S; s += 2) {
+        if (s + 2 < S) gload(s + 2, 0);
+        compute(0);
+        if (s + 1 < S) lstore(1, 1);
+        __syncthreads();
+        if (s + 1 >= S) break;
+        if (s + 3 < S) gload(s + 3, 1);
+        compute(1);
+        if (s + 2 < S) lstore(0, 0);
         __syncthreads();
     }
-    auto sum = [&](int mt, int r, int t) {
-        if (KW == 1) return acc[mt][t][r];
-        float s = 0.0f;
-        for (int w = 0; w < KW; w++) s += red[(((w * MT + mt) * 4 + r) * NW + t) * kWave + lane];
-        return s;
-    };
-    if constexpr (E == DE_CFM) {
-        // lane rows 4j + {0,1} and 4j + {2,3}: (cond, uncond) of two sequences; wave w takes the pairs u % KW == w
+    if (a.ks > 1) {  // split K: f32 partials of this slice; dreduce_kernel finishes
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++)
+        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + 32 * wm + 16 * mt + 4 * j + r;
+                if (m >= a.R) continue;
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    const int n = ns0 + (BM == 64 ? 32 : 16) * wn + 16 * t + c;
+                    if (n < NS) gst(a.part + ((size_t)blockIdx.z * a.R + m) * a.N + n, acc[mt][t][r]);
+                }
+            }
+        return;
+    }
+    const int cb = ns0 + (BM == 64 ? 32 : 16) * wn;  // this wave's first column within the segment
+    if constexpr (E == DE_CFM) {
+        // lane rows 4j + {0,1} and 4j + {2,3}: (cond, uncond) of two sequences
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
 #pragma unroll
             for (int pr = 0; pr < 2; pr++) {
-                if ((mt * 2 + pr) % KW != wave) continue;
-                const int m = 16 * (mt0 + mt) + 4 * j + 2 * pr;
-                if (mt0 + mt >= MTT || m + 1 >= a.R) continue;
+                const int m = m0 + 32 * wm + 16 * mt + 4 * j + 2 * pr;
+                if (m + 1 >= a.R) continue;
                 const int sb = m / 2;
 #pragma unroll
-                for (int t = 0; t < NW; t++) {
-                    const int n = n0 + 16 * t + c;
+                for (int t = 0; t < NT; t++) {
+                    const int n = cb + 16 * t + c;
                     if (n >= a.N) continue;
                     const float bb = bf2f(gld(B + n));
-                    const float pc = rb(sum(mt, 2 * pr, t) + bb), pn = rb(sum(mt, 2 * pr + 1, t) + bb);
+                    const float pc = rb(acc[mt][t][2 * pr] + bb), pn = rb(acc[mt][t][2 * pr + 1] + bb);
                     const float f0 = rb(pc + rb(rb(pc - pn) * rb(a.cfg)));
                     float y = rb(bf2f(gld(a.y + (size_t)sb * a.N + n)) + rb(bf2f(gld(a.dt + a.step)) * f0));
                     if (a.shift != 0.0f)
@@ -172,16 +203,15 @@ __global__ __launch_bounds__(256) void dgemm_kernel(DGemm a) {
         return;
     }
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++)
+    for (int mt = 0; mt < 2; mt++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            if ((mt * 4 + r) % KW != wave) continue;
-            const int m = 16 * (mt0 + mt) + 4 * j + r;
-            const bool row_ok = mt0 + mt < MTT && m < a.R;
+            const int m = m0 + 32 * wm + 16 * mt + 4 * j + r;
+            const bool row_ok = m < a.R;
 #pragma unroll
-            for (int t = 0; t < NW; t++) {
-                const int nn = ns0 + 16 * t + c;  // column within the segment
-                const float e = rb(sum(mt, r, t) + bf2f(gld(B + min(nn, NS - 1))));
+            for (int t = 0; t < NT; t++) {
+                const int nn = cb + 16 * t + c;  // column within the segment
+                const float e = rb(acc[mt][t][r] + bf2f(gld(B + min(nn, NS - 1))));
                 if constexpr (E == DE_QKV) {
                     // interleaved rotary on q, k: the pair (2i, 2i+1) is lanes (c, c ^ 1)
                     const float other = __shfl_xor(e, 1, kWave);
@@ -260,31 +290,42 @@ __global__ __launch_bounds__(256) void cfm_rows_kernel(const uint16_t* __restric
     }
 }
 
-template <int MT, int NW, int E>
-hipError_t dlaunch(hipStream_t st, const DGemm& a, int kw) {
-    const int mtt = (a.R + 15) / 16, gy = (mtt + MT - 1) / MT, gx = (a.N + 16 * NW - 1) / (16 * NW);
-    const size_t lds = kw > 1 ? sizeof(float) * (size_t)kw * MT * 4 * NW * kWave : 0;
-    hipLaunchKernelGGL((dgemm_kernel<MT, NW, E>), dim3(gx, gy), dim3(64 * kw), lds, st, a);
-    return hipGetLastError();
+// Split-K epilogue: sum the ks partials in slice order, then bias and the epilogue.
+template <int E>
+__global__ __launch_bounds__(256) void dreduce_kernel(DGemm a) {
+    const int k = blockIdx.x * 256 + threadIdx.x;
+    if (k >= a.R * a.N) return;
+    const int m = k / a.N, n = k % a.N;
+    float sum = 0.0f;
+    for (int z = 0; z < a.ks; z++) sum += gld(a.part + (size_t)z * a.R * a.N + k);
+    const float e = rb(sum + bf2f(gld(a.b[0] + n)));
+    const size_t off = (size_t)m * a.ldo + n;
+    if constexpr (E == DE_BIAS) gst(a.out + off, f2bf(e));
+    if constexpr (E == DE_RES) gst(a.out + off, f2bf(bf2f(gld(a.res + off)) + e));
+    if constexpr (E == DE_GELU) gst(a.out + off, f2bf(gelu_chain_b(e)));
 }
 
-// Row tiles per wave and K split from the shape: enough workgroups to cover
-// the CUs, at most 4 row tiles, at most 4 waves (one per SIMD: a wave may
-// hold 512 registers), LDS for the K split within 64 KB.
+// 64-row tiles when they still give >= 128 workgroups, else 32-row tiles.
+// K >= 2048 (plain epilogues, with a partials buffer) splits four ways across
+// workgroups; the split depends on K alone, so a row's arithmetic does not
+// depend on how many rows are batched.
 template <int E>
-hipError_t dpick(hipStream_t st, const DGemm& a) {
-    const int mtt = (a.R + 15) / 16, G = a.K / 64, gx = (a.N + 63) / 64;
-    int mt = 1;
-    if (mtt % 4 == 0 && gx * (mtt / 4) >= 128) mt = 4;
-    else if (mtt % 2 == 0 && gx * (mtt / 2) >= 128) mt = 2;
-    int kw = G >= 8 ? 4 : (G >= 2 ? 2 : 1);
-    while (kw > 1 && (size_t)kw * mt * 4 * 4 * kWave * 4 > 65536) kw /= 2;
-    if (E == DE_CFM) mt = 1;
-    switch (mt) {
-        case 4: return dlaunch<4, 4, E>(st, a, kw);
-        case 2: return dlaunch<2, 4, E>(st, a, kw);
-        default: return dlaunch<1, 4, E>(st, a, kw);
+hipError_t dpick(hipStream_t st, DGemm a) {
+    const int gx = (a.N + kBN - 1) / kBN;
+    a.ks = (E == DE_BIAS || E == DE_RES || E == DE_GELU) && a.part && a.K >= 2048 && a.K % (4 * kBK) == 0 ? 4 : 1;
+    if (a.K % (kBK * a.ks)) return hipErrorInvalidValue;
+    if (gx * ((a.R + 63) / 64) * a.ks >= 128) {
+        hipLaunchKernelGGL((dgemm_kernel<64, E>), dim3(gx, (a.R + 63) / 64, a.ks), dim3(256), 0, st, a);
+    } else {
+        hipLaunchKernelGGL((dgemm_kernel<32, E>), dim3(gx, (a.R + 31) / 32, a.ks), dim3(256), 0, st, a);
     }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.ks == 1) return e;
+    if constexpr (E == DE_BIAS || E == DE_RES || E == DE_GELU) {
+        hipLaunchKernelGGL(dreduce_kernel<E>, dim3((a.R * a.N + 255) / 256), dim3(256), 0, st, a);
+        e = hipGetLastError();
+    }
+    return e;
 }
 
 DGemm gemm_args(const uint16_t* x, int R, int N, int K, const uint16_t* w, const uint16_t* b, uint16_t* out) {
@@ -298,6 +339,7 @@ DGemm gemm_args(const uint16_t* x, int R, int N, int K, const uint16_t* w, const
     a.b[0] = a.b[1] = a.b[2] = b;
     a.out = out;
     a.ldo = N;
+    a.ks = 1;
     return a;
 }
 
@@ -305,10 +347,11 @@ DGemm gemm_args(const uint16_t* x, int R, int N, int K, const uint16_t* w, const
 
 // One DiT block over R rows of L positions: rms1 -> q/k/v (+ rotary) -> attention
 // -> out_proj + residual -> rms2 -> ff1 + gelu -> ff2 + residual.  x and out may
-// not alias; hn [R][D], qkv [3][R][D], att [R][D], x1 [R][D], hh [R][F] scratch.
+// not alias; hn [R][D], qkv [3][R][D], att [R][D], x1 [R][D], hh [R][F] and
+// part [4][R][D] f32 scratch.
 hipError_t launch_dit_block_gemm(hipStream_t st, const DitBlockDev& w, const uint16_t* x, int R, int L,
                                  const float* cos_t, const float* sin_t, uint16_t* hn, uint16_t* qkv, uint16_t* att,
-                                 uint16_t* x1, uint16_t* hh, uint16_t* out) {
+                                 uint16_t* x1, uint16_t* hh, uint16_t* out, float* part) {
     const int D = w.D, F = w.F;
     hipError_t e;
     hipLaunchKernelGGL(drms_kernel, dim3(R), dim3(256), 0, st, x, D, 0, w.norm1, w.eps, hn);
@@ -333,6 +376,7 @@ hipError_t launch_dit_block_gemm(hipStream_t st, const DitBlockDev& w, const uin
     if ((e = dpick<DE_GELU>(st, a)) != hipSuccess) return e;
     a = gemm_args(hh, R, D, F, w.w2, w.b2, out);
     a.res = x1;
+    a.part = part;  // [4][R][D] f32: ff2's K = F splits
     return dpick<DE_RES>(st, a);
 }
 
