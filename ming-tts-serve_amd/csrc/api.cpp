@@ -50,6 +50,24 @@ bool env_off(const char* name) {
 
 bool alive(const ming_ctx* c) { return c && c->alive; }
 
+// Stages of the persistent schedule whose inputs the per-XCD hubs stage
+// (HUB_* bits).  Measured on MI355X at ctx 2048: the hubs pay off where many
+// workgroups read one normalised vector (q/k/v, gate/up, head); o and down
+// (64 workgroups each) are faster staging their inputs themselves.
+// MING_LM_HUB_STAGES (a decimal bit mask) overrides the choice.
+int hub_stages() {
+    static const int v = [] {
+        const char* e = std::getenv("MING_LM_HUB_STAGES");
+        if (e && *e) {
+            char* end = nullptr;
+            const long x = std::strtol(e, &end, 10);
+            if (end && *end == '\0' && x >= 0 && x < 32) return (int)x;
+        }
+        return (int)(HUB_QKV | HUB_UP | HUB_HEAD);
+    }();
+    return v;
+}
+
 [[maybe_unused]] int64_t numel(const ming_tensor* t) {
     int64_t n = 1;
     for (int i = 0; i < t->ndim; i++) n *= t->shape[i];
@@ -699,6 +717,7 @@ static int lm_step_impl(ming_ctx* ctx, ming_lm_model* m, const int32_t* token_de
         a.counters = static_cast<int32_t*>(m->counters.p);
         a.tstamp = m->tstamp;
         a.nhubs = nhubs;
+        a.hub_stages = hub_stages();
         a.img = static_cast<uint32_t*>(m->img.p);
         a.img_stride = m->img_stride;
         a.hflag = static_cast<uint32_t*>(m->hflag.p);

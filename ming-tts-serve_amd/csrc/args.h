@@ -71,12 +71,16 @@ struct StepArgs {
     // the staged GEMV input of every stage into memory that the other
     // workgroups of its XCD read through their shared L2.
     int nhubs;                // 0: every workgroup stages its own inputs
+    int hub_stages;           // stages whose inputs come from the hubs (HUB_* bits); the others stage their own
     uint32_t* img;            // [kMaxHubs][kImgSlots][img_stride] stage images
     int img_stride;           // u32 words per image slot
     uint32_t* hflag;          // [kMaxHubs][nflag] epoch of each published image
     int nflag;                // flag words per hub (>= 4 * n_layers + 1)
     uint64_t* hubtab;         // [kMaxHubs] tagged XCC id of each hub
 };
+
+// Stages of the persistent schedule, as bits of StepArgs::hub_stages.
+enum : int { HUB_QKV = 1, HUB_O = 2, HUB_UP = 4, HUB_DOWN = 8, HUB_HEAD = 16 };
 
 // One DiT block (fused.Block, src/ming_fused.zig:482-500): bf16 [out, in]
 // linears with biases, two RMSNorm weights; D = hidden, F = feed-forward.

@@ -262,14 +262,16 @@ __device__ __forceinline__ void build_image(const StepArgs& a, uint32_t* lds, co
 }
 
 // Worker: the stage image of flag fidx / image slot `slot` into LDS (xs at
-// kXsOff).  With a hub, wave 0 waits for its flag and copies the image (waves
-// 1..7 meanwhile have their weight loads in flight); without one, all waves
-// build it here.  The first barrier also ends the previous stage's use of LDS.
+// kXsOff).  With a hub serving this stage, wave 0 waits for its flag and
+// copies the image (waves 1..7 meanwhile have their weight loads in flight);
+// otherwise all waves build it here.  The first barrier also ends the previous stage's use of LDS.
+__device__ __forceinline__ bool hub_on(const StepArgs& a, int stage) { return a.nhubs > 0 && (a.hub_stages & stage); }
+
 template <int Q4>
-__device__ __forceinline__ void get_image(const Ctx& c, int fidx, int slot, const uint64_t* src, int K,
+__device__ __forceinline__ void get_image(const Ctx& c, int stage, int fidx, int slot, const uint64_t* src, int K,
                                           const uint16_t* norm_w, uint16_t* hidden) {
     const StepArgs& a = c.a;
-    if (c.hub < 0) {
+    if (c.hub < 0 || !(a.hub_stages & stage)) {
         lds_sync();
         build_image<Q4, true>(a, c.lds, src, K, norm_w, c.lds + kXsOff, hidden);
         lds_sync();
@@ -311,13 +313,18 @@ __device__ __forceinline__ void hub_main(const StepArgs& a, const LayerDev* __re
     const size_t st = a.img_stride;
     for (int l = 0; l < L; l++) {
         const LayerDev& Ld = layers[l];
-        hub_publish<Q4>(a, lds, a.tx + (size_t)l * (H / 2), H, Ld.ln1, img, fl + 4 * l, nullptr);
-        hub_publish<Q4>(a, lds, a.ta + (size_t)l * (H / 2), H, nullptr, img + st, fl + 4 * l + 1, nullptr);
-        hub_publish<Q4>(a, lds, a.tx1 + (size_t)l * (H / 2), H, Ld.ln2, img + 2 * st, fl + 4 * l + 2, nullptr);
-        hub_publish<Q4>(a, lds, a.th + (size_t)l * (a.I / 2), a.I, nullptr, img + 3 * st, fl + 4 * l + 3, nullptr);
+        const int hs = a.hub_stages;
+        if (hs & HUB_QKV) hub_publish<Q4>(a, lds, a.tx + (size_t)l * (H / 2), H, Ld.ln1, img, fl + 4 * l, nullptr);
+        if (hs & HUB_O)
+            hub_publish<Q4>(a, lds, a.ta + (size_t)l * (H / 2), H, nullptr, img + st, fl + 4 * l + 1, nullptr);
+        if (hs & HUB_UP)
+            hub_publish<Q4>(a, lds, a.tx1 + (size_t)l * (H / 2), H, Ld.ln2, img + 2 * st, fl + 4 * l + 2, nullptr);
+        if (hs & HUB_DOWN)
+            hub_publish<Q4>(a, lds, a.th + (size_t)l * (a.I / 2), a.I, nullptr, img + 3 * st, fl + 4 * l + 3, nullptr);
     }
-    hub_publish<Q4>(a, lds, a.tx + (size_t)L * (H / 2), H, a.final_norm, img + 4 * st, fl + 4 * L,
-                    b == 0 ? a.hidden : nullptr);
+    if (a.hub_stages & HUB_HEAD)
+        hub_publish<Q4>(a, lds, a.tx + (size_t)L * (H / 2), H, a.final_norm, img + 4 * st, fl + 4 * L,
+                        b == 0 ? a.hidden : nullptr);
 }
 
 // Worker: the first hub whose XCC id equals this workgroup's, or -1.
@@ -428,7 +435,7 @@ __device__ __forceinline__ void st_qkv(const Ctx& c, const LayerDev& Ld, int l) 
         row_load<Q4, 32, Nc<Q4>::t32>(L, r0, c.tl, 0, W.w0);
         row_load<Q4, 32, Nc<Q4>::t32>(L, r0 + 1, c.tl, 0, W.w1);
     }
-    get_image<Q4>(c, 4 * l, 0, a.tx + (size_t)l * (a.H / 2), a.H, Ld.ln1, nullptr);
+    get_image<Q4>(c, HUB_QKV, 4 * l, 0, a.tx + (size_t)l * (a.H / 2), a.H, Ld.ln1, nullptr);
     stamp(a, slot_in(l, 0));
     if (!g.has) return;
     const XStage st = xs_of(c.lds, a.H);
@@ -711,7 +718,7 @@ __device__ __forceinline__ void st_o(const Ctx& c, const LayerDev& Ld, int l) {
         if (c.lane == 0) xpre = tload(xsrc);
         row_load<Q4, 32, Nc<Q4>::t32>(Ld.o, r, c.tl, 0, W);
     }
-    get_image<Q4>(c, 4 * l + 1, 1, a.ta + (size_t)l * (a.H / 2), a.H, nullptr, nullptr);
+    get_image<Q4>(c, HUB_O, 4 * l + 1, 1, a.ta + (size_t)l * (a.H / 2), a.H, nullptr, nullptr);
     stamp(a, slot_in(l, 2));
     if (!has) return;
     const float acc = row_dot_pf<Q4, 32, Nc<Q4>::t32>(Ld.o, r, xs_of(c.lds, a.H), c.tl, W);
@@ -748,7 +755,7 @@ __device__ __forceinline__ void st_up(const Ctx& c, const LayerDev& Ld, int l) {
             }
         }
     }
-    get_image<Q4>(c, 4 * l + 2, 2, a.tx1 + (size_t)l * (a.H / 2), a.H, Ld.ln2, nullptr);
+    get_image<Q4>(c, HUB_UP, 4 * l + 2, 2, a.tx1 + (size_t)l * (a.H / 2), a.H, Ld.ln2, nullptr);
     stamp(a, slot_in(l, 3));
     if (c.wave == 0) return;
     const XStage st = xs_of(c.lds, a.H);
@@ -762,15 +769,24 @@ __device__ __forceinline__ void st_up(const Ctx& c, const LayerDev& Ld, int l) {
             gst(reinterpret_cast<uint32_t*>(a.hh + l * a.sh) + p, wv);
         }
     };
+    // Every preloaded unit's dot products before any unit's stores: stores
+    // count in the same memory counter as loads, so a dot product issued
+    // after a store would wait for that store's device-coherent round trip.
+    float acc[MU][2];
 #pragma unroll
     for (int i = 0; i < MU; i++) {
         const int s = c.wave - 1 + i * kCW;
+        acc[i][0] = acc[i][1] = 0.0f;
         if (s < slots) {
             const int p = c.w + s * c.W;
-            const float acc0 = row_dot_pf<Q4, 32, Nc<Q4>::t32>(L, 2 * p, st, c.tl, W[i][0]);
-            const float acc1 = row_dot_pf<Q4, 32, Nc<Q4>::t32>(L, 2 * p + 1, st, c.tl, W[i][1]);
-            finish(p, acc0, acc1);
+            acc[i][0] = row_dot_pf<Q4, 32, Nc<Q4>::t32>(L, 2 * p, st, c.tl, W[i][0]);
+            acc[i][1] = row_dot_pf<Q4, 32, Nc<Q4>::t32>(L, 2 * p + 1, st, c.tl, W[i][1]);
         }
+    }
+#pragma unroll
+    for (int i = 0; i < MU; i++) {
+        const int s = c.wave - 1 + i * kCW;
+        if (s < slots) finish(c.w + s * c.W, acc[i][0], acc[i][1]);
     }
     // units beyond the preloaded ones (only when a worker has more than MU * kCW)
     for (int s = c.wave - 1 + MU * kCW; s < slots; s += kCW) {
@@ -785,23 +801,33 @@ __device__ __forceinline__ void st_up(const Ctx& c, const LayerDev& Ld, int l) {
 }
 
 // ---- LE: down + residual (unit = row pair, packed on the compute waves) --------------
+// The weight loads are issued before the gate/up stage (down_pre): a wave's
+// loads complete in issue order, so loads issued after gate/up would hold
+// back this stage's receipt of its input behind them.
 template <int Q4>
-__device__ __forceinline__ void st_down(const Ctx& c, const LayerDev& Ld, int l) {
+struct DownPre {
+    RowRegs<Nc<Q4>::down> W;
+};
+
+template <int Q4>
+__device__ __forceinline__ void down_pre(const Ctx& c, const LayerDev& Ld, DownPre<Q4>& d) {
+    const int p = c.w * kCW + c.wave - 1;
+    if (c.wave > 0 && p < c.a.H / 2) row_load<Q4, 32, Nc<Q4>::down>(Ld.d, 2 * p + c.team, c.tl, 0, d.W);
+}
+
+template <int Q4>
+__device__ __forceinline__ void st_down(const Ctx& c, const LayerDev& Ld, int l, const DownPre<Q4>& d) {
     const StepArgs& a = c.a;
     const int p = c.w * kCW + c.wave - 1;
     const bool has = c.wave > 0 && p < a.H / 2;
     const int r = 2 * p + c.team;
     const uint64_t* xsrc = a.tx1 + (size_t)l * (a.H / 2) + p;  // residual, produced two stages ago
     uint64_t xpre = 0;
-    RowRegs<Nc<Q4>::down> W;
-    if (has) {
-        if (c.lane == 0) xpre = tload(xsrc);
-        row_load<Q4, 32, Nc<Q4>::down>(Ld.d, r, c.tl, 0, W);
-    }
-    get_image<Q4>(c, 4 * l + 3, 3, a.th + (size_t)l * (a.I / 2), a.I, nullptr, nullptr);
+    if (has && c.lane == 0) xpre = tload(xsrc);
+    get_image<Q4>(c, HUB_DOWN, 4 * l + 3, 3, a.th + (size_t)l * (a.I / 2), a.I, nullptr, nullptr);
     stamp(a, slot_in(l, 4));
     if (!has) return;
-    const float acc = row_dot_pf<Q4, 32, Nc<Q4>::down>(Ld.d, r, xs_of(c.lds, a.I), c.tl, W);
+    const float acc = row_dot_pf<Q4, 32, Nc<Q4>::down>(Ld.d, r, xs_of(c.lds, a.I), c.tl, d.W);
     const float a0 = __shfl(acc, 0, kWave), a1 = __shfl(acc, 32, kWave);
     if (c.lane == 0) {
         const uint32_t xw = tfinish(xsrc, xpre, a.epoch, a.flags);
@@ -860,8 +886,9 @@ template <int Q4>
 __device__ __forceinline__ void st_head(const Ctx& c) {
     const StepArgs& a = c.a;
     if (!a.logits && !a.argmax_out) {  // hidden only: hub 0 (or worker 0) writes it, no head
-        if (a.nhubs == 0 && c.w == 0)
-            get_image<Q4>(c, 4 * a.n_layers, 4, a.tx + (size_t)a.n_layers * (a.H / 2), a.H, a.final_norm, a.hidden);
+        if (!hub_on(a, HUB_HEAD) && c.w == 0)
+            get_image<Q4>(c, HUB_HEAD, 4 * a.n_layers, 4, a.tx + (size_t)a.n_layers * (a.H / 2), a.H, a.final_norm,
+                          a.hidden);
         return;
     }
     const int V = a.head.N, nunits = V / 2 + (V & 1);
@@ -871,9 +898,9 @@ __device__ __forceinline__ void st_head(const Ctx& c) {
 #pragma unroll
         for (int i = 0; i < kHeadDepth; i++) head_slot_load<Q4>(c, me + i * nw, W.w[i]);
     }
-    // the hidden output comes from hub 0, or from worker 0 when there are no hubs
-    get_image<Q4>(c, 4 * a.n_layers, 4, a.tx + (size_t)a.n_layers * (a.H / 2), a.H, a.final_norm,
-                  a.nhubs == 0 && c.w == 0 ? a.hidden : nullptr);
+    // the hidden output comes from hub 0, or from worker 0 when no hub serves the head
+    get_image<Q4>(c, HUB_HEAD, 4 * a.n_layers, 4, a.tx + (size_t)a.n_layers * (a.H / 2), a.H, a.final_norm,
+                  !hub_on(a, HUB_HEAD) && c.w == 0 ? a.hidden : nullptr);
     stamp(a, slot_in(a.n_layers, 0));
     const XStage st = xs_of(c.lds, a.H);
     float bv = -INFINITY;
@@ -982,10 +1009,12 @@ __global__ __launch_bounds__(kT) void decode_tagged_kernel(StepArgs args, const 
             st_o<Q4>(c, Ld, l);
             done_stamp(a, slot_in(l, 2) + 1);
         }
+        DownPre<Q4> dp;
+        if (po) down_pre<Q4>(c, Ld, dp);
         st_up<Q4>(c, Ld, l);
         done_stamp(a, slot_in(l, 3) + 1);
         if (po) {
-            st_down<Q4>(c, Ld, l);
+            st_down<Q4>(c, Ld, l, dp);
             done_stamp(a, slot_in(l, 4) + 1);
         }
     }
