@@ -66,6 +66,8 @@ typedef struct {
 typedef struct ming_ctx ming_ctx;
 
 int ming_ctx_create(ming_ctx** out, int device);
+/* Model, batch and weights handles may be destroyed before or after the
+ * context they were created on (their destroy calls do not touch it). */
 int ming_ctx_destroy(ming_ctx* ctx);
 /* Run on a caller-owned hipStream_t, used as given: NULL is HIP's null
  * (default) stream.  A new context runs on a stream of its own until this is

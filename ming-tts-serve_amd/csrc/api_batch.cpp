@@ -101,7 +101,8 @@ int ming_lm_batch_create(ming_ctx* ctx, ming_lm_model* m, int32_t max_seqs, int3
 
 int ming_lm_batch_destroy(ming_lm_batch* b) {
     if (!b) return MING_OK;
-    if (b->ctx && b->ctx->stream) (void)hipStreamSynchronize(b->ctx->stream);
+    // the context may already be destroyed: wait for the device, not its stream
+    (void)hipDeviceSynchronize();
     for (DevBuf* d : {&b->x, &b->x1, &b->qkv, &b->att, &b->hh, &b->xs, &b->xsum, &b->part, &b->pmax, &b->pidx,
                       &b->hid, &b->rope, &b->prows, &b->ppos})
         d->release();

@@ -13,10 +13,6 @@ namespace ming {
 
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ bf16x8_t as_bf8(uint4 v) { return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w}); }
 
 // 8 bf16 of a 16-byte word in natural order -> pair order (x0,x4) (x1,x5) (x2,x6) (x3,x7).
 __device__ __forceinline__ uint4 pair_order(uint4 e) {

@@ -166,4 +166,9 @@ __device__ __forceinline__ uint4 ldg4(const void* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// MFMA operand and accumulator types (v_mfma_f32_16x16x32_bf16).
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x8_t as_bf8(uint4 v) { return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w}); }
+
 }  // namespace ming

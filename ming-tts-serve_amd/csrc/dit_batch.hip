@@ -20,8 +20,6 @@ namespace ming {
 
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 enum DEpi : int { DE_BIAS = 0, DE_RES = 1, DE_GELU = 2, DE_QKV = 3, DE_CFM = 4 };
 

@@ -565,7 +565,8 @@ int ming_weights_load(ming_ctx* ctx, const char* path, const char* const* prefix
 
 int ming_weights_destroy(ming_weights* w) {
     if (!w) return MING_OK;
-    if (w->ctx && w->ctx->stream) (void)hipStreamSynchronize(w->ctx->stream);
+    // the context may already be destroyed: wait for the device, not its stream
+    (void)hipDeviceSynchronize();
     for (void* p : w->extra) (void)hipFree(p);
     if (w->base) (void)hipFree(w->base);
     delete w;

@@ -134,7 +134,7 @@ def test_flow_head_aggregator_stop_from_checkpoint(ming, ctx, tmp_path):
     ps = []
     for head, bias in ((w.linear("stop_head", 2, spec.lm_hidden), w.get("stop_head.bias").data),
                        (flow.lin_w("stop_head"), flow.ptr("stop_head.bias"))):
-        p = torch.empty(2, dtype=torch.float32, device="cuda")
+        p = torch.empty(1, dtype=torch.float32, device="cuda")  # ming_stop_prob writes one f32
         ctx.stop_prob(head, bias, z, p)
         ps.append(p)
     ctx.sync()
@@ -167,4 +167,23 @@ def test_missing_and_misshapen_weights(ming, ctx, tmp_path):
     with pytest.raises(ming.MingError) as e:  # the checkpoint holds 2 layers
         w.lm_model(short)
     assert e.value.status == ming.MING_E_SHAPE
+    w.close()
+
+
+def test_handles_outlive_their_context(ming, tmp_path):
+    """Weights, models and batches destroyed after their context (as at
+    interpreter exit) release their memory without touching the context."""
+    S = syn_mod()
+    ctx2 = ming.Context(0)
+    spec = S.LmSpec(**SMALL)
+    syn = S.SyntheticLm(ctx2, spec, seed=49, quant=True)
+    path = tmp_path / "lm.safetensors"
+    save(path, lm_tensors(syn))
+    w = ming.Weights(ctx2, path)
+    m = w.lm_model(spec.cfg())
+    b = ming.LmBatch(m, 4, 256)
+    ctx2.sync()
+    ctx2.close()
+    b.close()
+    m.close()
     w.close()
