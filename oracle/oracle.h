@@ -271,6 +271,53 @@ void or_adaln_sample(const or_adaln_model* m, const uint16_t* z, const uint16_t*
 void or_set_threads(int n);
 int or_get_threads(void);
 
+/* ---- VAE decoder (oracle_vae.c; src/ming_model.zig:1257-1340, :566-636) ---- */
+typedef struct {
+    int hidden, heads, kv_heads, head_dim, inter, n_layers;
+    float eps, log2_theta;
+    int window;                 /* sliding attention window (64) */
+    int latent, patch;          /* latent width (64), upsample factor (4) */
+    int n_fft, hop;             /* ISTFT (3528, 882; n_fft = 4 hop) */
+} or_vae_cfg;
+
+typedef struct {
+    or_vae_cfg cfg;
+    or_linear fc1;              /* [hidden, latent] */
+    const uint16_t* fc1_bias;   /* bf16 [hidden] or NULL */
+    const or_lm_layer* layers;  /* [n_layers]; q/k/v biases may be NULL */
+    const uint16_t* norm;       /* bf16 [hidden] */
+    or_linear head;             /* [n_fft + 2, hidden] */
+    const uint16_t* head_bias;  /* bf16 [n_fft + 2] or NULL */
+    const float* window_fn;     /* f32 [n_fft] */
+} or_vae_model;
+
+/* Intermediates of one VAE layer over F rows (optional, f32). */
+typedef struct {
+    float* qkv;  /* [F][hidden + 2 kv_heads head_dim] roped q | roped k | v */
+    float* att;  /* [F][hidden] */
+    float* x1;   /* [F][hidden] */
+    float* hh;   /* [F][inter] */
+} or_vae_trace;
+
+/* f32 activations through a bf16 or affine linear (+ bf16 bias): y [M][N] f32. */
+void or_linear_f32(const or_linear* L, const float* x, int64_t M, const uint16_t* bias, float* y);
+/* fast::rms_norm on f32 rows, bf16 weight: out = w * (x * rsqrt(mean(x^2) + eps)) in f32. */
+void or_rms_f32(const float* x, const uint16_t* w, int64_t M, int64_t n, float eps, float* out);
+/* fast::rope, traditional=false, f32 heads [nh][hd] in place. */
+void or_rope_f32(float* x, int nh, int hd, int pos, float log2_base);
+/* linear upsample x scale, align_corners=False: bf16 [T][C] -> f32 [T*scale][C]. */
+void or_linear_upsample(const uint16_t* x, int T, int C, int scale, float* y);
+/* sliding-window causal attention: q [F][heads][hd], k/v [F][kv_heads][hd] f32 -> [F][heads][hd]. */
+void or_window_attention(const float* q, const float* k, const float* v, int F, int heads, int kv_heads, int hd,
+                         int window, float scale, float* out);
+/* one backbone layer over F rows (positions 0..F-1): x [F][hidden] -> x_out. */
+void or_vae_layer(const or_vae_cfg* c, const or_lm_layer* l, const float* x, int F, float* x_out, or_vae_trace* tr);
+/* ISTFT head: p [F][n_fft + 2] (log-magnitudes | phases) -> wave [F * hop]; frames (optional) [F][n_fft]. */
+void or_vae_istft(const float* p, int F, int n_fft, int hop, const float* win, float* wave, float* frames);
+/* Model.vaeDecode: latents bf16 [T][latent] -> wave f32 [T * patch * hop]; xs (optional)
+ * [n_layers + 1][F][hidden] layer inputs (xs[0] = upsampled fc1 rows); head_out (optional) [F][n_fft + 2]. */
+void or_vae_decode(const or_vae_model* m, const uint16_t* latents, int T, float* wave, float* xs, float* head_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -79,6 +79,21 @@ class OrAggModel(ctypes.Structure):
                 ("cos_t", c_void_p), ("sin_t", c_void_p)]
 
 
+class OrVaeCfg(ctypes.Structure):
+    _fields_ = [("hidden", c_int), ("heads", c_int), ("kv_heads", c_int), ("head_dim", c_int), ("inter", c_int),
+                ("n_layers", c_int), ("eps", c_f32), ("log2_theta", c_f32), ("window", c_int), ("latent", c_int),
+                ("patch", c_int), ("n_fft", c_int), ("hop", c_int)]
+
+
+class OrVaeModel(ctypes.Structure):
+    _fields_ = [("cfg", OrVaeCfg), ("fc1", OrLinear), ("fc1_bias", c_void_p), ("layers", c_void_p),
+                ("norm", c_void_p), ("head", OrLinear), ("head_bias", c_void_p), ("window_fn", c_void_p)]
+
+
+class OrVaeTrace(ctypes.Structure):
+    _fields_ = [("qkv", c_void_p), ("att", c_void_p), ("x1", c_void_p), ("hh", c_void_p)]
+
+
 _lib = None
 
 
@@ -134,6 +149,15 @@ def lib():
                                   c_void_p]),
         "or_adaln_sample": (None, [P(OrAdalnModel), c_void_p, c_void_p, c_void_p, c_f32, c_f32, c_void_p,
                                    c_void_p]),
+        "or_linear_f32": (None, [P(OrLinear), c_void_p, c_i64, c_void_p, c_void_p]),
+        "or_rms_f32": (None, [c_void_p, c_void_p, c_i64, c_i64, c_f32, c_void_p]),
+        "or_rope_f32": (None, [c_void_p, c_int, c_int, c_int, c_f32]),
+        "or_linear_upsample": (None, [c_void_p, c_int, c_int, c_int, c_void_p]),
+        "or_window_attention": (None, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_f32,
+                                       c_void_p]),
+        "or_vae_layer": (None, [P(OrVaeCfg), P(OrLmLayer), c_void_p, c_int, c_void_p, P(OrVaeTrace)]),
+        "or_vae_istft": (None, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+        "or_vae_decode": (None, [P(OrVaeModel), c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
         "or_set_threads": (None, [c_int]),
         "or_get_threads": (c_int, []),
     }
@@ -545,3 +569,106 @@ def adaln_sample(m, z, noise, sde, cfg, shift):
                           _p(None if sde is None else _c(sde, np.uint16)), float(cfg), float(shift), _p(out),
                           _p(steps))
     return out, steps
+
+
+# ---- VAE decoder (oracle_vae.c) -----------------------------------------------
+
+def vae_cfg(hidden=896, heads=14, kv_heads=2, head_dim=64, inter=4864, n_layers=24, eps=1e-6, theta=1e6,
+            window=64, latent=64, patch=4, n_fft=3528, hop=882):
+    return OrVaeCfg(hidden, heads, kv_heads, head_dim, inter, n_layers, eps, float(np.log2(np.float32(theta))),
+                    window, latent, patch, n_fft, hop)
+
+
+def linear_f32(L, x, bias=None):
+    x = _c(x, np.float32)
+    M = x.size // L.K
+    y = np.empty((M, L.N), np.float32)
+    lib().or_linear_f32(ctypes.byref(L.c), _p(x), M, _p(None if bias is None else _c(bias, np.uint16)), _p(y))
+    return y.reshape(x.shape[:-1] + (L.N,))
+
+
+def rms_f32(x, w, eps=1e-6):
+    x, w = _c(x, np.float32), _c(w, np.uint16)
+    out = np.empty_like(x)
+    lib().or_rms_f32(_p(x), _p(w), x.size // w.size, w.size, eps, _p(out))
+    return out
+
+
+def rope_f32(x, pos, log2_base):
+    x = np.array(x, dtype=np.float32, copy=True, order="C")
+    nh, hd = x.shape
+    lib().or_rope_f32(_p(x), nh, hd, int(pos), float(log2_base))
+    return x
+
+
+def linear_upsample(x, scale):
+    """bf16 [T, C] -> f32 [T*scale, C]."""
+    x = _c(x, np.uint16)
+    T, C = x.shape
+    y = np.empty((T * scale, C), np.float32)
+    lib().or_linear_upsample(_p(x), T, C, int(scale), _p(y))
+    return y
+
+
+def window_attention(q, k, v, window, scale=None):
+    """q [F, heads, hd], k/v [F, kv_heads, hd] f32 -> [F, heads, hd]."""
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    F, heads, hd = q.shape
+    out = np.empty_like(q)
+    lib().or_window_attention(_p(q), _p(k), _p(v), F, heads, k.shape[1], hd, int(window),
+                              float(scale if scale is not None else 1.0 / np.sqrt(np.float32(hd))), _p(out))
+    return out
+
+
+def vae_layer(c, layer, x, trace=False):
+    """One backbone layer over F rows: x f32 [F, hidden] -> f32 [F, hidden]."""
+    x = _c(x, np.float32)
+    F = x.shape[0]
+    out = np.empty_like(x)
+    arrs, tr = {}, None
+    if trace:
+        kvd = c.kv_heads * c.head_dim
+        arrs = dict(qkv=np.empty((F, c.hidden + 2 * kvd), np.float32), att=np.empty((F, c.hidden), np.float32),
+                    x1=np.empty((F, c.hidden), np.float32), hh=np.empty((F, c.inter), np.float32))
+        tr = OrVaeTrace(*(_p(arrs[k]) for k in ("qkv", "att", "x1", "hh")))
+    lib().or_vae_layer(ctypes.byref(c), ctypes.byref(layer.c), _p(x), F, _p(out),
+                       ctypes.byref(tr) if tr is not None else None)
+    return (out, arrs) if trace else out
+
+
+def vae_istft(p, n_fft, hop, win, frames=False):
+    """p f32 [F, n_fft + 2] (log-magnitudes | phases) -> wave f32 [F * hop] (and the windowed frames)."""
+    p, win = _c(p, np.float32), _c(win, np.float32)
+    F = p.shape[0]
+    wave = np.empty(F * hop, np.float32)
+    fr = np.empty((F, n_fft), np.float32) if frames else None
+    lib().or_vae_istft(_p(p), F, int(n_fft), int(hop), _p(win), _p(wave), _p(fr))
+    return (wave, fr) if frames else wave
+
+
+class VaeModel:
+    """The VAE decoder's arrays (fc1, layers as LmLayer, final norm, head, window) and their OrVaeModel view."""
+
+    def __init__(self, c, fc1, fc1_bias, layers, norm, head, head_bias, window_fn):
+        self.keep = [None if fc1_bias is None else _c(fc1_bias, np.uint16), _c(norm, np.uint16),
+                     None if head_bias is None else _c(head_bias, np.uint16), _c(window_fn, np.float32)]
+        self.layers = layers
+        self.fc1, self.head = fc1, head
+        self.arr = (OrLmLayer * len(layers))(*(l.c for l in layers))
+        self.c = OrVaeModel(c, fc1.c, _p(self.keep[0]), ctypes.cast(self.arr, c_void_p), _p(self.keep[1]), head.c,
+                            _p(self.keep[2]), _p(self.keep[3]))
+        self.cfg = c
+
+
+def vae_decode(m, latents, trace=False):
+    """latents bf16 [T, latent] -> wave f32 [T * patch * hop] (and the layer inputs xs
+    [n_layers + 1, F, hidden] and the head output [F, n_fft + 2] when trace)."""
+    latents = _c(latents, np.uint16)
+    c = m.cfg
+    T = latents.shape[0]
+    F = T * c.patch
+    wave = np.empty(F * c.hop, np.float32)
+    xs = np.empty((c.n_layers + 1, F, c.hidden), np.float32) if trace else None
+    ho = np.empty((F, c.n_fft + 2), np.float32) if trace else None
+    lib().or_vae_decode(ctypes.byref(m.c), _p(latents), T, _p(wave), _p(xs), _p(ho))
+    return (wave, xs, ho) if trace else wave
