@@ -69,10 +69,11 @@ HBM_PEAK_GBS = 8000.0
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--workload", choices=["lm", "cfm", "c4", "loop", "server", "prefill"], default="lm")
+    p.add_argument("--workload", choices=["lm", "cfm", "c4", "loop", "server", "prefill", "vae"], default="lm")
     p.add_argument("--seqs", type=int, default=64, help="server workload: concurrent sequences")
     p.add_argument("--lm-only", action="store_true", help="server workload: no DiT head")
     p.add_argument("--prompt", type=int, default=512, help="prefill workload: prompt tokens")
+    p.add_argument("--latents", type=int, default=100, help="vae workload: latents per decode")
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--ctx", type=int, default=2048)
@@ -98,6 +99,8 @@ def main():
         return bench_server(args)
     if args.workload == "prefill":
         return bench_prefill(args)
+    if args.workload == "vae":
+        return bench_vae(args)
     import torch
 
     ming = importlib.import_module("ming-tts-serve_amd")
@@ -377,6 +380,69 @@ def bench_prefill(args):
                       "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": nbytes,
                       "launch_ms": round(ms, 5)},
                      cpu, "synthetic (random-init N(0,0.02) weights quantized to MLX affine 4-bit/g64)")
+    print(json.dumps(line), flush=True)
+
+
+METRIC_VAE = "VAE decoder latents/s (fc1, 4x upsample, 24-layer sliding-window Qwen2, ISTFT head; f32 graph) + achieved TFLOP/s"
+MFMA_F32_PEAK_TFLOPS = 157.3
+
+
+def vae_flops(spec, T):
+    """Algorithmic FLOPs of one decode of T latents: every linear (2 per weight per row), the
+    window attention (q.k and p.v over at most `window` keys) and the irfft as a matrix product."""
+    F = T * spec.patch
+    H, kvd, I = spec.hidden, spec.kvd, spec.inter
+    layer = H * H * 2 + 2 * kvd * H + 3 * H * I
+    keys = sum(min(i + 1, spec.window) for i in range(F))
+    attn = 2 * 2 * keys * spec.heads * spec.head_dim
+    return (2 * T * H * spec.latent + 2 * F * layer * spec.n_layers + spec.n_layers * attn
+            + 2 * F * (spec.n_fft + 2) * H + 2 * F * (spec.n_fft + 2) * spec.n_fft)
+
+
+def bench_vae(args):
+    import numpy as np
+    import torch
+
+    ming = importlib.import_module("ming-tts-serve_amd")
+    S = importlib.import_module("ming-tts-serve_amd.synthetic")
+    spec, T = S.MING_VAE, args.latents
+    ctx = ming.Context(0)
+    syn = S.SyntheticVae(ctx, spec, seed=0)
+    m = syn.model(T)
+    lat = torch.from_numpy(ming.synth_normal_bf16(0, "vae.latents", T * spec.latent).view(np.int16)).cuda().view(
+        torch.bfloat16)
+    wave = torch.empty(T * spec.patch * spec.hop, dtype=torch.float32, device="cuda")
+    ms = timed_events(lambda: m.decode(T, lat, wave), args.steps, args.warmup)
+    ctx.sync()
+    flops = vae_flops(spec, T)
+    achieved = flops / (ms * 1e-3) / 1e12
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        from vaekit import oracle_vae
+
+        oracle.set_threads(int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1))
+        om = oracle_vae(syn)
+        lat_h = lat.view(torch.int16).cpu().numpy().view(np.uint16).reshape(T, spec.latent)
+        chunk, n, t1 = min(T, 8), 0, time.time()
+        while time.time() - t1 < args.cpu_seconds:  # fragments of 8 latents until the sample bound
+            oracle.vae_decode(om, lat_h[:chunk])
+            n += chunk
+        dt = time.time() - t1
+        cpu = {"value": round(n / dt, 4), "unit": "latents/s", "cores": oracle.get_threads(), "kind": "port",
+               "sample": f"{n // chunk} fragments of {chunk} latents ({chunk * spec.patch} frames each) through the "
+                         f"same decoder ({dt:.1f} s, C restatement of the f32 graph)"}
+    line = base_line(METRIC_VAE, T * 1000.0 / ms, "latents/s", args, ms,
+                     {"workload": f"one fragment of {T} latents ({T * spec.patch} frames, "
+                                  f"{T * spec.patch * spec.hop / 44100:.2f} s of 44.1 kHz audio) through the VAE "
+                                  f"decoder: fc1 64->896, 4x upsample, 24-layer Qwen2-0.5B-shaped stack with a "
+                                  f"64-row sliding window, head 896->3530, ISTFT n_fft 3528 / hop 882",
+                      "global_batch": 1, "seq_len": T * spec.patch},
+                     {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F32_PEAK_TFLOPS,
+                      "unit": "TFLOP/s", "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 4), "traffic": None,
+                      "flops_per_launch": flops, "launch_ms": round(ms, 5)},
+                     cpu, "synthetic (random-init N(0,0.02) bf16 weights, periodic Hann window; latents N(0,1))")
+    line["dtype"] = "f32"
     print(json.dumps(line), flush=True)
 
 

@@ -428,6 +428,47 @@ int ming_aggregate(ming_ctx* ctx, ming_agg_model* m, const void* latent, void* o
  * softmax(f32(stop_head(z)))[1]; head [2, lm_hidden] bf16 with bias. */
 int ming_stop_prob(ming_ctx* ctx, const ming_linear* head, const void* bias, const void* z, float* p_dev);
 
+/* ---- VAE decoder (the step after the loop) ----------------------------------
+ * Model.vaeDecode (src/ming_model.zig:1257-1309): fc1 on the bf16 latents,
+ * 4x linear upsample (align_corners=False, :1316-1340), a Qwen2 stack with a
+ * causal sliding-window mask (QStack.forward with window 64, :566-636), final
+ * norm, the head linear to n_fft + 2 values per frame and the ISTFT head:
+ * magnitude min(exp(.), 100), phase, irfft of n_fft points, synthesis
+ * window, overlap-add with hop n_fft / 4, division by the window envelope,
+ * "same" trim.  As in the reference graph every activation after the
+ * upsample is f32 (bf16 or 4-bit weights are widened exactly).  Reference
+ * shape: 896, 14 / 2 heads of 64, 4864, 24 layers, eps 1e-6, theta 1e6,
+ * window 64, latent 64, patch 4, n_fft 3528, hop 882. */
+typedef struct {
+    int32_t hidden, heads, kv_heads, head_dim, inter, n_layers;
+    float eps, log2_theta;
+    int32_t window, latent, patch, n_fft, hop;
+} ming_vae_cfg;
+
+typedef struct {
+    ming_linear fc1;                  /* [hidden, latent] */
+    const void* fc1_bias;             /* bf16 [hidden] or NULL */
+    const ming_lm_layer_w* layers;    /* [n_layers]; q/k/v biases may be NULL */
+    const void* norm;                 /* bf16 [hidden] */
+    ming_linear head;                 /* [n_fft + 2, hidden] */
+    const void* head_bias;            /* bf16 [n_fft + 2] or NULL */
+    const void* window;               /* f32 [n_fft] (istft.window) */
+} ming_vae_w;
+
+typedef struct ming_vae_model ming_vae_model;
+/* Builds the irfft basis and the workspace for up to max_latents latents per
+ * call; weights stay caller-owned. */
+int ming_vae_model_create(ming_ctx* ctx, const ming_vae_cfg* cfg, const ming_vae_w* w, int32_t max_latents,
+                          ming_vae_model** out);
+int ming_vae_model_destroy(ming_vae_model* m);
+/* latents bf16 [T][latent] (device) -> wave_out f32 [T * patch * hop] (device). */
+int ming_vae_decode(ming_ctx* ctx, ming_vae_model* m, int32_t T, const void* latents, float* wave_out);
+/* The last decode's intermediates (device, f32; NULL skips one): xs
+ * [n_layers + 1][F][hidden] the layer inputs (xs[0] = the upsampled rows,
+ * xs[n_layers] the stack output before the final norm), head_out
+ * [F][n_fft + 2]; F = T * patch. */
+int ming_vae_trace(ming_vae_model* m, float* xs, float* head_out);
+
 /* ---- adaLN DiT flow head (config 4) ----------------------------------------
  * No reference implementation exists (the reference DiT conditions by an
  * additive row, src/ming_model.zig:1078-1091); this build defines the variant
@@ -582,6 +623,12 @@ int ming_cfm_model_from_weights(ming_ctx* ctx, ming_weights* w, const ming_dit_c
                                 int32_t lm_hidden, int32_t latent, ming_cfm_model** out);
 int ming_agg_model_from_weights(ming_ctx* ctx, ming_weights* w, const ming_dit_cfg* cfg, int32_t n_blocks,
                                 int32_t lm_hidden, int32_t latent, ming_agg_model** out);
+/* The VAE decoder of a checkpoint (Model.load, src/ming_model.zig:963-965,
+ * :994-996): `audio.decoder.fc1`, the stack `audio.decoder.decoder`
+ * (QStack.load with window 64), `audio.decoder.head.out` and the f32 (or
+ * bf16, widened at load) `audio.decoder.head.istft.window`. */
+int ming_vae_model_from_weights(ming_ctx* ctx, ming_weights* w, const ming_vae_cfg* cfg, int32_t quantize,
+                                int32_t max_latents, ming_vae_model** out);
 
 #ifdef __cplusplus
 }

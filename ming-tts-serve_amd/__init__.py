@@ -113,6 +113,16 @@ class AggW(ctypes.Structure):
     ] + [(n, c_void_p) for n in ("bx", "cls", "final_norm", "bf")]
 
 
+class VaeCfg(ctypes.Structure):
+    _fields_ = [(n, c_i32) for n in ("hidden", "heads", "kv_heads", "head_dim", "inter", "n_layers")] + [
+        ("eps", c_f32), ("log2_theta", c_f32)] + [(n, c_i32) for n in ("window", "latent", "patch", "n_fft", "hop")]
+
+
+class VaeW(ctypes.Structure):
+    _fields_ = [("fc1", Linear), ("fc1_bias", c_void_p), ("layers", c_void_p), ("norm", c_void_p), ("head", Linear),
+                ("head_bias", c_void_p), ("window", c_void_p)]
+
+
 class AdalnBlockW(ctypes.Structure):
     _fields_ = [("base", DitBlockW), ("ada", Linear), ("bada", c_void_p)]
 
@@ -192,6 +202,11 @@ def lib():
         "ming_lm_model_from_weights": (c_i32, [c_void_p, c_void_p, P(LmCfg), c_i32, P(c_void_p)]),
         "ming_cfm_model_from_weights": (c_i32, [c_void_p, c_void_p, P(DitCfg), c_i32, c_i32, c_i32, P(c_void_p)]),
         "ming_agg_model_from_weights": (c_i32, [c_void_p, c_void_p, P(DitCfg), c_i32, c_i32, c_i32, P(c_void_p)]),
+        "ming_vae_model_from_weights": (c_i32, [c_void_p, c_void_p, P(VaeCfg), c_i32, c_i32, P(c_void_p)]),
+        "ming_vae_model_create": (c_i32, [c_void_p, P(VaeCfg), P(VaeW), c_i32, P(c_void_p)]),
+        "ming_vae_model_destroy": (c_i32, [c_void_p]),
+        "ming_vae_decode": (c_i32, [c_void_p, c_void_p, c_i32, c_void_p, c_void_p]),
+        "ming_vae_trace": (c_i32, [c_void_p, c_void_p, c_void_p]),
         "ming_lm_prefill": (c_i32, [c_void_p, c_i32, c_void_p, c_void_p, P(KvPages), c_void_p, c_i32, c_i32,
                                     c_void_p, c_void_p, c_void_p]),
         "ming_rotary_table": (c_i32, [c_void_p, c_void_p, c_i32, c_i32, c_void_p, c_void_p]),
@@ -518,6 +533,41 @@ class AggModel:
         self.ctx.check(self.ctx.L.ming_aggregate(self.ctx.h, self.h, ptr(latent), ptr(out)))
 
 
+class VaeModel:
+    """ming_vae_model: the VAE decoder's irfft basis and workspace (up to max_latents per decode)."""
+
+    @classmethod
+    def wrap(cls, ctx, cfg, h, keep=None):
+        m = cls.__new__(cls)
+        m.ctx, m.cfg, m.w, m.h = ctx, cfg, keep, h
+        return m
+
+    def __init__(self, ctx, cfg, w, max_latents):
+        self.ctx, self.cfg, self.w = ctx, cfg, w
+        h = c_void_p()
+        ctx.check(ctx.L.ming_vae_model_create(ctx.h, ctypes.byref(cfg), ctypes.byref(w), int(max_latents),
+                                              ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.ctx.L.ming_vae_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def decode(self, T, latents, wave):
+        self.ctx.check(self.ctx.L.ming_vae_decode(self.ctx.h, self.h, int(T), ptr(latents), ptr(wave)))
+
+    def trace(self, xs=None, head_out=None):
+        self.ctx.check(self.ctx.L.ming_vae_trace(self.h, ptr(xs) if xs is not None else None,
+                                                 ptr(head_out) if head_out is not None else None))
+
+
 class LmModel:
     """ming_lm_model: prepared decode stack (QStack.fuse)."""
 
@@ -710,6 +760,12 @@ class Weights:
         self.ctx.check(self.ctx.L.ming_agg_model_from_weights(self.ctx.h, self.h, ctypes.byref(cfg), int(n_blocks),
                                                               int(lm_hidden), int(latent), ctypes.byref(h)))
         return AggModel.wrap(self.ctx, h, keep=self)
+
+    def vae_model(self, cfg, max_latents, quantize=False):
+        h = c_void_p()
+        self.ctx.check(self.ctx.L.ming_vae_model_from_weights(self.ctx.h, self.h, ctypes.byref(cfg), int(quantize),
+                                                              int(max_latents), ctypes.byref(h)))
+        return VaeModel.wrap(self.ctx, cfg, h, keep=self)
 
 
 # ---- synthetic inputs ---------------------------------------------------------

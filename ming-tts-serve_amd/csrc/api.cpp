@@ -233,6 +233,11 @@ int layer_scratch(ming_ctx* ctx, DevBuf& part, size_t floats) {
 
 }  // namespace
 
+ming::LinearDev ming::linear_dev(const ming_linear& l) { return to_dev(l); }
+int ming::check_linear_w(ming_ctx* ctx, const ming_linear& l, int N, int K, const char* name) {
+    return check_linear(ctx, l, N, K, name);
+}
+
 bool ming::lm_model_view(const ming_lm_model* m, LmView& v) {
     if (!m || !m->ctx) return false;
     v.cfg = m->cfg;

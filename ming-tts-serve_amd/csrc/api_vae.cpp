@@ -1,0 +1,258 @@
+// C-ABI glue of the VAE decoder (include/ming_hip.h, "VAE decoder";
+// Model.vaeDecode, src/ming_model.zig:1257-1309): the model handle with the
+// ISTFT basis built at load time, and the per-fragment decode.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <string>
+#include <vector>
+
+#include "internal.h"
+
+using namespace ming;
+
+struct ming_vae_model {
+    ming_ctx* ctx = nullptr;
+    ming_vae_cfg cfg{};
+    int max_t = 0, ldspec = 0;
+    ming_linear fc1{}, head{};
+    const uint16_t *fc1_bias = nullptr, *head_bias = nullptr, *norm = nullptr;
+    const float* window = nullptr;
+    std::vector<ming_lm_layer_w> layers;
+    DevBuf basis;                                     // f32 [n_fft][ldspec]: irfft rows
+    DevBuf lat, y1, xs, h, qkv, att, x1, hh, p, spec, frames;
+    int last_f = 0;
+};
+
+namespace {
+
+int vae_err(ming_ctx* ctx, int st, const std::string& m) { return set_err(ctx, st, "vae: " + m); }
+
+// The weight view of a linear for the f32 GEMM.
+void set_w(VGemm& g, const ming_linear& l, int& wf, bool second = false) {
+    const LinearDev d = linear_dev(l);
+    wf = d.kind == 1 ? VW_Q4 : VW_BF16;
+    if (second) {
+        g.w1 = d.w;
+        g.s1 = d.s;
+        g.b1 = d.b;
+        g.g1 = d.kind == 1 ? d.gscale : 1.0f;
+    } else {
+        g.w0 = d.w;
+        g.s0 = d.s;
+        g.b0 = d.b;
+        g.g0 = d.kind == 1 ? d.gscale : 1.0f;
+    }
+}
+
+VGemm gemm(const float* a, int lda, int M, int N, int K, float* y, int ldy) {
+    VGemm g{};
+    g.a = a;
+    g.lda = lda;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.y = y;
+    g.ldy = ldy;
+    g.g0 = g.g1 = 1.0f;
+    return g;
+}
+
+int check_cfg(ming_ctx* ctx, const ming_vae_cfg* c) {
+    if (!c) return vae_err(ctx, MING_E_ARG, "null cfg");
+    if (c->head_dim != 64) return vae_err(ctx, MING_E_UNSUPPORTED, "head_dim must be 64");
+    if (c->kv_heads < 1 || c->heads % c->kv_heads || c->hidden != c->heads * c->head_dim)
+        return vae_err(ctx, MING_E_SHAPE, "heads / kv_heads / hidden inconsistent");
+    if (c->hidden % 64 || c->inter % 64 || c->latent % 32 || c->latent < 32)
+        return vae_err(ctx, MING_E_UNSUPPORTED, "hidden and inter must be multiples of 64, latent of 32");
+    if (c->window < 1 || c->window > 64) return vae_err(ctx, MING_E_UNSUPPORTED, "window must be in [1, 64]");
+    if (c->hop < 1 || c->n_fft != 4 * c->hop || c->n_fft % 2)
+        return vae_err(ctx, MING_E_UNSUPPORTED, "n_fft must be 4 * hop and even");
+    if (c->patch < 1 || c->n_layers < 1) return vae_err(ctx, MING_E_ARG, "patch and n_layers must be >= 1");
+    return MING_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ming_vae_model_create(ming_ctx* ctx, const ming_vae_cfg* cfg, const ming_vae_w* w, int32_t max_latents,
+                          ming_vae_model** out) {
+    if (!ctx || !ctx->alive) return MING_E_NOT_INIT;
+    if (!w || !out || max_latents < 1) return vae_err(ctx, MING_E_ARG, "bad arguments");
+    int st;
+    if ((st = check_cfg(ctx, cfg))) return st;
+    const int H = cfg->hidden, kvd = cfg->kv_heads * cfg->head_dim, I = cfg->inter, P = cfg->n_fft + 2;
+    if (!w->layers || !w->norm || !w->window) return vae_err(ctx, MING_E_ARG, "null layers, norm or window");
+    if ((st = check_linear_w(ctx, w->fc1, H, cfg->latent, "fc1")) ||
+        (st = check_linear_w(ctx, w->head, P, H, "head")))
+        return st;
+    for (int i = 0; i < cfg->n_layers; i++) {
+        const ming_lm_layer_w& l = w->layers[i];
+        if (!l.ln1 || !l.ln2) return vae_err(ctx, MING_E_ARG, "null layer norm");
+        if ((st = check_linear_w(ctx, l.wq, H, H, "wq")) || (st = check_linear_w(ctx, l.wk, kvd, H, "wk")) ||
+            (st = check_linear_w(ctx, l.wv, kvd, H, "wv")) || (st = check_linear_w(ctx, l.wo, H, H, "wo")) ||
+            (st = check_linear_w(ctx, l.wg, I, H, "wg")) || (st = check_linear_w(ctx, l.wu, I, H, "wu")) ||
+            (st = check_linear_w(ctx, l.wd, H, I, "wd")))
+            return st;
+    }
+    ming_vae_model* m = new ming_vae_model();
+    m->ctx = ctx;
+    m->cfg = *cfg;
+    m->max_t = max_latents;
+    m->fc1 = w->fc1;
+    m->head = w->head;
+    m->fc1_bias = static_cast<const uint16_t*>(w->fc1_bias);
+    m->head_bias = static_cast<const uint16_t*>(w->head_bias);
+    m->norm = static_cast<const uint16_t*>(w->norm);
+    m->window = static_cast<const float*>(w->window);
+    m->layers.assign(w->layers, w->layers + cfg->n_layers);
+    const int N = cfg->n_fft, nb = N / 2 + 1;
+    m->ldspec = (2 * nb + 31) / 32 * 32;
+    // irfft (backward norm) as rows of a matrix: frame[n] = sum_k spec[k] basis[n][k] with
+    // spec = [re_0 .. re_{nb-1} | im_0 .. im_{nb-1} | 0 pad]; bins 1 .. N/2-1 count twice and
+    // the imaginary parts of bins 0 and N/2 are ignored (evaluated in double, rounded once).
+    std::vector<float> basis((size_t)N * m->ldspec, 0.0f);
+    for (int n = 0; n < N; n++) {
+        float* row = basis.data() + (size_t)n * m->ldspec;
+        for (int k = 0; k < nb; k++) {
+            const double c = (k == 0 || 2 * k == N) ? 1.0 : 2.0;
+            const double th = 2.0 * M_PI * (double)(((int64_t)k * n) % N) / (double)N;
+            row[k] = (float)(c * std::cos(th) / N);
+            row[nb + k] = (k == 0 || 2 * k == N) ? 0.0f : (float)(-c * std::sin(th) / N);
+        }
+    }
+    const size_t F = (size_t)max_latents * cfg->patch, nq = H + 2 * kvd;
+    hipError_t e = m->basis.ensure(basis.size() * sizeof(float));
+    if (e == hipSuccess)
+        e = hipMemcpy(m->basis.p, basis.data(), basis.size() * sizeof(float), hipMemcpyHostToDevice);
+    const std::pair<DevBuf*, size_t> bufs[] = {
+        {&m->lat, (size_t)max_latents * cfg->latent}, {&m->y1, (size_t)max_latents * H},
+        {&m->xs, (cfg->n_layers + 1) * F * H},        {&m->h, F * H},
+        {&m->qkv, F * nq},                            {&m->att, F * H},
+        {&m->x1, F * H},                              {&m->hh, F * I},
+        {&m->p, F * P},                               {&m->spec, F * m->ldspec},
+        {&m->frames, F * N}};
+    for (const auto& b : bufs)
+        if (e == hipSuccess) e = b.first->ensure(b.second * sizeof(float));
+    if (e != hipSuccess) {
+        ming_vae_model_destroy(m);
+        return hip_check(ctx, e, "vae workspace");
+    }
+    *out = m;
+    return MING_OK;
+}
+
+int ming_vae_model_destroy(ming_vae_model* m) {
+    if (!m) return MING_E_NOT_INIT;
+    for (DevBuf* b : {&m->basis, &m->lat, &m->y1, &m->xs, &m->h, &m->qkv, &m->att, &m->x1, &m->hh, &m->p, &m->spec,
+                      &m->frames})
+        b->release();
+    delete m;
+    return MING_OK;
+}
+
+int ming_vae_decode(ming_ctx* ctx, ming_vae_model* m, int32_t T, const void* latents, float* wave_out) {
+    if (!ctx || !ctx->alive || !m) return MING_E_NOT_INIT;
+    if (!latents || !wave_out) return vae_err(ctx, MING_E_ARG, "null latents or output");
+    if (T < 1 || T > m->max_t)
+        return vae_err(ctx, MING_E_SHAPE, "T = " + std::to_string(T) + " outside [1, " + std::to_string(m->max_t) + "]");
+    const ming_vae_cfg& c = m->cfg;
+    const int H = c.hidden, kvd = c.kv_heads * c.head_dim, I = c.inter, nq = H + 2 * kvd, P = c.n_fft + 2;
+    const int F = T * c.patch;
+    hipStream_t st = ctx->stream;
+    float* xs = static_cast<float*>(m->xs.p);
+    float *h = static_cast<float*>(m->h.p), *qkv = static_cast<float*>(m->qkv.p), *att = static_cast<float*>(m->att.p);
+    float *x1 = static_cast<float*>(m->x1.p), *hh = static_cast<float*>(m->hh.p);
+    hipError_t e = launch_vwiden(st, static_cast<const uint16_t*>(latents), (int64_t)T * c.latent,
+                                 static_cast<float*>(m->lat.p));
+    int wf = 0;
+    if (e == hipSuccess) {  // fc1: bias and the bf16 rounding are applied by the upsample kernel
+        VGemm g = gemm(static_cast<float*>(m->lat.p), c.latent, T, H, c.latent, static_cast<float*>(m->y1.p), H);
+        set_w(g, m->fc1, wf);
+        e = launch_vgemm(st, g, wf, VE_PLAIN);
+    }
+    if (e == hipSuccess)
+        e = launch_vup(st, static_cast<float*>(m->y1.p), m->fc1_bias, wf == VW_Q4, T, H, c.patch, xs);
+    const float scale = 1.0f / std::sqrt((float)c.head_dim);
+    for (int l = 0; l < c.n_layers && e == hipSuccess; l++) {
+        const ming_lm_layer_w& L = m->layers[l];
+        float* x = xs + (size_t)l * F * H;
+        float* xo = xs + (size_t)(l + 1) * F * H;
+        e = launch_vrms(st, x, F, H, static_cast<const uint16_t*>(L.ln1), c.eps, h);
+        const struct {
+            const ming_linear* w;
+            const void* b;
+            int N, col0, rope;
+        } proj[3] = {{&L.wq, L.bq, H, 0, H}, {&L.wk, L.bk, kvd, H, kvd}, {&L.wv, L.bv, kvd, H + kvd, 0}};
+        for (const auto& pj : proj) {
+            if (e != hipSuccess) break;
+            VGemm g = gemm(h, H, F, pj.N, H, qkv + pj.col0, nq);
+            set_w(g, *pj.w, wf);
+            g.bias = static_cast<const uint16_t*>(pj.b);
+            g.rope_cols = pj.rope;
+            g.log2_theta = c.log2_theta;
+            e = launch_vgemm(st, g, wf, VE_QKV);
+        }
+        if (e == hipSuccess) e = launch_vattn(st, qkv, F, nq, H, c.heads, c.kv_heads, c.window, scale, att);
+        if (e == hipSuccess) {
+            VGemm g = gemm(att, H, F, H, H, x1, H);
+            set_w(g, L.wo, wf);
+            g.res = x;
+            g.ldres = H;
+            e = launch_vgemm(st, g, wf, VE_RES);
+        }
+        if (e == hipSuccess) e = launch_vrms(st, x1, F, H, static_cast<const uint16_t*>(L.ln2), c.eps, h);
+        if (e == hipSuccess) {
+            VGemm g = gemm(h, H, F, I, H, hh, I);
+            set_w(g, L.wg, wf);
+            set_w(g, L.wu, wf, true);
+            e = launch_vgemm(st, g, wf, VE_SWIGLU);
+        }
+        if (e == hipSuccess) {
+            VGemm g = gemm(hh, I, F, H, I, xo, H);
+            set_w(g, L.wd, wf);
+            g.res = x1;
+            g.ldres = H;
+            e = launch_vgemm(st, g, wf, VE_RES);
+        }
+    }
+    float* p = static_cast<float*>(m->p.p);
+    if (e == hipSuccess) e = launch_vrms(st, xs + (size_t)c.n_layers * F * H, F, H, m->norm, c.eps, h);
+    if (e == hipSuccess) {
+        VGemm g = gemm(h, H, F, P, H, p, P);
+        set_w(g, m->head, wf);
+        g.bias = m->head_bias;
+        e = launch_vgemm(st, g, wf, VE_PLAIN);
+    }
+    float* spec = static_cast<float*>(m->spec.p);
+    float* frames = static_cast<float*>(m->frames.p);
+    if (e == hipSuccess) e = launch_vspec(st, p, F, c.n_fft, m->ldspec, spec);
+    if (e == hipSuccess) {
+        VGemm g = gemm(spec, m->ldspec, F, c.n_fft, m->ldspec, frames, c.n_fft);
+        g.w0 = m->basis.p;
+        g.win = m->window;
+        e = launch_vgemm(st, g, VW_F32, VE_WIN);
+    }
+    if (e == hipSuccess) e = launch_vola(st, frames, F, c.n_fft, c.hop, m->window, wave_out);
+    if (e == hipSuccess) m->last_f = F;
+    return hip_check(ctx, e, "vae_decode launch");
+}
+
+int ming_vae_trace(ming_vae_model* m, float* xs, float* head_out) {
+    if (!m || !m->ctx || !m->ctx->alive) return MING_E_NOT_INIT;
+    if (!m->last_f) return vae_err(m->ctx, MING_E_ARG, "no decode yet");
+    const ming_vae_cfg& c = m->cfg;
+    const size_t F = m->last_f, H = c.hidden;
+    hipError_t e = hipSuccess;
+    if (xs)
+        for (int l = 0; l <= c.n_layers && e == hipSuccess; l++)
+            e = hipMemcpyAsync(xs + l * F * H, static_cast<float*>(m->xs.p) + l * F * H, F * H * sizeof(float),
+                               hipMemcpyDeviceToDevice, m->ctx->stream);
+    if (head_out && e == hipSuccess)
+        e = hipMemcpyAsync(head_out, m->p.p, F * (c.n_fft + 2) * sizeof(float), hipMemcpyDeviceToDevice,
+                           m->ctx->stream);
+    return hip_check(m->ctx, e, "vae_trace copy");
+}
+
+}  // extern "C"

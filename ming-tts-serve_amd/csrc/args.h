@@ -97,4 +97,36 @@ constexpr int kImgSlots = 5;  // q/k/v, o_proj, gate/up, down, LM head
 
 constexpr int kMaxParts = 4096;
 
+// ---- VAE decoder GEMM (vae.hip) ----------------------------------------------
+// Weight formats and epilogues of the f32 GEMM.
+enum VWf : int { VW_BF16 = 0, VW_Q4 = 1, VW_F32 = 2 };
+enum VEpi : int {
+    VE_PLAIN = 0,   // y = acc (+ bias)
+    VE_QKV = 1,     // y = acc + bias, rope on columns < rope_cols (heads of 64, position = row)
+    VE_RES = 2,     // y = res + acc
+    VE_SWIGLU = 3,  // y = (g * sigmoid(g)) * u, g from w0, u from w1
+    VE_WIN = 4,     // y = acc * win[col]
+};
+
+// C [M][N] = A [M][K] (f32) x W^T with W [N][K]: bf16, MLX affine 4-bit (u32
+// [N][K/8] + bf16 scales/biases [N][K/64]) or f32.
+struct VGemm {
+    const float* a;
+    int lda, M, N, K;
+    const void* w0;
+    const uint16_t *s0, *b0;
+    float g0;
+    const void* w1;
+    const uint16_t *s1, *b1;
+    float g1;
+    const uint16_t* bias;   // bf16 [N] or null (VE_PLAIN, VE_QKV)
+    const float* res;       // VE_RES: f32 [M][ldres]
+    int ldres;
+    const float* win;       // VE_WIN: f32 [N]
+    float* y;
+    int ldy;
+    int rope_cols;          // VE_QKV
+    float log2_theta;
+};
+
 }  // namespace ming

@@ -101,4 +101,18 @@ struct LmView {
 };
 bool lm_model_view(const ming_lm_model* m, LmView& v);
 
+// ---- VAE decoder (vae.hip) ----
+hipError_t launch_vgemm(hipStream_t st, const VGemm& g, int wf, int epi);
+hipError_t launch_vrms(hipStream_t st, const float* x, int M, int K, const uint16_t* w, float eps, float* out);
+hipError_t launch_vattn(hipStream_t st, const float* qkv, int M, int ldq, int H, int heads, int kvh, int window,
+                        float scale, float* att);
+hipError_t launch_vup(hipStream_t st, const float* y, const uint16_t* bias, int q4, int T, int C, int scale,
+                      float* x);
+hipError_t launch_vspec(hipStream_t st, const float* p, int F, int nfft, int ld, float* spec);
+hipError_t launch_vola(hipStream_t st, const float* fr, int F, int nfft, int hop, const float* win, float* wave);
+hipError_t launch_vwiden(hipStream_t st, const uint16_t* x, int64_t n, float* y);
+// Weight views and checks shared with the LM glue (api.cpp).
+LinearDev linear_dev(const ming_linear& l);
+int check_linear_w(ming_ctx* ctx, const ming_linear& l, int N, int K, const char* name);
+
 }  // namespace ming

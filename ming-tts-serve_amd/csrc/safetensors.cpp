@@ -623,6 +623,61 @@ int ming_lm_model_from_weights(ming_ctx* ctx, ming_weights* w, const ming_lm_cfg
     return ming_lm_model_create(ctx, cfg, layers.data(), norm, &emb, &emb, out);
 }
 
+int ming_vae_model_from_weights(ming_ctx* ctx, ming_weights* w, const ming_vae_cfg* cfg, int32_t quantize,
+                                int32_t max_latents, ming_vae_model** out) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!w || !cfg || !out) return set_err(ctx, MING_E_ARG, "vae_model_from_weights: bad arguments");
+    const std::string D = "audio.decoder", P = D + ".decoder";
+    const int64_t H = cfg->hidden, kvd = (int64_t)cfg->kv_heads * cfg->head_dim, I = cfg->inter;
+    std::vector<ming_lm_layer_w> layers(cfg->n_layers);
+    auto opt = [&](const std::string& name, int64_t n, const void*& ptr) {  // optional bf16 bias
+        ptr = nullptr;
+        return wget(w, name) ? vec(w, name, n, ptr) : MING_OK;
+    };
+    int st;
+    for (int i = 0; i < cfg->n_layers; i++) {
+        const std::string L = P + ".layers." + std::to_string(i) + ".";
+        ming_lm_layer_w& l = layers[i];
+        if ((st = vec(w, L + "input_layernorm.weight", H, l.ln1)) ||
+            (st = vec(w, L + "post_attention_layernorm.weight", H, l.ln2)) ||
+            (st = make_linear(w, L + "self_attn.q_proj", quantize, H, H, l.wq)) ||
+            (st = make_linear(w, L + "self_attn.k_proj", quantize, kvd, H, l.wk)) ||
+            (st = make_linear(w, L + "self_attn.v_proj", quantize, kvd, H, l.wv)) ||
+            (st = make_linear(w, L + "self_attn.o_proj", quantize, H, H, l.wo)) ||
+            (st = make_linear(w, L + "mlp.gate_proj", quantize, I, H, l.wg)) ||
+            (st = make_linear(w, L + "mlp.up_proj", quantize, I, H, l.wu)) ||
+            (st = make_linear(w, L + "mlp.down_proj", quantize, H, I, l.wd)) ||
+            (st = opt(L + "self_attn.q_proj.bias", H, l.bq)) || (st = opt(L + "self_attn.k_proj.bias", kvd, l.bk)) ||
+            (st = opt(L + "self_attn.v_proj.bias", kvd, l.bv)))
+            return st;
+    }
+    if (wget(w, P + ".layers." + std::to_string(cfg->n_layers) + ".input_layernorm.weight"))
+        return set_err(ctx, MING_E_SHAPE, "vae_model_from_weights: the checkpoint has more layers than cfg->n_layers");
+    ming_vae_w vw{};
+    vw.layers = layers.data();
+    if ((st = make_linear(w, D + ".fc1", quantize, H, cfg->latent, vw.fc1)) ||
+        (st = opt(D + ".fc1.bias", H, vw.fc1_bias)) || (st = vec(w, P + ".norm.weight", H, vw.norm)) ||
+        (st = make_linear(w, D + ".head.out", quantize, cfg->n_fft + 2, H, vw.head)) ||
+        (st = opt(D + ".head.out.bias", cfg->n_fft + 2, vw.head_bias)))
+        return st;
+    const std::string wn = D + ".head.istft.window";
+    const ming_tensor* wt = wget(w, wn);
+    if (!wt) return set_err(ctx, MING_E_ARG, "missing weight " + wn);
+    if ((st = vec(w, wn, cfg->n_fft, vw.window, wt->dtype == MING_DT_F32 ? MING_DT_F32 : MING_DT_BF16))) return st;
+    if (wt->dtype != MING_DT_F32) {  // the graph casts the window to f32 (src/ming_model.zig:994)
+        void* buf = nullptr;
+        if ((st = hip_check(ctx, hipMalloc(&buf, sizeof(float) * cfg->n_fft), "hipMalloc(window)"))) return st;
+        w->extra.push_back(buf);
+        if ((st = hip_check(ctx, launch_vwiden(ctx->stream, static_cast<const uint16_t*>(vw.window), cfg->n_fft,
+                                               static_cast<float*>(buf)),
+                            "widen window")))
+            return st;
+        vw.window = buf;
+    }
+    if ((st = hip_check(ctx, hipStreamSynchronize(ctx->stream), "quantize at load"))) return st;
+    return ming_vae_model_create(ctx, cfg, &vw, max_latents, out);
+}
+
 int ming_cfm_model_from_weights(ming_ctx* ctx, ming_weights* w, const ming_dit_cfg* cfg, int32_t n_blocks,
                                 int32_t lm_hidden, int32_t latent, ming_cfm_model** out) {
     if (!alive(ctx)) return MING_E_NOT_INIT;

@@ -1,0 +1,388 @@
+// VAE decoder (Model.vaeDecode, src/ming_model.zig:1257-1309): the f32 graph
+// after the latent projection -- linear upsample, the sliding-window Qwen2
+// stack (QStack.forward with window 64, :566-636) and the ISTFT head.
+//
+// Every activation after the upsample is f32 in the reference graph (MLX
+// promotes the bf16 weights), so the GEMMs here run on
+// v_mfma_f32_16x16x4f32 with f32 operands: weights are widened exactly (bf16
+// -> f32, MLX affine s*q + b in f32), products are exact and accumulation is
+// f32.  The inverse real FFT is one more GEMM, against an f32 basis of
+// cos/sin rows built at load time, with the synthesis window applied in its
+// epilogue.
+#include "common.h"
+#include "internal.h"
+
+namespace ming {
+
+namespace {
+
+constexpr int kVBM = 64, kVBN = 64, kVBK = 32, kVT = 256;
+constexpr int kVLd = kVBK + 4;  // f32 per LDS row: k permuted so a lane's 8 k-steps are contiguous
+
+// Position of k (0..31 within a stage) in an LDS row: k = 4 kk + j -> j * 8 + kk,
+// so lane group j = lane / 16 reads its 8 values (k-steps kk = 0..7) as two 16-byte words.
+__device__ __forceinline__ int vperm(int k) { return (k & 3) * 8 + (k >> 2); }
+
+struct VTile {  // one thread's share of a stage's global loads
+    float4 a[2];
+    uint4 w[2];    // bf16: w[0] = 8 values; f32: w[0..1] = 8 values as bits; q4: w[0].x = 8 nibbles
+    uint32_t s, b; // q4: scale, bias (bf16 bits)
+};
+
+template <int WF>
+__device__ __forceinline__ void vload_w(const VGemm& g, const void* w, const uint16_t* sc, const uint16_t* bi, int n0,
+                                        int k0, uint4 (&r)[2], uint32_t& s, uint32_t& b) {
+    const int t = threadIdx.x;
+    if (WF == VW_F32) {
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const int f = t + kVT * p, col = f / 8, kq = f % 8;
+            const int n = min(n0 + col, g.N - 1);
+            r[p] = ldg4(static_cast<const float*>(w) + (size_t)n * g.K + k0 + 4 * kq);
+        }
+    } else {
+        const int col = t / 4, kq = t % 4;
+        const int n = min(n0 + col, g.N - 1);
+        if (WF == VW_BF16) {
+            r[0] = ldg4(static_cast<const uint16_t*>(w) + (size_t)n * g.K + k0 + 8 * kq);
+        } else {
+            r[0].x = gld(static_cast<const uint32_t*>(w) + (size_t)n * (g.K / 8) + (k0 + 8 * kq) / 8);
+            s = gld(sc + (size_t)n * (g.K / 64) + (k0 + 8 * kq) / 64);
+            b = gld(bi + (size_t)n * (g.K / 64) + (k0 + 8 * kq) / 64);
+        }
+    }
+}
+
+template <int WF>
+__device__ __forceinline__ void vstore_w(float* lw, const uint4 (&r)[2], uint32_t s, uint32_t b, float gscale) {
+    const int t = threadIdx.x;
+    if (WF == VW_F32) {
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const int f = t + kVT * p, col = f / 8, kq = f % 8;
+            const uint32_t e[4] = {r[p].x, r[p].y, r[p].z, r[p].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) lw[col * kVLd + vperm(4 * kq + i)] = __uint_as_float(e[i]);
+        }
+    } else {
+        const int col = t / 4, kq = t % 4;
+        float v[8];
+        if (WF == VW_BF16) {
+            const uint32_t e[4] = {r[0].x, r[0].y, r[0].z, r[0].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[2 * i] = bf_lo(e[i]);
+                v[2 * i + 1] = bf_hi(e[i]);
+            }
+        } else {  // MLX affine: s * q + b in f32 (times the global scale)
+            const float fs = bf2f((uint16_t)s), fb = bf2f((uint16_t)b);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                v[i] = fs * (float)((r[0].x >> (4 * i)) & 15u) + fb;
+                if (gscale != 1.0f) v[i] *= gscale;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) lw[col * kVLd + vperm(8 * kq + i)] = v[i];
+    }
+}
+
+// C [M][N] = A [M][K] (f32, row stride lda) x W^T, W [N][K] in format WF;
+// workgroup = 64 x 64 outputs, wave w = rows 16w .. 16w + 15, all 64 columns;
+// K in stages of 32 through double-buffered LDS (the next stage's global loads
+// are in flight during the current stage's MFMAs).  SWIGLU carries a second
+// weight (up) next to the first (gate).
+template <int WF, int EPI>
+__global__ __launch_bounds__(kVT) void vgemm_kernel(VGemm g) {
+    constexpr bool DUAL = EPI == VE_SWIGLU;
+    __shared__ __align__(16) float la[2][kVBM * kVLd];
+    __shared__ __align__(16) float lw[2][kVBN * kVLd];
+    __shared__ __align__(16) float lu[DUAL ? 2 : 1][DUAL ? kVBN * kVLd : 4];
+    const int t = threadIdx.x, wave = t / kWave, lane = t % kWave, c = lane % 16, j = lane / 16;
+    const int n0 = blockIdx.x * kVBN, m0 = blockIdx.y * kVBM;
+    const int S = g.K / kVBK;
+    VTile r;
+    uint4 ru[2];
+    uint32_t us = 0, ub = 0;
+    auto gload = [&](int s) {
+        const int k0 = s * kVBK;
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const int f = t + kVT * p, row = f / 8, kq = f % 8;
+            r.a[p] = *reinterpret_cast<const float4*>(g.a + (size_t)min(m0 + row, g.M - 1) * g.lda + k0 + 4 * kq);
+        }
+        vload_w<WF>(g, g.w0, g.s0, g.b0, n0, k0, r.w, r.s, r.b);
+        if (DUAL) vload_w<WF>(g, g.w1, g.s1, g.b1, n0, k0, ru, us, ub);
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const int f = t + kVT * p, row = f / 8, kq = f % 8;
+            const float e[4] = {r.a[p].x, r.a[p].y, r.a[p].z, r.a[p].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) la[buf][row * kVLd + vperm(4 * kq + i)] = e[i];
+        }
+        vstore_w<WF>(lw[buf], r.w, r.s, r.b, g.g0);
+        if (DUAL) vstore_w<WF>(lu[buf], ru, us, ub, g.g1);
+    };
+    f32x4_t acc[4], accu[DUAL ? 4 : 1];
+#pragma unroll
+    for (int b = 0; b < 4; b++) acc[b] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int b = 0; b < (DUAL ? 4 : 1); b++) accu[b] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int s = 0; s < S; s++) {
+        const int buf = s & 1;
+        if (s + 1 < S) gload(s + 1);
+        const float* ar = &la[buf][(16 * wave + c) * kVLd + 8 * j];
+        const float4 a0 = *reinterpret_cast<const float4*>(ar), a1 = *reinterpret_cast<const float4*>(ar + 4);
+        const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const float* wr = &lw[buf][(16 * b + c) * kVLd + 8 * j];
+            const float4 w0 = *reinterpret_cast<const float4*>(wr), w1 = *reinterpret_cast<const float4*>(wr + 4);
+            const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[kk], wv[kk], acc[b], 0, 0, 0);
+            if (DUAL) {
+                const float* ur = &lu[buf][(16 * b + c) * kVLd + 8 * j];
+                const float4 u0 = *reinterpret_cast<const float4*>(ur), u1 = *reinterpret_cast<const float4*>(ur + 4);
+                const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+                for (int kk = 0; kk < 8; kk++)
+                    accu[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[kk], uv[kk], accu[b], 0, 0, 0);
+            }
+        }
+        if (s + 1 < S) lstore(buf ^ 1);
+        __syncthreads();
+    }
+    // lane (c, j): acc[b][i] = C[row 16 wave + 4 j + i][col 16 b + c]
+    float v[4][4];
+#pragma unroll
+    for (int b = 0; b < 4; b++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[b][i] = acc[b][i];
+    if (EPI == VE_PLAIN || EPI == VE_QKV) {
+        if (g.bias)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const float bb = bf2f(gld(g.bias + min(n0 + 16 * b + c, g.N - 1)));
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[b][i] += bb;
+            }
+    }
+    if (EPI == VE_QKV && n0 < g.rope_cols) {  // MLX fast::rope, pairs (d, d + 32) of this 64-column head
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            const int d = 16 * b + c;
+            const float inv = exp2f(-((float)d / 32.0f) * g.log2_theta);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int row = m0 + 16 * wave + 4 * j + i;
+                const float th = (float)row * inv;
+                const float cs = cosf(th), sn = sinf(th);
+                const float x1 = v[b][i], x2 = v[b + 2][i];
+                v[b][i] = x1 * cs - x2 * sn;
+                v[b + 2][i] = x1 * sn + x2 * cs;
+            }
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        const int col = n0 + 16 * b + c;
+        if (col >= g.N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int row = m0 + 16 * wave + 4 * j + i;
+            if (row >= g.M) continue;
+            float o = v[b][i];
+            if (EPI == VE_RES) o = g.res[(size_t)row * g.ldres + col] + o;
+            if (EPI == VE_SWIGLU) {
+                const float sg = 1.0f / (1.0f + expf(-o));
+                o = (o * sg) * accu[b][i];
+            }
+            if (EPI == VE_WIN) o = o * g.win[col];
+            g.y[(size_t)row * g.ldy + col] = o;
+        }
+    }
+}
+
+// fast::rms_norm of f32 rows with a bf16 weight: w * (x * rsqrt(mean(x^2) + eps)); one wave per row.
+__global__ __launch_bounds__(256) void vrms_kernel(const float* x, int M, int K, const uint16_t* w, float eps,
+                                                   float* out) {
+    const int row = blockIdx.x * 4 + threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    if (row >= M) return;
+    const float* xr = x + (size_t)row * K;
+    float ss = 0.0f;
+    for (int i = lane; i < K; i += kWave) ss += xr[i] * xr[i];
+    ss = team_sum<kWave>(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)K + eps);
+    for (int i = lane; i < K; i += kWave) out[(size_t)row * K + i] = bf2f(gld(w + i)) * (xr[i] * inv);
+}
+
+// Sliding-window attention (mask of src/ming_model.zig:618-636: key j is
+// visible to query i when i - window < j <= i, window <= 64).  One wave per
+// (row, head): lane j scores key j0 + j; then lane = dim for P.V.
+__global__ __launch_bounds__(256) void vattn_kernel(const float* qkv, int M, int ldq, int H, int heads, int kvh,
+                                                    int window, float scale, float* att) {
+    const int item = blockIdx.x * 4 + threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    if (item >= M * heads) return;
+    const int i = item / heads, h = item % heads, kh = h / (heads / kvh);
+    const int j0 = max(0, i - window + 1), n = i - j0 + 1;
+    const float* q = qkv + (size_t)i * ldq + h * 64;
+    const int kj = min(j0 + lane, i);
+    const float* kr = qkv + (size_t)kj * ldq + H + kh * 64;
+    float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int d = 0; d < 64; d += 4) {
+        const float4 qa = *reinterpret_cast<const float4*>(q + d), ka = *reinterpret_cast<const float4*>(kr + d);
+        p[0] = fmaf(qa.x, ka.x, p[0]);
+        p[1] = fmaf(qa.y, ka.y, p[1]);
+        p[2] = fmaf(qa.z, ka.z, p[2]);
+        p[3] = fmaf(qa.w, ka.w, p[3]);
+    }
+    const float s = lane < n ? ((p[0] + p[1]) + (p[2] + p[3])) * scale : -INFINITY;
+    const float m = team_max<kWave>(s);
+    const float e = lane < n ? expf(s - m) : 0.0f;
+    const float l = team_sum<kWave>(e);
+    const float* vb = qkv + H + kvh * 64 + kh * 64 + lane;  // v of kv head kh, dim = lane
+    float o = 0.0f;
+    for (int jj = 0; jj < n; jj++) {
+        const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), jj));
+        o = fmaf(pj, vb[(size_t)(j0 + jj) * ldq], o);
+    }
+    att[(size_t)i * H + h * 64 + lane] = o / l;
+}
+
+// Decoder._linear_upsample_1d (align_corners=False, f32) of the fc1 rows,
+// which the graph materialises in bf16 first: y [T][C] f32 accumulators of
+// fc1 -> x [T * scale][C].  The fc1 row is bf16(acc + bias) for bf16
+// weights (addmm, one rounding) and bf16(bf16(acc) + bias) for 4-bit ones
+// (quantized_matmul, then the bias add).
+__device__ __forceinline__ float fc1_row(const float* y, const uint16_t* bias, int q4, int r, int C, int c) {
+    const float a = y[(size_t)r * C + c], b = bias ? bf2f(bias[c]) : 0.0f;
+    return q4 ? rb(rb(a) + b) : rb(a + b);
+}
+
+__global__ __launch_bounds__(256) void vup_kernel(const float* y, const uint16_t* bias, int q4, int T, int C, int scale,
+                                                  float* x) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)T * scale * C) return;
+    const int i = (int)(idx / C), c = (int)(idx % C);
+    const float pos = ((float)i + 0.5f) / (float)scale - 0.5f;
+    const int left = (int)floorf(pos);
+    const float wr = pos - (float)left, wl = 1.0f - wr;
+    const int l = min(max(left, 0), T - 1), r = min(max(left + 1, 0), T - 1);
+    x[idx] = fc1_row(y, bias, q4, l, C, c) * wl + fc1_row(y, bias, q4, r, C, c) * wr;
+}
+
+// ISTFT spectrum: p [F][n_fft + 2] (log-magnitudes | phases) -> the GEMM's
+// A rows [F][ld]: mag cos(ph) for bins 0 .. nb-1, mag sin(ph) after them,
+// zeros to ld; mag = min(exp(.), 100).
+__global__ __launch_bounds__(256) void vspec_kernel(const float* p, int F, int nfft, int ld, float* spec) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)F * ld) return;
+    const int f = (int)(idx / ld), k = (int)(idx % ld), nb = nfft / 2 + 1;
+    const float* pr = p + (size_t)f * (nfft + 2);
+    float v = 0.0f;
+    if (k < 2 * nb) {
+        const int b = k < nb ? k : k - nb;
+        const float mag = fminf(expf(pr[b]), 100.0f);
+        const float ph = pr[nb + b];
+        v = k < nb ? mag * cosf(ph) : mag * sinf(ph);
+    }
+    spec[idx] = v;
+}
+
+// Overlap-add of the windowed frames [F][n_fft] (n_fft = 4 hop), divided by
+// the window envelope, "same" trim: block b sums ((frame b-3 part 3 + frame
+// b-2 part 2) + frame b-1 part 1) + frame b part 0, in the graph's order.
+__global__ __launch_bounds__(256) void vola_kernel(const float* fr, int F, int nfft, int hop, const float* win,
+                                                   float* wave) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int pad = (nfft - hop) / 2, n_out = (F + 3) * hop - 2 * pad;
+    if (i >= n_out) return;
+    const int s = pad + i, b = s / hop, k = s % hop;
+    float acc = 0.0f, env = 0.0f;
+#pragma unroll
+    for (int j = 3; j >= 0; j--) {
+        const int t = b - j;
+        const bool ok = t >= 0 && t < F;
+        const float fv = ok ? fr[(size_t)t * nfft + j * hop + k] : 0.0f;
+        const float wv = win[j * hop + k];
+        acc = j == 3 ? fv : acc + fv;
+        env = env + (ok ? wv * wv : 0.0f);
+    }
+    wave[i] = acc / fmaxf(env, 1e-11f);
+}
+
+// bf16 -> f32 (exact), for the latents fed to the f32 GEMM.
+__global__ __launch_bounds__(256) void vwiden_kernel(const uint16_t* x, int64_t n, float* y) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) y[i] = bf2f(x[i]);
+}
+
+template <int WF>
+hipError_t vgemm_wf(hipStream_t st, const VGemm& g, int epi) {
+    const dim3 grid((g.N + kVBN - 1) / kVBN, (g.M + kVBM - 1) / kVBM);
+    switch (epi) {
+        case VE_PLAIN: hipLaunchKernelGGL((vgemm_kernel<WF, VE_PLAIN>), grid, dim3(kVT), 0, st, g); break;
+        case VE_QKV: hipLaunchKernelGGL((vgemm_kernel<WF, VE_QKV>), grid, dim3(kVT), 0, st, g); break;
+        case VE_RES: hipLaunchKernelGGL((vgemm_kernel<WF, VE_RES>), grid, dim3(kVT), 0, st, g); break;
+        case VE_SWIGLU: hipLaunchKernelGGL((vgemm_kernel<WF, VE_SWIGLU>), grid, dim3(kVT), 0, st, g); break;
+        case VE_WIN: hipLaunchKernelGGL((vgemm_kernel<WF, VE_WIN>), grid, dim3(kVT), 0, st, g); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_vgemm(hipStream_t st, const VGemm& g, int wf, int epi) {
+    if (g.K % kVBK || (wf == VW_Q4 && g.K % 64) || g.lda % 4 || g.M < 1 || g.N < 1) return hipErrorInvalidValue;
+    if (wf == VW_BF16) return vgemm_wf<VW_BF16>(st, g, epi);
+    if (wf == VW_Q4) return vgemm_wf<VW_Q4>(st, g, epi);
+    if (wf == VW_F32) return vgemm_wf<VW_F32>(st, g, epi);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_vrms(hipStream_t st, const float* x, int M, int K, const uint16_t* w, float eps, float* out) {
+    hipLaunchKernelGGL(vrms_kernel, dim3((M + 3) / 4), dim3(256), 0, st, x, M, K, w, eps, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_vattn(hipStream_t st, const float* qkv, int M, int ldq, int H, int heads, int kvh, int window,
+                        float scale, float* att) {
+    if (window < 1 || window > 64) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(vattn_kernel, dim3((M * heads + 3) / 4), dim3(256), 0, st, qkv, M, ldq, H, heads, kvh, window,
+                       scale, att);
+    return hipGetLastError();
+}
+
+hipError_t launch_vup(hipStream_t st, const float* y, const uint16_t* bias, int q4, int T, int C, int scale,
+                      float* x) {
+    const int64_t n = (int64_t)T * scale * C;
+    hipLaunchKernelGGL(vup_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, bias, q4, T, C, scale, x);
+    return hipGetLastError();
+}
+
+hipError_t launch_vspec(hipStream_t st, const float* p, int F, int nfft, int ld, float* spec) {
+    const int64_t n = (int64_t)F * ld;
+    hipLaunchKernelGGL(vspec_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p, F, nfft, ld, spec);
+    return hipGetLastError();
+}
+
+hipError_t launch_vola(hipStream_t st, const float* fr, int F, int nfft, int hop, const float* win, float* wave) {
+    const int n_out = (F + 3) * hop - (nfft - hop);
+    hipLaunchKernelGGL(vola_kernel, dim3((n_out + 255) / 256), dim3(256), 0, st, fr, F, nfft, hop, win, wave);
+    return hipGetLastError();
+}
+
+hipError_t launch_vwiden(hipStream_t st, const uint16_t* x, int64_t n, float* y) {
+    hipLaunchKernelGGL(vwiden_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, n, y);
+    return hipGetLastError();
+}
+
+}  // namespace ming

@@ -14,7 +14,8 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import (Context, Kv, KvPages, Linear, LmCfg, LmLayerW, LmModel, W_AFFINE, W_BF16, linear, synth_normal_bf16)
+from . import (Context, Kv, KvPages, Linear, LmCfg, LmLayerW, LmModel, VaeCfg, VaeModel, VaeW, W_AFFINE, W_BF16,
+               linear, synth_normal_bf16)
 
 
 @dataclass
@@ -154,6 +155,153 @@ class SyntheticLm:
         if isinstance(t, dict):
             return {k: cpu(v) for k, v in t.items()}
         return cpu(t)
+
+
+@dataclass
+class VaeSpec:
+    """The VAE decoder's shape (reference: the LM-shaped Qwen2 stack with a
+    window of 64, latent 64, patch 4, n_fft 3528, hop 882)."""
+    hidden: int = 896
+    heads: int = 14
+    kv_heads: int = 2
+    head_dim: int = 64
+    inter: int = 4864
+    n_layers: int = 24
+    eps: float = 1e-6
+    theta: float = 1e6
+    window: int = 64
+    latent: int = 64
+    patch: int = 4
+    n_fft: int = 3528
+    hop: int = 882
+
+    @property
+    def kvd(self):
+        return self.kv_heads * self.head_dim
+
+    def cfg(self):
+        return VaeCfg(self.hidden, self.heads, self.kv_heads, self.head_dim, self.inter, self.n_layers, self.eps,
+                      float(np.log2(np.float32(self.theta))), self.window, self.latent, self.patch, self.n_fft,
+                      self.hop)
+
+    def weight_params(self):
+        H, I, kvd = self.hidden, self.inter, self.kvd
+        per_layer = H * H * 2 + 2 * kvd * H + 3 * H * I
+        return per_layer * self.n_layers + H * self.latent + (self.n_fft + 2) * H
+
+
+MING_VAE = VaeSpec()
+
+
+def hann_window(n):
+    """Periodic Hann window (torch.hann_window's default), f32."""
+    k = np.arange(n)
+    return (0.5 - 0.5 * np.cos(2.0 * np.pi * k / n)).astype(np.float32)
+
+
+class SyntheticVae:
+    """Device weights of the VAE decoder under the checkpoint's key names
+    (audio.decoder.fc1 / .decoder.layers.* / .decoder.norm / .head.out /
+    .head.istft.window): bf16 N(0, std) linears (4-bit when quant), biases on
+    fc1, q/k/v and the head, norms 1 + N(0, norm_std), a periodic Hann window."""
+
+    def __init__(self, ctx: Context, spec: VaeSpec = MING_VAE, seed=0, quant=False, std=0.02, norm_std=0.0,
+                 device="cuda", threads=None):
+        import torch
+
+        self.ctx, self.spec, self.quant = ctx, spec, quant
+        self.tensors = {}
+        H, I, kvd = spec.hidden, spec.inter, spec.kvd
+
+        def normal(name, n, mean=0.0, sd=std):
+            return synth_normal_bf16(seed, name, n, mean, sd, threads)
+
+        def add_linear(name, N, K, sd=std):
+            w = _to_dev(normal(name + ".weight", N * K, 0.0, sd), (N, K), device)
+            if not quant:
+                self.tensors[name] = dict(w=w)
+                return
+            wq = torch.empty((N, K // 8), dtype=torch.int32, device=device)
+            sc = torch.empty((N, K // 64), dtype=torch.bfloat16, device=device)
+            bi = torch.empty((N, K // 64), dtype=torch.bfloat16, device=device)
+            ctx.quantize(w, wq, sc, bi)
+            ctx.sync()
+            self.tensors[name] = dict(w=wq, s=sc, b=bi)
+
+        def add_vec(name, n, mean=0.0, sd=std):
+            self.tensors[name] = _to_dev(normal(name, n, mean, sd), (n,), device)
+
+        def add_norm(name, n):
+            if norm_std == 0.0:
+                self.tensors[name] = torch.ones(n, dtype=torch.bfloat16, device=device)
+            else:
+                add_vec(name, n, 1.0, norm_std)
+
+        D, P = "audio.decoder", "audio.decoder.decoder"
+        add_linear(f"{D}.fc1", H, spec.latent, 0.1)
+        add_vec(f"{D}.fc1.bias", H)
+        for i in range(spec.n_layers):
+            L = f"{P}.layers.{i}"
+            add_norm(f"{L}.input_layernorm.weight", H)
+            add_norm(f"{L}.post_attention_layernorm.weight", H)
+            add_linear(f"{L}.self_attn.q_proj", H, H)
+            add_linear(f"{L}.self_attn.k_proj", kvd, H)
+            add_linear(f"{L}.self_attn.v_proj", kvd, H)
+            add_vec(f"{L}.self_attn.q_proj.bias", H)
+            add_vec(f"{L}.self_attn.k_proj.bias", kvd)
+            add_vec(f"{L}.self_attn.v_proj.bias", kvd)
+            add_linear(f"{L}.self_attn.o_proj", H, H)
+            add_linear(f"{L}.mlp.gate_proj", I, H)
+            add_linear(f"{L}.mlp.up_proj", I, H)
+            add_linear(f"{L}.mlp.down_proj", H, I)
+        add_norm(f"{P}.norm.weight", H)
+        add_linear(f"{D}.head.out", spec.n_fft + 2, H)
+        add_vec(f"{D}.head.out.bias", spec.n_fft + 2)
+        self.tensors[f"{D}.head.istft.window"] = torch.from_numpy(hann_window(spec.n_fft)).to(device)
+        self._build_views()
+
+    def lin(self, name):
+        t = self.tensors[name]
+        if "s" in t:
+            return linear(t["w"], t["s"], t["b"])
+        return linear(t["w"])
+
+    def _build_views(self):
+        spec, D, P = self.spec, "audio.decoder", "audio.decoder.decoder"
+        t = self.tensors
+        self.layers = (LmLayerW * spec.n_layers)()
+        for i in range(spec.n_layers):
+            L = f"{P}.layers.{i}"
+            self.layers[i] = LmLayerW(
+                t[f"{L}.input_layernorm.weight"].data_ptr(), t[f"{L}.post_attention_layernorm.weight"].data_ptr(),
+                self.lin(f"{L}.self_attn.q_proj"), self.lin(f"{L}.self_attn.k_proj"),
+                self.lin(f"{L}.self_attn.v_proj"), self.lin(f"{L}.self_attn.o_proj"),
+                self.lin(f"{L}.mlp.gate_proj"), self.lin(f"{L}.mlp.up_proj"), self.lin(f"{L}.mlp.down_proj"),
+                t[f"{L}.self_attn.q_proj.bias"].data_ptr(), t[f"{L}.self_attn.k_proj.bias"].data_ptr(),
+                t[f"{L}.self_attn.v_proj.bias"].data_ptr())
+        import ctypes
+
+        self.w = VaeW(self.lin(f"{D}.fc1"), t[f"{D}.fc1.bias"].data_ptr(), ctypes.cast(self.layers, ctypes.c_void_p),
+                      t[f"{P}.norm.weight"].data_ptr(), self.lin(f"{D}.head.out"), t[f"{D}.head.out.bias"].data_ptr(),
+                      t[f"{D}.head.istft.window"].data_ptr())
+        self.cfg = spec.cfg()
+
+    def model(self, max_latents):
+        return VaeModel(self.ctx, self.cfg, self.w, max_latents)
+
+    def host(self, name):
+        """numpy copy: bf16 -> uint16, packed -> uint32, f32 as is; dict for linears."""
+        import torch
+
+        def cpu(x):
+            if x.dtype == torch.bfloat16:
+                return x.view(torch.int16).cpu().numpy().view(np.uint16)
+            if x.dtype == torch.float32:
+                return x.cpu().numpy()
+            return x.cpu().numpy().view(np.uint32)
+
+        v = self.tensors[name]
+        return {k: cpu(x) for k, x in v.items()} if isinstance(v, dict) else cpu(v)
 
 
 class KvCache:
@@ -548,5 +696,5 @@ class SyntheticAdaln:
         return AdalnModel(self.ctx, self.w)
 
 
-__all__ = ["AdalnSpec", "MING_ADALN", "SyntheticAdaln", "DitSpec", "MING_DIT", "SyntheticFlow", "LmSpec", "QWEN2_05B", "SyntheticLm", "KvCache", "lm_bytes_per_token", "W_AFFINE", "W_BF16",
+__all__ = ["VaeSpec", "MING_VAE", "SyntheticVae", "hann_window", "AdalnSpec", "MING_ADALN", "SyntheticAdaln", "DitSpec", "MING_DIT", "SyntheticFlow", "LmSpec", "QWEN2_05B", "SyntheticLm", "KvCache", "lm_bytes_per_token", "W_AFFINE", "W_BF16",
            "Linear", "math"]

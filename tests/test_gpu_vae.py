@@ -1,0 +1,110 @@
+"""VAE decoder on the GPU (ming_vae_decode; Model.vaeDecode,
+src/ming_model.zig:1257-1309) against the oracle (oracle/oracle_vae.c).
+
+The graph after the upsample is f32, so the bar is f32 summation order:
+every layer teacher forced on the GPU's own input (1e-5 of max|ref|), the
+head on the GPU's final hidden, the ISTFT on the GPU's head output (f32
+basis vs the oracle's double irfft: 2e-5), and end to end (2e-4).  fc1 runs
+in bf16 as in the graph, so the upsampled rows may differ by one bf16 ulp
+where the two summation orders round differently (2^-7 of max|ref|)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from vaekit import assert_close_f32, oracle_vae
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(hidden=128, heads=2, kv_heads=1, head_dim=64, inter=256, n_layers=2, window=8, latent=64, patch=4,
+             n_fft=64, hop=16)
+
+
+def syn_mod():
+    import importlib
+
+    return importlib.import_module("ming-tts-serve_amd.synthetic")
+
+
+def run(ming, ctx, syn, T, seed=3, max_latents=None):
+    spec = syn.spec
+    m = syn.model(max_latents or T)
+    lat_h = ming.synth_normal_bf16(seed, "vae.lat", T * spec.latent).reshape(T, spec.latent)
+    lat = torch.from_numpy(lat_h.view(np.int16)).cuda().view(torch.bfloat16)
+    F = T * spec.patch
+    wave = torch.empty(F * spec.hop, dtype=torch.float32, device="cuda")
+    m.decode(T, lat, wave)
+    xs = torch.empty((spec.n_layers + 1, F, spec.hidden), dtype=torch.float32, device="cuda")
+    ho = torch.empty((F, spec.n_fft + 2), dtype=torch.float32, device="cuda")
+    m.trace(xs, ho)
+    ctx.sync()
+    m.close()
+    return lat_h, wave.cpu().numpy(), xs.cpu().numpy(), ho.cpu().numpy()
+
+
+def check(ming, ctx, syn, T, end_to_end=True):
+    S = syn_mod()
+    spec = syn.spec
+    om = oracle_vae(syn)
+    c = om.cfg
+    lat, wave, xs, ho = run(ming, ctx, syn, T)
+    x0 = oracle.linear_upsample(oracle.linear(om.fc1, lat, om.keep[0]), spec.patch)
+    assert_close_f32(xs[0], x0, "fc1 + upsample", 2.0 ** -7)
+    for l in range(spec.n_layers):
+        assert_close_f32(xs[l + 1], oracle.vae_layer(c, om.layers[l], xs[l]), f"layer {l} (teacher forced)", 1e-5)
+    p = oracle.linear_f32(om.head, oracle.rms_f32(xs[-1], om.keep[1]), om.keep[2])
+    assert_close_f32(ho, p, "final norm + head (teacher forced)", 1e-5)
+    assert_close_f32(wave, oracle.vae_istft(ho, spec.n_fft, spec.hop, om.keep[3]), "ISTFT (teacher forced)", 2e-5)
+    if end_to_end:
+        assert_close_f32(wave, oracle.vae_decode(om, lat), "wave (end to end)", 2e-4)
+    assert np.isfinite(wave).all()
+
+
+@pytest.mark.parametrize("T", [1, 5, 17])
+def test_vae_small_bf16(ming, ctx, T):
+    S = syn_mod()
+    syn = S.SyntheticVae(ctx, S.VaeSpec(**SMALL), seed=21, std=0.05, norm_std=0.1)
+    check(ming, ctx, syn, T)
+
+
+def test_vae_small_4bit(ming, ctx):
+    S = syn_mod()
+    syn = S.SyntheticVae(ctx, S.VaeSpec(**SMALL), seed=22, quant=True, std=0.05, norm_std=0.1)
+    check(ming, ctx, syn, 9)
+
+
+def test_vae_window_covers_all_rows(ming, ctx):
+    S = syn_mod()
+    syn = S.SyntheticVae(ctx, S.VaeSpec(**dict(SMALL, window=64)), seed=23, std=0.05)
+    check(ming, ctx, syn, 3)  # F = 12 rows < 64: plain causal attention
+
+
+def test_vae_reference_shape(ming, ctx):
+    """The reference decoder (24 layers, 896, n_fft 3528) on 6 latents."""
+    S = syn_mod()
+    syn = S.SyntheticVae(ctx, S.MING_VAE, seed=24)
+    check(ming, ctx, syn, 6, end_to_end=False)
+
+
+def test_vae_decode_independent_of_capacity(ming, ctx):
+    S = syn_mod()
+    syn = S.SyntheticVae(ctx, S.VaeSpec(**SMALL), seed=25, std=0.05)
+    a = run(ming, ctx, syn, 7)
+    b = run(ming, ctx, syn, 7, max_latents=40)
+    assert np.array_equal(a[1], b[1])
+
+
+def test_vae_rejects(ming, ctx):
+    S = syn_mod()
+    syn = S.SyntheticVae(ctx, S.VaeSpec(**SMALL), seed=26, std=0.05)
+    m = syn.model(4)
+    lat = torch.zeros((5, 64), dtype=torch.bfloat16, device="cuda")
+    wave = torch.empty(5 * 4 * 16, dtype=torch.float32, device="cuda")
+    with pytest.raises(ming.MingError) as e:
+        m.decode(5, lat, wave)
+    assert e.value.status == ming.MING_E_SHAPE
+    m.close()
+    bad = S.VaeSpec(**dict(SMALL, window=65)).cfg()
+    with pytest.raises(ming.MingError) as e:
+        ming.VaeModel(ctx, bad, syn.w, 4)
+    assert e.value.status == ming.MING_E_UNSUPPORTED

@@ -187,3 +187,36 @@ def test_handles_outlive_their_context(ming, tmp_path):
     b.close()
     m.close()
     w.close()
+
+
+def test_vae_from_checkpoint(ming, ctx, tmp_path):
+    """audio.decoder.* (fc1, decoder stack, head, istft.window stored bf16 and widened at load) ->
+    the same waveform bit for bit as the directly built decoder."""
+    S = syn_mod()
+    spec = S.VaeSpec(hidden=128, heads=2, kv_heads=1, head_dim=64, inter=256, n_layers=2, window=8, latent=64,
+                     patch=4, n_fft=64, hop=16)
+    syn = S.SyntheticVae(ctx, spec, seed=51, std=0.05, norm_std=0.1)
+    t = lm_tensors(syn)
+    t["audio.decoder.head.istft.window"] = syn.tensors["audio.decoder.head.istft.window"].to(torch.bfloat16)
+    path = tmp_path / "vae.safetensors"
+    save(path, t)
+    w = ming.Weights(ctx, path, prefixes=["audio.decoder."])
+    m = w.vae_model(spec.cfg(), 8)
+    ref = syn.model(8)
+    # the direct model gets the same bf16-rounded window
+    win = syn.tensors["audio.decoder.head.istft.window"].to(torch.bfloat16).float()
+    ref.close()
+    syn.tensors["audio.decoder.head.istft.window"] = win
+    syn._build_views()
+    ref = syn.model(8)
+    lat = torch.from_numpy(ming.synth_normal_bf16(52, "w.vae", 5 * 64).view(np.int16)).cuda().view(torch.bfloat16)
+    outs = []
+    for mdl in (m, ref):
+        wave = torch.empty(5 * 4 * 16, dtype=torch.float32, device="cuda")
+        mdl.decode(5, lat, wave)
+        outs.append(wave)
+    ctx.sync()
+    assert torch.equal(outs[0], outs[1])
+    m.close()
+    ref.close()
+    w.close()
