@@ -3,6 +3,7 @@
 // ISTFT basis built at load time, and the per-fragment decode.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <string>
 #include <vector>
@@ -20,7 +21,7 @@ struct ming_vae_model {
     const float* window = nullptr;
     std::vector<ming_lm_layer_w> layers;
     DevBuf basis;                                     // f32 [n_fft][ldspec]: irfft rows
-    DevBuf lat, y1, xs, h, qkv, att, x1, hh, p, spec, frames;
+    DevBuf lat, y1, xs, h, qkv, att, x1, hh, p, spec, frames, part;  // part: split-K partials
     int last_f = 0;
 };
 
@@ -28,34 +29,46 @@ namespace {
 
 int vae_err(ming_ctx* ctx, int st, const std::string& m) { return set_err(ctx, st, "vae: " + m); }
 
-// The weight view of a linear for the f32 GEMM.
-void set_w(VGemm& g, const ming_linear& l, int& wf, bool second = false) {
+// The weight of a linear as a GEMM segment; wf receives its format.
+VSeg seg_of(const ming_linear& l, const void* bias, int rope, int& wf) {
     const LinearDev d = linear_dev(l);
     wf = d.kind == 1 ? VW_Q4 : VW_BF16;
-    if (second) {
-        g.w1 = d.w;
-        g.s1 = d.s;
-        g.b1 = d.b;
-        g.g1 = d.kind == 1 ? d.gscale : 1.0f;
-    } else {
-        g.w0 = d.w;
-        g.s0 = d.s;
-        g.b0 = d.b;
-        g.g0 = d.kind == 1 ? d.gscale : 1.0f;
-    }
+    VSeg s{};
+    s.w = d.w;
+    s.s = d.s;
+    s.b = d.b;
+    s.gs = d.kind == 1 ? d.gscale : 1.0f;
+    s.bias = static_cast<const uint16_t*>(bias);
+    s.n = l.out_features;
+    s.rope = rope;
+    return s;
 }
 
-VGemm gemm(const float* a, int lda, int M, int N, int K, float* y, int ldy) {
+VGemm gemm(const float* a, int lda, int M, int K, float* y, int ldy) {
     VGemm g{};
     g.a = a;
     g.lda = lda;
     g.M = M;
-    g.N = N;
     g.K = K;
     g.y = y;
     g.ldy = ldy;
-    g.g0 = g.g1 = 1.0f;
+    g.nseg = 1;
+    g.ks = 1;
     return g;
+}
+
+// K slices for a GEMM of N columns: enough 64 x 64 workgroups (with the
+// slices) to cover the 256 CUs, each slice whole stages (and whole affine
+// groups), at most 8.
+int split_k(int M, int N, int K, int wf) {
+    const int tiles = ((N + 63) / 64) * ((M + 63) / 64);
+    const int unit = wf == VW_Q4 ? 64 : 32;
+    for (int ks = 1; ks <= 8; ks++)
+        if (K % (unit * ks) == 0 && (tiles * ks >= 256 || ks == 8)) return ks;
+    int best = 1;
+    for (int ks = 1; ks <= 8; ks++)
+        if (K % (unit * ks) == 0) best = ks;
+    return best;
 }
 
 int check_cfg(ming_ctx* ctx, const ming_vae_cfg* c) {
@@ -132,7 +145,7 @@ int ming_vae_model_create(ming_ctx* ctx, const ming_vae_cfg* cfg, const ming_vae
         {&m->qkv, F * nq},                            {&m->att, F * H},
         {&m->x1, F * H},                              {&m->hh, F * I},
         {&m->p, F * P},                               {&m->spec, F * m->ldspec},
-        {&m->frames, F * N}};
+        {&m->frames, F * N},                          {&m->part, 8 * F * std::max(nq, (size_t)P)}};
     for (const auto& b : bufs)
         if (e == hipSuccess) e = b.first->ensure(b.second * sizeof(float));
     if (e != hipSuccess) {
@@ -146,7 +159,7 @@ int ming_vae_model_create(ming_ctx* ctx, const ming_vae_cfg* cfg, const ming_vae
 int ming_vae_model_destroy(ming_vae_model* m) {
     if (!m) return MING_E_NOT_INIT;
     for (DevBuf* b : {&m->basis, &m->lat, &m->y1, &m->xs, &m->h, &m->qkv, &m->att, &m->x1, &m->hh, &m->p, &m->spec,
-                      &m->frames})
+                      &m->frames, &m->part})
         b->release();
     delete m;
     return MING_OK;
@@ -166,11 +179,18 @@ int ming_vae_decode(ming_ctx* ctx, ming_vae_model* m, int32_t T, const void* lat
     float *x1 = static_cast<float*>(m->x1.p), *hh = static_cast<float*>(m->hh.p);
     hipError_t e = launch_vwiden(st, static_cast<const uint16_t*>(latents), (int64_t)T * c.latent,
                                  static_cast<float*>(m->lat.p));
+    float* part = static_cast<float*>(m->part.p);
+    // one GEMM: split K where the columns alone leave CUs idle
+    auto run = [&](VGemm g, int wf, int epi, int N) {
+        g.ks = epi == VE_SWIGLU ? 1 : split_k(g.M, N, g.K, wf);
+        g.part = part;
+        return launch_vgemm(st, g, wf, epi);
+    };
     int wf = 0;
     if (e == hipSuccess) {  // fc1: bias and the bf16 rounding are applied by the upsample kernel
-        VGemm g = gemm(static_cast<float*>(m->lat.p), c.latent, T, H, c.latent, static_cast<float*>(m->y1.p), H);
-        set_w(g, m->fc1, wf);
-        e = launch_vgemm(st, g, wf, VE_PLAIN);
+        VGemm g = gemm(static_cast<float*>(m->lat.p), c.latent, T, c.latent, static_cast<float*>(m->y1.p), H);
+        g.seg[0] = seg_of(m->fc1, nullptr, 0, wf);
+        e = run(g, wf, VE_PLAIN, H);
     }
     if (e == hipSuccess)
         e = launch_vup(st, static_cast<float*>(m->y1.p), m->fc1_bias, wf == VW_Q4, T, H, c.patch, xs);
@@ -180,59 +200,53 @@ int ming_vae_decode(ming_ctx* ctx, ming_vae_model* m, int32_t T, const void* lat
         float* x = xs + (size_t)l * F * H;
         float* xo = xs + (size_t)(l + 1) * F * H;
         e = launch_vrms(st, x, F, H, static_cast<const uint16_t*>(L.ln1), c.eps, h);
-        const struct {
-            const ming_linear* w;
-            const void* b;
-            int N, col0, rope;
-        } proj[3] = {{&L.wq, L.bq, H, 0, H}, {&L.wk, L.bk, kvd, H, kvd}, {&L.wv, L.bv, kvd, H + kvd, 0}};
-        for (const auto& pj : proj) {
-            if (e != hipSuccess) break;
-            VGemm g = gemm(h, H, F, pj.N, H, qkv + pj.col0, nq);
-            set_w(g, *pj.w, wf);
-            g.bias = static_cast<const uint16_t*>(pj.b);
-            g.rope_cols = pj.rope;
+        if (e == hipSuccess) {  // q | k | v in one launch, rotary on q and k
+            VGemm g = gemm(h, H, F, H, qkv, nq);
+            g.seg[0] = seg_of(L.wq, L.bq, 1, wf);
+            g.seg[1] = seg_of(L.wk, L.bk, 1, wf);
+            g.seg[2] = seg_of(L.wv, L.bv, 0, wf);
+            g.nseg = 3;
             g.log2_theta = c.log2_theta;
-            e = launch_vgemm(st, g, wf, VE_QKV);
+            e = run(g, wf, VE_QKV, nq);
         }
         if (e == hipSuccess) e = launch_vattn(st, qkv, F, nq, H, c.heads, c.kv_heads, c.window, scale, att);
         if (e == hipSuccess) {
-            VGemm g = gemm(att, H, F, H, H, x1, H);
-            set_w(g, L.wo, wf);
+            VGemm g = gemm(att, H, F, H, x1, H);
+            g.seg[0] = seg_of(L.wo, nullptr, 0, wf);
             g.res = x;
             g.ldres = H;
-            e = launch_vgemm(st, g, wf, VE_RES);
+            e = run(g, wf, VE_RES, H);
         }
         if (e == hipSuccess) e = launch_vrms(st, x1, F, H, static_cast<const uint16_t*>(L.ln2), c.eps, h);
         if (e == hipSuccess) {
-            VGemm g = gemm(h, H, F, I, H, hh, I);
-            set_w(g, L.wg, wf);
-            set_w(g, L.wu, wf, true);
-            e = launch_vgemm(st, g, wf, VE_SWIGLU);
+            VGemm g = gemm(h, H, F, H, hh, I);
+            g.seg[0] = seg_of(L.wg, nullptr, 0, wf);
+            g.up = seg_of(L.wu, nullptr, 0, wf);
+            e = run(g, wf, VE_SWIGLU, I);
         }
         if (e == hipSuccess) {
-            VGemm g = gemm(hh, I, F, H, I, xo, H);
-            set_w(g, L.wd, wf);
+            VGemm g = gemm(hh, I, F, I, xo, H);
+            g.seg[0] = seg_of(L.wd, nullptr, 0, wf);
             g.res = x1;
             g.ldres = H;
-            e = launch_vgemm(st, g, wf, VE_RES);
+            e = run(g, wf, VE_RES, H);
         }
     }
     float* p = static_cast<float*>(m->p.p);
     if (e == hipSuccess) e = launch_vrms(st, xs + (size_t)c.n_layers * F * H, F, H, m->norm, c.eps, h);
     if (e == hipSuccess) {
-        VGemm g = gemm(h, H, F, P, H, p, P);
-        set_w(g, m->head, wf);
-        g.bias = m->head_bias;
-        e = launch_vgemm(st, g, wf, VE_PLAIN);
+        VGemm g = gemm(h, H, F, H, p, P);
+        g.seg[0] = seg_of(m->head, m->head_bias, 0, wf);
+        e = run(g, wf, VE_PLAIN, P);
     }
     float* spec = static_cast<float*>(m->spec.p);
     float* frames = static_cast<float*>(m->frames.p);
     if (e == hipSuccess) e = launch_vspec(st, p, F, c.n_fft, m->ldspec, spec);
     if (e == hipSuccess) {
-        VGemm g = gemm(spec, m->ldspec, F, c.n_fft, m->ldspec, frames, c.n_fft);
-        g.w0 = m->basis.p;
+        VGemm g = gemm(spec, m->ldspec, F, m->ldspec, frames, c.n_fft);
+        g.seg[0] = VSeg{m->basis.p, nullptr, nullptr, 1.0f, nullptr, c.n_fft, 0};
         g.win = m->window;
-        e = launch_vgemm(st, g, VW_F32, VE_WIN);
+        e = run(g, VW_F32, VE_WIN, c.n_fft);
     }
     if (e == hipSuccess) e = launch_vola(st, frames, F, c.n_fft, c.hop, m->window, wave_out);
     if (e == hipSuccess) m->last_f = F;

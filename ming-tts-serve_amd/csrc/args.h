@@ -108,25 +108,35 @@ enum VEpi : int {
     VE_WIN = 4,     // y = acc * win[col]
 };
 
-// C [M][N] = A [M][K] (f32) x W^T with W [N][K]: bf16, MLX affine 4-bit (u32
-// [N][K/8] + bf16 scales/biases [N][K/64]) or f32.
+// One weight of the f32 GEMM: bf16 [n][K], MLX affine 4-bit (u32 [n][K/8] +
+// bf16 scales/biases [n][K/64]) or f32 [n][K].
+struct VSeg {
+    const void* w;
+    const uint16_t *s, *b;
+    float gs;               // affine global scale
+    const uint16_t* bias;   // bf16 [n] or null (VE_PLAIN, VE_QKV)
+    int n;                  // output columns (a multiple of 64 except in the last segment)
+    int rope;               // VE_QKV: 1 = rotary on these columns (heads of 64, position = row)
+};
+
+// C [M][N] = A [M][K] (f32) x W^T; the output columns are the segments'
+// columns one after another (N = sum of seg[i].n).  ks > 1 splits K into ks
+// slices whose partials [ks][M][N] (f32, in part) a reduce kernel sums in
+// slice order before the epilogue.
 struct VGemm {
     const float* a;
-    int lda, M, N, K;
-    const void* w0;
-    const uint16_t *s0, *b0;
-    float g0;
-    const void* w1;
-    const uint16_t *s1, *b1;
-    float g1;
-    const uint16_t* bias;   // bf16 [N] or null (VE_PLAIN, VE_QKV)
+    int lda, M, K;
+    VSeg seg[3];
+    int nseg;
+    VSeg up;                // VE_SWIGLU: the up weight over seg[0]'s columns
     const float* res;       // VE_RES: f32 [M][ldres]
     int ldres;
     const float* win;       // VE_WIN: f32 [N]
     float* y;
     int ldy;
-    int rope_cols;          // VE_QKV
     float log2_theta;
+    int ks;
+    float* part;
 };
 
 }  // namespace ming

@@ -30,25 +30,25 @@ struct VTile {  // one thread's share of a stage's global loads
 };
 
 template <int WF>
-__device__ __forceinline__ void vload_w(const VGemm& g, const void* w, const uint16_t* sc, const uint16_t* bi, int n0,
-                                        int k0, uint4 (&r)[2], uint32_t& s, uint32_t& b) {
+__device__ __forceinline__ void vload_w(const VSeg& sg, int K, int n0, int k0, uint4 (&r)[2], uint32_t& s,
+                                        uint32_t& b) {
     const int t = threadIdx.x;
     if (WF == VW_F32) {
 #pragma unroll
         for (int p = 0; p < 2; p++) {
             const int f = t + kVT * p, col = f / 8, kq = f % 8;
-            const int n = min(n0 + col, g.N - 1);
-            r[p] = ldg4(static_cast<const float*>(w) + (size_t)n * g.K + k0 + 4 * kq);
+            const int n = min(n0 + col, sg.n - 1);
+            r[p] = ldg4(static_cast<const float*>(sg.w) + (size_t)n * K + k0 + 4 * kq);
         }
     } else {
         const int col = t / 4, kq = t % 4;
-        const int n = min(n0 + col, g.N - 1);
+        const int n = min(n0 + col, sg.n - 1);
         if (WF == VW_BF16) {
-            r[0] = ldg4(static_cast<const uint16_t*>(w) + (size_t)n * g.K + k0 + 8 * kq);
+            r[0] = ldg4(static_cast<const uint16_t*>(sg.w) + (size_t)n * K + k0 + 8 * kq);
         } else {
-            r[0].x = gld(static_cast<const uint32_t*>(w) + (size_t)n * (g.K / 8) + (k0 + 8 * kq) / 8);
-            s = gld(sc + (size_t)n * (g.K / 64) + (k0 + 8 * kq) / 64);
-            b = gld(bi + (size_t)n * (g.K / 64) + (k0 + 8 * kq) / 64);
+            r[0].x = gld(static_cast<const uint32_t*>(sg.w) + (size_t)n * (K / 8) + (k0 + 8 * kq) / 8);
+            s = gld(sg.s + (size_t)n * (K / 64) + (k0 + 8 * kq) / 64);
+            b = gld(sg.b + (size_t)n * (K / 64) + (k0 + 8 * kq) / 64);
         }
     }
 }
@@ -87,11 +87,38 @@ __device__ __forceinline__ void vstore_w(float* lw, const uint4 (&r)[2], uint32_
     }
 }
 
-// C [M][N] = A [M][K] (f32, row stride lda) x W^T, W [N][K] in format WF;
-// workgroup = 64 x 64 outputs, wave w = rows 16w .. 16w + 15, all 64 columns;
-// K in stages of 32 through double-buffered LDS (the next stage's global loads
-// are in flight during the current stage's MFMAs).  SWIGLU carries a second
-// weight (up) next to the first (gate).
+__device__ __forceinline__ int vtotal_n(const VGemm& g) {
+    return g.seg[0].n + (g.nseg > 1 ? g.seg[1].n : 0) + (g.nseg > 2 ? g.seg[2].n : 0);
+}
+
+// The segment holding output column c (segments start at multiples of 64) and its first column.
+__device__ __forceinline__ int vseg_of(const VGemm& g, int c, int& start) {
+    start = 0;
+    int i = 0;
+    while (i + 1 < g.nseg && c >= start + g.seg[i].n) {
+        start += g.seg[i].n;
+        i++;
+    }
+    return i;
+}
+
+// MLX fast::rope of the pair (d, d + 32) of a 64-column head at position `row`.
+__device__ __forceinline__ void vrope(float& x1, float& x2, int d, int row, float log2_theta) {
+    const float inv = exp2f(-((float)d / 32.0f) * log2_theta);
+    const float th = (float)row * inv;
+    const float cs = cosf(th), sn = sinf(th);
+    const float a = x1, b = x2;
+    x1 = a * cs - b * sn;
+    x2 = a * sn + b * cs;
+}
+
+// C [M][N] = A [M][K] (f32, row stride lda) x W^T in format WF; workgroup =
+// 64 x 64 outputs of one segment, wave w = rows 16w .. 16w + 15, all 64
+// columns; K (or its slice blockIdx.z of ks) in stages of 32 through
+// double-buffered LDS (the next stage's global loads are in flight during the
+// current stage's MFMAs).  SWIGLU carries the up weight next to the gate.
+// With ks > 1 the raw sums go to the partials and vreduce_kernel applies the
+// epilogue.
 template <int WF, int EPI>
 __global__ __launch_bounds__(kVT) void vgemm_kernel(VGemm g) {
     constexpr bool DUAL = EPI == VE_SWIGLU;
@@ -99,20 +126,25 @@ __global__ __launch_bounds__(kVT) void vgemm_kernel(VGemm g) {
     __shared__ __align__(16) float lw[2][kVBN * kVLd];
     __shared__ __align__(16) float lu[DUAL ? 2 : 1][DUAL ? kVBN * kVLd : 4];
     const int t = threadIdx.x, wave = t / kWave, lane = t % kWave, c = lane % 16, j = lane / 16;
-    const int n0 = blockIdx.x * kVBN, m0 = blockIdx.y * kVBM;
-    const int S = g.K / kVBK;
+    const int n0 = blockIdx.x * kVBN, m0 = blockIdx.y * kVBM, z = blockIdx.z;
+    const int N = vtotal_n(g);
+    int sstart;
+    const int si = vseg_of(g, n0, sstart);
+    const VSeg& sg = g.seg[si];
+    const int ln0 = n0 - sstart;  // the tile's first column within its segment
+    const int Ks = g.K / g.ks, S = Ks / kVBK, kb = z * Ks;
     VTile r;
     uint4 ru[2];
     uint32_t us = 0, ub = 0;
     auto gload = [&](int s) {
-        const int k0 = s * kVBK;
+        const int k0 = kb + s * kVBK;
 #pragma unroll
         for (int p = 0; p < 2; p++) {
             const int f = t + kVT * p, row = f / 8, kq = f % 8;
             r.a[p] = *reinterpret_cast<const float4*>(g.a + (size_t)min(m0 + row, g.M - 1) * g.lda + k0 + 4 * kq);
         }
-        vload_w<WF>(g, g.w0, g.s0, g.b0, n0, k0, r.w, r.s, r.b);
-        if (DUAL) vload_w<WF>(g, g.w1, g.s1, g.b1, n0, k0, ru, us, ub);
+        vload_w<WF>(sg, g.K, ln0, k0, r.w, r.s, r.b);
+        if (DUAL) vload_w<WF>(g.up, g.K, ln0, k0, ru, us, ub);
     };
     auto lstore = [&](int buf) {
 #pragma unroll
@@ -122,8 +154,8 @@ __global__ __launch_bounds__(kVT) void vgemm_kernel(VGemm g) {
 #pragma unroll
             for (int i = 0; i < 4; i++) la[buf][row * kVLd + vperm(4 * kq + i)] = e[i];
         }
-        vstore_w<WF>(lw[buf], r.w, r.s, r.b, g.g0);
-        if (DUAL) vstore_w<WF>(lu[buf], ru, us, ub, g.g1);
+        vstore_w<WF>(lw[buf], r.w, r.s, r.b, sg.gs);
+        if (DUAL) vstore_w<WF>(lu[buf], ru, us, ub, g.up.gs);
     };
     f32x4_t acc[4], accu[DUAL ? 4 : 1];
 #pragma unroll
@@ -164,35 +196,35 @@ __global__ __launch_bounds__(kVT) void vgemm_kernel(VGemm g) {
     for (int b = 0; b < 4; b++)
 #pragma unroll
         for (int i = 0; i < 4; i++) v[b][i] = acc[b][i];
-    if (EPI == VE_PLAIN || EPI == VE_QKV) {
-        if (g.bias)
+    if (g.ks > 1) {  // raw sums of this K slice
 #pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const float bb = bf2f(gld(g.bias + min(n0 + 16 * b + c, g.N - 1)));
-#pragma unroll
-                for (int i = 0; i < 4; i++) v[b][i] += bb;
-            }
-    }
-    if (EPI == VE_QKV && n0 < g.rope_cols) {  // MLX fast::rope, pairs (d, d + 32) of this 64-column head
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-            const int d = 16 * b + c;
-            const float inv = exp2f(-((float)d / 32.0f) * g.log2_theta);
+        for (int b = 0; b < 4; b++) {
+            const int col = n0 + 16 * b + c;
+            if (col >= N) continue;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int row = m0 + 16 * wave + 4 * j + i;
-                const float th = (float)row * inv;
-                const float cs = cosf(th), sn = sinf(th);
-                const float x1 = v[b][i], x2 = v[b + 2][i];
-                v[b][i] = x1 * cs - x2 * sn;
-                v[b + 2][i] = x1 * sn + x2 * cs;
+                if (row < g.M) g.part[((size_t)z * g.M + row) * N + col] = v[b][i];
             }
         }
+        return;
     }
+    if ((EPI == VE_PLAIN || EPI == VE_QKV) && sg.bias)
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const float bb = bf2f(gld(sg.bias + min(ln0 + 16 * b + c, sg.n - 1)));
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[b][i] += bb;
+        }
+    if (EPI == VE_QKV && sg.rope)
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) vrope(v[b][i], v[b + 2][i], 16 * b + c, m0 + 16 * wave + 4 * j + i, g.log2_theta);
 #pragma unroll
     for (int b = 0; b < 4; b++) {
         const int col = n0 + 16 * b + c;
-        if (col >= g.N) continue;
+        if (col >= N) continue;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int row = m0 + 16 * wave + 4 * j + i;
@@ -200,12 +232,46 @@ __global__ __launch_bounds__(kVT) void vgemm_kernel(VGemm g) {
             float o = v[b][i];
             if (EPI == VE_RES) o = g.res[(size_t)row * g.ldres + col] + o;
             if (EPI == VE_SWIGLU) {
-                const float sg = 1.0f / (1.0f + expf(-o));
-                o = (o * sg) * accu[b][i];
+                const float sgm = 1.0f / (1.0f + expf(-o));
+                o = (o * sgm) * accu[b][i];
             }
             if (EPI == VE_WIN) o = o * g.win[col];
             g.y[(size_t)row * g.ldy + col] = o;
         }
+    }
+}
+
+// Split-K reduce + epilogue: thread = (row, 64-column tile, d < 32) owns the
+// columns d and d + 32 of the tile (a rotary pair); the ks partials are summed
+// in slice order.
+template <int EPI>
+__global__ __launch_bounds__(256) void vreduce_kernel(VGemm g) {
+    const int N = vtotal_n(g), tiles = (N + 63) / 64;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)g.M * tiles * 32) return;
+    const int row = (int)(idx / (tiles * 32)), rem = (int)(idx % (tiles * 32)), tile = rem / 32, d = rem % 32;
+    int sstart;
+    const VSeg& sg = g.seg[vseg_of(g, tile * 64, sstart)];
+    float v[2];
+    bool ok[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int col = tile * 64 + d + 32 * h;
+        ok[h] = col < N;
+        float sum = 0.0f;
+        for (int z = 0; z < g.ks; z++) sum += ok[h] ? g.part[((size_t)z * g.M + row) * N + col] : 0.0f;
+        if ((EPI == VE_PLAIN || EPI == VE_QKV) && sg.bias && ok[h]) sum += bf2f(sg.bias[col - sstart]);
+        v[h] = sum;
+    }
+    if (EPI == VE_QKV && sg.rope) vrope(v[0], v[1], d, row, g.log2_theta);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        if (!ok[h]) continue;
+        const int col = tile * 64 + d + 32 * h;
+        float o = v[h];
+        if (EPI == VE_RES) o = g.res[(size_t)row * g.ldres + col] + o;
+        if (EPI == VE_WIN) o = o * g.win[col];
+        g.y[(size_t)row * g.ldy + col] = o;
     }
 }
 
@@ -325,8 +391,8 @@ __global__ __launch_bounds__(256) void vwiden_kernel(const uint16_t* x, int64_t 
 }
 
 template <int WF>
-hipError_t vgemm_wf(hipStream_t st, const VGemm& g, int epi) {
-    const dim3 grid((g.N + kVBN - 1) / kVBN, (g.M + kVBM - 1) / kVBM);
+hipError_t vgemm_wf(hipStream_t st, const VGemm& g, int epi, int N) {
+    const dim3 grid((N + kVBN - 1) / kVBN, (g.M + kVBM - 1) / kVBM, g.ks);
     switch (epi) {
         case VE_PLAIN: hipLaunchKernelGGL((vgemm_kernel<WF, VE_PLAIN>), grid, dim3(kVT), 0, st, g); break;
         case VE_QKV: hipLaunchKernelGGL((vgemm_kernel<WF, VE_QKV>), grid, dim3(kVT), 0, st, g); break;
@@ -335,16 +401,42 @@ hipError_t vgemm_wf(hipStream_t st, const VGemm& g, int epi) {
         case VE_WIN: hipLaunchKernelGGL((vgemm_kernel<WF, VE_WIN>), grid, dim3(kVT), 0, st, g); break;
         default: return hipErrorInvalidValue;
     }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || g.ks == 1) return e;
+    const int64_t items = (int64_t)g.M * ((N + 63) / 64) * 32;
+    const dim3 rg((unsigned)((items + 255) / 256));
+    switch (epi) {
+        case VE_PLAIN: hipLaunchKernelGGL((vreduce_kernel<VE_PLAIN>), rg, dim3(256), 0, st, g); break;
+        case VE_QKV: hipLaunchKernelGGL((vreduce_kernel<VE_QKV>), rg, dim3(256), 0, st, g); break;
+        case VE_RES: hipLaunchKernelGGL((vreduce_kernel<VE_RES>), rg, dim3(256), 0, st, g); break;
+        case VE_WIN: hipLaunchKernelGGL((vreduce_kernel<VE_WIN>), rg, dim3(256), 0, st, g); break;
+        default: return hipErrorInvalidValue;  // SwiGLU has no split form
+    }
     return hipGetLastError();
 }
 
 }  // namespace
 
+// Host checks of a VGemm: segments start at multiples of 64, each K slice is
+// whole stages of 32 (and whole groups of 64 for affine weights), split K
+// has a partial buffer and no SwiGLU.
+static int vgemm_total_n(const VGemm& g) {
+    int n = 0;
+    for (int i = 0; i < g.nseg; i++) n += g.seg[i].n;
+    return n;
+}
+
 hipError_t launch_vgemm(hipStream_t st, const VGemm& g, int wf, int epi) {
-    if (g.K % kVBK || (wf == VW_Q4 && g.K % 64) || g.lda % 4 || g.M < 1 || g.N < 1) return hipErrorInvalidValue;
-    if (wf == VW_BF16) return vgemm_wf<VW_BF16>(st, g, epi);
-    if (wf == VW_Q4) return vgemm_wf<VW_Q4>(st, g, epi);
-    if (wf == VW_F32) return vgemm_wf<VW_F32>(st, g, epi);
+    if (g.nseg < 1 || g.nseg > 3 || g.ks < 1 || g.K % (kVBK * g.ks) || g.lda % 4 || g.M < 1) return hipErrorInvalidValue;
+    if (wf == VW_Q4 && (g.K / g.ks) % 64) return hipErrorInvalidValue;
+    for (int i = 0; i + 1 < g.nseg; i++)
+        if (g.seg[i].n % 64) return hipErrorInvalidValue;
+    if (g.ks > 1 && (!g.part || epi == VE_SWIGLU)) return hipErrorInvalidValue;
+    const int N = vgemm_total_n(g);
+    if (N < 1) return hipErrorInvalidValue;
+    if (wf == VW_BF16) return vgemm_wf<VW_BF16>(st, g, epi, N);
+    if (wf == VW_Q4) return vgemm_wf<VW_Q4>(st, g, epi, N);
+    if (wf == VW_F32) return vgemm_wf<VW_F32>(st, g, epi, N);
     return hipErrorInvalidValue;
 }
 
