@@ -693,10 +693,17 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l, AttnTile tile) {
     }
     lds_sync();
     if (!*last || h >= grp) return;
+    // the smallest batch that holds every split: each lane loads one o value per split
     if (ns <= 16)
         attn_merge<16>(c, l, q);
+    else if (ns <= 24)
+        attn_merge<24>(c, l, q);
     else if (ns <= 32)
         attn_merge<32>(c, l, q);
+    else if (ns <= 40)
+        attn_merge<40>(c, l, q);
+    else if (ns <= 48)
+        attn_merge<48>(c, l, q);
     else
         attn_merge<64>(c, l, q);
 }
