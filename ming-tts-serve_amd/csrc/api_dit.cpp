@@ -3,6 +3,7 @@
 // Model.load (rotary tables, flow schedule, timestep embeddings;
 // src/ming_model.zig:976-1004) and the per-call launch sequences of
 // cfmSample / aggregate / stopProb (src/ming_model.zig:1033-1053, :1143-1203).
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <vector>
@@ -515,7 +516,7 @@ int ming_cfm_sample_batch(ming_ctx* ctx, ming_cfm_model* m, int32_t n, const voi
     grow(m->by[0], (size_t)n * lat * b2);
     grow(m->by[1], (size_t)n * lat * b2);
     grow(m->bhf, (size_t)2 * n * D * b2);
-    grow(m->bpart, (size_t)4 * R * D * sizeof(float));
+    grow(m->bpart, (size_t)R * std::max(4 * D, 2 * F) * sizeof(float));  // split-K partials of ff2 / ff1
     if (e != hipSuccess) return hip_check(ctx, e, "cfm_sample_batch workspace");
     const float eps = m->cfg.eps;
     // once per sample: c_emb(z) (the unconditional half is c_emb(0) = bias) and x_emb(hist) (:1196-1197)

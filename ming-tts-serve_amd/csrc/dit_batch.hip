@@ -310,13 +310,16 @@ __global__ __launch_bounds__(256) void dreduce_kernel(DGemm a) {
 template <int E>
 hipError_t dpick(hipStream_t st, DGemm a) {
     const int gx = (a.N + kBN - 1) / kBN;
-    a.ks = (E == DE_BIAS || E == DE_RES || E == DE_GELU) && a.part && a.K >= 2048 && a.K % (4 * kBK) == 0 ? 4 : 1;
+    // Latency-bound at these sizes: 32-row tiles and K split over workgroups (4 slices from
+    // K = 2048; 2 from K = 1024 while the grid has under 512 workgroups; for the epilogues the
+    // reduce kernel applies) keep more workgroups per CU in flight (measured on the 16- and
+    // 64-sequence server step: +9-11 %; splitting a grid already at 768 workgroups loses 5 %).
+    constexpr bool SPLIT = E == DE_BIAS || E == DE_RES || E == DE_GELU;
+    const int tiles = gx * ((a.R + 31) / 32);
+    a.ks = SPLIT && a.part && a.K >= 2048 && a.K % (4 * kBK) == 0 ? 4
+           : (SPLIT && a.part && a.K >= 1024 && a.K % (2 * kBK) == 0 && tiles < 512 ? 2 : 1);
     if (a.K % (kBK * a.ks)) return hipErrorInvalidValue;
-    if (gx * ((a.R + 63) / 64) * a.ks >= 128) {
-        hipLaunchKernelGGL((dgemm_kernel<64, E>), dim3(gx, (a.R + 63) / 64, a.ks), dim3(256), 0, st, a);
-    } else {
-        hipLaunchKernelGGL((dgemm_kernel<32, E>), dim3(gx, (a.R + 31) / 32, a.ks), dim3(256), 0, st, a);
-    }
+    hipLaunchKernelGGL((dgemm_kernel<32, E>), dim3(gx, (a.R + 31) / 32, a.ks), dim3(256), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.ks == 1) return e;
     if constexpr (E == DE_BIAS || E == DE_RES || E == DE_GELU) {
@@ -346,7 +349,7 @@ DGemm gemm_args(const uint16_t* x, int R, int N, int K, const uint16_t* w, const
 // One DiT block over R rows of L positions: rms1 -> q/k/v (+ rotary) -> attention
 // -> out_proj + residual -> rms2 -> ff1 + gelu -> ff2 + residual.  x and out may
 // not alias; hn [R][D], qkv [3][R][D], att [R][D], x1 [R][D], hh [R][F] and
-// part [4][R][D] f32 scratch.
+// part f32 scratch of max(4 R D, 2 R F) floats (split-K partials).
 hipError_t launch_dit_block_gemm(hipStream_t st, const DitBlockDev& w, const uint16_t* x, int R, int L,
                                  const float* cos_t, const float* sin_t, uint16_t* hn, uint16_t* qkv, uint16_t* att,
                                  uint16_t* x1, uint16_t* hh, uint16_t* out, float* part) {
@@ -367,10 +370,12 @@ hipError_t launch_dit_block_gemm(hipStream_t st, const DitBlockDev& w, const uin
     if ((e = launch_dit_attn(st, qkv, R / L, L, D, w.heads, w.hd, att)) != hipSuccess) return e;
     a = gemm_args(att, R, D, D, w.wo, w.bo, x1);
     a.res = x;
+    a.part = part;  // [2][R][D] of the [4][R][D] scratch
     if ((e = dpick<DE_RES>(st, a)) != hipSuccess) return e;
     hipLaunchKernelGGL(drms_kernel, dim3(R), dim3(256), 0, st, x1, D, 0, w.norm2, w.eps, hn);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     a = gemm_args(hn, R, F, D, w.w1, w.b1, hh);
+    a.part = part;  // [2][R][F]
     if ((e = dpick<DE_GELU>(st, a)) != hipSuccess) return e;
     a = gemm_args(hh, R, D, F, w.w2, w.b2, out);
     a.res = x1;
