@@ -56,24 +56,25 @@ __device__ __forceinline__ float gelu_chain_b(float x) {
     return rb(rb(0.5f * x) * rb(1.0f + th));
 }
 
-// LDS-tiled GEMM: workgroup tile BM rows x 64 columns, K staged 64 at a time
-// through two LDS buffers (rows padded to 72 values: the 16 rows a fragment
-// read touches fall in distinct banks).  256 threads load each stage
+// LDS-tiled GEMM: workgroup tile BM rows x 64 columns, K staged kBK (128 where
+// K allows, else 64) at a time through two LDS buffers (rows padded by 8
+// values: the 16 rows a fragment read touches fall in distinct banks).  256 threads load each stage
 // cooperatively (16 bytes each, coalesced) while the previous stage's MFMAs
 // run; wave w owns rows 32 (w / 2) .. + 32 and columns 32 (w % 2) .. + 32 of
 // a 64-row tile (BM = 64), or rows 0 .. 32 and columns 16 w .. + 16 (BM = 32).
-constexpr int kBN = 64, kBK = 64, kPad = 72;
+constexpr int kBN = 64;
 
-template <int BM>
+template <int BM, int kBK>
 struct DTile {
     static constexpr int NT = BM == 64 ? 2 : 1;       // 16-column tiles per wave
     static constexpr int AL = BM * kBK / 8 / 256;    // A chunks (16 B) per thread per stage
     static constexpr int BL = kBN * kBK / 8 / 256;   // B chunks per thread per stage
 };
 
-template <int BM, int E>
+template <int BM, int kBK, int E>
 __global__ __launch_bounds__(256) void dgemm_kernel(DGemm a) {
-    using T = DTile<BM>;
+    constexpr int kPad = kBK + 8, kCPR = kBK / 8;
+    using T = DTile<BM, kBK>;
     constexpr int NT = T::NT;
     __shared__ __align__(16) uint16_t As[2][BM * kPad];
     __shared__ __align__(16) uint16_t Bs[2][kBN * kPad];
@@ -84,18 +85,18 @@ __global__ __launch_bounds__(256) void dgemm_kernel(DGemm a) {
     const uint16_t* B = si == 0 ? a.b[0] : (si == 1 ? a.b[1] : a.b[2]);
     const int m0 = blockIdx.y * BM, S = a.K / kBK / a.ks, s0 = blockIdx.z * S;
     const int wm = BM == 64 ? wave / 2 : 0, wn = BM == 64 ? wave % 2 : wave;
-    // this thread's global chunks: chunk q -> (row q / 8, k 8 (q % 8))
+    // this thread's global chunks: chunk q -> (row q / kCPR, k 8 (q % kCPR))
     const uint16_t* ag[T::AL];
     const uint16_t* bg[T::BL];
 #pragma unroll
     for (int i = 0; i < T::AL; i++) {
-        const int q = tid + 256 * i, r = min(m0 + q / 8, a.R - 1);
-        ag[i] = a.x + (size_t)r * a.ldx + 8 * (q % 8);
+        const int q = tid + 256 * i, r = min(m0 + q / kCPR, a.R - 1);
+        ag[i] = a.x + (size_t)r * a.ldx + 8 * (q % kCPR);
     }
 #pragma unroll
     for (int i = 0; i < T::BL; i++) {
-        const int q = tid + 256 * i, n = min(ns0 + q / 8, NS - 1);
-        bg[i] = W + (size_t)n * a.K + 8 * (q % 8);
+        const int q = tid + 256 * i, n = min(ns0 + q / kCPR, NS - 1);
+        bg[i] = W + (size_t)n * a.K + 8 * (q % kCPR);
     }
     // two register sets: the stage about to be stored to LDS and the one after it, in flight
     uint4 ar[2][T::AL], br[2][T::BL];
@@ -109,12 +110,12 @@ __global__ __launch_bounds__(256) void dgemm_kernel(DGemm a) {
 #pragma unroll
         for (int i = 0; i < T::AL; i++) {
             const int q = tid + 256 * i;
-            *reinterpret_cast<uint4*>(&As[buf][(q / 8) * kPad + 8 * (q % 8)]) = ar[set][i];
+            *reinterpret_cast<uint4*>(&As[buf][(q / kCPR) * kPad + 8 * (q % kCPR)]) = ar[set][i];
         }
 #pragma unroll
         for (int i = 0; i < T::BL; i++) {
             const int q = tid + 256 * i;
-            *reinterpret_cast<uint4*>(&Bs[buf][(q / 8) * kPad + 8 * (q % 8)]) = br[set][i];
+            *reinterpret_cast<uint4*>(&Bs[buf][(q / kCPR) * kPad + 8 * (q % kCPR)]) = br[set][i];
         }
     };
     f32x4_t acc[2][NT];
@@ -124,7 +125,7 @@ __global__ __launch_bounds__(256) void dgemm_kernel(DGemm a) {
         for (int t = 0; t < NT; t++) acc[mt][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     auto compute = [&](int buf) {
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
+        for (int ks = 0; ks < kBK / 32; ks++) {
             uint4 af[2], bfr[NT];
 #pragma unroll
             for (int mt = 0; mt < 2; mt++)
@@ -316,10 +317,14 @@ hipError_t dpick(hipStream_t st, DGemm a) {
     // 64-sequence server step: +9-11 %; splitting a grid already at 768 workgroups loses 5 %).
     constexpr bool SPLIT = E == DE_BIAS || E == DE_RES || E == DE_GELU;
     const int tiles = gx * ((a.R + 31) / 32);
-    a.ks = SPLIT && a.part && a.K >= 2048 && a.K % (4 * kBK) == 0 ? 4
-           : (SPLIT && a.part && a.K >= 1024 && a.K % (2 * kBK) == 0 && tiles < 512 ? 2 : 1);
-    if (a.K % (kBK * a.ks)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((dgemm_kernel<32, E>), dim3(gx, (a.R + 31) / 32, a.ks), dim3(256), 0, st, a);
+    a.ks = SPLIT && a.part && a.K >= 2048 && a.K % (4 * 64) == 0 ? 4
+           : (SPLIT && a.part && a.K >= 1024 && a.K % (2 * 64) == 0 && tiles < 512 ? 2 : 1);
+    if (a.K % (64 * a.ks)) return hipErrorInvalidValue;
+    // 128-wide K stages put twice the bytes of each stage in flight (measured: +10 % at 96 rows)
+    if (a.K % (128 * a.ks) == 0)
+        hipLaunchKernelGGL((dgemm_kernel<32, 128, E>), dim3(gx, (a.R + 31) / 32, a.ks), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((dgemm_kernel<32, 64, E>), dim3(gx, (a.R + 31) / 32, a.ks), dim3(256), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.ks == 1) return e;
     if constexpr (E == DE_BIAS || E == DE_RES || E == DE_GELU) {
