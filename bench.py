@@ -80,6 +80,8 @@ def parse():
     p.add_argument("--mode", choices=["auto", "kernels", "persistent", "direct"], default="auto")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--cooperative", action="store_true",
+                   help="lm/loop: cooperative persistent launch (default: ordinary launch, the bench owns the device)")
     return p.parse_args()
 
 
@@ -107,6 +109,7 @@ def main():
     S = importlib.import_module("ming-tts-serve_amd.synthetic")
     spec = S.QWEN2_05B
     ctx = ming.Context(0)
+    ctx.set_exclusive(not args.cooperative)
     t0 = time.time()
     syn = S.SyntheticLm(ctx, spec, seed=0, quant=True)
     m = syn.model()
@@ -168,6 +171,7 @@ def main():
             "weights": "MLX affine u32 4-bit, group 64, bf16 scales/biases, global scale 1.0",
             "kv_cache": "bf16 in place",
             "schedule": args.mode,
+            "launch": "cooperative" if args.cooperative else "ordinary (device held by this process alone)",
             "global_batch": 1,
             "seq_len": args.ctx,
         },
@@ -580,6 +584,7 @@ def bench_loop(args):
     S = importlib.import_module("ming-tts-serve_amd.synthetic")
     lspec, dspec = S.QWEN2_05B, S.MING_DIT
     ctx = ming.Context(0)
+    ctx.set_exclusive(not args.cooperative)
     lm = S.SyntheticLm(ctx, lspec, seed=0, quant=True)
     lmm = lm.model()
     flow = S.SyntheticFlow(ctx, dspec, seed=1)
@@ -616,7 +621,8 @@ def bench_loop(args):
     line = base_line(METRIC_LOOP, 1000.0 / ms, "tokens/s", args, ms,
                      {"workload": f"one sampleLatents step after a {L}-row prompt: flow head (8 blocks x 10 Euler "
                                   "steps), aggregator (8 blocks), Qwen2-0.5B-shaped 24-layer 4-bit LM decode "
-                                  "(hidden only), stop head", "global_batch": 1, "seq_len": L + K},
+                                  "(hidden only), stop head", "global_batch": 1, "seq_len": L + K,
+                      "launch": "cooperative" if args.cooperative else "ordinary (device held by this process alone)"},
                      {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                       "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": nbytes,
                       "launch_ms": round(ms, 5)},

@@ -74,6 +74,13 @@ int ming_ctx_destroy(ming_ctx* ctx);
  * called; ming_ctx_use_own_stream() returns to it. */
 int ming_ctx_set_stream(ming_ctx* ctx, void* hip_stream);
 int ming_ctx_use_own_stream(ming_ctx* ctx);
+/* on != 0: the caller promises that nothing else runs on the device while this
+ * context's persistent decode step runs, so the step is dispatched as an
+ * ordinary launch instead of a cooperative one (about 16 us less per token).
+ * Off by default.  A broken promise surfaces as MING_E_TIMEOUT from the
+ * bounded waits, never as a hang.  No counterpart in the reference: MLX
+ * dispatches per op (src/ming_fused.zig has no persistent step). */
+int ming_ctx_set_exclusive(ming_ctx* ctx, int on);
 void* ming_ctx_stream(ming_ctx* ctx);
 /* The eval point (mlx_eval, src/ming_model.zig:269-274); also reports any
  * device-side error flag (MING_E_TIMEOUT). */

@@ -155,6 +155,7 @@ def lib():
         "ming_ctx_destroy": (c_i32, [c_void_p]),
         "ming_ctx_set_stream": (c_i32, [c_void_p, c_void_p]),
         "ming_ctx_use_own_stream": (c_i32, [c_void_p]),
+        "ming_ctx_set_exclusive": (c_i32, [c_void_p, c_i32]),
         "ming_ctx_stream": (c_void_p, [c_void_p]),
         "ming_sync": (c_i32, [c_void_p]),
         "ming_last_error": (ctypes.c_char_p, [c_void_p]),
@@ -336,6 +337,9 @@ class Context:
 
     def set_stream(self, s):
         self.check(self.L.ming_ctx_set_stream(self.h, c_void_p(s)))
+
+    def set_exclusive(self, on=True):
+        self.check(self.L.ming_ctx_set_exclusive(self.h, int(bool(on))))
 
     def sync(self):
         self.check(self.L.ming_sync(self.h))

@@ -14,7 +14,7 @@ namespace ming {
 
 hipError_t launch_lm_layer(hipStream_t st, const StepArgs& a, const LayerDev& Ld, int l);
 hipError_t launch_lm_step_kernels(hipStream_t st, const StepArgs& a, const LayerDev* host_layers);
-hipError_t launch_lm_step_tagged(hipStream_t st, const StepArgs& a, int q4, int grid);
+hipError_t launch_lm_step_tagged(hipStream_t st, const StepArgs& a, int q4, int grid, bool cooperative);
 hipError_t launch_copy_token(hipStream_t st, const int32_t* src, int32_t* dst);
 int tagged_grid(int num_cus);
 int tagged_split_len(int n);
@@ -298,6 +298,12 @@ int ming_ctx_set_stream(ming_ctx* ctx, void* s) {
 int ming_ctx_use_own_stream(ming_ctx* ctx) {
     if (!alive(ctx)) return MING_E_NOT_INIT;
     ctx->stream = ctx->own_stream;
+    return MING_OK;
+}
+
+int ming_ctx_set_exclusive(ming_ctx* ctx, int on) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    ctx->exclusive = on != 0;
     return MING_OK;
 }
 
@@ -731,7 +737,7 @@ static int lm_step_impl(ming_ctx* ctx, ming_lm_model* m, const int32_t* token_de
         a.split_len = tsl;
         a.epoch = ++m->epoch;
         if (a.epoch == 0) a.epoch = ++m->epoch;
-        st = hip_check(ctx, launch_lm_step_tagged(ctx->stream, a, m->head.kind == 1, m->pgrid),
+        st = hip_check(ctx, launch_lm_step_tagged(ctx->stream, a, m->head.kind == 1, m->pgrid, !ctx->exclusive),
                        "lm_step persistent launch");
     } else
         st = hip_check(ctx, launch_lm_step_kernels(ctx->stream, a, m->layers.data()), "lm_step launch");

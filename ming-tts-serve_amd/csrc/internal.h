@@ -43,6 +43,7 @@ struct ming_ctx {
     ming::DevBuf part;                // attention partials of ming_lm_layer
     ming::DevBuf qstage;              // staged activations of ming_qgemm
     bool timeout_seen = false;        // ming_sync saw the device error flag
+    bool exclusive = false;           // caller keeps the device to this context's work
 };
 
 namespace ming {

@@ -1056,13 +1056,19 @@ int tagged_img_stride(int H, int I) {
 int tagged_max_layers() { return kMaxLdsLayers; }
 int tagged_units_per_worker() { return kCW; }
 
-hipError_t launch_lm_step_tagged(hipStream_t st, const StepArgs& a, int q4, int grid) {
+// The grid is one workgroup per CU and every workgroup waits on others, so all
+// of them must be resident at once.  A cooperative launch guarantees it; an
+// ordinary one (about 16 us less per step) relies on the caller keeping other
+// work off the device while the step runs.  Either way each wait is bounded:
+// a workgroup that never starts turns into MING_E_TIMEOUT, not a hang.
+hipError_t launch_lm_step_tagged(hipStream_t st, const StepArgs& a, int q4, int grid, bool cooperative) {
     StepArgs args = a;
     const LayerDev* layers = a.layers;
     void* params[] = {&args, &layers};
     const void* f = q4 ? reinterpret_cast<const void*>(decode_tagged_kernel<1>)
                        : reinterpret_cast<const void*>(decode_tagged_kernel<0>);
-    return hipLaunchCooperativeKernel(f, dim3(grid), dim3(kT), params, 0, st);
+    if (cooperative) return hipLaunchCooperativeKernel(f, dim3(grid), dim3(kT), params, 0, st);
+    return hipLaunchKernel(f, dim3(grid), dim3(kT), params, 0, st);
 }
 
 int tagged_grid(int num_cus) {

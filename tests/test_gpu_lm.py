@@ -191,6 +191,28 @@ def test_schedules_agree_and_deterministic(ming, ctx, q4_model):
     assert_close_bf16(p[1], k[1], "persistent vs kernels hidden", atol=0.2, rtol=0.1)
 
 
+def test_ordinary_launch_matches_cooperative(ming, ctx, q4_model):
+    """With the device held exclusively the persistent step is an ordinary
+    launch; the kernel is the same, so the bits are the same, in both the hub
+    and the direct schedule, over a few steps that grow the cache."""
+    S = syn_mod(ming)
+    syn, m, _ = q4_model
+    try:
+        for mode in (ming.LM_PERSISTENT, ming.LM_PERSISTENT_DIRECT):
+            got = {}
+            for excl in (False, True):
+                ctx.set_exclusive(excl)
+                cache = S.KvCache(syn.spec, 600)
+                cache.fill_random(500, seed=11)
+                got[excl] = [run_step(ming, syn, m, cache, t, mode) for t in (17, 9000, 151000)]
+                assert cache.kv.len == 503
+            for a, b in zip(got[False], got[True]):
+                assert a[0] == b[0] and np.array_equal(a[1], b[1]) and np.array_equal(a[2], b[2]), \
+                    f"mode {mode}: ordinary launch differs from cooperative"
+    finally:
+        ctx.set_exclusive(False)
+
+
 def test_greedy_generate(ming, ctx, q4_model):
     """A prompt of 8 random ids fed one by one, then 12 greedy steps with the
     token fed back.  Every step is checked teacher-forced (each layer on the
