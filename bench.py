@@ -628,6 +628,8 @@ def bench_loop(args):
                       "launch_ms": round(ms, 5)},
                      cpu, "synthetic (random-init N(0,0.02) weights, LM quantized to MLX affine 4-bit/g64; "
                           "prompt rows N(0,0.25); noise bank N(0,1))")
+    # one whole call with one step: workspace set-up, the prompt's prefill, the first latent
+    line["first_latent_ms"] = round(t1 * 1e3, 3)
     print(json.dumps(line), flush=True)
 
 

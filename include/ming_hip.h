@@ -546,8 +546,12 @@ typedef struct {
  * "flow.noise").  MLX's own RNG stream is not reproduced. */
 int ming_noise_bank(ming_ctx* ctx, uint64_t seed, int32_t steps, int32_t latent, void* bank_dev);
 
-/* sampleLatents: embeds [L][hidden] (device bf16) are decoded one position at
- * a time into kv (appended at kv->len), z = the last row's final-normed hidden;
+/* sampleLatents: embeds [L][hidden] (device bf16) are prefilled into kv
+ * (appended at kv->len), z = the last row's final-normed hidden.  On an empty
+ * cache (kv->len 0) with a model ming_lm_batch_create accepts, the prompt is
+ * one multi-row forward (ming_lm_prefill over a page pool of the call's own,
+ * then copied into kv; src/ming_model.zig:576-614); otherwise one decode step
+ * per row;
  * then for step k < min(max_steps, capacity - len - L): latent_k =
  * cfmSample(z_k, history, bank[k]) into latents_out[k] (device bf16
  * [max_steps][latent]); z_{k+1} = LM(aggregate(latent_k)); stop_k =

@@ -6,6 +6,7 @@
 // enqueues CFM(k) and the LM pass for k+1 before the host reads stop_k, so
 // the GPU is never idle while the host decides whether to stop.
 #include <cstring>
+#include <string>
 #include <vector>
 
 #include "internal.h"
@@ -33,6 +34,70 @@ struct LoopBufs {
             if (e) (void)hipEventDestroy(e);
     }
 };
+
+// Buffers of the batched prompt pass; released after the stream has drained.
+struct PrefillBufs {
+    hipStream_t s = nullptr;
+    ming_lm_batch* batch = nullptr;
+    DevBuf kp, vp, table, hid;
+    std::vector<int32_t> ids;  // host source of the page table's upload
+    ~PrefillBufs() {
+        if (s) (void)hipStreamSynchronize(s);
+        if (batch) (void)ming_lm_batch_destroy(batch);
+        for (DevBuf* b : {&kp, &vp, &table, &hid}) b->release();
+    }
+};
+
+// The prompt rows as one multi-row forward (QStack.forward over the prompt,
+// src/ming_model.zig:576-614): ming_lm_prefill over a page pool of its own
+// (pages 0, 1, 2, ... in position order), then the pages copied into kv rows
+// [0, L) and z = the last row's final-normed hidden.  Returns
+// MING_E_UNSUPPORTED, with the context's error text left as it was, when the
+// batched step does not run this model (not 4-bit, head_dim not 64).
+int prefill_batched(ming_ctx* ctx, ming_lm_model* lm, const uint16_t* emb, int L, ming_kv* kv, uint16_t* z, int H,
+                    PrefillBufs& pb) {
+    LmView v;
+    if (!lm_model_view(lm, v)) return set_err(ctx, MING_E_NOT_INIT, "sample_latents: null LM model");
+    if (!kv->k || !kv->v) return set_err(ctx, MING_E_ARG, "sample_latents: null kv cache");
+    if (kv->kv_heads != v.cfg.kv_heads || kv->head_dim != v.cfg.head_dim || kv->n_layers != v.cfg.n_layers)
+        return set_err(ctx, MING_E_SHAPE, "sample_latents: kv cache geometry does not match the model");
+    hipStream_t s = ctx->stream;
+    const int n_pages = (L + 63) / 64;
+    const std::string err = ctx->err;
+    int st = ming_lm_batch_create(ctx, lm, L < 64 ? L : 64, n_pages * 64, &pb.batch);
+    if (st == MING_E_UNSUPPORTED) {
+        ctx->err = err;
+        return st;
+    }
+    if (st) return st;
+    pb.s = s;
+    const size_t page_bytes = (size_t)kv->n_layers * n_pages * kv->kv_heads * 64 * 64 * sizeof(uint16_t);
+    hipError_t e = pb.kp.ensure(page_bytes);
+    if (e == hipSuccess) e = pb.vp.ensure(page_bytes);
+    if (e == hipSuccess) e = pb.table.ensure(sizeof(int32_t) * n_pages);
+    if (e == hipSuccess) e = pb.hid.ensure(sizeof(uint16_t) * (size_t)L * H);
+    // unwritten positions of the last page are masked out of attention; zeros keep them finite
+    if (e == hipSuccess) e = hipMemsetAsync(pb.kp.p, 0, page_bytes, s);
+    if (e == hipSuccess) e = hipMemsetAsync(pb.vp.p, 0, page_bytes, s);
+    pb.ids.resize(n_pages);
+    for (int i = 0; i < n_pages; i++) pb.ids[i] = i;
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(pb.table.p, pb.ids.data(), sizeof(int32_t) * n_pages, hipMemcpyHostToDevice, s);
+    if ((st = hip_check(ctx, e, "sample_latents prefill buffers"))) return st;
+    const ming_kv_pages pages{pb.kp.p, pb.vp.p, kv->n_layers, kv->kv_heads, kv->head_dim, 64, n_pages};
+    if ((st = ming_lm_prefill(pb.batch, L, nullptr, emb, &pages, static_cast<const int32_t*>(pb.table.p), n_pages, 0,
+                              pb.hid.p, nullptr, nullptr)))
+        return st;
+    e = launch_pages_to_rows(s, static_cast<const uint16_t*>(pb.kp.p), static_cast<const uint16_t*>(pb.vp.p),
+                             kv->n_layers, kv->kv_heads, n_pages, 0, L, static_cast<uint16_t*>(kv->k),
+                             static_cast<uint16_t*>(kv->v), kv->capacity);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(z, static_cast<const uint16_t*>(pb.hid.p) + (size_t)(L - 1) * H, sizeof(uint16_t) * H,
+                           hipMemcpyDeviceToDevice, s);
+    if ((st = hip_check(ctx, e, "sample_latents prefill copy"))) return st;
+    kv->len = L;
+    return MING_OK;
+}
 
 }  // namespace
 
@@ -89,9 +154,18 @@ int ming_sample_latents(ming_ctx* ctx, ming_lm_model* lm, ming_cfm_model* cfm, m
     const uint16_t* emb = static_cast<const uint16_t*>(embeds);
     uint16_t* lats = static_cast<uint16_t*>(latents_out);
     const uint16_t* bank = static_cast<const uint16_t*>(noise_bank);
-    // prefill: one decode step per prompt row; z = the last row's final-normed hidden
-    for (int i = 0; i < L; i++)
-        if ((st = ming_lm_step(ctx, lm, nullptr, emb + (size_t)i * H, kv, z, nullptr, nullptr))) return st;
+    // prefill; z = the last row's final-normed hidden.  An empty cache takes the
+    // prompt in one batched pass where the model allows it; otherwise (or when
+    // continuing a cache) one decode step per prompt row.
+    PrefillBufs pb;
+    st = kv->len == 0 && kv->head_dim == 64 && L > 1 ? prefill_batched(ctx, lm, emb, L, kv, z, H, pb)
+                                                     : MING_E_UNSUPPORTED;
+    if (st == MING_E_UNSUPPORTED) {
+        for (int i = 0; i < L; i++)
+            if ((st = ming_lm_step(ctx, lm, nullptr, emb + (size_t)i * H, kv, z, nullptr, nullptr))) return st;
+    } else if (st) {
+        return st;
+    }
     // history: the prompt's last latent, or zeros (history_patch_size 1)
     e = prompt_latent ? hipMemcpyAsync(b.hist.p, prompt_latent, sizeof(uint16_t) * lat, hipMemcpyDeviceToDevice, s)
                       : hipMemsetAsync(b.hist.p, 0, sizeof(uint16_t) * lat, s);

@@ -329,7 +329,52 @@ __global__ __launch_bounds__(256) void prefill_rows_kernel(const int32_t* __rest
     if (k < n) gst(pos + k, p0 + k);
 }
 
+// ---- pages -> contiguous cache rows -------------------------------------------------
+// Positions [p0, p0 + n) of one sequence whose pages are 0, 1, 2, ... in
+// position order, copied into a contiguous cache [n_layers][kvh][cap][64].
+// Thread = (layer, head, position, 8-dim chunk): K rows are contiguous in
+// both layouts (one 16-byte load and store); a V page is stored transposed
+// ([dim][64 positions]), so its 8 dims are gathered 64 elements apart.
+__global__ __launch_bounds__(256) void pages_to_rows_kernel(const uint16_t* __restrict__ kp,
+                                                            const uint16_t* __restrict__ vp, int n_layers, int kvh,
+                                                            int n_pages, int p0, int n, uint16_t* __restrict__ kc,
+                                                            uint16_t* __restrict__ vc, int cap) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t total = (int64_t)n_layers * kvh * n * 8;
+    if (t >= total) return;
+    const int c = (int)(t & 7);
+    int64_t r = t >> 3;
+    const int i = (int)(r % n);
+    r /= n;
+    const int h = (int)(r % kvh);
+    const int l = (int)(r / kvh);
+    const int p = p0 + i;
+    const int64_t page = ((int64_t)l * n_pages + p / 64) * kvh + h;  // [layer][page][head] block of 64 x 64
+    const int64_t dst = (((int64_t)l * kvh + h) * cap + p) * 64 + c * 8;
+    gst(reinterpret_cast<uint4*>(kc + dst), ldg4(kp + page * 4096 + (p % 64) * 64 + c * 8));
+    const uint16_t* vs = vp + page * 4096 + (c * 8) * 64 + p % 64;
+    uint16_t v8[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) v8[j] = gld(vs + j * 64);
+    uint4 o;
+    o.x = v8[0] | (uint32_t)v8[1] << 16;
+    o.y = v8[2] | (uint32_t)v8[3] << 16;
+    o.z = v8[4] | (uint32_t)v8[5] << 16;
+    o.w = v8[6] | (uint32_t)v8[7] << 16;
+    gst(reinterpret_cast<uint4*>(vc + dst), o);
+}
+
 }  // namespace
+
+hipError_t launch_pages_to_rows(hipStream_t st, const uint16_t* kp, const uint16_t* vp, int n_layers, int kvh,
+                                int n_pages, int p0, int n, uint16_t* kc, uint16_t* vc, int cap) {
+    if (n_layers < 1 || kvh < 1 || n < 1 || p0 < 0 || p0 + n > n_pages * 64 || p0 + n > cap)
+        return hipErrorInvalidValue;
+    const int64_t total = (int64_t)n_layers * kvh * n * 8;
+    hipLaunchKernelGGL(pages_to_rows_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, kp, vp,
+                       n_layers, kvh, n_pages, p0, n, kc, vc, cap);
+    return hipGetLastError();
+}
 
 hipError_t launch_stage(hipStream_t st, const uint16_t* x, int ldx, int M, int K, const uint16_t* norm_w, float eps,
                         void* xs, float* xsum, uint16_t* hout, int32_t* pos_inc) {

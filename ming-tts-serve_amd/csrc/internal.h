@@ -76,6 +76,10 @@ hipError_t launch_rope_table(hipStream_t st, float* cs, int max_ctx, int half, f
 hipError_t launch_paged_attn(hipStream_t st, const PagedAttnArgs& a, int n_seq);
 hipError_t launch_merge_stage(hipStream_t st, const MergeArgs& a);
 // rows [n][pps] = n copies of table [pps]; pos [n] = p0, p0 + 1, ...
+// Positions [p0, p0 + n) of the pages 0, 1, 2, ... (head_dim 64) into a
+// contiguous [n_layers][kvh][cap][64] cache.
+hipError_t launch_pages_to_rows(hipStream_t st, const uint16_t* kp, const uint16_t* vp, int n_layers, int kvh,
+                                int n_pages, int p0, int n, uint16_t* kc, uint16_t* vc, int cap);
 hipError_t launch_prefill_rows(hipStream_t st, const int32_t* table, int pps, int n, int p0, int32_t* rows,
                                int32_t* pos);
 

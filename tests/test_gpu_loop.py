@@ -114,3 +114,71 @@ def test_sample_latents_rejects(ming, ctx, models):
                            lats)
     assert e.value.status == ming.MING_E_CTX_OVER_CAPACITY
     assert cache.len == 0
+
+
+def run_loop(ctx, models, emb, cache, max_steps=1):
+    ming, S = mods()
+    spec, flow = models["spec"], models["flow"]
+    H, lat = spec.hidden, flow.spec.latent
+    bias_d = dev_u16(oracle.to_bf16(np.array((20.0, 0.0), np.float32)))  # never stops
+    bank = torch.empty((max_steps, 11, lat), dtype=torch.bfloat16, device="cuda")
+    ctx.noise_bank(99, max_steps, lat, bank)
+    lats = torch.zeros((max_steps, lat), dtype=torch.bfloat16, device="cuda")
+    ztr = torch.zeros((max_steps, H), dtype=torch.bfloat16, device="cuda")
+    n, _ = ctx.sample_latents(models["lm_model"], models["cfm"], models["agg"], flow.lin_w("stop_head"), bias_d,
+                              dev_u16(emb), cache.kv, bank, ming.SampleParams(max_steps, 2.0, 0.25, 0.0), lats,
+                              z_trace=ztr)
+    assert n == max_steps
+    return host_u16(ztr)
+
+
+def test_prompt_prefill_batched_on_empty_cache(ming, ctx, models):
+    """A 70-row prompt on an empty cache is one batched prefill (a 64-row and a
+    6-row chunk over two pages): the cache rows and z_0 equal ming_lm_prefill's
+    own pages and last hidden row bit for bit, and z_0 and the cached rows
+    agree with the oracle's one-row-at-a-time prefill."""
+    ming, S = mods()
+    spec = models["spec"]
+    H, L = spec.hidden, 70
+    print(f"[sample_latents] batched prompt prefill L={L}", flush=True)
+    emb = ming.synth_normal_bf16(72, "loop.embeds.long", L * H, 0.0, 0.5).reshape(L, H)
+    cache = S.KvCache(spec, L + 4)
+    g_z = run_loop(ctx, models, emb, cache)
+    assert cache.len == L
+    gk, gv = cache.host()
+    b = ming.LmBatch(models["lm_model"], 64, 128)
+    pk = S.PagedKv(spec, 1, 2, spare=3, seed=8)
+    hid = torch.empty((L, H), dtype=torch.bfloat16, device="cuda")
+    b.prefill(pk, pk.table[0].contiguous(), 0, x_in=dev_u16(emb), hidden=hid)
+    ctx.sync()
+    pk_k, pk_v = pk.gather(0, L)
+    assert np.array_equal(gk[:, :, :L], pk_k) and np.array_equal(gv[:, :, :L], pk_v), "cache rows differ from prefill"
+    assert np.array_equal(g_z[0], host_u16(hid[L - 1])), "z_0 differs from the prefill's last hidden row"
+    b.close()
+    cfg, layers, norm, head = models["olm"]
+    kc = np.zeros((spec.n_layers, spec.kv_heads, L + 4, spec.head_dim), np.uint16)
+    vc = np.zeros_like(kc)
+    for i in range(L):
+        _, z_ref, _, _, _ = oracle_step(cfg, layers, norm, head, emb[i], i, kc, vc)
+    assert_close_bf16(g_z[0], z_ref, "z_0 (batched prefill)")
+    assert_close_bf16(gk[:, :, :L], kc[:, :, :L], "cached k")
+    assert_close_bf16(gv[:, :, :L], vc[:, :, :L], "cached v")
+
+
+def test_prompt_prefill_row_by_row_on_filled_cache(ming, ctx, models):
+    """A cache that already holds rows takes the prompt one decode step per row:
+    z_0 against the oracle over the same cached rows."""
+    ming, S = mods()
+    spec = models["spec"]
+    H, L, pre = spec.hidden, 3, 9
+    print(f"[sample_latents] row-by-row prompt prefill after {pre} cached rows", flush=True)
+    emb = ming.synth_normal_bf16(73, "loop.embeds.cont", L * H, 0.0, 0.5).reshape(L, H)
+    cache = S.KvCache(spec, pre + L + 4)
+    cache.fill_random(pre, seed=21)
+    kc, vc = (a.copy() for a in cache.host())
+    g_z = run_loop(ctx, models, emb, cache)
+    assert cache.len == pre + L
+    cfg, layers, norm, head = models["olm"]
+    for i in range(L):
+        _, z_ref, _, _, _ = oracle_step(cfg, layers, norm, head, emb[i], pre + i, kc, vc)
+    assert_close_bf16(g_z[0], z_ref, "z_0 (row-by-row prefill)")
