@@ -167,6 +167,35 @@ def test_lm_step_matches_oracle(ming, ctx, q4_model, ctx_len, mode):
           f"max|dlogit| {dl:.3e}", flush=True)
 
 
+@pytest.fixture(scope="module")
+def bf16_model(ming, ctx):
+    S = syn_mod(ming)
+    print("[lm] building 4-layer bf16 model at the Qwen2-0.5B layer shape", flush=True)
+    syn = S.SyntheticLm(ctx, S.LmSpec(n_layers=4, vocab=8192), seed=12, quant=False)
+    m = syn.model()
+    yield syn, m, oracle_model(syn)
+    m.close()
+
+
+@pytest.mark.parametrize("mode", ["kernels", "persistent", "direct"])
+def test_bf16_lm_step_matches_oracle(ming, ctx, bf16_model, mode):
+    """bf16 weights (the persistent kernel's second instance, plain bf16 rows
+    instead of 4-bit chunks) at hidden 896, 14/2 heads, inter 4864, vocab
+    8192, ctx 700: every layer teacher forced, head, logits and argmax."""
+    S = syn_mod(ming)
+    syn, m, orc = bf16_model
+    print(f"[lm_step bf16] mode={mode}", flush=True)
+    cache = S.KvCache(syn.spec, 704)
+    cache.fill_random(700, seed=70)
+    before = cache.host()
+    am, hid, lg = run_step(ming, syn, m, cache, 4321, getattr(ming, MODES[mode]))
+    assert cache.len == 701
+    worst, dl, ram, margin = check_step_teacher_forced(ming, m, before, cache.host(), orc, 700, 4321, am, hid, lg,
+                                                       f"bf16 {mode}")
+    print(f"[lm_step bf16] {mode} argmax {am} ref {ram} margin {margin:.3e} worst layer max|d| {worst:.3e} "
+          f"max|dlogit| {dl:.3e}", flush=True)
+
+
 def test_schedules_agree_and_deterministic(ming, ctx, q4_model):
     """Each schedule is bit-for-bit reproducible; the persistent kernel gives
     the same bits with and without per-XCD hubs (the stage images are built by
