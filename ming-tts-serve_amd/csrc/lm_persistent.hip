@@ -1033,13 +1033,15 @@ __global__ __launch_bounds__(kT) void decode_tagged_kernel(StepArgs args, const 
 
 }  // namespace
 
-// Positions per attention split on this schedule: a multiple of the 64-row
-// tile, doubled until a kv head has at most 64 splits (each split is one
-// workgroup; the last one to finish merges them, one split per lane).
+// Positions per attention split on this schedule: the fewest whole 64-row
+// tiles (at most 16) that leave a kv head at most 64 splits (each split is
+// one workgroup; the last one to finish merges them, one split per lane).
+// A split's tiles run one after another, so fewer tiles per split is a
+// shorter chain: ctx 8192 takes 43 splits of 3 tiles, ctx 16384 52 of 5.
 int tagged_split_len(int n) {
-    int sl = kTile;
-    while ((n + sl - 1) / sl > 64 && sl < 16 * kTile) sl *= 2;
-    return sl;
+    const int tiles = (n + kTile - 1) / kTile;
+    const int per = (tiles + 63) / 64;
+    return (per < 1 ? 1 : per > 16 ? 16 : per) * kTile;
 }
 
 // Hubs for a grid of `grid` workgroups: one per XCD when the grid is large
