@@ -149,7 +149,7 @@ MODES = {"kernels": "LM_KERNELS", "persistent": "LM_PERSISTENT", "direct": "LM_P
 
 
 @pytest.mark.parametrize("mode", ["kernels", "persistent", "direct"])
-@pytest.mark.parametrize("ctx_len", [512, 2048, 8192])
+@pytest.mark.parametrize("ctx_len", [512, 2048, 8192, 16384])
 def test_lm_step_matches_oracle(ming, ctx, q4_model, ctx_len, mode):
     S = syn_mod(ming)
     syn, m, orc = q4_model
