@@ -276,6 +276,36 @@ __global__ __launch_bounds__(256) void vreduce_kernel(VGemm g) {
 }
 
 // fast::rms_norm of f32 rows with a bf16 weight: w * (x * rsqrt(mean(x^2) + eps)); one wave per row.
+// Rows of K <= 1024, a multiple of 4: the row is read once, as up to four 16-byte chunks per lane held
+// in registers, so its loads are all in flight together.
+__global__ __launch_bounds__(256) void vrms4_kernel(const float* x, int M, int K, const uint16_t* w, float eps,
+                                                    float* out) {
+    const int row = blockIdx.x * 4 + threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    if (row >= M) return;
+    const float4* xr = reinterpret_cast<const float4*>(x + (size_t)row * K);
+    const int n4 = K / 4;
+    float4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int c = lane + kWave * j;
+        v[j] = c < n4 ? xr[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) ss += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+    ss = team_sum<kWave>(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)K + eps);
+    float4* o = reinterpret_cast<float4*>(out + (size_t)row * K);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int c = lane + kWave * j;
+        if (c < n4)
+            o[c] = make_float4(bf2f(gld(w + 4 * c)) * (v[j].x * inv), bf2f(gld(w + 4 * c + 1)) * (v[j].y * inv),
+                               bf2f(gld(w + 4 * c + 2)) * (v[j].z * inv), bf2f(gld(w + 4 * c + 3)) * (v[j].w * inv));
+    }
+}
+
+// Any K: two passes over the row, 4-byte accesses.
 __global__ __launch_bounds__(256) void vrms_kernel(const float* x, int M, int K, const uint16_t* w, float eps,
                                                    float* out) {
     const int row = blockIdx.x * 4 + threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -314,10 +344,16 @@ __global__ __launch_bounds__(256) void vattn_kernel(const float* qkv, int M, int
     const float e = lane < n ? expf(s - m) : 0.0f;
     const float l = team_sum<kWave>(e);
     const float* vb = qkv + H + kvh * 64 + kh * 64 + lane;  // v of kv head kh, dim = lane
+    // a fixed 64 steps, fully unrolled, so every row load is issued up front; rows past the
+    // window reload row i and carry probability 0 (lane jj >= n has e = 0), adding nothing
+    float vj[64];
+#pragma unroll
+    for (int jj = 0; jj < 64; jj++) vj[jj] = vb[(size_t)min(j0 + jj, i) * ldq];
     float o = 0.0f;
-    for (int jj = 0; jj < n; jj++) {
+#pragma unroll
+    for (int jj = 0; jj < 64; jj++) {
         const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), jj));
-        o = fmaf(pj, vb[(size_t)(j0 + jj) * ldq], o);
+        o = fmaf(pj, vj[jj], o);
     }
     att[(size_t)i * H + h * 64 + lane] = o / l;
 }
@@ -441,7 +477,12 @@ hipError_t launch_vgemm(hipStream_t st, const VGemm& g, int wf, int epi) {
 }
 
 hipError_t launch_vrms(hipStream_t st, const float* x, int M, int K, const uint16_t* w, float eps, float* out) {
-    hipLaunchKernelGGL(vrms_kernel, dim3((M + 3) / 4), dim3(256), 0, st, x, M, K, w, eps, out);
+    const bool v4 = K % 4 == 0 && K <= 4 * 4 * kWave && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    if (v4)
+        hipLaunchKernelGGL(vrms4_kernel, dim3((M + 3) / 4), dim3(256), 0, st, x, M, K, w, eps, out);
+    else
+        hipLaunchKernelGGL(vrms_kernel, dim3((M + 3) / 4), dim3(256), 0, st, x, M, K, w, eps, out);
     return hipGetLastError();
 }
 
