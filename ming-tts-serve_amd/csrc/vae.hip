@@ -358,6 +358,50 @@ __global__ __launch_bounds__(256) void vattn_kernel(const float* qkv, int M, int
     att[(size_t)i * H + h * 64 + lane] = o / l;
 }
 
+// The same attention with the window's K and V rows of one kv head staged in
+// LDS once for the q heads that share them: one workgroup per (row i, kv
+// head), wave w = q head kh * grp + w; the arithmetic (and its order) is the
+// one-wave-per-head kernel's.  K rows are padded to 68 floats so the lanes'
+// 16-byte reads of 64 different rows spread over the banks.
+constexpr int kVKs = 68;
+__global__ __launch_bounds__(1024) void vattn_gqa_kernel(const float* qkv, int M, int ldq, int H, int heads, int kvh,
+                                                         int window, float scale, float* att) {
+    __shared__ __align__(16) float ks[64 * kVKs];
+    __shared__ __align__(16) float vs[64 * 64];
+    const int i = blockIdx.x / kvh, kh = blockIdx.x % kvh, grp = heads / kvh;
+    const int j0 = max(0, i - window + 1), n = i - j0 + 1;
+    for (int f = threadIdx.x; f < 64 * 16; f += blockDim.x) {
+        const int r = f / 16, c4 = f % 16;
+        const float* base = qkv + (size_t)min(j0 + r, i) * ldq + H + kh * 64 + 4 * c4;
+        *reinterpret_cast<float4*>(ks + r * kVKs + 4 * c4) = *reinterpret_cast<const float4*>(base);
+        *reinterpret_cast<float4*>(vs + r * 64 + 4 * c4) = *reinterpret_cast<const float4*>(base + kvh * 64);
+    }
+    __syncthreads();
+    const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave, h = kh * grp + w;
+    const float* q = qkv + (size_t)i * ldq + h * 64;
+    const float* kr = ks + lane * kVKs;
+    float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int d = 0; d < 64; d += 4) {
+        const float4 qa = *reinterpret_cast<const float4*>(q + d), ka = *reinterpret_cast<const float4*>(kr + d);
+        p[0] = fmaf(qa.x, ka.x, p[0]);
+        p[1] = fmaf(qa.y, ka.y, p[1]);
+        p[2] = fmaf(qa.z, ka.z, p[2]);
+        p[3] = fmaf(qa.w, ka.w, p[3]);
+    }
+    const float s = lane < n ? ((p[0] + p[1]) + (p[2] + p[3])) * scale : -INFINITY;
+    const float m = team_max<kWave>(s);
+    const float e = lane < n ? expf(s - m) : 0.0f;
+    const float l = team_sum<kWave>(e);
+    float o = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < 64; jj++) {
+        const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), jj));
+        o = fmaf(pj, vs[jj * 64 + lane], o);
+    }
+    att[(size_t)i * H + h * 64 + lane] = o / l;
+}
+
 // Decoder._linear_upsample_1d (align_corners=False, f32) of the fc1 rows,
 // which the graph materialises in bf16 first: y [T][C] f32 accumulators of
 // fc1 -> x [T * scale][C].  The fc1 row is bf16(acc + bias) for bf16
@@ -488,9 +532,14 @@ hipError_t launch_vrms(hipStream_t st, const float* x, int M, int K, const uint1
 
 hipError_t launch_vattn(hipStream_t st, const float* qkv, int M, int ldq, int H, int heads, int kvh, int window,
                         float scale, float* att) {
-    if (window < 1 || window > 64) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(vattn_kernel, dim3((M * heads + 3) / 4), dim3(256), 0, st, qkv, M, ldq, H, heads, kvh, window,
-                       scale, att);
+    if (window < 1 || window > 64 || kvh < 1 || heads % kvh) return hipErrorInvalidValue;
+    const int grp = heads / kvh;
+    if (grp <= 16)
+        hipLaunchKernelGGL(vattn_gqa_kernel, dim3(M * kvh), dim3(64 * grp), 0, st, qkv, M, ldq, H, heads, kvh, window,
+                           scale, att);
+    else
+        hipLaunchKernelGGL(vattn_kernel, dim3((M * heads + 3) / 4), dim3(256), 0, st, qkv, M, ldq, H, heads, kvh,
+                           window, scale, att);
     return hipGetLastError();
 }
 
