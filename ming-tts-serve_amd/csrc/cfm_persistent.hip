@@ -235,10 +235,10 @@ __device__ __forceinline__ void dots6(const uint4 (&wr)[NU][NCH], const uint32_t
         for (int r = 0; r < kPR; r++) {
 #pragma unroll
             for (int u = 0; u < NU; u++) {
-                float s = dot2(wr[u][j].x, x[r].x, acc[u][r]);
-                s = dot2(wr[u][j].y, x[r].y, s);
-                s = dot2(wr[u][j].z, x[r].z, s);
-                acc[u][r] = dot2(wr[u][j].w, x[r].w, s);
+                float s = fma_bf2(wr[u][j].x, x[r].x, acc[u][r]);
+                s = fma_bf2(wr[u][j].y, x[r].y, s);
+                s = fma_bf2(wr[u][j].z, x[r].z, s);
+                acc[u][r] = fma_bf2(wr[u][j].w, x[r].w, s);
             }
         }
     }
@@ -258,7 +258,7 @@ __device__ __forceinline__ float pick6(const float (&acc)[kPR], int tl) {
 
 // Attention of one (CFG half, head) task as the launch path's attention
 // kernel computes it: lane d owns dimension d; scores sum_d (q/8) k over the
-// wave, p = exp(s - max), o = sum_j p_j v_j / sum_j p_j (rounded by the caller).
+// wave, p = exp_rep(s - max), o = sum_j p_j v_j / sum_j p_j (rounded by the caller).
 __device__ __forceinline__ void attn_math(const float (&qv)[kPL], const float (&kv)[kPL], const float (&vv)[kPL],
                                           float (&r)[kPL]) {
     const float scale = 1.0f / 8.0f;
@@ -274,7 +274,7 @@ __device__ __forceinline__ void attn_math(const float (&qv)[kPL], const float (&
         float l = 0.0f, o = 0.0f;
 #pragma unroll
         for (int jj = 0; jj < kPL; jj++) {
-            const float p = expf(sc[jj] - m);
+            const float p = exp_rep(sc[jj] - m);
             l += p;
             o += p * vv[jj];
         }
@@ -711,10 +711,10 @@ __device__ __forceinline__ void head_step(const CfmPArgs& a, uint32_t* lds, int 
 #pragma unroll
                 for (int r = 0; r < 2; r++) {
                     const u32x4_t xv = xr[r][jj];
-                    float sacc = dot2(wf[j][jj].x, xv.x, acc[r]);
-                    sacc = dot2(wf[j][jj].y, xv.y, sacc);
-                    sacc = dot2(wf[j][jj].z, xv.z, sacc);
-                    acc[r] = dot2(wf[j][jj].w, xv.w, sacc);
+                    float sacc = fma_bf2(wf[j][jj].x, xv.x, acc[r]);
+                    sacc = fma_bf2(wf[j][jj].y, xv.y, sacc);
+                    sacc = fma_bf2(wf[j][jj].z, xv.z, sacc);
+                    acc[r] = fma_bf2(wf[j][jj].w, xv.w, sacc);
                 }
             }
             acc[0] = team_sum<32>(acc[0]);
@@ -751,10 +751,10 @@ __device__ __forceinline__ void head_step(const CfmPArgs& a, uint32_t* lds, int 
         for (int j = 0; j < 16; j++) {
             const int n = 64 * j + 8 * wave + tm;
             const u32x4_t wv = wvs[j];
-            float acc = dot2(wv.x, yv.x, 0.0f);
-            acc = dot2(wv.y, yv.y, acc);
-            acc = dot2(wv.z, yv.z, acc);
-            acc = dot2(wv.w, yv.w, acc);
+            float acc = fma_bf2(wv.x, yv.x, 0.0f);
+            acc = fma_bf2(wv.y, yv.y, acc);
+            acc = fma_bf2(wv.z, yv.z, acc);
+            acc = fma_bf2(wv.w, yv.w, acc);
             acc = team_sum<8>(acc);
             acc = (acc + 0.0f) + 0.0f;
             if (t8 == 0) xe16[n] = f2bf(rb(acc + bf2f(bx16[n])));

@@ -34,10 +34,47 @@ __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 
+// e^x for the flow head's softmax and sigmoids, built only from correctly
+// rounded f32 operations (multiply, rint, fma, ldexp), so that a CPU that
+// evaluates the same steps gets the same bits: Cody-Waite reduction
+// x = n ln2 + r with ln2 split into a 15-bit head and its f32 tail (|r| <=
+// ln2/2 + a few ulps), the degree-7 Taylor polynomial of e^r in Horner form
+// (truncation below 2^-27 relative) and an exact scaling by 2^n.  Measured
+// against double exp over [-86, 88]: at most 0.92 ulp.  Below -86 the result
+// is 0 (e^-86 < 2^-124; the scaled polynomial would reach denormals), above 88
+// +inf; NaN stays NaN.
+__device__ __forceinline__ float exp_rep(float x) {
+    if (x < -86.0f) return 0.0f;
+    if (x > 88.0f) return __builtin_inff();
+    const float n = __builtin_rintf(x * 0x1.715476p+0f);
+    float r = __builtin_fmaf(n, -0x1.62e4p-1f, x);
+    r = __builtin_fmaf(n, -0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;              // 1/7!
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);  // 1/6!
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);   // 1/5!
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);   // 1/4!
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);   // 1/3!
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return __builtin_ldexpf(p, (int)n);
+}
+
 // acc + a.lo*b.lo + a.hi*b.hi with bf16 pairs packed in u32 (v_dot2c_f32_bf16).
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), acc,
                                            false);
+}
+
+// acc + a.lo*b.lo, then + a.hi*b.hi, as two IEEE fused multiply-adds.  A
+// product of two bf16 values is exact in f32, so each step is one correctly
+// rounded addition and a CPU reproduces the result bit for bit from the same
+// order.  (v_dot2c_f32_bf16 above is cheaper, but its internal rounding is not
+// an IEEE sequence: measured on the device it differs from every sequential
+// and single-rounding model in a few results per thousand.)
+__device__ __forceinline__ float fma_bf2(uint32_t a, uint32_t b, float acc) {
+    acc = __builtin_fmaf(bf_lo(a), bf_lo(b), acc);
+    return __builtin_fmaf(bf_hi(a), bf_hi(b), acc);
 }
 
 // ---- MLX affine 4-bit unpack ------------------------------------------------

@@ -326,10 +326,10 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
         const u32x4_t(&x)[RC] = xv[j % NB];
 #pragma unroll
         for (int r = 0; r < RC; r++) {
-            float s = dot2(wr[j].x, x[r].x, acc[r]);
-            s = dot2(wr[j].y, x[r].y, s);
-            s = dot2(wr[j].z, x[r].z, s);
-            acc[r] = dot2(wr[j].w, x[r].w, s);
+            float s = fma_bf2(wr[j].x, x[r].x, acc[r]);
+            s = fma_bf2(wr[j].y, x[r].y, s);
+            s = fma_bf2(wr[j].z, x[r].z, s);
+            acc[r] = fma_bf2(wr[j].w, x[r].w, s);
         }
     }
 #pragma unroll
@@ -386,7 +386,7 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
         const float x = rb(v + ep.b);
         const float x1 = __shfl(x, lane ^ 32, kWave);
         if (blockIdx.x != 0 || wave != 0 || lane != 0) return;
-        const float m = fmaxf(x, x1), e0 = expf(x - m), e1 = expf(x1 - m);
+        const float m = fmaxf(x, x1), e0 = exp_rep(x - m), e1 = exp_rep(x1 - m);
         gst(a.p_out, e1 / (e0 + e1));
         return;
     }
@@ -405,7 +405,7 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
     } else if (E == E_GELU) {
         gst(a.out + r * a.ostride + n, f2bf(gelu_chain(e)));
     } else if (E == E_SILU) {
-        gst(a.out + r * a.ostride + n, f2bf(e * rb(1.0f / (1.0f + expf(-e)))));
+        gst(a.out + r * a.ostride + n, f2bf(e * rb(1.0f / (1.0f + exp_rep(-e)))));
     } else if (E == E_CFMROWS) {
         // rows [t_emb + c_emb, x_emb(hist), x_emb(y)] of both CFG halves
         const uint16_t xe = f2bf(e);
@@ -425,14 +425,14 @@ __global__ __launch_bounds__(256) void adaln_cond_kernel(const uint16_t* te, con
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= steps * 2 * D) return;
     const float v = rb(bf2f(gld(te + i)) + bf2f(gld(ce + i % (2 * D))));
-    const float sg = rb(1.0f / (1.0f + expf(-v)));
+    const float sg = rb(1.0f / (1.0f + exp_rep(-v)));
     gst(out + i, f2bf(v * sg));
 }
 
 // Attention over the L positions of each sequence, one wave per (sequence,
 // head), lane d owning dimension d (lanes past head_dim add zeros): every
 // q/k/v load is issued first; scores sum_d (q/8) k in f32 (wave sums),
-// p = exp(s - max), l = sum p, o = (sum_j p_j v_j) / l rounded once.
+// p = exp_rep(s - max), l = sum p, o = (sum_j p_j v_j) / l rounded once.
 __global__ __launch_bounds__(kWave) void dit_attn_kernel(const uint16_t* qkv, int R, int L, int D, int heads,
                                                          int hd, uint16_t* att) {
     const int b = blockIdx.x / heads, h = blockIdx.x % heads, d = threadIdx.x, dd = min(d, hd - 1);
@@ -464,7 +464,7 @@ __global__ __launch_bounds__(kWave) void dit_attn_kernel(const uint16_t* qkv, in
 #pragma unroll
             for (int j = 0; j < kMaxL; j++)
                 if (j < L) {
-                    const float p = expf(sc[j] - m);
+                    const float p = exp_rep(sc[j] - m);
                     l += p;
                     o += p * vv[j];
                 }

@@ -146,6 +146,21 @@ typedef struct {
     uint16_t* hh;   /* [R][ff] gelu_approx(ff1(rms(x1))) */
 } or_dit_trace;
 
+/* Summation order of every DiT function below (blocks, flow head, aggregator, stop head,
+ * adaLN head): OR_DIT_ORDER_MLX (default) sums dot products over 8 interleaved f32 partials and
+ * uses libm expf; OR_DIT_ORDER_DEVICE takes each f32 sum in the order of the library's batch-1
+ * DiT kernels (team lanes over 16-byte chunks, fused multiply-adds in element order, the pairwise
+ * lane tree, wave sums in order) and e^x by or_exp_rep, with the same graph and rounding points. */
+enum { OR_DIT_ORDER_MLX = 0, OR_DIT_ORDER_DEVICE = 1 };
+void or_set_dit_order(int mode);
+int or_get_dit_order(void);
+/* e^x from correctly rounded f32 steps (Cody-Waite reduction, degree-7 Taylor, 2^n scaling). */
+float or_exp_rep(float x);
+/* One dot product of bf16 w, x [K] in the device order with a team of T (32 or 64) lanes. */
+float or_dot_dev(const uint16_t* w, const uint16_t* x, int64_t K, int T);
+/* Sum of squares of x [K] (K <= 1024) in the device order. */
+float or_sumsq_dev(const uint16_t* x, int64_t K);
+
 /* x_transformers RotaryEmbedding table: cos/sin[l][i] = cos/sin(l * inv_freq[i]) in f32. */
 void or_rotary_table(const float* inv_freq, int half, int L, float* cos_t, float* sin_t);
 /* Interleaved-pair rotary (2i, 2i+1) of every head of the R = B*L rows of x [R][heads*hd]

@@ -158,6 +158,11 @@ def lib():
         "or_vae_layer": (None, [P(OrVaeCfg), P(OrLmLayer), c_void_p, c_int, c_void_p, P(OrVaeTrace)]),
         "or_vae_istft": (None, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
         "or_vae_decode": (None, [P(OrVaeModel), c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
+        "or_set_dit_order": (None, [c_int]),
+        "or_get_dit_order": (c_int, []),
+        "or_exp_rep": (c_f32, [c_f32]),
+        "or_dot_dev": (c_f32, [c_void_p, c_void_p, c_i64, c_int]),
+        "or_sumsq_dev": (c_f32, [c_void_p, c_i64]),
         "or_set_threads": (None, [c_int]),
         "or_get_threads": (c_int, []),
     }
@@ -352,6 +357,45 @@ def embed(table, idx):
 
 def set_threads(n):
     lib().or_set_threads(int(n))
+
+
+DIT_ORDER_MLX, DIT_ORDER_DEVICE = 0, 1
+
+
+class dit_order:
+    """Context manager: the DiT functions (blocks, flow head, aggregator, stop head, adaLN head)
+    sum in `mode` inside the block -- DIT_ORDER_DEVICE follows the library's batch-1 DiT kernels
+    (team lanes over 16-byte chunks, fused multiply-adds in element order, pairwise lane trees,
+    exp_rep)."""
+
+    def __init__(self, mode):
+        self.mode = int(mode)
+
+    def __enter__(self):
+        self.prev = lib().or_get_dit_order()
+        lib().or_set_dit_order(self.mode)
+        return self
+
+    def __exit__(self, *exc):
+        lib().or_set_dit_order(self.prev)
+        return False
+
+
+def exp_rep(x):
+    return float(lib().or_exp_rep(float(x)))
+
+
+def dot_dev(w, x, team):
+    w = np.ascontiguousarray(w, np.uint16)
+    x = np.ascontiguousarray(x, np.uint16)
+    assert w.shape == x.shape and w.size % 8 == 0
+    return float(lib().or_dot_dev(_p(w), _p(x), w.size, int(team)))
+
+
+def sumsq_dev(x):
+    x = np.ascontiguousarray(x, np.uint16)
+    assert x.size % 8 == 0 and x.size <= 1024
+    return float(lib().or_sumsq_dev(_p(x), x.size))
 
 
 def get_threads():

@@ -23,6 +23,125 @@
 
 static float sum8(const float* p) { return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])); }
 
+/* ---- summation order ------------------------------------------------------------------
+ * Mode 0 (default): the MLX restatement above and below -- dot products over 8 interleaved
+ * f32 partials, libm expf.  Mode 1 (OR_DIT_ORDER_DEVICE): the same graph and rounding points,
+ * but every f32 sum taken in the order of the library's batch-1 DiT kernels
+ * (ming-tts-serve_amd/csrc/dit.hip: dit_gemv_kernel, stage_rows, dit_attn_kernel; the
+ * persistent flow head keeps the same orders) and e^x by the library's exp_rep steps, so that
+ * the free-running flow head can be compared bit for bit.  Only the order differs between the
+ * modes: each mode's f32 sums are the exact sums up to f32 rounding. */
+static int g_dit_order = 0;
+
+void or_set_dit_order(int mode) { g_dit_order = mode; }
+int or_get_dit_order(void) { return g_dit_order; }
+
+/* e^x from correctly rounded f32 steps (the device's exp_rep, csrc/common.h): Cody-Waite
+ * reduction with a 15-bit ln2 head and its f32 tail, degree-7 Taylor polynomial of e^r
+ * (coefficients 1/k! rounded to f32) in Horner form with fused multiply-adds, exact scaling
+ * by 2^n; 0 below -86, +inf above 88. */
+float or_exp_rep(float x) {
+    if (x < -86.0f) return 0.0f;
+    if (x > 88.0f) return INFINITY;
+    const float n = rintf(x * 0x1.715476p+0f);
+    float r = fmaf(n, -0x1.62e4p-1f, x);
+    r = fmaf(n, -0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;
+    p = fmaf(p, r, 0x1.6c16c2p-10f);
+    p = fmaf(p, r, 0x1.111112p-7f);
+    p = fmaf(p, r, 0x1.555556p-5f);
+    p = fmaf(p, r, 0x1.555556p-3f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)n);
+}
+
+static float dit_exp(float x) { return g_dit_order ? or_exp_rep(x) : expf(x); }
+
+/* Balanced pairwise sum of n = 2^k lane values in lane order (the DPP / permlane butterfly
+ * of csrc/common.h team_sum: lane i meets i^1, then pairs meet pairs, ...).  v is clobbered. */
+static float tree_sum(float* v, int n) {
+    for (int s = 1; s < n; s *= 2)
+        for (int i = 0; i + s < n; i += 2 * s) v[i] = v[i] + v[i + s];
+    return v[0];
+}
+
+/* One output of dit_gemv_kernel: a team of T lanes (64 for rows longer than 1024 without a
+ * paired epilogue, else 32) walks the row in 16-byte chunks of 8 weights, lane l taking chunks
+ * l, l + T, l + 2T, ...; within a chunk the 8 products enter the lane's accumulator in order
+ * through IEEE fused multiply-adds (a product of two bf16 values is exact in f32, so each step
+ * is acc = RN(w_k x_k + acc)); the T lane sums meet in the pairwise tree.  K % 8 == 0. */
+float or_dot_dev(const uint16_t* w, const uint16_t* x, int64_t K, int T) {
+    float lane[64];
+    const int64_t NC = K / 8;
+    for (int l = 0; l < T; l++) {
+        float acc = 0.0f;
+        for (int64_t c = l; c < NC; c += T)
+            for (int e = 0; e < 8; e++) {
+                const int64_t k = 8 * c + e;
+                acc = or_f32(w[k]) * or_f32(x[k]) + acc;
+            }
+        lane[l] = acc;
+    }
+    return tree_sum(lane, T);
+}
+
+/* A DiT linear (bf16 weights, addmm bias) in the selected order; `paired`: the q/k/v, stop and
+ * frame-CFG epilogues, which keep 32-lane teams at any K. */
+static void dit_linear(const or_linear* L, const uint16_t* x, int64_t M, const uint16_t* bias, uint16_t* y,
+                       int paired) {
+    if (!g_dit_order || L->kind != OR_W_BF16) {
+        or_linear_fwd(L, x, M, bias, y);
+        return;
+    }
+    const int64_t N = L->N, K = L->K;
+    const int T = (!paired && K > 1024) ? 64 : 32;
+    const uint16_t* W = (const uint16_t*)L->w;
+    for (int64_t m = 0; m < M; m++) {
+#pragma omp parallel for schedule(static)
+        for (int64_t n = 0; n < N; n++) {
+            const float a = or_dot_dev(W + n * K, x + m * K, K, T);
+            y[m * N + n] = or_bf16(bias ? a + or_f32(bias[n]) : a);
+        }
+    }
+}
+
+/* Sum of squares of a row of K <= 1024 values as stage_rows (and the persistent head's image
+ * builders) take it: thread t holds chunk t (8 values, squares added in order), each wave's 64
+ * threads meet in the pairwise tree, and the wave sums are added in wave order from 0. */
+float or_sumsq_dev(const uint16_t* x, int64_t K) {
+    const int64_t NC = K / 8;
+    float s = 0.0f;
+    for (int64_t w0 = 0; w0 < NC; w0 += 64) {
+        float lane[64];
+        for (int l = 0; l < 64; l++) {
+            float ss = 0.0f;
+            const int64_t c = w0 + l;
+            if (c < NC)
+                for (int e = 0; e < 8; e++) {
+                    const float v = or_f32(x[8 * c + e]);
+                    ss = ss + v * v;
+                }
+            lane[l] = ss;
+        }
+        s = s + tree_sum(lane, 64);
+    }
+    return s;
+}
+
+static void dit_rms(const uint16_t* x, const uint16_t* w, int64_t M, int64_t n, float eps, uint16_t* out) {
+    if (!g_dit_order || n > 1024 || n % 8) {
+        or_rms_norm(x, w, M, n, eps, out);
+        return;
+    }
+    for (int64_t m = 0; m < M; m++) {
+        const uint16_t* xr = x + m * n;
+        const float inv = 1.0f / sqrtf(or_sumsq_dev(xr, n) / (float)n + eps);
+        for (int64_t i = 0; i < n; i++) out[m * n + i] = or_bf16(or_f32(w[i]) * or_rb(or_f32(xr[i]) * inv));
+    }
+}
+
 /* Rotary.table (:688-696): pos = arange(L) in inv_freq's dtype (f32), outer product, cos/sin in f32. */
 void or_rotary_table(const float* inv_freq, int half, int L, float* cos_t, float* sin_t) {
     for (int l = 0; l < L; l++)
@@ -57,6 +176,36 @@ void or_rotary(uint16_t* x, int R, int L, int heads, int hd, const float* cos_t,
 static void sdpa_small(const uint16_t* q, const uint16_t* k, const uint16_t* v, int B, int L, int heads, int hd,
                        float scale, uint16_t* out) {
     const int D = heads * hd;
+    if (g_dit_order && hd <= 64) {
+        /* dit_attn_kernel: lane d holds dimension d; a score is the pairwise tree over the 64
+         * lanes of (scale q_d) k_d (lanes past head_dim add 0); p_j = exp_rep(s_j - max); l and
+         * o add over j in order from 0; o / l rounded once */
+        for (int b = 0; b < B; b++)
+            for (int h = 0; h < heads; h++)
+                for (int i = 0; i < L; i++) {
+                    const uint16_t* qr = q + ((int64_t)(b * L + i)) * D + h * hd;
+                    float sc[8], m = -INFINITY;
+                    for (int j = 0; j < L; j++) {
+                        const uint16_t* kr = k + ((int64_t)(b * L + j)) * D + h * hd;
+                        float lane[64];
+                        for (int d = 0; d < 64; d++)
+                            lane[d] = d < hd ? (scale * or_f32(qr[d])) * or_f32(kr[d]) : 0.0f;
+                        sc[j] = tree_sum(lane, 64);
+                        m = fmaxf(m, sc[j]);
+                    }
+                    float p[8];
+                    for (int j = 0; j < L; j++) p[j] = or_exp_rep(sc[j] - m);
+                    for (int d = 0; d < hd; d++) {
+                        float l = 0.0f, o = 0.0f;
+                        for (int j = 0; j < L; j++) {
+                            l = l + p[j];
+                            o = o + p[j] * or_f32(v[((int64_t)(b * L + j)) * D + h * hd + d]);
+                        }
+                        out[((int64_t)(b * L + i)) * D + h * hd + d] = or_bf16(o / l);
+                    }
+                }
+        return;
+    }
     for (int b = 0; b < B; b++)
         for (int h = 0; h < heads; h++)
             for (int i = 0; i < L; i++) {
@@ -119,24 +268,24 @@ static void block_fwd(const or_dit_cfg* c, const or_dit_block* b, const uint16_t
     uint16_t* x1 = malloc(sizeof(uint16_t) * (size_t)R * D);
     uint16_t* f1 = malloc(sizeof(uint16_t) * (size_t)R * F);
     uint16_t* hh = malloc(sizeof(uint16_t) * (size_t)R * F);
-    or_rms_norm(x, b->norm1, R, D, c->eps, h);
+    dit_rms(x, b->norm1, R, D, c->eps, h);
     if (mod) modulate(h, R, L, D, mod, 6 * D, 0, 1);
-    or_linear_fwd(&b->q, h, R, b->bq, qkv);
-    or_linear_fwd(&b->k, h, R, b->bk, qkv + (size_t)R * D);
-    or_linear_fwd(&b->v, h, R, b->bv, qkv + (size_t)2 * R * D);
+    dit_linear(&b->q, h, R, b->bq, qkv, 1);
+    dit_linear(&b->k, h, R, b->bk, qkv + (size_t)R * D, 1);
+    dit_linear(&b->v, h, R, b->bv, qkv + (size_t)2 * R * D, 1);
     or_rotary(qkv, R, L, c->heads, c->head_dim, cos_t, sin_t);
     or_rotary(qkv + (size_t)R * D, R, L, c->heads, c->head_dim, cos_t, sin_t);
     sdpa_small(qkv, qkv + (size_t)R * D, qkv + (size_t)2 * R * D, B, L, c->heads, c->head_dim, 1.0f / 8.0f, att);
-    or_linear_fwd(&b->o, att, R, b->bo, t1);
+    dit_linear(&b->o, att, R, b->bo, t1, 0);
     if (mod)
         gated_add(x, t1, R, L, D, mod, 6 * D, 2, x1);
     else
         or_add(x, t1, (int64_t)R * D, x1);
-    or_rms_norm(x1, b->norm2, R, D, c->eps, h);
+    dit_rms(x1, b->norm2, R, D, c->eps, h);
     if (mod) modulate(h, R, L, D, mod, 6 * D, 3, 4);
-    or_linear_fwd(&b->ff1, h, R, b->b1, f1);
+    dit_linear(&b->ff1, h, R, b->b1, f1, 0);
     or_gelu_approx(f1, (int64_t)R * F, hh);
-    or_linear_fwd(&b->ff2, hh, R, b->b2, t1);
+    dit_linear(&b->ff2, hh, R, b->b2, t1, 0);
     if (mod)
         gated_add(x1, t1, R, L, D, mod, 6 * D, 5, out);
     else
@@ -207,13 +356,13 @@ void or_timestep_embed(const or_linear* mlp0, const uint16_t* b0, const or_linea
         }
     const int64_t D = mlp0->N;
     uint16_t* te = malloc(sizeof(uint16_t) * 2 * D);
-    or_linear_fwd(mlp0, sc, 2, b0, te);
+    dit_linear(mlp0, sc, 2, b0, te, 0);
     for (int64_t i = 0; i < 2 * D; i++) {  /* silu: x * sigmoid(x), each op rounded */
         const float v = or_f32(te[i]);
-        const float sg = or_rb(1.0f / (1.0f + expf(-v)));
+        const float sg = or_rb(1.0f / (1.0f + dit_exp(-v)));
         te[i] = or_bf16(v * sg);
     }
-    or_linear_fwd(mlp2, te, 2, b2, out);
+    dit_linear(mlp2, te, 2, b2, out, 0);
     free(te);
 }
 
@@ -228,9 +377,9 @@ void or_cfm_rows(const or_cfm_model* m, const uint16_t* z, const uint16_t* hist,
     uint16_t* ce = malloc(sizeof(uint16_t) * 2 * D);
     uint16_t* zc = calloc((size_t)2 * H, sizeof(uint16_t));
     memcpy(zc, z, sizeof(uint16_t) * H);  /* [z, zeros] */
-    or_linear_fwd(&m->x_emb, y, 1, m->bx, xn);
-    or_linear_fwd(&m->x_emb, hist, 1, m->bx, xh);
-    or_linear_fwd(&m->c_emb, zc, 2, m->bc, ce);
+    dit_linear(&m->x_emb, y, 1, m->bx, xn, 0);
+    dit_linear(&m->x_emb, hist, 1, m->bx, xh, 0);
+    dit_linear(&m->c_emb, zc, 2, m->bc, ce, 0);
     const uint16_t* te = m->t_emb + (size_t)step * 2 * D;
     for (int b = 0; b < 2; b++) {
         or_add(te + (size_t)b * D, ce + (size_t)b * D, D, rows + (size_t)(b * 3 + 0) * D);
@@ -253,9 +402,9 @@ void or_cfm_final(const or_cfm_model* m, const uint16_t* h, int L, const uint16_
     uint16_t last[2 * 4096];
     memcpy(last, h + (size_t)(L - 1) * D, sizeof(uint16_t) * D);
     memcpy(last + D, h + (size_t)(2 * L - 1) * D, sizeof(uint16_t) * D);
-    or_rms_norm(last, m->final_norm, 2, D, m->c.eps, hn);
+    dit_rms(last, m->final_norm, 2, D, m->c.eps, hn);
     uint16_t* o = malloc(sizeof(uint16_t) * 2 * n);
-    or_linear_fwd(&m->final, hn, 2, m->bf, o);
+    dit_linear(&m->final, hn, 2, m->bf, o, 0);
     const float cf = or_rb(cfg), dt = or_f32(m->dt[step]), sq = or_f32(m->sq[step]), sk = or_rb(shift_k);
     for (int64_t i = 0; i < n; i++) {
         const float pc = or_f32(o[i]), pu = or_f32(o[n + i]);
@@ -299,7 +448,7 @@ void or_aggregate(const or_agg_model* m, const uint16_t* latent, uint16_t* out) 
     uint16_t* a = malloc(sizeof(uint16_t) * 2 * D);
     uint16_t* b2 = malloc(sizeof(uint16_t) * 2 * D);
     memcpy(a, m->cls, sizeof(uint16_t) * D);
-    or_linear_fwd(&m->x_emb, latent, 1, m->bx, a + D);
+    dit_linear(&m->x_emb, latent, 1, m->bx, a + D, 0);
     for (int k = 0; k < m->n_blocks; k++) {
         or_dit_block_fwd(&m->c, &m->blocks[k], a, 1, 2, m->cos_t, m->sin_t, b2, NULL);
         uint16_t* t = a;
@@ -307,8 +456,8 @@ void or_aggregate(const or_agg_model* m, const uint16_t* latent, uint16_t* out) 
         b2 = t;
     }
     uint16_t* hn = malloc(sizeof(uint16_t) * D);
-    or_rms_norm(a, m->final_norm, 1, D, m->c.eps, hn);  /* row 0 only: rms and the linear are per row */
-    or_linear_fwd(&m->final, hn, 1, m->bf, out);
+    dit_rms(a, m->final_norm, 1, D, m->c.eps, hn);  /* row 0 only: rms and the linear are per row */
+    dit_linear(&m->final, hn, 1, m->bf, out, 0);
     free(hn);
     free(a);
     free(b2);
@@ -317,10 +466,10 @@ void or_aggregate(const or_agg_model* m, const uint16_t* latent, uint16_t* out) 
 /* stopProb (:1033-1038): softmax(f32(stop_head(z)))[1]. */
 float or_stop_prob(const or_linear* head, const uint16_t* bias, const uint16_t* z) {
     uint16_t lg[2];
-    or_linear_fwd(head, z, 1, bias, lg);
+    dit_linear(head, z, 1, bias, lg, 1);
     const float l0 = or_f32(lg[0]), l1 = or_f32(lg[1]);
     const float mx = fmaxf(l0, l1);
-    const float e0 = expf(l0 - mx), e1 = expf(l1 - mx);
+    const float e0 = dit_exp(l0 - mx), e1 = dit_exp(l1 - mx);
     return e1 / (e0 + e1);
 }
 
@@ -329,7 +478,7 @@ float or_stop_prob(const or_linear* head, const uint16_t* bias, const uint16_t* 
 static void silu_rows(const uint16_t* c, int64_t n, uint16_t* out) {
     for (int64_t i = 0; i < n; i++) {  /* silu: x * sigmoid(x), each op rounded (as the timestep MLP) */
         const float v = or_f32(c[i]);
-        const float sg = or_rb(1.0f / (1.0f + expf(-v)));
+        const float sg = or_rb(1.0f / (1.0f + dit_exp(-v)));
         out[i] = or_bf16(v * sg);
     }
 }
@@ -341,7 +490,7 @@ void or_adaln_cond(const or_adaln_model* m, const uint16_t* z, uint16_t* silu_c)
     uint16_t* ce = malloc(sizeof(uint16_t) * 2 * D);
     uint16_t* cc = malloc(sizeof(uint16_t) * 2 * D);
     memcpy(zc, z, sizeof(uint16_t) * H);  /* [z, zeros] */
-    or_linear_fwd(&m->c_emb, zc, 2, m->bc, ce);
+    dit_linear(&m->c_emb, zc, 2, m->bc, ce, 0);
     for (int s = 0; s < m->steps; s++) {
         or_add(m->t_emb + (size_t)s * 2 * D, ce, 2 * D, cc);
         silu_rows(cc, 2 * D, silu_c + (size_t)s * 2 * D);
@@ -354,13 +503,13 @@ void or_adaln_cond(const or_adaln_model* m, const uint16_t* z, uint16_t* silu_c)
 void or_adaln_mods(const or_adaln_model* m, const uint16_t* silu_c, uint16_t* mods, uint16_t* modf) {
     const int D = m->c.D, rows = 2 * m->steps;
     for (int k = 0; k < m->n_blocks; k++)
-        or_linear_fwd(&m->blocks[k].ada, silu_c, rows, m->blocks[k].bada, mods + (size_t)k * rows * 6 * D);
-    or_linear_fwd(&m->final_ada, silu_c, rows, m->bfa, modf);
+        dit_linear(&m->blocks[k].ada, silu_c, rows, m->blocks[k].bada, mods + (size_t)k * rows * 6 * D, 0);
+    dit_linear(&m->final_ada, silu_c, rows, m->bfa, modf, 0);
 }
 
 void or_adaln_rows(const or_adaln_model* m, const uint16_t* y, uint16_t* rows) {
     const int D = m->c.D, F = m->frames;
-    or_linear_fwd(&m->x_emb, y, F, m->bx, rows);
+    dit_linear(&m->x_emb, y, F, m->bx, rows, 0);
     memcpy(rows + (size_t)F * D, rows, sizeof(uint16_t) * (size_t)F * D);
 }
 
@@ -370,9 +519,9 @@ void or_adaln_final(const or_adaln_model* m, const uint16_t* h, const uint16_t* 
     const int64_t n = m->final.N;
     uint16_t* hn = malloc(sizeof(uint16_t) * (size_t)R * D);
     uint16_t* o = malloc(sizeof(uint16_t) * (size_t)R * n);
-    or_rms_norm(h, m->final_norm, R, D, m->c.eps, hn);
+    dit_rms(h, m->final_norm, R, D, m->c.eps, hn);
     modulate(hn, R, F, D, modf_step, 2 * D, 0, 1);
-    or_linear_fwd(&m->final, hn, R, m->bf, o);
+    dit_linear(&m->final, hn, R, m->bf, o, 1);
     const float cf = or_rb(cfg), dt = or_f32(m->dt[step]), sq = or_f32(m->sq[step]), sk = or_rb(shift_k);
     for (int f = 0; f < F; f++)
         for (int64_t i = 0; i < n; i++) {

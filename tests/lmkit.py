@@ -22,6 +22,17 @@ def assert_close_bf16(got_u16, ref_u16, what, atol=ATOL, rtol=RTOL):
     return float(d.max())
 
 
+def assert_bits(got_u16, ref_u16, what):
+    """Bit-for-bit equality of two bf16 arrays, naming the first difference."""
+    g = np.ascontiguousarray(got_u16, np.uint16).reshape(-1)
+    r = np.ascontiguousarray(ref_u16, np.uint16).reshape(-1)
+    assert g.shape == r.shape, (what, g.shape, r.shape)
+    bad = np.flatnonzero(g != r)
+    assert bad.size == 0, (f"{what}: {bad.size} of {g.size} differ in bits; first at {bad[0]}: "
+                           f"{int(g[bad[0]]):#06x} ({float(f32(g[bad[0]:bad[0] + 1])[0]):.6g}) vs {int(r[bad[0]]):#06x} "
+                           f"({float(f32(r[bad[0]:bad[0] + 1])[0]):.6g})")
+
+
 def oracle_linear(host):
     if "s" in host:
         return oracle.Linear(host["w"], host["s"], host["b"])

@@ -3,7 +3,7 @@ launch path (MING_CFM_KERNELS, about 42 launches per Euler step, itself held
 to the oracle teacher-forced per step in test_gpu_dit.py): every Euler
 step's latent bit-identical, for several inputs and CFG / SDE settings, over
 repeated and interleaved launches (each launch tags its hand-offs with a
-new epoch), plus the stage-stamp profile, the mode checks and AUTO's choice
+new epoch), at 1, 2, 8 and 16 blocks, plus the stage-stamp profile, the mode checks and AUTO's choice
 of the persistent kernel at the reference shape."""
 import numpy as np
 import pytest
@@ -75,6 +75,27 @@ def test_persistent_equals_kernels(ming, ctx, flow, seed, cfg, sigma, temperatur
     _, as_ = run(ctx, m, ming.CFM_AUTO, x, cfg, sigma, temperature)
     same(ks, as_, "auto vs kernels")
     m.close()
+
+
+@pytest.mark.parametrize("nblk", [1, 2, 16])
+def test_persistent_block_counts(ming, ctx, nblk):
+    """AUTO sends every reference-width flow head of 1..16 blocks to the persistent kernel: at 1
+    block (the head publishes image A and reads the last block's output in the same step), 2 and
+    16 (a full block table and flag range) its latents equal the launch path's bit for bit, and
+    AUTO's too."""
+    S = syn_mod()
+    print(f"[cfmp] {nblk} blocks", flush=True)
+    syn = S.SyntheticFlow(ctx, S.DitSpec(cfm_blocks=nblk), seed=90 + nblk, norm_std=0.05, parts=("cfm",))
+    m = syn.cfm_model()
+    for seed in (91, 92):
+        x = inputs(ming, syn.spec, seed)
+        ko, ks = run(ctx, m, ming.CFM_KERNELS, x, 2.0, 0.25, 1.0)
+        po, ps = run(ctx, m, ming.CFM_PERSISTENT, x, 2.0, 0.25, 1.0)
+        same(ks, ps, f"{nblk} blocks: persistent vs kernels")
+        _, as_ = run(ctx, m, ming.CFM_AUTO, x, 2.0, 0.25, 1.0)
+        same(ks, as_, f"{nblk} blocks: auto vs kernels")
+    m.close()
+    del syn
 
 
 def test_persistent_repeated_and_interleaved(ming, ctx, flow):

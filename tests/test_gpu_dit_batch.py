@@ -6,10 +6,17 @@ ff 4096).
 
 Bars (those of the single-sequence flow head): every Euler step of every
 sequence, teacher forced on the GPU's own previous latent, within
-2e-2 + 1e-2 |ref| (the free-running latent against the same bar is a
-separate non-strict expected failure: f32 summation order); each sequence
-equal to a one-sequence batch call
-(bit for bit: the GEMMs' per-row arithmetic does not depend on n)."""
+2e-2 + 1e-2 |ref|; each sequence equal to a one-sequence batch call (bit for
+bit: the GEMMs' per-row arithmetic does not depend on n); the free-running
+ten-step latent of every sequence finite and within 6e-2 + 2e-2 |ref| (mean
+|d| <= 2e-2) of the oracle.  The free-running latent against the per-step
+2e-2 + 1e-2 |ref| bar is a separate non-strict expected failure: the matrix
+cores' f32 accumulation of a 32-product block is not IEEE sequential, pairwise
+or single-rounding (measured with chosen operands: up to a few f32 ulps away
+from every such model), so no CPU order reproduces it bit for bit, and the
+8-block, 10-step CFG loop grows the bf16 flips this causes past the bar on some
+seeds (the batch-1 flow head, whose order the oracle reproduces, is held to
+that bar bit for bit in test_gpu_dit.py)."""
 import numpy as np
 import pytest
 import torch
@@ -117,9 +124,7 @@ def test_cfm_batch_deterministic(ming, ctx, flowb):
         assert np.array_equal(host_u16(outs[i]), first), f"repeat {i} differs from the first batched sample"
 
 
-@pytest.mark.xfail(strict=False, reason="free-running ten-step latent at 2e-2 + 1e-2|ref|: the GPU and the oracle sum the DiT GEMVs in different f32 orders, so 1-5 outputs per block differ by one bf16 ulp and the 8-block, 10-step CFG loop grows them to 3-4 ulps on some seeds (teacher-forced steps meet the bar)")
-@pytest.mark.parametrize("n,cfg,sigma,temperature", [(5, 2.0, 0.25, 1.0), (16, 2.0, 0.0, 0.0)])
-def test_cfm_batch_end_to_end(ming, ctx, flowb, n, cfg, sigma, temperature):
+def _batch_free_run(ming, ctx, flowb, n, cfg, sigma, temperature):
     syn, m, oc = flowb
     spec = syn.spec
     z, hist, noise, sde = inputs(ming, spec, n, f"b{n}")
@@ -128,6 +133,26 @@ def test_cfm_batch_end_to_end(ming, ctx, flowb, n, cfg, sigma, temperature):
     ctx.sync()
     shift = float(np.float32(sigma) * np.sqrt(np.float32(temperature)))
     g = host_u16(out)
+    refs = [oracle.cfm_sample(oc, z[b], hist[b], noise[b], sde[b], cfg, shift)[0] for b in range(n)]
+    return g, refs
+
+
+@pytest.mark.parametrize("n,cfg,sigma,temperature", [(5, 2.0, 0.25, 1.0), (16, 2.0, 0.0, 0.0)])
+def test_cfm_batch_end_to_end_bound(ming, ctx, flowb, n, cfg, sigma, temperature):
+    """Free-running latents of every sequence: finite and within the order-difference bound."""
+    print(f"[cfm_batch_end_to_end] n={n}", flush=True)
+    g, refs = _batch_free_run(ming, ctx, flowb, n, cfg, sigma, temperature)
     for b in range(n):
-        ref_out, _ = oracle.cfm_sample(oc, z[b], hist[b], noise[b], sde[b], cfg, shift)
-        assert_close_bf16(g[b], ref_out, f"sequence {b} latent (end to end)")
+        gf = (g[b].astype(np.uint32) << 16).view(np.float32)
+        rf = (refs[b].astype(np.uint32) << 16).view(np.float32)
+        assert np.isfinite(gf).all(), b
+        assert_close_bf16(g[b], refs[b], f"sequence {b} latent (end to end)", atol=6e-2, rtol=2e-2)
+        assert float(np.abs(gf - rf).mean()) <= 2e-2, b
+
+
+@pytest.mark.xfail(strict=False, reason="free-running ten-step latent at 2e-2 + 1e-2|ref|: the matrix cores' f32 accumulation is not reproduced by any CPU summation order, and the 8-block, 10-step CFG loop grows the resulting bf16 flips past the bar on some seeds (teacher-forced steps meet it; the batch-1 flow head is bit-exact free-running)")
+@pytest.mark.parametrize("n,cfg,sigma,temperature", [(5, 2.0, 0.25, 1.0)])
+def test_cfm_batch_end_to_end_strict(ming, ctx, flowb, n, cfg, sigma, temperature):
+    g, refs = _batch_free_run(ming, ctx, flowb, n, cfg, sigma, temperature)
+    for b in range(n):
+        assert_close_bf16(g[b], refs[b], f"sequence {b} latent (end to end)")

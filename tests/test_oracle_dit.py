@@ -8,7 +8,8 @@ unconditional row is t_emb + bias), and a zero-velocity flow whose sampled
 latent has a closed form.  Each check is chosen so that a plausible slip
 (rotary pairing or sign, attention scale, row selection of the final layer,
 CFG sign, dt/sq/sde step index, [sin | cos] order, a dropped bias or norm
-weight) fails it."""
+weight) fails it.  Every check runs in both of the oracle's summation orders (the MLX
+restatement's, and the library kernels' order used for bit-exact GPU comparisons)."""
 import importlib
 import math
 
@@ -22,6 +23,13 @@ from ditkit import ADA, AGG, CFM, oblock, ocfg, olin, oracle_adaln, oracle_agg, 
 S = importlib.import_module("ming-tts-serve_amd.synthetic")
 
 ATOL, RTOL = 2e-2, 1e-2
+
+
+@pytest.fixture(autouse=True, params=[oracle.DIT_ORDER_MLX, oracle.DIT_ORDER_DEVICE], ids=["mlx_order", "device_order"])
+def order(request):
+    """Every pin of this module holds in both summation orders of the oracle's DiT functions."""
+    with oracle.dit_order(request.param):
+        yield request.param
 
 
 def f64(u16):
