@@ -114,7 +114,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--stamps", action="store_true",
-                   help="cfm workload with --mode persistent: per-stage timing from the device stamps (stderr)")
+                   help="cfm workload with --mode persistent, or lm with the persistent schedule: per-stage timing "
+                        "from the device stamps (stderr, after the timed run)")
     p.add_argument("--cooperative", action="store_true",
                    help="lm/loop: cooperative persistent launch (default: ordinary launch, the bench owns the device)")
     return p.parse_args()
@@ -191,6 +192,9 @@ def main():
     bytes_tok = int(round(sum(S.lm_bytes_per_token(spec, args.ctx + i) for i in range(args.steps)) / args.steps))
     achieved = bytes_tok / (launch_ms * 1e-3) / 1e9
 
+    if args.stamps and args.mode in ("auto", "persistent", "direct"):
+        lm_stage_report(ctx, m, spec, cache, step, args.ctx)
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(ming, S, syn, cache, args)
@@ -235,6 +239,89 @@ def main():
     m.close()
     ctx.close()
     print(json.dumps(out), flush=True)
+
+
+def lm_stage_report(ctx, m, spec, cache, step, pos, reps=5):
+    """Per-stage timing of the persistent decode step from its device stamps
+    (ming_lm_model_profile: every workgroup stamps each stage's input arrival
+    and its done, wall clock at 100 MHz), printed to stderr.  Per stage, over
+    layers 2 .. L-3 and `reps` steps (medians over steps, means over layers):
+    exchange = the previous stage's last done -> the median worker's arrival,
+    work = the median worker's arrival -> its done, span = the previous
+    stage's last done -> this stage's last done (the stage's share of the
+    step), and the hubs' legs of the two normalised hand-offs."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    ns, g = ctypes.c_int32(), ctypes.c_int32()
+    ctx.check(ctx.L.ming_lm_model_profile_shape(m.h, ctypes.byref(ns), ctypes.byref(g)))
+    ns, g = ns.value, g.value
+    L, nh = spec.n_layers, 8
+    st = torch.zeros((ns, g), dtype=torch.int64, device="cuda")
+    runs = []
+    for _ in range(reps):
+        st.zero_()
+        cache.kv.len = pos  # each profiled step decodes position pos again
+        ctx.check(ctx.L.ming_lm_model_profile(m.h, ctypes.c_void_p(st.data_ptr())))
+        step()
+        ctx.sync()
+        ctx.check(ctx.L.ming_lm_model_profile(m.h, ctypes.c_void_p(0)))
+        runs.append(st.cpu().numpy().astype(np.float64))
+    slot = lambda l, s: 1 + 2 * (5 * l + s)
+    names = ("q/k/v", "attention", "o_proj", "gate/up", "down")
+    rows = {n: [] for n in names}
+    hubs = {"q/k/v": [], "gate/up": []}
+    head = []
+    for T in runs:
+        T = T / 100.0  # ticks -> us
+        W = T[:, nh:]
+        prev_done = None
+        seq = [(l, s) for l in range(L) for s in range(5)]
+        for i, (l, s) in enumerate(seq):
+            arr, done = W[slot(l, s)], W[slot(l, s) + 1]
+            on = (arr > 0) & (done > 0)
+            if i > 0:
+                pl, ps = seq[i - 1]
+                pd = W[slot(pl, ps) + 1]
+                prev_done = pd[pd > 0].max()
+                if 2 <= l < L - 2 and on.any():
+                    rows[names[s]].append((np.median(arr[on]) - prev_done, np.median(done[on] - arr[on]),
+                                           done[on].max() - prev_done))
+                    if s in (0, 3):
+                        H = T[:, :nh]
+                        ha, hd = H[slot(l, s)], H[slot(l, s) + 1]
+                        if (ha > 0).all() and (hd > 0).all():
+                            hubs[names[s]].append((ha.max() - prev_done, hd.max() - ha.max(),
+                                                   np.median(arr[on]) - hd.max()))
+        ha, hd = W[slot(L, 0)], W[slot(L, 0) + 1]
+        ld = W[slot(L - 1, 4) + 1]
+        on = (ha > 0) & (hd > 0)
+        if on.any():
+            head.append((np.median(ha[on]) - ld[ld > 0].max(), np.median(hd[on] - ha[on]),
+                         hd[on].max() - ld[ld > 0].max()))
+    print(f"[lm stages] position {pos}, {reps} steps; us per layer (mean over layers 2..{L - 3}): "
+          f"exchange = previous stage's last done -> median arrival, work = median arrival -> done, "
+          f"span = previous stage's last done -> last done", file=sys.stderr)
+    total = 0.0
+    for n in names:
+        if not rows[n]:
+            continue
+        a = np.array(rows[n])
+        total += a[:, 2].mean()
+        extra = ""
+        if hubs.get(n):
+            h = np.array(hubs[n])
+            extra = (f"   hubs: last producer -> hub holds the vector {h[:, 0].mean():5.2f}, image built and flagged "
+                     f"{h[:, 1].mean():5.2f}, flag -> median worker {h[:, 2].mean():5.2f}")
+        print(f"[lm stages] {n:10s} exchange {a[:, 0].mean():5.2f}  work {a[:, 1].mean():5.2f}  "
+              f"span {a[:, 2].mean():5.2f}{extra}", file=sys.stderr)
+    print(f"[lm stages] layer total {total:.2f} us", file=sys.stderr)
+    if head:
+        h = np.array(head)
+        print(f"[lm stages] head       exchange {h[:, 0].mean():5.2f}  work {h[:, 1].mean():5.2f}  "
+              f"span {h[:, 2].mean():5.2f}", file=sys.stderr)
 
 
 def measured_traffic(args):

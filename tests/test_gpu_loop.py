@@ -6,9 +6,12 @@ Each step is recomputed on the oracle from the GPU's own inputs (teacher
 forced): z_0 from the prompt prefill, stop_k = stopProb(z_k), latent_k =
 cfmSample(z_k, history_k, noise bank row k), aggregate(latent_k) against the
 GPU kernel's row, and z_{k+1} = LM(that row) with the oracle's own cache.
-Bars: hidden states, aggregator rows and the ten-step latent (free running
-within the step, as the flow head's own end-to-end test) 2e-2 + 1e-2 |ref|;
-stop probabilities 1e-2; the step count follows the stop
+Bars: hidden states and aggregator rows 2e-2 + 1e-2 |ref| of the oracle in
+its MLX order; stop probabilities 1e-2; the ten-step latent (free running
+within the step, as the flow head's own end-to-end test), the aggregator row
+and the stop probability bit for bit with the oracle in the kernels'
+summation order (and the latent within 6e-2 + 2e-2 |ref| of the MLX-order
+oracle); the step count follows the stop
 rule (stop after latent_k when stop_k > 0.5 and k > 3) applied to the GPU's
 stop values, and the cache grows by the documented number of positions."""
 import importlib
@@ -19,7 +22,7 @@ import torch
 
 import oracle
 from ditkit import AGG, oblock, ocfg, olin, oracle_agg, oracle_cfm
-from lmkit import assert_close_bf16, oracle_model, oracle_step
+from lmkit import assert_bits, assert_close_bf16, oracle_model, oracle_step
 
 pytestmark = pytest.mark.gpu
 
@@ -43,8 +46,11 @@ def models(ctx):
     lm = S.SyntheticLm(ctx, spec, seed=3, quant=True, norm_std=0.1)
     flow = S.SyntheticFlow(ctx, S.DitSpec(cfm_blocks=2, agg_blocks=2), seed=5, norm_std=0.05)
     oracle.set_threads(16)
+    with oracle.dit_order(oracle.DIT_ORDER_DEVICE):
+        ocfm_dev, oagg_dev = oracle_cfm(flow), oracle_agg(flow)
     return dict(spec=spec, lm=lm, flow=flow, lm_model=lm.model(), cfm=flow.cfm_model(), agg=flow.agg_model(),
-                olm=oracle_model(lm), ocfm=oracle_cfm(flow), oagg=oracle_agg(flow))
+                olm=oracle_model(lm), ocfm=oracle_cfm(flow), oagg=oracle_agg(flow), ocfm_dev=ocfm_dev,
+                oagg_dev=oagg_dev)
 
 
 @pytest.mark.parametrize("case,stop_bias,max_steps", [("stops", (0.0, 20.0), 8), ("runs_out", (20.0, 0.0), 6)])
@@ -85,8 +91,14 @@ def test_sample_latents_matches_oracle(ming, ctx, models, case, stop_bias, max_s
     hist = np.zeros(lat, np.uint16)
     for k in range(n):
         assert abs(stops[k] - oracle.stop_prob(stop_lin, bias, g_z[k])) <= 1e-2, (k, stops[k])
-        ref, _ = oracle.cfm_sample(oc, g_z[k], hist, g_bank[k, 0], g_bank[k, 1:], 2.0, 0.0)
-        assert_close_bf16(g_lat[k], ref, f"latent {k}")
+        with oracle.dit_order(oracle.DIT_ORDER_DEVICE):
+            # the step's ten free-running Euler steps and the stop head: bit for bit with the
+            # oracle in the kernels' summation order, on the GPU's own z and history
+            assert np.float32(stops[k]) == np.float32(oracle.stop_prob(stop_lin, bias, g_z[k])), k
+            ref, _ = oracle.cfm_sample(models["ocfm_dev"], g_z[k], hist, g_bank[k, 0], g_bank[k, 1:], 2.0, 0.0)
+        assert_bits(g_lat[k], ref, f"latent {k} (device order)")
+        ref_mlx, _ = oracle.cfm_sample(oc, g_z[k], hist, g_bank[k, 0], g_bank[k, 1:], 2.0, 0.0)
+        assert_close_bf16(g_lat[k], ref_mlx, f"latent {k} (MLX order)", atol=6e-2, rtol=2e-2)
         hist = g_lat[k]
         if k + 1 < n:
             # the LM input row the loop used: the same aggregate kernel on the same latent
@@ -95,6 +107,8 @@ def test_sample_latents_matches_oracle(ming, ctx, models, case, stop_bias, max_s
             ctx.sync()
             xrow = host_u16(xd)
             assert_close_bf16(xrow, oracle.aggregate(oa, g_lat[k]), f"aggregate {k}")
+            with oracle.dit_order(oracle.DIT_ORDER_DEVICE):
+                assert_bits(xrow, oracle.aggregate(models["oagg_dev"], g_lat[k]), f"aggregate {k} (device order)")
             _, z_ref, _, _, _ = oracle_step(cfg, layers, norm, head, xrow, L + k, kc, vc)
             assert_close_bf16(g_z[k + 1], z_ref, f"z_{k + 1}")
     assert not np.any(g_lat[n:]), "no latent past the last step"
