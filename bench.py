@@ -272,7 +272,7 @@ def lm_stage_report(ctx, m, spec, cache, step, pos, reps=5):
     slot = lambda l, s: 1 + 2 * (5 * l + s)
     names = ("q/k/v", "attention", "o_proj", "gate/up", "down")
     rows = {n: [] for n in names}
-    hubs = {"q/k/v": [], "gate/up": []}
+    hubs = {"q/k/v": [], "o_proj": [], "gate/up": []}
     head = []
     for T in runs:
         T = T / 100.0  # ticks -> us
@@ -289,7 +289,7 @@ def lm_stage_report(ctx, m, spec, cache, step, pos, reps=5):
                 if 2 <= l < L - 2 and on.any():
                     rows[names[s]].append((np.median(arr[on]) - prev_done, np.median(done[on] - arr[on]),
                                            done[on].max() - prev_done))
-                    if s in (0, 3):
+                    if s in (0, 2, 3):
                         H = T[:, :nh]
                         ha, hd = H[slot(l, s)], H[slot(l, s) + 1]
                         if (ha > 0).all() and (hd > 0).all():
@@ -313,7 +313,7 @@ def lm_stage_report(ctx, m, spec, cache, step, pos, reps=5):
         extra = ""
         if hubs.get(n):
             h = np.array(hubs[n])
-            extra = (f"   hubs: last producer -> hub holds the vector {h[:, 0].mean():5.2f}, image built and flagged "
+            extra = (f"   hubs: last producer -> hub holds the input {h[:, 0].mean():5.2f}, image built and flagged "
                      f"{h[:, 1].mean():5.2f}, flag -> median worker {h[:, 2].mean():5.2f}")
         print(f"[lm stages] {n:10s} exchange {a[:, 0].mean():5.2f}  work {a[:, 1].mean():5.2f}  "
               f"span {a[:, 2].mean():5.2f}{extra}", file=sys.stderr)

@@ -832,8 +832,9 @@ static int lm_step_impl(ming_ctx* ctx, ming_lm_model* m, const int32_t* token_de
                         hipMemcpyAsync(a.x, x_in, sizeof(uint16_t) * c->hidden, hipMemcpyDeviceToDevice, ctx->stream),
                         "copy x_in")))
         return st;
-    // The persistent schedule runs every attention split on its own
-    // workgroup and merges at most 64 splits per kv head.
+    // The persistent schedule runs every attention split (a workgroup's
+    // LDS-resident K/V rows) on its own workgroup, on workgroups that do not
+    // also run q/k/v, o_proj or down (the first ones).
     const int tsl = tagged_split_len(kv->len + 1);
     const int nsplit = (kv->len + 1 + tsl - 1) / tsl;
     const bool want_persistent =
@@ -842,8 +843,9 @@ static int lm_step_impl(ming_ctx* ctx, ming_lm_model* m, const int32_t* token_de
     const int workers = m->pgrid - nhubs;
     const int nq = c->hidden + 2 * c->kv_heads * c->head_dim;
     const int upw = tagged_units_per_worker();
-    const bool fits = m->pgrid > 0 && c->kv_heads * nsplit <= workers && nsplit <= 64 && nq / 4 <= upw * workers &&
-                      c->hidden / 2 <= upw * workers && c->n_layers <= tagged_max_layers();
+    const int front = std::max((nq / 4 + upw - 1) / upw, (c->hidden / 2 + upw - 1) / upw);  // q/k/v, o/down workers
+    const bool fits = m->pgrid > 0 && c->head_dim == 64 && c->heads / c->kv_heads <= 8 &&
+                      c->kv_heads * nsplit + front <= workers && c->n_layers <= tagged_max_layers();
     const bool persistent = want_persistent && fits;
     if (want_persistent && m->mode != MING_LM_AUTO && !fits)
         return set_err(ctx, MING_E_UNSUPPORTED, "lm_step: context too long for the persistent schedule");

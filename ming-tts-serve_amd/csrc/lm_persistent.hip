@@ -27,13 +27,14 @@
 // before its weights; the split keeps the receive path free of them.  A
 // worker issues a stage's loads as soon as it enters the stage, which for
 // most workers is long before the input arrives (they skip the stages in
-// between), and attention workers issue their first K/V tile before they wait
-// for q.
+// between), and attention workers hold their split's K/V in LDS before they
+// wait for q.
 //
-// Attention splits meet through a per-(layer, kv head) arrival counter: the
-// workgroup that arrives last merges the partials.  The LM head's
-// per-workgroup argmax partials meet the same way.  Partials are written with
-// device-coherent stores and waited on (s_waitcnt) before the arrival.
+// Attention splits hold their K rows and V^T in LDS, loaded a layer ahead,
+// and meet through a per-(layer, kv head) arrival counter: the workgroup that
+// arrives last merges the partials.  The LM head's per-workgroup argmax
+// partials meet the same way.  Partials are written with device-coherent
+// stores and waited on (s_waitcnt) before the arrival.
 //
 // Every wait is bounded: past the spin limit a workgroup raises flags[0] and
 // continues, so the grid always drains; the host reports MING_E_TIMEOUT.
@@ -55,11 +56,24 @@ constexpr int kRedOff = 9520;    // reduction scratch (64 words)
 constexpr int kFlagOff = 9584;   // broadcast flags (16 words)
 constexpr int kLayOff = 12288;   // the layer table, copied once per launch: a stage's weight pointers and
                                  // shapes are then LDS reads, not global loads that would queue behind prefetches
-constexpr int kMaxLdsLayers = 48;
+constexpr int kMaxLdsLayers = 32;
 constexpr int kLayWords = (int)(sizeof(LayerDev) / 4);
 constexpr int kLdsTotal = kLayOff + kMaxLdsLayers * kLayWords;
 static_assert(sizeof(LayerDev) % 8 == 0, "layer table entries must keep 8-byte alignment in LDS");
 constexpr int kTile = 64;
+// Attention: a split of kAttTiles 64-position tiles per workgroup, its K rows
+// and V^T resident in LDS after the layer table.
+constexpr int kAttTiles = 6;
+constexpr int kAttP = kAttTiles * kTile;      // positions per split
+constexpr int kVtRowP = kAttP / 2 + 4;        // u32 per V^T row (position pairs), padded: conflict-free reads
+constexpr int kKvOff = kLdsTotal;             // K rows [kAttP][64] bf16
+constexpr int kVtOffP = kKvOff + kAttP * 32;  // V^T [64][kVtRowP]
+constexpr int kLdsAll = kVtOffP + 64 * kVtRowP;
+constexpr int kAttOt = 5248;                  // the tiles' partials [kAttTiles][8][66] f32 (attention stage)
+constexpr int kAttWords = 5248;               // a merged attention row, H/2 u32 (o_proj staging)
+static_assert(kKvOff % 4 == 0 && kVtOffP % 4 == 0 && kVtRowP % 4 == 0, "16-byte LDS operands");
+static_assert(kLdsAll * 4 <= 160 * 1024, "LDS of one workgroup");
+static_assert(kAttOt + kAttTiles * 8 * 66 <= kRedOff, "attention partials below the reduction scratch");
 constexpr int kSc1 = 16;         // buffer-load cache policy bit: device scope
 
 template <int Q4>
@@ -107,10 +121,33 @@ __device__ __forceinline__ XStage xs_of(uint32_t* lds, int K) {
 // null, receives the (normalised) vector.  Thread t owns the 8-value groups
 // t and t + kT (K <= 8192).  All threads of the block call it.
 template <int Q4, bool TO_LDS>
+__device__ __forceinline__ void image_finish(const StepArgs& a, uint32_t* lds, uint32_t (&v)[8], const uint4 (&nw)[2],
+                                             int K, const uint16_t* norm_w, uint32_t* dst, uint16_t* hidden,
+                                             int stamp_slot);
+
+template <int Q4, bool TO_LDS>
 __device__ __forceinline__ void build_image(const StepArgs& a, uint32_t* lds, const uint64_t* src, int K,
                                             const uint16_t* norm_w, uint32_t* dst, uint16_t* hidden,
                                             int stamp_slot = -1) {
-    // dst is LDS (a worker staging for itself) or global memory (a hub image)
+    const int ng = K / 8;
+    uint4 nw[2];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const int g = tix() + p * kT;
+        nw[p] = (norm_w && g < ng) ? ldg4(norm_w + 8 * g) : make_uint4(0, 0, 0, 0);
+    }
+    uint32_t v[8];
+    trecv_groups<kT>(src, ng, a.epoch, v, a.flags);
+    image_finish<Q4, TO_LDS>(a, lds, v, nw, K, norm_w, dst, hidden, stamp_slot);
+}
+
+// The rest of build_image for the groups v[] a thread holds (groups t and
+// t + kT of the vector, 4 u32 each), with its rms weight chunks nw.  dst is
+// LDS (a worker staging for itself) or global memory (a hub image).
+template <int Q4, bool TO_LDS>
+__device__ __forceinline__ void image_finish(const StepArgs& a, uint32_t* lds, uint32_t (&v)[8], const uint4 (&nw)[2],
+                                             int K, const uint16_t* norm_w, uint32_t* dst, uint16_t* hidden,
+                                             int stamp_slot) {
     auto put4 = [&](int word, uint4 v) {
         if (TO_LDS)
             *reinterpret_cast<uint4*>(dst + word) = v;
@@ -124,14 +161,6 @@ __device__ __forceinline__ void build_image(const StepArgs& a, uint32_t* lds, co
             gst(reinterpret_cast<float*>(dst) + word, v);
     };
     const int ng = K / 8, NC = K / 32;
-    uint4 nw[2];
-#pragma unroll
-    for (int p = 0; p < 2; p++) {
-        const int g = tix() + p * kT;
-        nw[p] = (norm_w && g < ng) ? ldg4(norm_w + 8 * g) : make_uint4(0, 0, 0, 0);
-    }
-    uint32_t v[8];
-    trecv_groups<kT>(src, ng, a.epoch, v, a.flags);
     if (norm_w) {
         float ss = 0.0f;
 #pragma unroll
@@ -178,6 +207,9 @@ __device__ __forceinline__ void build_image(const StepArgs& a, uint32_t* lds, co
 __device__ __forceinline__ bool hub_on(const StepArgs& a, int stage) { return a.nhubs > 0 && (a.hub_stages & stage); }
 
 template <int Q4>
+__device__ __forceinline__ void copy_hub_image(const Ctx& c, int fidx, int slot, int K);
+
+template <int Q4>
 __device__ __forceinline__ void get_image(const Ctx& c, int stage, int fidx, int slot, const uint64_t* src, int K,
                                           const uint16_t* norm_w, uint16_t* hidden) {
     const StepArgs& a = c.a;
@@ -187,6 +219,14 @@ __device__ __forceinline__ void get_image(const Ctx& c, int stage, int fidx, int
         lds_sync();
         return;
     }
+    copy_hub_image<Q4>(c, fidx, slot, K);
+}
+
+// Worker: wave 0 waits for the hub's flag fidx and copies image slot `slot`
+// (an image of K values) into LDS.
+template <int Q4>
+__device__ __forceinline__ void copy_hub_image(const Ctx& c, int fidx, int slot, int K) {
+    const StepArgs& a = c.a;
     if (c.wave == 0 && c.lane == 0) wait_flag(a.hflag + (size_t)c.hub * a.nflag + fidx, a.epoch, a.flags);
     lds_sync();
     if (c.wave == 0) {
@@ -396,45 +436,52 @@ __device__ __forceinline__ void st_qkv(const Ctx& c, const LayerDev& Ld, int l) 
     }
 }
 
-// ---- LB: split-K GQA attention + last-arriver merge ----------------------------
-// Unit = (kv head g, split of positions), on the last workers.  The split is
-// walked in tiles of 64 positions: each thread loads one 16 B chunk of K and
-// one of V per tile (the next tile's loads are issued before the current one
-// is computed; the new row pos replaces its cache row as the tile is stored
-// to LDS); wave 1 computes the tile on the matrix cores (attn_run).  The
-// last split to arrive merges all splits of the kv head with one batch of
-// loads (lane s holds split s's max and sum, readlane broadcasts weights).
+// ---- LB: split GQA attention over LDS-resident K/V + last-arriver merge ------------------
+// Unit = (kv head g, split of kAttP positions), on the last workers.  A
+// split's K rows and V^T stay in this workgroup's LDS: they are loaded one
+// layer ahead (attn_prefetch, after the workgroup's gate/up stage of the
+// layer before, or at launch for layer 0), so that once q arrives the six
+// 64-position tiles of the split are computed at once, one per compute wave,
+// on the matrix cores, and merged through LDS into one partial per split
+// (per q head: max, sum, unnormalised output).  The splits of a kv head meet
+// through a per-(layer, kv head) arrival counter: every split stores its
+// partial device-coherently and waits for the stores before it counts itself
+// in, and the last to arrive merges all of them (a kv head has a few splits of
+// six tiles each -- 6 at ctx 2048 -- where one-tile splits made it 33).
 struct ALds {
-    float* q;       // [8][64] q * 1/sqrt(hd)
-    uint16_t* k;    // [64][64] the tile's K rows (V goes transposed to kVtOff)
-    uint32_t* kn;   // [32] new k row (bf16 pairs)
-    uint32_t* vn;   // [32] new v row
+    uint4* qb;      // [64 lanes][2] the score MFMAs' B operands: q * 1/8 in bf16, per lane (head c, dims 16 j ..)
+    float* ot;      // [kAttTiles][8 heads][66] each tile's (max, sum, o[64])
 };
 
 __device__ __forceinline__ ALds alds(uint32_t* lds) {
     ALds s;
-    s.q = reinterpret_cast<float*>(lds);
-    s.k = reinterpret_cast<uint16_t*>(lds + 512);
-    s.kn = lds + 5152;  // 16-byte aligned
-    s.vn = lds + 5184;
+    s.qb = reinterpret_cast<uint4*>(lds);
+    s.ot = reinterpret_cast<float*>(lds + kAttOt);
     return s;
 }
 
-// This worker's attention unit: kv head g, positions [j0, j1) of ns splits.
+// K rows in LDS are stored with their 16-byte chunks permuted within the row
+// (chunk q of row p at slot q ^ kswz(p)), so that the 16 rows that one pass
+// of the score MFMAs' A-operand reads touches fall in distinct banks.
+__device__ __forceinline__ int kswz(int p) { return ((p >> 2) & 6) | ((p >> 1) & 1); }
+
+// This worker's attention unit: kv head g, positions [j0, j1) of split sp of ns.
 struct AttnGeom {
     int u, ns, g, sp, j0, j1;
 };
+
+__device__ __forceinline__ int attn_splits(int pos) { return (pos + 1 + kAttP - 1) / kAttP; }
 
 __device__ __forceinline__ AttnGeom attn_geom(const Ctx& c) {
     const StepArgs& a = c.a;
     AttnGeom q;
     const int n = a.pos + 1;
-    q.ns = (n + a.split_len - 1) / a.split_len;
+    q.ns = attn_splits(a.pos);
     q.u = c.W - 1 - c.w;  // attention units on the last workers
     q.g = q.u / q.ns;
     q.sp = q.u % q.ns;
-    q.j0 = q.sp * a.split_len;
-    q.j1 = min(n, q.j0 + a.split_len);
+    q.j0 = q.sp * kAttP;
+    q.j1 = min(n, q.j0 + kAttP);
     return q;
 }
 
@@ -443,35 +490,58 @@ __device__ __forceinline__ bool in_attn(const Ctx& c) {
     return q.u >= 0 && q.u < c.a.kvh * q.ns;
 }
 
-// K/V chunk of this thread in a 64-position tile: cached rows (< pos) come
-// from the cache; row pos arrives with q through the tagged q|k|v.
-struct AttnTile {
-    uint4 k, v;
-};
-
-// Rows past the split or not yet cached load row min(row, ...) instead (the
-// loads take no branch); attn_tile_valid() tells which rows to zero.
-__device__ __forceinline__ void attn_tile_load(const Ctx& c, int l, const AttnGeom& q, int t0, AttnTile& r) {
+// The split's K rows [j0, j0 + kAttP) of layer l into LDS (direct buffer
+// loads: each 16 bytes of a row land at the row's place, no registers) and
+// its V rows through registers into V^T (u32 at vt[dim * kVtRowP + m] holds
+// dimension dim of positions 2m and 2m + 1; rows 2m and 2m + 1 meet through a
+// lane shuffle).  Rows the cache does not hold yet read as whatever the cache
+// holds there (rows past its capacity as zeros) and are masked by the
+// attention; the new row pos arrives with q.  Every wave waits for its loads.
+__device__ __forceinline__ void attn_prefetch(const Ctx& c, int l) {
     const StepArgs& a = c.a;
-    const int row = t0 + tix() / 8, col = tix() % 8;
-    const int rr = max(0, min(row, min(q.j1, a.pos) - 1));
-    const size_t off = ((((size_t)l * a.kvh + q.g) * a.cap) + rr) * a.hd + 8 * col;
-    r.k = ldg4(a.kc + off);
-    r.v = ldg4(a.vc + off);
-}
-__device__ __forceinline__ bool attn_tile_valid(const Ctx& c, const AttnGeom& q, int t0) {
-    const int row = t0 + tix() / 8;
-    return row < q.j1 && row < c.a.pos;
-}
-
-// The first tile's loads, issued a stage ahead.
-__device__ __forceinline__ void attn_pre(const Ctx& c, int l, AttnTile& r) {
     const AttnGeom q = attn_geom(c);
-    attn_tile_load(c, l, q, q.j0, r);
+    const size_t base = (((size_t)l * a.kvh + q.g) * a.cap + q.j0) * a.hd;  // element offset of row j0
+    const int rows = max(0, min(kAttP, a.cap - q.j0));
+    const uint32_t nbytes = (uint32_t)rows * (uint32_t)a.hd * 2u;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(a.kc + base, 0, nbytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(a.vc + base, 0, nbytes, 0x00020000);
+    // K: kAttP rows x 8 chunks of 16 bytes; wave w loads rounds of 64 chunks w, w + 8, ...
+    for (int i0 = kWave * c.wave; i0 < kAttP * 8; i0 += kT) {
+        const int i = i0 + c.lane, r = i / 8;  // this lane fills slot i % 8 of LDS row r
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(c.lds + kKvOff + 4 * i0),
+                                                 16, (8 * r + ((i % 8) ^ kswz(r))) * 16, 0, 0, 0);
+    }
+    // V: chunk i = tix() + kT k is row i / 8, dimensions 8 (i % 8) .. + 7
+    constexpr int NV = kAttP * 8 / kT;
+    uint4 vv[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rv, (tix() + kT * k) * 16, 0, 0);
+        vv[k] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+    uint32_t* vt = c.lds + kVtOffP;
+    const int t = tix(), ch = t % 8;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const uint32_t e1[4] = {(uint32_t)__shfl((int)vv[k].x, c.lane + 8, kWave),
+                                (uint32_t)__shfl((int)vv[k].y, c.lane + 8, kWave),
+                                (uint32_t)__shfl((int)vv[k].z, c.lane + 8, kWave),
+                                (uint32_t)__shfl((int)vv[k].w, c.lane + 8, kWave)};
+        if (((t / 8) & 1) == 0) {
+            const uint32_t e0[4] = {vv[k].x, vv[k].y, vv[k].z, vv[k].w};
+            const int m = t / 16 + 32 * k;  // pair of rows 2m, 2m + 1
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                vt[(8 * ch + 2 * d) * kVtRowP + m] = (e0[d] & 0xffffu) | (e1[d] << 16);
+                vt[(8 * ch + 2 * d + 1) * kVtRowP + m] = (e0[d] >> 16) | (e1[d] & 0xffff0000u);
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's K rows are in LDS
 }
 
 // Wait for this unit's q rows (and, in the split holding position pos, the
-// new k/v row) and stage them in LDS.
+// new k/v row, which replaces its row in the LDS K and V^T) and stage q.
 __device__ __forceinline__ void attn_recv(const Ctx& c, int l) {
     const StepArgs& a = c.a;
     const AttnGeom q = attn_geom(c);
@@ -480,227 +550,199 @@ __device__ __forceinline__ void attn_recv(const Ctx& c, int l) {
     const int nq = a.H + 2 * a.kvh * hd;
     const uint64_t* tq = a.tq + (size_t)l * (nq / 2);
     const float scale = 1.0f / sqrtf((float)hd);
-    lds_sync();  // the previous stage is done with LDS
-    for (int i = t; i < grp * hd / 2; i += kT) {
-        const uint32_t w = trecv1(tq + (g * grp * hd) / 2 + i, a.epoch, a.flags);
-        S.q[2 * i] = scale * bf_lo(w);
-        S.q[2 * i + 1] = scale * bf_hi(w);
+    lds_sync();  // the previous stage is done with LDS; every wave's prefetched K rows are visible
+    if (t < 2 * kWave) {
+        // B operand h of lane (head c, j): q of head c, dimensions 16 j + 8 h .. + 7, times 1/8 (exact in bf16)
+        const int ln = t % kWave, h = t / kWave, cc = ln % 16, jj = ln / 16;
+        uint4 b = make_uint4(0u, 0u, 0u, 0u);
+        if (cc < grp) {
+            const uint64_t* src = tq + (g * grp + cc) * (hd / 2) + 8 * jj + 4 * h;
+            uint32_t w[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) w[k] = trecv1(src + k, a.epoch, a.flags);
+#pragma unroll
+            for (int k = 0; k < 4; k++) w[k] = pack_bf2(scale * bf_lo(w[k]), scale * bf_hi(w[k]));
+            b = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        S.qb[2 * ln + h] = b;
     }
-    if (q.j1 > a.pos && t < hd) {  // this split holds the new row
+    if (q.j1 > a.pos && t >= 2 * kWave && t < 2 * kWave + hd) {  // this split holds the new row (waves 2, 3)
+        const int r = a.pos - q.j0, u = t - 2 * kWave;
         const uint64_t* src =
-            t < hd / 2 ? tq + (a.H + g * hd) / 2 + t : tq + (a.H + a.kvh * hd + g * hd) / 2 + t - hd / 2;
+            u < hd / 2 ? tq + (a.H + g * hd) / 2 + u : tq + (a.H + a.kvh * hd + g * hd) / 2 + u - hd / 2;
         const uint32_t w = trecv1(src, a.epoch, a.flags);
-        if (t < hd / 2)
-            S.kn[t] = w;
-        else
-            S.vn[t - hd / 2] = w;
+        if (u < hd / 2) {
+            c.lds[kKvOff + r * (hd / 2) + 4 * ((u / 4) ^ kswz(r)) + u % 4] = w;
+        } else {
+            const int d = 2 * (u - hd / 2);
+            uint16_t* vt16 = reinterpret_cast<uint16_t*>(c.lds + kVtOffP);
+            vt16[d * (2 * kVtRowP) + r] = (uint16_t)(w & 0xffffu);
+            vt16[(d + 1) * (2 * kVtRowP) + r] = (uint16_t)(w >> 16);
+        }
     }
     stamp(a, slot_in(l, 1));
 }
 
-// Merge of the ns <= NS splits of kv head g (last arriver), wave h = q head h,
-// lane d = dim d: every partial is loaded in one batch (clamped indices).
-template <int NS>
-__device__ __forceinline__ void attn_merge(const Ctx& c, int l, const AttnGeom& q) {
-    const StepArgs& a = c.a;
-    const int grp = a.heads / a.kvh, hd = a.hd, ns = q.ns, g = q.g, h = c.wave, d = c.lane;
-    const size_t sstride = (size_t)grp * (hd + 2);
-    const float* pb = a.part + (size_t)(g * ns) * sstride + (size_t)h * (hd + 2);
-    const int sl = min(d, ns - 1);
-    const float ms = cload(pb + sl * sstride), ls = cload(pb + sl * sstride + 1);
-    float v[NS];
-#pragma unroll
-    for (int s = 0; s < NS; s++) v[s] = cload(pb + min(s, ns - 1) * sstride + 2 + d);
-    const float m = d < ns ? ms : -INFINITY;
-    const float M = team_max<kWave>(m);
-    const float w = d < ns ? expf(m - M) : 0.0f;
-    const float lw = team_sum<kWave>(w * (d < ns ? ls : 0.0f));
-    float o = 0.0f;
-#pragma unroll
-    for (int s = 0; s < NS; s++) o += v[s] * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), s));
-    const float val = o / lw;
-    const float nxt = __shfl_down(val, 1, kWave);
-    const int col = (g * grp + h) * hd + d;
-    if ((d & 1) == 0) {
-        const uint32_t wv = pack_bf2(val, nxt);
-        tstore(a.ta + (size_t)l * (a.H / 2) + col / 2, wv, a.epoch);
-        gst(reinterpret_cast<uint32_t*>(a.att + l * a.sx) + col / 2, wv);
-    }
-}
-
-// V^T of the tile in LDS: the u32 at vt[dim * kVtRow + m] holds dimension dim
-// of positions 2m and 2m + 1 (rows padded to 36 words: a fragment read's 16
-// rows fall in different bank groups).  Above the attention's other LDS data.
-constexpr int kVtRow = 36;
-constexpr int kVtOff = 5248;
-constexpr int kOtOff = kVtOff + 64 * kVtRow;  // a split's partials, [8 heads][66] f32
-static_assert(kOtOff + 8 * 66 <= kRedOff, "V^T and the partials below the reduction scratch");
-
-// One split: wave 1 computes every q head of the kv head on the matrix cores,
-// tile by tile with the running max / sum / output in registers (online
-// softmax).  Scores: C[position][head] over two v_mfma_f32_16x16x32_bf16 per
-// 16 positions, A = the K rows (position 32 (t/2) + 8 (c/4) + 4 (t%2) + c%4 in
-// A row c of tile t, so that lane (c, j) ends with head c's scores of
-// positions 32 (t/2) + 8 j + 4 (t%2) + r -- the k order P.V wants), B = q of
-// head c pre-scaled by 1/8 (exact in bf16), dimensions 16 j + 8 h .. + 7.
-// P.V: C[dim][head], A = V^T rows, B = the probabilities split into bf16
-// hi + lo (two MFMAs, so P keeps about 16 bits).  The other waves stage the
-// tile: K row-major and V transposed (rows 2m and 2m + 1 meet through a lane
-// shuffle), the new row pos replacing its cache row.
-__device__ __forceinline__ void attn_run(const Ctx& c, int l, AttnTile tile) {
+// The split's tiles on the matrix cores, compute wave 1 + t taking tile t
+// (positions j0 + 64 t ..), each with its own max / sum / output.  Scores:
+// C[position][head] over two v_mfma_f32_16x16x32_bf16 per 16 positions, A =
+// the K rows (position 32 (s/2) + 8 (c/4) + 4 (s%2) + c%4 in A row c of
+// sub-tile s, so that lane (c, j) ends with head c's scores of positions
+// 32 (s/2) + 8 j + 4 (s%2) + r -- the k order P.V wants), B = q of head c
+// pre-scaled by 1/8 (exact in bf16), dimensions 16 j + 8 h .. + 7.  P.V:
+// C[dim][head], A = V^T rows, B = the probabilities split into bf16 hi + lo
+// (two MFMAs, so P keeps about 16 bits).  The tiles' partials meet through
+// LDS (in tile order) into the split's partial, which leaves as tagged words.
+__device__ __forceinline__ void attn_run(const Ctx& c, int l) {
     const StepArgs& a = c.a;
     const AttnGeom q = attn_geom(c);
-    const int ns = q.ns, g = q.g, sp = q.sp, j0 = q.j0, j1 = q.j1;
-    const int grp = a.heads / a.kvh, hd = a.hd, t = tix();
+    const int grp = a.heads / a.kvh, hd = a.hd;
     const ALds S = alds(c.lds);
-    uint32_t* vt = c.lds + kVtOff;
-    const bool mw = c.wave == 1;
+    lds_sync();  // q and the new row staged
+    const int tile = c.wave - 1, p0 = q.j0 + kTile * tile;
+    const int cnt = (c.wave >= 1 && c.wave <= kAttTiles) ? max(0, min(kTile, q.j1 - p0)) : 0;
     const int cc = c.lane % 16, jj = c.lane / 16;
-    float mrun = -INFINITY, lrun = 0.0f;
-    f32x4_t o[4];
+    if (cnt > 0) {
+        const uint4 qb[2] = {S.qb[2 * c.lane], S.qb[2 * c.lane + 1]};
+        const uint4* kt = reinterpret_cast<const uint4*>(c.lds + kKvOff) + (size_t)kTile * tile * 8;  // 8 chunks a row
+        f32x4_t sc[4];
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++) o[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    uint4 qb[2] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
-    for (int t0 = j0; t0 < j1; t0 += kTile) {
-        const int cnt = min(kTile, j1 - t0);
-        lds_sync();  // the previous tile (or the q staging) is done with LDS
-        if (mw && t0 == j0 && cc < grp) {
+        for (int tt = 0; tt < 4; tt++) {
+            const int p = 32 * (tt / 2) + 8 * (cc / 4) + 4 * (tt % 2) + cc % 4, pr = kTile * tile + p;
+            const uint4* kr = kt + 8 * p;
+            sc[tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            sc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(kr[(2 * jj) ^ kswz(pr)]), as_bf8(qb[0]), sc[tt],
+                                                            0, 0, 0);
+            sc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(kr[(2 * jj + 1) ^ kswz(pr)]), as_bf8(qb[1]),
+                                                            sc[tt], 0, 0, 0);
+        }
+        float mx = -INFINITY;
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const float* qh = S.q + cc * hd + 16 * jj + 8 * h;
-                qb[h] = make_uint4(pack_bf2(qh[0], qh[1]), pack_bf2(qh[2], qh[3]), pack_bf2(qh[4], qh[5]),
-                                   pack_bf2(qh[6], qh[7]));
+        for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int p = 32 * (tt / 2) + 8 * jj + 4 * (tt % 2) + r;
+                if (p >= cnt) sc[tt][r] = -INFINITY;
+                mx = fmaxf(mx, sc[tt][r]);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        float lp = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float e = sc[tt][r] == -INFINITY ? 0.0f : expf(sc[tt][r] - mx);
+                sc[tt][r] = e;
+                lp += e;
+            }
+        lp += __shfl_xor(lp, 16, kWave);
+        lp += __shfl_xor(lp, 32, kWave);
+        const uint32_t* vt = c.lds + kVtOffP + (kTile / 2) * tile;
+        f32x4_t o[4];
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) o[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            uint32_t hi[4], lo[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float e0 = sc[2 * u + k / 2][2 * (k % 2)], e1 = sc[2 * u + k / 2][2 * (k % 2) + 1];
+                hi[k] = pack_bf2(e0, e1);
+                lo[k] = pack_bf2(e0 - bf_lo(hi[k]), e1 - bf_hi(hi[k]));
+            }
+            const bf16x8_t ph = as_bf8(make_uint4(hi[0], hi[1], hi[2], hi[3]));
+            const bf16x8_t pl = as_bf8(make_uint4(lo[0], lo[1], lo[2], lo[3]));
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                const uint4 va = *reinterpret_cast<const uint4*>(vt + (16 * dt + cc) * kVtRowP + 16 * u + 4 * jj);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(va), ph, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(va), pl, o[dt], 0, 0, 0);
             }
         }
-        {
-            const int row = t0 + t / 8, ch = t % 8;
-            const bool ok = attn_tile_valid(c, q, t0);
-            uint4 kk = ok ? tile.k : make_uint4(0, 0, 0, 0);
-            uint4 vv = ok ? tile.v : make_uint4(0, 0, 0, 0);
-            if (row == a.pos) {  // the new row, received with q
-                kk = reinterpret_cast<const uint4*>(S.kn)[ch];
-                vv = reinterpret_cast<const uint4*>(S.vn)[ch];
+        // lane (c, j) holds head c's o at dimensions 16 dt + 4 j + r
+        float* ot = S.ot + (size_t)tile * 8 * (hd + 2);
+        if (cc < grp) {
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) ot[cc * (hd + 2) + 2 + 16 * dt + 4 * jj + r] = o[dt][r];
+            if (jj == 0) {
+                ot[cc * (hd + 2)] = mx;
+                ot[cc * (hd + 2) + 1] = lp;
             }
-            reinterpret_cast<uint4*>(S.k)[t] = kk;
-            const uint32_t e1[4] = {(uint32_t)__shfl((int)vv.x, c.lane + 8, kWave), (uint32_t)__shfl((int)vv.y, c.lane + 8, kWave),
-                                    (uint32_t)__shfl((int)vv.z, c.lane + 8, kWave), (uint32_t)__shfl((int)vv.w, c.lane + 8, kWave)};
-            if (((t / 8) & 1) == 0) {
-                const uint32_t e0[4] = {vv.x, vv.y, vv.z, vv.w};
-                const int m = t / 16;
-#pragma unroll
-                for (int d = 0; d < 4; d++) {
-                    vt[(8 * ch + 2 * d) * kVtRow + m] = (e0[d] & 0xffffu) | (e1[d] << 16);
-                    vt[(8 * ch + 2 * d + 1) * kVtRow + m] = (e0[d] >> 16) | (e1[d] & 0xffff0000u);
-                }
-            }
-        }
-        lds_sync();
-        if (t0 + kTile < j1) attn_tile_load(c, l, q, t0 + kTile, tile);
-        if (mw) {
-            f32x4_t sc[4];
-#pragma unroll
-            for (int tt = 0; tt < 4; tt++) {
-                const int p = 32 * (tt / 2) + 8 * (cc / 4) + 4 * (tt % 2) + cc % 4;
-                const uint16_t* kr = S.k + p * hd + 16 * jj;
-                sc[tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-                sc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(*reinterpret_cast<const uint4*>(kr)),
-                                                                as_bf8(qb[0]), sc[tt], 0, 0, 0);
-                sc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(*reinterpret_cast<const uint4*>(kr + 8)),
-                                                                as_bf8(qb[1]), sc[tt], 0, 0, 0);
-            }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int tt = 0; tt < 4; tt++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int p = 32 * (tt / 2) + 8 * jj + 4 * (tt % 2) + r;
-                    if (p >= cnt) sc[tt][r] = -INFINITY;
-                    mx = fmaxf(mx, sc[tt][r]);
-                }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-            const float mn = fmaxf(mrun, mx);
-            const float corr = expf(mrun - mn);  // 0 on the first tile
-            float lp = 0.0f;
-#pragma unroll
-            for (int tt = 0; tt < 4; tt++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float e = sc[tt][r] == -INFINITY ? 0.0f : expf(sc[tt][r] - mn);
-                    sc[tt][r] = e;
-                    lp += e;
-                }
-            lp += __shfl_xor(lp, 16, kWave);
-            lp += __shfl_xor(lp, 32, kWave);
-            lrun = lrun * corr + lp;
-            mrun = mn;
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++) o[dt] = o[dt] * corr;
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                uint32_t hi[4], lo[4];
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const float p0 = sc[2 * u + k / 2][2 * (k % 2)], p1 = sc[2 * u + k / 2][2 * (k % 2) + 1];
-                    hi[k] = pack_bf2(p0, p1);
-                    lo[k] = pack_bf2(p0 - bf_lo(hi[k]), p1 - bf_hi(hi[k]));
-                }
-                const bf16x8_t ph = as_bf8(make_uint4(hi[0], hi[1], hi[2], hi[3]));
-                const bf16x8_t pl = as_bf8(make_uint4(lo[0], lo[1], lo[2], lo[3]));
-#pragma unroll
-                for (int dt = 0; dt < 4; dt++) {
-                    const uint4 va = *reinterpret_cast<const uint4*>(vt + (16 * dt + cc) * kVtRow + 16 * u + 4 * jj);
-                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(va), ph, o[dt], 0, 0, 0);
-                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(va), pl, o[dt], 0, 0, 0);
-                }
-            }
-        }
-    }
-    // partials (per head: max, sum, o[hd]): wave 1's lane (c, j) holds head c's o
-    // at dimensions 16 dt + 4 j + r; they go through LDS so that the workgroup
-    // stores them as one contiguous run (device-coherent stores write whole
-    // granules: scattered 4-byte stores doubled the step's write traffic)
-    float* ot = reinterpret_cast<float*>(c.lds + kOtOff);
-    if (mw && cc < grp) {
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) ot[cc * (hd + 2) + 2 + 16 * dt + 4 * jj + r] = o[dt][r];
-        if (jj == 0) {
-            ot[cc * (hd + 2)] = mrun;
-            ot[cc * (hd + 2) + 1] = lrun;
         }
     }
     lds_sync();
+    // the split's partial: per head the max over its tiles, the sum and output rescaled to it;
+    // device-coherent stores, completed before the arrival
+    const int ntl = min(kAttTiles, (q.j1 - q.j0 + kTile - 1) / kTile);  // tiles holding positions
+    const int t = tix();
     {
-        float* out = a.part + (size_t)(g * ns + sp) * grp * (hd + 2);
-        for (int i = t; i < grp * (hd + 2); i += kT) cstore(out + i, ot[i]);
+        const int h = t / hd, d = t % hd;
+        if (h < grp) {
+            float M = -INFINITY;
+            for (int i = 0; i < ntl; i++) M = fmaxf(M, S.ot[(i * 8 + h) * (hd + 2)]);
+            float o = 0.0f, Ls = 0.0f;
+            for (int i = 0; i < ntl; i++) {
+                const float* pi = S.ot + (i * 8 + h) * (hd + 2);
+                const float wgt = expf(pi[0] - M);
+                o += wgt * pi[2 + d];
+                Ls += wgt * pi[1];
+            }
+            float* out = a.part + (((size_t)q.g * q.ns + q.sp) * grp + h) * (hd + 2);
+            cstore(out + 2 + d, o);
+            if (d == 0) {
+                cstore(out, M);
+                cstore(out + 1, Ls);
+            }
+        }
     }
-    // partials: device-coherent stores, completed before the arrival
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     int* last = reinterpret_cast<int*>(c.lds + kFlagOff);
     if (t == 0) {
-        int* ctr = a.counters + l * a.kvh + g;
+        int* ctr = a.counters + l * a.kvh + q.g;
         const int old = __hip_atomic_fetch_add((MING_GLOBAL int*)ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *last = old == ns - 1;
-        if (old == ns - 1) astore(ctr, 0);
+        *last = old == q.ns - 1;
+        if (old == q.ns - 1) astore(ctr, 0);
     }
     lds_sync();
-    if (!*last || c.wave >= grp) return;
-    // the smallest batch that holds every split: each lane loads one o value per split
-    if (ns <= 16)
-        attn_merge<16>(c, l, q);
-    else if (ns <= 24)
-        attn_merge<24>(c, l, q);
-    else if (ns <= 32)
-        attn_merge<32>(c, l, q);
-    else if (ns <= 40)
-        attn_merge<40>(c, l, q);
-    else if (ns <= 48)
-        attn_merge<48>(c, l, q);
-    else
-        attn_merge<64>(c, l, q);
+    if (!*last) return;
+    // the last split to arrive merges the kv head's splits, in split order: a running (M, L, o),
+    // M' = max(M, m_s), L' = L e^(M - M') + l_s e^(m_s - M'), o likewise; the row is o / L
+    for (int w = t; w < grp * hd / 2; w += kT) {
+        const int h = (2 * w) / hd, d = (2 * w) % hd;
+        const float* base = a.part + ((size_t)q.g * q.ns * grp + h) * (hd + 2);
+        const size_t sstride = (size_t)grp * (hd + 2);
+        float M = -INFINITY, L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+        for (int s0 = 0; s0 < q.ns; s0 += 8) {
+            const int nb = min(8, q.ns - s0);
+            float v[8][4];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float* p = base + (size_t)(s0 + min(i, nb - 1)) * sstride;
+                v[i][0] = cload(p);
+                v[i][1] = cload(p + 1);
+                v[i][2] = cload(p + 2 + d);
+                v[i][3] = cload(p + 3 + d);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (i >= nb) break;
+                const float Mn = fmaxf(M, v[i][0]);
+                const float cold = M == -INFINITY ? 0.0f : expf(M - Mn), cnew = expf(v[i][0] - Mn);
+                L = L * cold + cnew * v[i][1];
+                o0 = o0 * cold + cnew * v[i][2];
+                o1 = o1 * cold + cnew * v[i][3];
+                M = Mn;
+            }
+        }
+        const uint32_t wv = pack_bf2(o0 / L, o1 / L);
+        const int cw = (q.g * grp * hd) / 2 + w;
+        tstore(a.ta + (size_t)l * (a.H / 2) + cw, wv, a.epoch);
+        gst(reinterpret_cast<uint32_t*>(a.att + l * a.sx) + cw, wv);
+    }
 }
 
 // ---- LC: o_proj + residual (unit = row pair, packed on the compute waves) ------
@@ -1018,7 +1060,7 @@ __global__ __launch_bounds__(kT) void decode_tagged_kernel(StepArgs args, const 
     // for the references that the stages take.
     (void)args;
     const StepArgs& a = *(const StepArgs*)__builtin_amdgcn_kernarg_segment_ptr();
-    __shared__ __align__(16) uint32_t lds[kLdsTotal];
+    __shared__ __align__(16) uint32_t lds[kLdsAll];
     stamp(a, 0);
     uint32_t xcc;
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
@@ -1044,6 +1086,7 @@ __global__ __launch_bounds__(kT) void decode_tagged_kernel(StepArgs args, const 
     const Ctx c0{a, lds, W, w, wave, lane, lane / 32, lane % 32, hub};
     const bool pq = in_qkv(c0), pa = in_attn(c0), po = in_rowpairs(c0);
     const int L = a.n_layers;
+    if (pa) attn_prefetch(c0, 0);
     for (int l = 0; l < L; l++) {
         const int ln = tix() % kWave;
         const Ctx c{a, lds, W, w, wave, ln, ln / 32, ln % 32, hub};
@@ -1053,10 +1096,8 @@ __global__ __launch_bounds__(kT) void decode_tagged_kernel(StepArgs args, const 
             done_stamp(a, slot_in(l, 0) + 1);
         }
         if (pa) {
-            AttnTile at;
-            attn_pre(c, l, at);
             attn_recv(c, l);
-            attn_run(c, l, at);
+            attn_run(c, l);
             done_stamp(a, slot_in(l, 1) + 1);
         }
         if (po) {
@@ -1067,6 +1108,7 @@ __global__ __launch_bounds__(kT) void decode_tagged_kernel(StepArgs args, const 
         if (po) down_pre<Q4>(c, Ld, dp);
         st_up<Q4>(c, Ld, l);
         done_stamp(a, slot_in(l, 3) + 1);
+        if (pa && l + 1 < L) attn_prefetch(c, l + 1);  // the next layer's K/V while down and q/k/v run
         if (po) {
             st_down<Q4>(c, Ld, l, dp);
             done_stamp(a, slot_in(l, 4) + 1);
@@ -1080,16 +1122,9 @@ __global__ __launch_bounds__(kT) void decode_tagged_kernel(StepArgs args, const 
 
 }  // namespace
 
-// Positions per attention split on this schedule: the fewest whole 64-row
-// tiles (at most 16) that leave a kv head at most 64 splits (each split is
-// one workgroup; the last one to finish merges them, one split per lane).
-// A split's tiles run one after another, so fewer tiles per split is a
-// shorter chain: ctx 8192 takes 43 splits of 3 tiles, ctx 16384 52 of 5.
-int tagged_split_len(int n) {
-    const int tiles = (n + kTile - 1) / kTile;
-    const int per = (tiles + 63) / 64;
-    return (per < 1 ? 1 : per > 16 ? 16 : per) * kTile;
-}
+// Positions per attention split on this schedule: a workgroup holds the
+// split's K rows and V^T in LDS, one 64-position tile per compute wave.
+int tagged_split_len(int) { return kAttP; }
 
 // Hubs for a grid of `grid` workgroups: one per XCD when the grid is large
 // enough to spare them.
