@@ -18,10 +18,6 @@ hipError_t launch_lm_layer(hipStream_t st, const StepArgs& a, const LayerDev& Ld
 hipError_t launch_lm_step_kernels(hipStream_t st, const StepArgs& a, const LayerDev* host_layers);
 hipError_t launch_lm_step_tagged(hipStream_t st, const StepArgs& a, int q4, int grid, bool cooperative);
 hipError_t launch_copy_token(hipStream_t st, const int32_t* src, int32_t* dst);
-hipError_t launch_lm_step_pipe(hipStream_t st, const StepArgs& a, int q4, int grid, bool cooperative);
-bool pipe_plan(int grid, int nhubs, int H, int I, int heads, int kvh, int hd, int n_layers, int pos, int up_workers,
-               int* nb, int* nq, int* nu, int* ns, int* split_len);
-int pipe_max_splits();
 int tagged_grid(int num_cus);
 int tagged_split_len(int n);
 int tagged_hubs(int grid);
@@ -61,21 +57,6 @@ bool alive(const ming_ctx* c) { return c && c->alive; }
 // workgroups read one normalised vector (q/k/v, gate/up, head); o and down
 // (64 workgroups each) are faster staging their inputs themselves.
 // MING_LM_HUB_STAGES (a decimal bit mask) overrides the choice.
-// Gate/up workers of the pipelined schedule (MING_LM_PIPE_UP, default: every
-// workgroup of that set).
-int pipe_up_workers() {
-    static const int v = [] {
-        const char* e = std::getenv("MING_LM_PIPE_UP");
-        if (e && *e) {
-            char* end = nullptr;
-            const long x = std::strtol(e, &end, 10);
-            if (end && *end == '\0' && x > 0 && x < 100000) return (int)x;
-        }
-        return 0;
-    }();
-    return v;
-}
-
 int hub_stages() {
     static const int v = [] {
         const char* e = std::getenv("MING_LM_HUB_STAGES");
@@ -243,7 +224,6 @@ struct ming_lm_model {
     DevBuf x, x1, att, qkv, hh, part, hidden, amax_v, amax_i;
     DevBuf tx, tq, ta, tx1, th, counters;  // tagged hand-off buffers, arrival counters
     DevBuf img, hflag, hubtab;             // per-XCD hub images, their flags, hub XCC ids
-    DevBuf tp;                             // tagged attention partials of the pipelined schedule
     int img_stride = 0, nflag = 0;
 };
 
@@ -728,10 +708,7 @@ int ming_lm_model_create(ming_ctx* ctx, const ming_lm_cfg* cfg, const ming_lm_la
     if (e == hipSuccess) e = m->img.ensure(sizeof(uint32_t) * (size_t)kMaxHubs * kImgSlots * m->img_stride);
     if (e == hipSuccess) e = m->hflag.ensure(sizeof(uint32_t) * (size_t)kMaxHubs * m->nflag);
     if (e == hipSuccess) e = m->hubtab.ensure(sizeof(uint64_t) * 32);
-    const int grp = cfg->heads / cfg->kv_heads;
-    if (e == hipSuccess)
-        e = m->tp.ensure(sizeof(uint64_t) * (size_t)L * cfg->kv_heads * pipe_max_splits() * grp * (cfg->head_dim + 2));
-    for (DevBuf* b : {&m->tx, &m->tq, &m->ta, &m->tx1, &m->th, &m->counters, &m->img, &m->hflag, &m->hubtab, &m->tp})
+    for (DevBuf* b : {&m->tx, &m->tq, &m->ta, &m->tx1, &m->th, &m->counters, &m->img, &m->hflag, &m->hubtab})
         if (e == hipSuccess) e = hipMemset(b->p, 0, b->bytes);
     if (e != hipSuccess) {
         ming_lm_model_destroy(m);
@@ -746,7 +723,7 @@ int ming_lm_model_destroy(ming_lm_model* m) {
     if (!m) return MING_E_NOT_INIT;
     if (m->d_layers) (void)hipFree(m->d_layers);
     for (DevBuf* b : {&m->x, &m->x1, &m->att, &m->qkv, &m->hh, &m->part, &m->hidden, &m->amax_v, &m->amax_i,
-                      &m->tx, &m->tq, &m->ta, &m->tx1, &m->th, &m->counters, &m->img, &m->hflag, &m->hubtab, &m->tp})
+                      &m->tx, &m->tq, &m->ta, &m->tx1, &m->th, &m->counters, &m->img, &m->hflag, &m->hubtab})
         b->release();
     delete m;
     return MING_OK;
@@ -767,7 +744,7 @@ int ming_lm_model_profile_shape(ming_lm_model* m, int32_t* n_stamps, int32_t* gr
 
 int ming_lm_model_set_mode(ming_lm_model* m, int32_t mode) {
     if (!m) return MING_E_NOT_INIT;
-    if (mode < MING_LM_AUTO || mode > MING_LM_PIPELINED) return set_err(m->ctx, MING_E_ARG, "unknown mode");
+    if (mode < MING_LM_AUTO || mode > MING_LM_PERSISTENT_DIRECT) return set_err(m->ctx, MING_E_ARG, "unknown mode");
     m->mode = mode;
     return MING_OK;
 }
@@ -849,51 +826,6 @@ static int lm_step_impl(ming_ctx* ctx, ming_lm_model* m, const int32_t* token_de
     const bool persistent = want_persistent && fits;
     if (want_persistent && m->mode != MING_LM_AUTO && !fits)
         return set_err(ctx, MING_E_UNSUPPORTED, "lm_step: context too long for the persistent schedule");
-    // the pipelined schedule, on request only: at ctx 2048 it measures 640-650 us per token against the
-    // tagged schedule's 580 us (its stage work runs longer while the next layer's loads are in flight)
-    int pnb = 0, pnq = 0, pnu = 0, pns = 0, psl = 0;
-    const bool want_pipe = m->mode == MING_LM_PIPELINED;
-    const bool pipe_fits = m->pgrid > 0 &&
-                           pipe_plan(m->pgrid, tagged_hubs(m->pgrid), c->hidden, c->inter, c->heads, c->kv_heads,
-                                     c->head_dim, c->n_layers, kv->len, pipe_up_workers(), &pnb, &pnq, &pnu, &pns,
-                                     &psl);
-    if (m->mode == MING_LM_PIPELINED && !pipe_fits)
-        return set_err(ctx, MING_E_UNSUPPORTED, "lm_step: shape or context outside the pipelined schedule");
-    if (want_pipe && pipe_fits) {
-        if (ctx->timeout_seen) {  // a timed-out step may have left the head's arrival counter raised
-            if ((st = hip_check(ctx, hipMemsetAsync(m->counters.p, 0, m->counters.bytes, ctx->stream),
-                                "reset counters")))
-                return st;
-            ctx->timeout_seen = false;
-        }
-        a.tx = static_cast<uint64_t*>(m->tx.p);
-        a.tq = static_cast<uint64_t*>(m->tq.p);
-        a.ta = static_cast<uint64_t*>(m->ta.p);
-        a.tx1 = static_cast<uint64_t*>(m->tx1.p);
-        a.th = static_cast<uint64_t*>(m->th.p);
-        a.tp = static_cast<uint64_t*>(m->tp.p);
-        a.counters = static_cast<int32_t*>(m->counters.p);
-        a.tstamp = m->tstamp;
-        a.nhubs = tagged_hubs(m->pgrid);
-        a.img = static_cast<uint32_t*>(m->img.p);
-        a.img_stride = m->img_stride;
-        a.hflag = static_cast<uint32_t*>(m->hflag.p);
-        a.nflag = m->nflag;
-        a.hubtab = static_cast<uint64_t*>(m->hubtab.p);
-        a.pipe_nb = pnb;
-        a.pipe_nq = pnq;
-        a.pipe_nu = pnu;
-        a.pipe_ns = pns;
-        a.pipe_max_splits = pipe_max_splits();
-        a.split_len = psl;
-        a.epoch = ++m->epoch;
-        if (a.epoch == 0) a.epoch = ++m->epoch;
-        st = hip_check(ctx, launch_lm_step_pipe(ctx->stream, a, m->head.kind == 1, m->pgrid, !ctx->exclusive),
-                       "lm_step pipelined launch");
-        if (st) return st;
-        kv->len += 1;
-        return MING_OK;
-    }
     if (persistent) {
         if (ctx->timeout_seen) {  // a timed-out step may have left arrival counters raised
             if ((st = hip_check(ctx, hipMemsetAsync(m->counters.p, 0, m->counters.bytes, ctx->stream),

@@ -77,13 +77,6 @@ struct StepArgs {
     uint32_t* hflag;          // [kMaxHubs][nflag] epoch of each published image
     int nflag;                // flag words per hub (>= 4 * n_layers + 1)
     uint64_t* hubtab;         // [kMaxHubs] tagged XCC id of each hub
-    // Pipelined schedule (lm_pipe.hip): disjoint workgroup sets per stage pair.
-    uint64_t* tp;             // [n_layers][kvh][pipe_max_splits][grp][hd + 2] tagged attention partials (f32 bits)
-    int pipe_nb;              // o_proj / down workers (the first workers)
-    int pipe_nq;              // q/k/v workers (the first workers after those)
-    int pipe_nu;              // gate/up workers (from the same start as q/k/v)
-    int pipe_ns;              // attention splits per kv head (one workgroup each, the last workers)
-    int pipe_max_splits;      // split axis of tp
 };
 
 // Stages of the persistent schedule, as bits of StepArgs::hub_stages.

@@ -150,19 +150,14 @@ def check_step_teacher_forced(ming, m, cache_before, cache_after, orc, pos, toke
     return worst, float(d.max()), ram, margin
 
 
-MODES = {"kernels": "LM_KERNELS", "persistent": "LM_PERSISTENT", "direct": "LM_PERSISTENT_DIRECT",
-         "pipelined": "LM_PIPELINED"}
-# the pipelined schedule covers up to 32 attention splits of 8 pages per kv head
-PIPE_MAX_CTX = 32 * 8 * 64 - 1
+MODES = {"kernels": "LM_KERNELS", "persistent": "LM_PERSISTENT", "direct": "LM_PERSISTENT_DIRECT"}
 
 
-@pytest.mark.parametrize("mode", ["kernels", "persistent", "direct", "pipelined"])
+@pytest.mark.parametrize("mode", ["kernels", "persistent", "direct"])
 @pytest.mark.parametrize("ctx_len", [0, 1, 63, 64, 512, 2048, 4095, 8192, 16384])
 def test_lm_step_matches_oracle(ming, ctx, q4_model, ctx_len, mode):
     S = syn_mod(ming)
     syn, m, orc = q4_model
-    if mode == "pipelined" and ctx_len > PIPE_MAX_CTX:
-        pytest.skip("beyond the pipelined schedule's 32 attention splits per kv head")
     md = getattr(ming, MODES[mode])
     print(f"[lm_step] ctx={ctx_len} mode={mode}", flush=True)
     cache = S.KvCache(syn.spec, ctx_len + 4)
@@ -221,7 +216,7 @@ def bf16_model(ming, ctx):
     m.close()
 
 
-@pytest.mark.parametrize("mode", ["kernels", "persistent", "direct", "pipelined"])
+@pytest.mark.parametrize("mode", ["kernels", "persistent", "direct"])
 def test_bf16_lm_step_matches_oracle(ming, ctx, bf16_model, mode):
     """bf16 weights (the persistent kernel's second instance, plain bf16 rows
     instead of 4-bit chunks) at hidden 896, 14/2 heads, inter 4864, vocab
@@ -248,7 +243,7 @@ def test_schedules_agree_and_deterministic(ming, ctx, q4_model):
     S = syn_mod(ming)
     syn, m, _ = q4_model
     outs = {}
-    for mode in (ming.LM_KERNELS, ming.LM_PERSISTENT, ming.LM_PERSISTENT_DIRECT, ming.LM_PIPELINED):
+    for mode in (ming.LM_KERNELS, ming.LM_PERSISTENT, ming.LM_PERSISTENT_DIRECT):
         for rep in range(3):
             cache = S.KvCache(syn.spec, 1100)
             cache.fill_random(1000, seed=7)
@@ -262,8 +257,6 @@ def test_schedules_agree_and_deterministic(ming, ctx, q4_model):
     k, p, d = outs[ming.LM_KERNELS], outs[ming.LM_PERSISTENT], outs[ming.LM_PERSISTENT_DIRECT]
     assert p[0] == d[0] and np.array_equal(p[1], d[1]) and np.array_equal(p[2], d[2]), "hubs change the result"
     assert_close_bf16(p[1], k[1], "persistent vs kernels hidden", atol=0.2, rtol=0.1)
-    q = outs[ming.LM_PIPELINED]
-    assert_close_bf16(q[1], k[1], "pipelined vs kernels hidden", atol=0.2, rtol=0.1)
 
 
 def test_ordinary_launch_matches_cooperative(ming, ctx, q4_model):
@@ -273,7 +266,7 @@ def test_ordinary_launch_matches_cooperative(ming, ctx, q4_model):
     S = syn_mod(ming)
     syn, m, _ = q4_model
     try:
-        for mode in (ming.LM_PERSISTENT, ming.LM_PERSISTENT_DIRECT, ming.LM_PIPELINED):
+        for mode in (ming.LM_PERSISTENT, ming.LM_PERSISTENT_DIRECT):
             got = {}
             for excl in (False, True):
                 ctx.set_exclusive(excl)
