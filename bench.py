@@ -68,6 +68,13 @@ Two more workloads print a line of the same form (`--workload`):
         batched chunk of up to 512 rows over a paged cache, causal); value is prompt
         tokens/s; roofline over the weights once per chunk plus the causal
         KV reads and appends.
+  c1    config 1's generate job per step: the bf16 Qwen2-0.5B-shaped LM
+        (random-init bf16 weights N(0, 0.02), vocab 151936), a 64-token prompt
+        of uniform ids fed one position at a time, then 128 greedy ids with the
+        argmax fed back on the device (ming_lm_generate), the cache emptied at
+        the start of each job; value is greedy ids/s over the whole job;
+        roofline over the bf16 weight bytes of each of the job's 191 steps
+        plus its KV reads and appends.
 """
 import argparse
 import importlib
@@ -87,6 +94,8 @@ METRIC_C4 = "adaLN flow-head samples/s (config 4: 4 blocks, hidden 896, 4-frame 
 METRIC_DIT = "DiT block kernels achieved GB/s (fused.single A-D, weights rotated through HBM, bf16)"
 METRIC_GEMV = "4-bit GEMV achieved GB/s (MLX affine g64, [896x151936] head shape, weights rotated through HBM)"
 GEMV_SHAPES = [(896, 896), (896, 128), (896, 4864), (4864, 896), (896, 151936)]  # [in, out]
+METRIC_C1 = ("LM generate greedy tokens/s (config 1: bf16 Qwen2-0.5B, 64-token prompt + 128 greedy steps, bs1) "
+             "+ achieved HBM GB/s")
 METRIC_LOOP = "TTS tokens/s (sampleLatents step: flow head + aggregator + 4-bit LM decode + stop head) + achieved GB/s"
 HBM_PEAK_GBS = 8000.0
 # the 4-bit paths' arithmetic: MLX-affine 4-bit weights, bf16 activations, f32 accumulation
@@ -96,7 +105,7 @@ DTYPE_W4 = "w4a16 (4-bit weights, bf16 activations, f32 accumulate)"
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--workload", choices=["lm", "cfm", "c4", "loop", "server", "prefill", "vae", "gemv", "dit"],
+    p.add_argument("--workload", choices=["lm", "c1", "cfm", "c4", "loop", "server", "prefill", "vae", "gemv", "dit"],
                    default="lm")
     p.add_argument("--shape", type=int, default=-1, help="gemv workload: one shape of the sweep (index), default all")
     p.add_argument("--rotate-mb", type=float, default=512.0, help="gemv and dit workloads: distinct weight bytes each kernel cycles through")
@@ -139,6 +148,8 @@ def main():
         return bench_prefill(args)
     if args.workload == "vae":
         return bench_vae(args)
+    if args.workload == "c1":
+        return bench_c1(args)
     if args.workload == "gemv":
         return bench_gemv(args)
     if args.workload == "dit":
@@ -543,6 +554,118 @@ def bench_prefill(args):
                      cpu, "synthetic (random-init N(0,0.02) weights quantized to MLX affine 4-bit/g64)",
                      dtype=DTYPE_W4)
     close_all(batch, m, ctx)
+    print(json.dumps(line), flush=True)
+
+
+C1_PROMPT, C1_STEPS = 64, 128
+
+
+def c1_bytes_per_step(spec, pos):
+    """Algorithmic HBM bytes of one bf16 decode step at position pos: every
+    linear and the tied head at 2 B/param, biases and norms, the KV read of
+    the pos cached rows and the one-row append."""
+    H, I, kvd, L = spec.hidden, spec.inter, spec.kvd, spec.n_layers
+    per_layer = H * H * 2 + 2 * kvd * H + 3 * H * I
+    small = L * (2 * H + (H + 2 * kvd)) * 2 + H * 2
+    kv_row = L * 2 * kvd * 2
+    return (per_layer * L + spec.vocab * H) * 2 + small + kv_row * pos + kv_row
+
+
+def bench_c1(args):
+    import numpy as np
+    import torch
+
+    ming = importlib.import_module("ming-tts-serve_amd")
+    S = importlib.import_module("ming-tts-serve_amd.synthetic")
+    spec = S.QWEN2_05B
+    ctx = ming.Context(0)
+    ctx.set_exclusive(not args.cooperative)
+    t0 = time.time()
+    syn = S.SyntheticLm(ctx, spec, seed=0, quant=False)
+    m = syn.model()
+    m.set_mode({"auto": ming.LM_AUTO, "kernels": ming.LM_KERNELS, "persistent": ming.LM_PERSISTENT,
+                "direct": ming.LM_PERSISTENT_DIRECT}[args.mode])
+    ids = [int(t) for t in ming.synth_uniform_i32(0, "c1.prompt", C1_PROMPT, spec.vocab)]
+    ptok = torch.tensor(ids, dtype=torch.int32, device="cuda")
+    cache = S.KvCache(spec, C1_PROMPT + C1_STEPS)
+    toks = torch.zeros(C1_STEPS + 1, dtype=torch.int32, device="cuda")
+    print(f"[bench c1] setup {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    nsteps = C1_PROMPT + C1_STEPS - 1
+    # events around every step of the timed jobs (the library launches on torch's current stream)
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nsteps)]
+          for _ in range(args.steps)]
+
+    def job(evs=None):
+        cache.kv.len = 0
+        toks[0:1].copy_(ptok[C1_PROMPT - 1:])
+        for i in range(nsteps):
+            if evs:
+                evs[i][0].record()
+            if i < C1_PROMPT - 1:  # prompt rows
+                m.step(cache.kv, token=ptok[i:i + 1])
+            else:  # one greedy step: argmax of step k is the input of step k + 1, on the device
+                k = i - (C1_PROMPT - 1)
+                m.generate(cache.kv, 1, toks[k:])
+            if evs:
+                evs[i][1].record()
+
+    for _ in range(args.warmup):
+        job()
+    torch.cuda.synchronize()
+    first = toks.cpu().numpy().copy()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for j in range(args.steps):
+        job(ev[j])
+    e1.record()
+    torch.cuda.synchronize()
+    ctx.sync()
+    assert cache.len == C1_PROMPT + C1_STEPS - 1
+    if args.warmup:
+        assert np.array_equal(first, toks.cpu().numpy()), "greedy ids differ between jobs"
+    ms = e0.elapsed_time(e1) / args.steps
+    per = np.array([[a.elapsed_time(b) for a, b in evj] for evj in ev])  # ms per step launch
+    launch_ms = float(per.mean())
+    prompt_ms = float(per[:, :C1_PROMPT - 1].sum(axis=1).mean())
+    nbytes = sum(c1_bytes_per_step(spec, p) for p in range(nsteps))
+    achieved = nbytes / nsteps / (launch_ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        from lmkit import oracle_model, oracle_step
+
+        oracle.set_threads(host_threads())
+        cfg, layers, norm, head = oracle_model(syn)
+        kc = np.zeros((spec.n_layers, spec.kv_heads, C1_PROMPT + C1_STEPS, spec.head_dim), np.uint16)
+        vc = np.zeros_like(kc)
+        done, feed, t1 = 0, ids[0], time.time()
+        while done < C1_PROMPT + C1_STEPS - 1:  # the same job, one position at a time, until the bound
+            am, _, _, _, _ = oracle_step(cfg, layers, norm, head, oracle.embed(head, feed), done, kc, vc)
+            done += 1
+            feed = ids[done] if done < C1_PROMPT else am
+            if time.time() - t1 >= args.cpu_seconds:
+                break
+        dt = time.time() - t1
+        cpu = {"value": round(done / dt, 3), "unit": "tokens/s (steps of the job)", "cores": oracle.get_threads(),
+               "kind": "port",
+               "sample": f"the first {done} of the job's {C1_PROMPT + C1_STEPS - 1} steps (prompt rows, then greedy "
+                         f"ids fed back) ({dt:.1f} s, scalar C restatement of the MLX CPU graph, OpenMP over output "
+                         f"rows); the GPU's steps/s over the whole job is {(C1_PROMPT + C1_STEPS - 1) * 1000.0 / ms:.1f}"}
+    line = base_line(METRIC_C1, C1_STEPS * 1000.0 / ms, "tokens/s", args, ms,
+                     {"workload": f"config 1 generate job: bf16 Qwen2-0.5B-shaped LM (24 layers, hidden 896, 14/2 heads, "
+                                  f"inter 4864, vocab 151936, tied head), {C1_PROMPT}-token uniform prompt (seed 0) fed "
+                                  f"one position at a time, then {C1_STEPS} greedy ids fed back on the device; one job "
+                                  f"per step, cache emptied at its start",
+                      "global_batch": 1, "seq_len": C1_PROMPT + C1_STEPS, "schedule": args.mode,
+                      "prompt_ms": round(prompt_ms, 3),
+                      "greedy_steps_tok_s": round(C1_STEPS * 1000.0 / (ms - prompt_ms), 2),
+                      "steps_per_job": C1_PROMPT + C1_STEPS - 1},
+                     {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                      "bytes_per_launch": int(round(nbytes / nsteps)), "launch_ms": round(launch_ms, 5),
+                      "bytes_per_job": nbytes},
+                     cpu, "synthetic (random-init bf16 weights N(0,0.02), uniform prompt ids)")
+    close_all(m, ctx)
     print(json.dumps(line), flush=True)
 
 
