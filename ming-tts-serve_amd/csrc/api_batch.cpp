@@ -80,7 +80,7 @@ int ming_lm_batch_create(ming_ctx* ctx, ming_lm_model* m, int32_t max_seqs, int3
     grab(b->hh, L * S * b->I * 2);
     grab(b->xs, Mp * kmax * 2);
     grab(b->xsum, Mp * (kmax / 64) * 4);
-    const size_t nblk = ((size_t)b->V + 63) / 64;  // column blocks of the head GEMM
+    const size_t nblk = ((size_t)b->V + 31) / 32;  // column blocks of the head GEMM (at most)
     grab(b->pmax, S * nblk * 4);
     grab(b->pidx, S * nblk * 4);
     grab(b->hid, S * b->H * 2);
@@ -245,7 +245,7 @@ int ming_lm_batch_step(ming_lm_batch* b, int32_t n_seq, const int32_t* tokens_de
         }
         e = launch_qgemm_epi(st, a, QE_PLAIN);
         if (e == hipSuccess && argmax_out)
-            e = launch_argmax_partials(st, a.pmax, a.pidx, (b->V + 63) / 64, n_seq, argmax_out);
+            e = launch_argmax_partials(st, a.pmax, a.pidx, qgemm_argmax_blocks(n_seq, H, b->V), n_seq, argmax_out);
     }
     if (e != hipSuccess) return hip_check(ctx, e, "lm_batch_step launch");
     b->last_n = n_seq;

@@ -83,7 +83,9 @@ hipError_t launch_quantize(hipStream_t st, const uint16_t* w, int64_t N, int64_t
 // is filled by the launcher.  epi is a QEpi.
 hipError_t launch_qgemm_epi(hipStream_t st, QgemmArgs a, int epi);
 // Per-row argmax of n rows from the wide GEMM's partials [n][nblk]
-// (nblk = ceil(N / 64) column blocks).
+// (nblk = qgemm_argmax_blocks: the column blocks of the launch for that shape,
+// at most ceil(N / 32)).
+int qgemm_argmax_blocks(int M, int K, int N);
 hipError_t launch_argmax_partials(hipStream_t st, const float* pmax, const int32_t* pidx, int nblk, int n,
                                   int32_t* out);
 // Rows [0, Mp) of x [M][ldx] (Mp = M rounded up to 16; rows >= M zero) staged

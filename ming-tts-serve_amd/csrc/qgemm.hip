@@ -597,6 +597,281 @@ hipError_t launch_k(hipStream_t st, const QgemmArgs& a, int kw_in = 0) {
     return hipGetLastError();
 }
 
+// ---- the wide head, at most 64 rows --------------------------------------------
+// QE_PLAIN with N >= 16384 or argmax partials (the LM head) and M <= 64, for
+// K = 896 or 1024: each workgroup (one per CU, W waves) copies the staged
+// activations of all rows into LDS once (rows padded to 9 uint4 so that a
+// 16-lane b128 read hits 8 distinct 16-byte bank groups), then every wave
+// streams units of 32 weight columns (2 column tiles x all MT row tiles), unit
+// u = the wave's grid index + k x the grid's waves.  A wave's weights are read
+// once from HBM and its A operands come from LDS, shared by its two column
+// tiles.  A wave's (unit, group) items run in order through a ring of R
+// groups in registers: item i + R's load is issued as soon as item i's slot
+// is read, unconditionally (past the end the last item is loaded again), and
+// held there by a scheduling barrier, so R groups are in flight.  The wave
+// index is read as a scalar, so the item loop's control is uniform (with a
+// divergent loop the compiler waits for every load at each step).  Only two
+// stores leave per unit when no logits are asked for (the argmax partials,
+// one row slot per lane), so the wait counter's bound never forces a full
+// wait.  Per row and column the arithmetic is group_mma's over the groups in
+// order with one K slice, exactly as qgemm_kernel computes this shape, so the
+// logits are the same bits; the argmax partials cover 32 columns each.
+constexpr int kHeadNW = 2;     // column tiles per unit
+constexpr int kHeadRow = 9;    // uint4 per staged row in LDS (8 + 1 of padding)
+
+__host__ __device__ constexpr size_t head_lds_bytes(int G, int Mp) {
+    return (size_t)G * Mp * kHeadRow * 16 + (size_t)G * Mp * 4;
+}
+
+
+template <int CTRL>
+__device__ __forceinline__ void head_argmax_step(float& best, int& idx) {
+    const float ov = dpp<CTRL>(best);
+    const int oi = __builtin_amdgcn_update_dpp(0, idx, CTRL, 0xf, 0xf, false);
+    if (ov > best || (ov == best && oi < idx)) {
+        best = ov;
+        idx = oi;
+    }
+}
+
+struct HeadGroup {
+    uint2 wq[kHeadNW];
+    float sc[kHeadNW], bi[kHeadNW];
+};
+
+// OUT: the logits are written (a.y / a.yf); without, only the argmax partials leave the kernel.
+// W waves per workgroup, R groups in flight per wave.
+template <int MT, int G, bool OUT, int W, int R>
+__global__ __launch_bounds__(64 * W) void qgemm_head_kernel(QgemmArgs a) {
+    extern __shared__ uint4 hl[];  // As [G][Mp][kHeadRow] uint4, then Xs [G][Mp] f32
+    constexpr int Mp = 16 * MT, KW8 = 8 * G;
+    static_assert(R >= 2 && R <= 12, "ring slots named below");
+    // the wave index as a scalar: the unit loop's bounds are then uniform, its branches scalar
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x % kWave, c = lane % 16, j = lane / 16;
+    const QSeg& S = a.seg[0];
+    const int N = S.N, units = (N + 16 * kHeadNW - 1) / (16 * kHeadNW);
+    const int gw = blockIdx.x * W + wave, stride = gridDim.x * W;
+    const int my_units = gw < units ? (units - gw + stride - 1) / stride : 0;
+    const int items = my_units * G;  // (unit, group) pairs of this wave, unit-major
+    // Item it's weights into a ring slot; past the last item the last one is loaded again (unused),
+    // so that every load is unconditional and the ring's waits are static.
+    auto load = [&](int it, HeadGroup& h) {
+        it = min(it, items - 1);
+        const int u = gw + (it / G) * stride, g = it % G;
+#pragma unroll
+        for (int t = 0; t < kHeadNW; t++) {
+            const int n = min(16 * (kHeadNW * u + t) + c, N - 1);
+            h.wq[t] = ldg2(S.w + (size_t)n * KW8 + 8 * g + 2 * j);
+            h.sc[t] = bf2f(gld(S.s + (size_t)n * G + g));
+            h.bi[t] = bf2f(gld(S.b + (size_t)n * G + g));
+        }
+    };
+    HeadGroup ring[R];
+    if (items > 0) {
+#pragma unroll
+        for (int k = 0; k < R; k++) load(k, ring[k]);
+    }
+    // the staged activations of all rows into LDS
+    uint4* As = hl;
+    float* Xs = reinterpret_cast<float*>(hl + (size_t)G * Mp * kHeadRow);
+    {
+        const uint4* xs = static_cast<const uint4*>(a.xs);
+        constexpr int total = G * Mp * 8, nsum = G * Mp, T = 64 * W, U = 8;
+        const int t = threadIdx.x;
+        float sv[(nsum + T - 1) / T];
+#pragma unroll
+        for (int k = 0; k < (nsum + T - 1) / T; k++)
+            if (t + k * T < nsum) sv[k] = gld(a.xsum + t + k * T);
+#pragma unroll 1
+        for (int base = 0; base < total; base += U * T) {  // passes of U loads a thread, then U stores
+            uint4 v[U];
+#pragma unroll
+            for (int k = 0; k < U; k++)
+                if (base + t + k * T < total) v[k] = ldg4(xs + base + t + k * T);
+#pragma unroll
+            for (int k = 0; k < U; k++) {
+                const int i = base + t + k * T;
+                if (i < total) As[(i / 8) * kHeadRow + i % 8] = v[k];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < (nsum + T - 1) / T; k++)
+            if (t + k * T < nsum) Xs[t + k * T] = sv[k];
+    }
+    __syncthreads();
+    if (items == 0) return;
+    const uint32_t mask = in_reg(0x000f000fu), magic = in_reg(kQ4Magic);
+    f32x4_t acc[MT][kHeadNW];
+    // One item: group g of its unit from ring slot h, whose next item is loaded as soon as the slot
+    // is read; the unit's epilogue after its last group.
+    auto step = [&](int it, HeadGroup& h) __attribute__((always_inline)) {
+        const int g = it % G;
+        if (g == 0) {
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int t = 0; t < kHeadNW; t++) acc[mt][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        bf16x8_t b[kHeadNW][2];
+        float sc[kHeadNW], off[kHeadNW];
+#pragma unroll
+        for (int t = 0; t < kHeadNW; t++) {
+            b[t][0] = unpack_b(h.wq[t].x, mask, magic);
+            b[t][1] = unpack_b(h.wq[t].y, mask, magic);
+            sc[t] = h.sc[t];
+            off[t] = fmaf(-128.0f, h.sc[t], h.bi[t]);
+        }
+        load(it + R, h);
+        // the loads stay here, six items ahead of their use (the scheduler would sink them to the
+        // use to save registers, which serialises the ring)
+        __builtin_amdgcn_sched_barrier(0);
+        // row tile by row tile, tile mt + 1's MFMAs issued before tile mt is folded (group_mma's
+        // arithmetic: two MFMAs from zero, then s * sum + (b - 128 s) * sum_k x_k)
+        f32x4_t agA[kHeadNW], agB[kHeadNW];  // two row tiles' MFMA sums in flight (named: no indexing)
+        float4 xsA, xsB;
+        auto issue = [&](int mt, f32x4_t (&dst)[kHeadNW], float4& xs4) __attribute__((always_inline)) {
+            const uint4* ar = As + (size_t)(g * Mp + 16 * mt + c) * kHeadRow + 2 * j;
+            const bf16x8_t a0 = as_a(ar[0]), a1 = as_a(ar[1]);
+            xs4 = *reinterpret_cast<const float4*>(Xs + g * Mp + 16 * mt + 4 * j);
+#pragma unroll
+            for (int t = 0; t < kHeadNW; t++)
+                dst[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[t][0], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < kHeadNW; t++)
+                dst[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[t][1], dst[t], 0, 0, 0);
+        };
+        auto fold = [&](int mt, const f32x4_t (&src)[kHeadNW], const float4& xs4) __attribute__((always_inline)) {
+            const float xv[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
+#pragma unroll
+            for (int t = 0; t < kHeadNW; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[mt][t][r] = fmaf(off[t], xv[r], fmaf(sc[t], src[t][r], acc[mt][t][r]));
+        };
+        issue(0, agA, xsA);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt += 2) {
+            if (mt + 1 < MT) issue(mt + 1, agB, xsB);
+            fold(mt, agA, xsA);
+            if (mt + 1 < MT) {
+                if (mt + 2 < MT) issue(mt + 2, agA, xsA);
+                fold(mt + 1, agB, xsB);
+            }
+        }
+        if (g + 1 < G) return;
+        // the unit's epilogue: g acc, the logits, one argmax partial per row.  Lane c of each
+        // 16-lane group keeps the partial of row slot c (row 16 (c / 4) + 4 j + c % 4), so the
+        // partials leave in one store per array: few stores keep the ring's waits exact (the
+        // wait counter holds at most 63 outstanding operations).
+        const int u = gw + (it / G) * stride;
+        float keep_v = -INFINITY;
+        int keep_i = 0x7fffffff;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = 16 * mt + 4 * j + r;
+                float best = -INFINITY;
+                int idx = 0x7fffffff;
+#pragma unroll
+                for (int t = 0; t < kHeadNW; t++) {
+                    const float v = acc[mt][t][r] * S.gscale;
+                    const int n = 16 * (kHeadNW * u + t) + c;
+                    if (n >= N) continue;
+                    if (OUT && m < a.M) {
+                        const size_t o = (size_t)m * a.ldy + S.col0 + n;
+                        if (a.y) gst(a.y + o, f2bf(v));
+                        if (a.yf) gst(a.yf + o, v);
+                    }
+                    if (v > best) {
+                        best = v;
+                        idx = n;
+                    }
+                }
+                // the 16 lanes of one j (one DPP row) hold one row: the symmetric DPP steps of
+                // team_reduce give every lane the row's maximum, lowest index on ties
+                head_argmax_step<0xB1>(best, idx);   // quad_perm [1,0,3,2]
+                head_argmax_step<0x4E>(best, idx);   // quad_perm [2,3,0,1]
+                head_argmax_step<0x141>(best, idx);  // row_half_mirror
+                head_argmax_step<0x140>(best, idx);  // row_mirror
+                if (c == 4 * mt + r) {
+                    keep_v = best;
+                    keep_i = idx;
+                }
+            }
+        if (a.pmax && c < 4 * MT) {
+            const int m = 16 * (c / 4) + 4 * j + c % 4;
+            if (m < a.M) {
+                gst(a.pmax + (size_t)m * a.nblk + u, keep_v);
+                gst(a.pidx + (size_t)m * a.nblk + u, keep_i);
+            }
+        }
+    };
+    for (int it = 0; it < items; it += R) {  // slots named one by one: the ring must not be indexed
+#define MING_HEAD_STEP(K)                     \
+    if (K < R) {                              \
+        if (it + K >= items) break;           \
+        step(it + K, ring[K % R]);            \
+    }
+        MING_HEAD_STEP(0) MING_HEAD_STEP(1) MING_HEAD_STEP(2) MING_HEAD_STEP(3)
+        MING_HEAD_STEP(4) MING_HEAD_STEP(5) MING_HEAD_STEP(6) MING_HEAD_STEP(7)
+        MING_HEAD_STEP(8) MING_HEAD_STEP(9) MING_HEAD_STEP(10) MING_HEAD_STEP(11)
+#undef MING_HEAD_STEP
+    }
+}
+
+int head_grid() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+bool head_fits(const QgemmArgs& a) { return a.nseg == 1 && a.M <= 64 && (a.K == 896 || a.K == 1024); }
+
+template <int MT, int G, bool OUT, int W, int R>
+hipError_t launch_head_g(hipStream_t st, QgemmArgs a) {
+    static_assert(head_lds_bytes(G, 16 * MT) <= 150 * 1024, "staged rows fit in LDS");
+    const int units = (a.seg[0].N + 16 * kHeadNW - 1) / (16 * kHeadNW);
+    a.nblk = units;
+    const size_t lds = head_lds_bytes(G, 16 * MT);
+    static bool raised[64] = {false};  // the kernel's LDS limit, raised once per device
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (!raised[dev]) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&qgemm_head_kernel<MT, G, OUT, W, R>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+        if (e != hipSuccess) return e;
+        raised[dev] = true;
+    }
+    const int grid = min(head_grid(), (units + W - 1) / W);
+    hipLaunchKernelGGL((qgemm_head_kernel<MT, G, OUT, W, R>), dim3(grid), dim3(64 * W), lds, st, a);
+    return hipGetLastError();
+}
+
+template <int G, bool OUT>
+hipError_t launch_head_k(hipStream_t st, const QgemmArgs& a) {
+    const int mt = (a.M + 15) / 16;
+    if (mt == 1) return launch_head_g<1, G, OUT, 8, 6>(st, a);
+    if (mt == 2) return launch_head_g<2, G, OUT, 8, 6>(st, a);
+    if (mt == 3) return launch_head_g<3, G, OUT, 8, 6>(st, a);
+    // four row tiles: 12 waves (3 a SIMD) with four groups in flight each measured 56.0 us at
+    // N = 151936, K = 896 against 57.6 for 8 waves x 6 groups, 58.0 for 12 x 6, 65-67 for 8 x 10
+    // and 8 x 12, 77 for 16 x 4 (spills)
+    return launch_head_g<4, G, OUT, 12, 4>(st, a);
+}
+
+hipError_t launch_head(hipStream_t st, const QgemmArgs& a) {
+    const bool out = a.y || a.yf;
+    if (a.K == 896) return out ? launch_head_k<14, true>(st, a) : launch_head_k<14, false>(st, a);
+    return out ? launch_head_k<16, true>(st, a) : launch_head_k<16, false>(st, a);
+}
+
 // row tiles per workgroup: 2 when MTMAX allows and the row-tile count is even, else 1
 template <int NW, int GPW, int KWMAX, int EPI, int MTMAX>
 hipError_t launch_mt(hipStream_t st, const QgemmArgs& a) {
@@ -643,8 +918,9 @@ hipError_t launch_qgemm_epi(hipStream_t st, QgemmArgs a, int epi) {
     };
     switch (epi) {
         case QE_PLAIN:
-            if (a.nseg == 1 && (a.seg[0].N >= 16384 || a.pmax)) {  // argmax partials: blocks of 64 columns
-                set_blocks(64);
+            if (a.nseg == 1 && (a.seg[0].N >= 16384 || a.pmax)) {
+                if (head_fits(a)) return launch_head(st, a);  // argmax partials: blocks of 32 columns
+                set_blocks(64);                               // argmax partials: blocks of 64 columns
                 a.nblk = a.blocks[0];
                 return launch_mt<4, 0, 1, QE_PLAIN, 2>(st, a);
             }
@@ -711,6 +987,14 @@ __global__ __launch_bounds__(256) void argmax_partials_kernel(const float* __res
             }
         gst(out + blockIdx.x, idx == 0x7fffffff ? 0 : idx);
     }
+}
+
+int qgemm_argmax_blocks(int M, int K, int N) {
+    QgemmArgs a{};
+    a.M = M;
+    a.K = K;
+    a.nseg = 1;
+    return head_fits(a) ? (N + 16 * kHeadNW - 1) / (16 * kHeadNW) : (N + 63) / 64;
 }
 
 hipError_t launch_argmax_partials(hipStream_t st, const float* pmax, const int32_t* pidx, int nblk, int n,

@@ -321,8 +321,8 @@ def test_prefill_matches_oracle(ming, ctx, small):
 def test_prefill_512_row_chunk_equals_64_row_chunks(ming, ctx, qwen):
     """The Qwen shape: a 300-row prompt after 40 cached rows through a batch of
     512 rows (one chunk: every GEMM call has 300 rows) equals the same prompt
-    through 64-row chunks bit for bit -- hidden rows and the cache (a GEMM of
-    more than 64 rows splits K exactly as one of <= 64 rows) -- and 4 rows
+    through 64-row chunks bit for bit -- hidden rows, the cache, logits and
+    ids (a GEMM of more than 64 rows splits K exactly as one of <= 64 rows) -- and 4 rows
     spread over the prompt match the oracle layer by layer on their own inputs
     and the rows cached before them."""
     S, syn, m, b64, orc = qwen
@@ -338,12 +338,19 @@ def test_prefill_512_row_chunk_equals_64_row_chunks(ming, ctx, qwen):
         pk = S.PagedKv(spec, 1, 6, spare=2, seed=9)
         pk.fill_random([pos0], seed=36)
         hid = torch.empty((L, spec.hidden), dtype=torch.bfloat16, device="cuda")
-        bt.prefill(pk, one_row_table(pk), pos0, x_in=xd, hidden=hid)
+        lg = torch.empty((L, spec.vocab), dtype=torch.float32, device="cuda")
+        am = torch.empty(L, dtype=torch.int32, device="cuda")
+        bt.prefill(pk, one_row_table(pk), pos0, x_in=xd, hidden=hid, logits=lg, argmax=am)
         ctx.sync()
-        outs.append((hid, pk.gather(0, pos0 + L)))
-    (h0, (k0, v0)), (h1, (k1, v1)) = outs
+        outs.append((hid, pk.gather(0, pos0 + L), lg, am))
+    (h0, (k0, v0), lg0, am0), (h1, (k1, v1), lg1, am1) = outs
     assert torch.equal(h0, h1), "hidden rows differ between 512-row and 64-row chunks"
     assert np.array_equal(k0, k1) and np.array_equal(v0, v1), "cache rows differ"
+    # the head of a 300-row call (the tiled GEMM) and of <= 64-row calls (the LDS-resident head
+    # kernel, 32-column argmax partials) give the same logits and ids
+    assert torch.equal(lg0, lg1), "logits differ between the head launches for 300 and 64 rows"
+    assert torch.equal(am0, am1), "argmax differs between the head launches for 300 and 64 rows"
+    del lg0, lg1
     tr = {k: host_u16(v) for k, v in big.trace().items()}
     big.close()
     for i in (0, 99, 199, 299):
