@@ -599,13 +599,17 @@ hipError_t launch_k(hipStream_t st, const QgemmArgs& a, int kw_in = 0) {
 
 // ---- the wide head, at most 64 rows --------------------------------------------
 // QE_PLAIN with N >= 16384 or argmax partials (the LM head) and M <= 64, for
-// K = 896 or 1024: each workgroup (one per CU, W waves) copies the staged
+// K = 896: each workgroup (one per CU, W waves) copies the staged
 // activations of all rows into LDS once (rows padded to 9 uint4 so that a
 // 16-lane b128 read hits 8 distinct 16-byte bank groups), then every wave
 // streams units of 32 weight columns (2 column tiles x all MT row tiles), unit
 // u = the wave's grid index + k x the grid's waves.  A wave's weights are read
 // once from HBM and its A operands come from LDS, shared by its two column
-// tiles.  A wave's (unit, group) items run in order through a ring of R
+// tiles.  A unit's 32 rows are consecutive, so its scales (and biases) are one
+// contiguous run of 32 x 14 bf16: a wave loads the next unit's two runs with
+// one 16-byte load a lane while the current unit runs, and writes them into
+// its LDS block once the current unit's are read (two loads a unit instead of
+// four 2-byte loads a group).  A wave's (unit, group) items run in order through a ring of R
 // groups in registers: item i + R's load is issued as soon as item i's slot
 // is read, unconditionally (past the end the last item is loaded again), and
 // held there by a scheduling barrier, so R groups are in flight.  The wave
@@ -624,20 +628,30 @@ __host__ __device__ constexpr size_t head_lds_bytes(int G, int Mp) {
 }
 
 
-template <int CTRL>
-__device__ __forceinline__ void head_argmax_step(float& best, int& idx) {
-    const float ov = dpp<CTRL>(best);
-    const int oi = __builtin_amdgcn_update_dpp(0, idx, CTRL, 0xf, 0xf, false);
-    if (ov > best || (ov == best && oi < idx)) {
-        best = ov;
-        idx = oi;
-    }
+// Maximum / minimum over the 16 lanes of a DPP row (the butterfly of team_reduce: every lane
+// gets the result).
+__device__ __forceinline__ float head_row_max(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, true)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, true)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, true)));
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xf, 0xf, true)));
+}
+
+__device__ __forceinline__ int head_row_min(int v) {
+    v = min(v, __builtin_amdgcn_mov_dpp(v, 0xB1, 0xf, 0xf, true));
+    v = min(v, __builtin_amdgcn_mov_dpp(v, 0x4E, 0xf, 0xf, true));
+    v = min(v, __builtin_amdgcn_mov_dpp(v, 0x141, 0xf, 0xf, true));
+    return min(v, __builtin_amdgcn_mov_dpp(v, 0x140, 0xf, 0xf, true));
 }
 
 struct HeadGroup {
     uint2 wq[kHeadNW];
-    float sc[kHeadNW], bi[kHeadNW];
 };
+
+// A wave's scale/bias block in LDS: the bf16 scales of its unit's 32 rows x G groups, then the
+// biases (rows of a unit are consecutive, so each block is one contiguous run of 64 G bytes).
+template <int G>
+__host__ __device__ constexpr int head_sb_bytes() { return 2 * 32 * G * 2; }
 
 // OUT: the logits are written (a.y / a.yf); without, only the argmax partials leave the kernel.
 // W waves per workgroup, R groups in flight per wave.
@@ -659,22 +673,40 @@ __global__ __launch_bounds__(64 * W) void qgemm_head_kernel(QgemmArgs a) {
     auto load = [&](int it, HeadGroup& h) {
         it = min(it, items - 1);
         const int u = gw + (it / G) * stride, g = it % G;
+        // a uniform base (the group) plus a 32-bit per-lane offset (the row)
+        const char* wb = reinterpret_cast<const char*>(S.w) + 32 * g;
 #pragma unroll
         for (int t = 0; t < kHeadNW; t++) {
-            const int n = min(16 * (kHeadNW * u + t) + c, N - 1);
-            h.wq[t] = ldg2(S.w + (size_t)n * KW8 + 8 * g + 2 * j);
-            h.sc[t] = bf2f(gld(S.s + (size_t)n * G + g));
-            h.bi[t] = bf2f(gld(S.b + (size_t)n * G + g));
+            const uint32_t n = (uint32_t)min(16 * (kHeadNW * u + t) + c, N - 1);
+            h.wq[t] = ldg2(wb + (n * (uint32_t)(4 * KW8) + 8u * j));
         }
+    };
+    // unit u's scale and bias blocks, 16 bytes a lane (lanes past the block load its last word)
+    constexpr int kSbWords = 32 * G * 2 / 16;  // uint4 per block
+    auto load_sb = [&](int u, uint4& vs, uint4& vb) {
+        const size_t w0 = (size_t)u * kSbWords + min(lane, kSbWords - 1);
+        vs = ldg4(reinterpret_cast<const uint4*>(S.s) + w0);
+        vb = ldg4(reinterpret_cast<const uint4*>(S.b) + w0);
     };
     HeadGroup ring[R];
     if (items > 0) {
 #pragma unroll
         for (int k = 0; k < R; k++) load(k, ring[k]);
     }
+    uint4 nbs, nbb;  // the next unit's scale and bias blocks, in flight during a unit
+    load_sb(min(gw, units - 1), nbs, nbb);
     // the staged activations of all rows into LDS
     uint4* As = hl;
     float* Xs = reinterpret_cast<float*>(hl + (size_t)G * Mp * kHeadRow);
+    uint4* SB = reinterpret_cast<uint4*>(Xs + G * Mp) + wave * (2 * kSbWords);  // this wave's blocks
+    const uint16_t* SBs = reinterpret_cast<const uint16_t*>(SB);
+    const uint16_t* SBb = SBs + 32 * G;
+    auto store_sb = [&]() {
+        if (lane < kSbWords) {
+            SB[lane] = nbs;
+            SB[kSbWords + lane] = nbb;
+        }
+    };
     {
         const uint4* xs = static_cast<const uint4*>(a.xs);
         constexpr int total = G * Mp * 8, nsum = G * Mp, T = 64 * W, U = 8;
@@ -699,6 +731,7 @@ __global__ __launch_bounds__(64 * W) void qgemm_head_kernel(QgemmArgs a) {
         for (int k = 0; k < (nsum + T - 1) / T; k++)
             if (t + k * T < nsum) Xs[t + k * T] = sv[k];
     }
+    store_sb();
     __syncthreads();
     if (items == 0) return;
     const uint32_t mask = in_reg(0x000f000fu), magic = in_reg(kQ4Magic);
@@ -707,11 +740,13 @@ __global__ __launch_bounds__(64 * W) void qgemm_head_kernel(QgemmArgs a) {
     // is read; the unit's epilogue after its last group.
     auto step = [&](int it, HeadGroup& h) __attribute__((always_inline)) {
         const int g = it % G;
+        const int u = gw + (it / G) * stride;
         if (g == 0) {
 #pragma unroll
             for (int mt = 0; mt < MT; mt++)
 #pragma unroll
                 for (int t = 0; t < kHeadNW; t++) acc[mt][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            load_sb(u + stride < units ? u + stride : u, nbs, nbb);  // the next unit's blocks
         }
         bf16x8_t b[kHeadNW][2];
         float sc[kHeadNW], off[kHeadNW];
@@ -719,8 +754,9 @@ __global__ __launch_bounds__(64 * W) void qgemm_head_kernel(QgemmArgs a) {
         for (int t = 0; t < kHeadNW; t++) {
             b[t][0] = unpack_b(h.wq[t].x, mask, magic);
             b[t][1] = unpack_b(h.wq[t].y, mask, magic);
-            sc[t] = h.sc[t];
-            off[t] = fmaf(-128.0f, h.sc[t], h.bi[t]);
+            const int row = (16 * t + c) * G + g;
+            sc[t] = bf2f(SBs[row]);
+            off[t] = fmaf(-128.0f, sc[t], bf2f(SBb[row]));
         }
         load(it + R, h);
         // the loads stay here, six items ahead of their use (the scheduler would sink them to the
@@ -729,17 +765,24 @@ __global__ __launch_bounds__(64 * W) void qgemm_head_kernel(QgemmArgs a) {
         // row tile by row tile, tile mt + 1's MFMAs issued before tile mt is folded (group_mma's
         // arithmetic: two MFMAs from zero, then s * sum + (b - 128 s) * sum_k x_k)
         f32x4_t agA[kHeadNW], agB[kHeadNW];  // two row tiles' MFMA sums in flight (named: no indexing)
-        float4 xsA, xsB;
-        auto issue = [&](int mt, f32x4_t (&dst)[kHeadNW], float4& xs4) __attribute__((always_inline)) {
+        struct AOp {
+            bf16x8_t a0, a1;
+            float4 xs;
+        };
+        // row tile mt's A operands and group sums from LDS
+        auto read = [&](int mt, AOp& o) __attribute__((always_inline)) {
             const uint4* ar = As + (size_t)(g * Mp + 16 * mt + c) * kHeadRow + 2 * j;
-            const bf16x8_t a0 = as_a(ar[0]), a1 = as_a(ar[1]);
-            xs4 = *reinterpret_cast<const float4*>(Xs + g * Mp + 16 * mt + 4 * j);
+            o.a0 = as_a(ar[0]);
+            o.a1 = as_a(ar[1]);
+            o.xs = *reinterpret_cast<const float4*>(Xs + g * Mp + 16 * mt + 4 * j);
+        };
+        auto mma = [&](const AOp& o, f32x4_t (&dst)[kHeadNW]) __attribute__((always_inline)) {
 #pragma unroll
             for (int t = 0; t < kHeadNW; t++)
-                dst[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[t][0], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                dst[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.a0, b[t][0], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
             for (int t = 0; t < kHeadNW; t++)
-                dst[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[t][1], dst[t], 0, 0, 0);
+                dst[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.a1, b[t][1], dst[t], 0, 0, 0);
         };
         auto fold = [&](int mt, const f32x4_t (&src)[kHeadNW], const float4& xs4) __attribute__((always_inline)) {
             const float xv[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
@@ -748,14 +791,20 @@ __global__ __launch_bounds__(64 * W) void qgemm_head_kernel(QgemmArgs a) {
 #pragma unroll
                 for (int r = 0; r < 4; r++) acc[mt][t][r] = fmaf(off[t], xv[r], fmaf(sc[t], src[t][r], acc[mt][t][r]));
         };
-        issue(0, agA, xsA);
+        // tile mt + 1's LDS reads are issued before tile mt's fold, its MFMAs after it: the fold's
+        // VALU work covers both the MFMA latency of tile mt and the LDS latency of tile mt + 1
+        AOp oA, oB;
+        read(0, oA);
+        mma(oA, agA);
 #pragma unroll
         for (int mt = 0; mt < MT; mt += 2) {
-            if (mt + 1 < MT) issue(mt + 1, agB, xsB);
-            fold(mt, agA, xsA);
+            if (mt + 1 < MT) read(mt + 1, oB);
+            fold(mt, agA, oA.xs);
             if (mt + 1 < MT) {
-                if (mt + 2 < MT) issue(mt + 2, agA, xsA);
-                fold(mt + 1, agB, xsB);
+                mma(oB, agB);
+                if (mt + 2 < MT) read(mt + 2, oA);
+                fold(mt + 1, agB, oB.xs);
+                if (mt + 2 < MT) mma(oA, agA);
             }
         }
         if (g + 1 < G) return;
@@ -763,7 +812,6 @@ __global__ __launch_bounds__(64 * W) void qgemm_head_kernel(QgemmArgs a) {
         // 16-lane group keeps the partial of row slot c (row 16 (c / 4) + 4 j + c % 4), so the
         // partials leave in one store per array: few stores keep the ring's waits exact (the
         // wait counter holds at most 63 outstanding operations).
-        const int u = gw + (it / G) * stride;
         float keep_v = -INFINITY;
         int keep_i = 0x7fffffff;
 #pragma unroll
@@ -771,32 +819,32 @@ __global__ __launch_bounds__(64 * W) void qgemm_head_kernel(QgemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int m = 16 * mt + 4 * j + r;
-                float best = -INFINITY;
-                int idx = 0x7fffffff;
+                // this lane's two columns (every column of a unit is < N): the larger, the lower
+                // column on ties, -inf and NaN never chosen -- the sequential rule "v > best"
+                float bv = -INFINITY;
+                int bn = 0x7fffffff;
 #pragma unroll
                 for (int t = 0; t < kHeadNW; t++) {
                     const float v = acc[mt][t][r] * S.gscale;
                     const int n = 16 * (kHeadNW * u + t) + c;
-                    if (n >= N) continue;
                     if (OUT && m < a.M) {
                         const size_t o = (size_t)m * a.ldy + S.col0 + n;
                         if (a.y) gst(a.y + o, f2bf(v));
                         if (a.yf) gst(a.yf + o, v);
                     }
-                    if (v > best) {
-                        best = v;
-                        idx = n;
+                    if (v > bv) {
+                        bv = v;
+                        bn = n;
                     }
                 }
-                // the 16 lanes of one j (one DPP row) hold one row: the symmetric DPP steps of
-                // team_reduce give every lane the row's maximum, lowest index on ties
-                head_argmax_step<0xB1>(best, idx);   // quad_perm [1,0,3,2]
-                head_argmax_step<0x4E>(best, idx);   // quad_perm [2,3,0,1]
-                head_argmax_step<0x141>(best, idx);  // row_half_mirror
-                head_argmax_step<0x140>(best, idx);  // row_mirror
+                // the 16 lanes of one j (one DPP row) hold one row: its maximum, then the lowest
+                // column holding a value equal to it (-0 equals +0, as in the sequential rule);
+                // a row of -inf / NaN keeps no column
+                const float rm = head_row_max(bv);
+                const int ri = head_row_min(bv == rm && rm > -INFINITY ? bn : 0x7fffffff);
                 if (c == 4 * mt + r) {
-                    keep_v = best;
-                    keep_i = idx;
+                    keep_v = rm;
+                    keep_i = ri;
                 }
             }
         if (a.pmax && c < 4 * MT) {
@@ -806,6 +854,7 @@ __global__ __launch_bounds__(64 * W) void qgemm_head_kernel(QgemmArgs a) {
                 gst(a.pidx + (size_t)m * a.nblk + u, keep_i);
             }
         }
+        store_sb();  // this unit's scales are read: the next unit's blocks take their place
     };
     for (int it = 0; it < items; it += R) {  // slots named one by one: the ring must not be indexed
 #define MING_HEAD_STEP(K)                     \
@@ -832,20 +881,24 @@ int head_grid() {
     return cus[dev];
 }
 
-bool head_fits(const QgemmArgs& a) { return a.nseg == 1 && a.M <= 64 && (a.K == 896 || a.K == 1024); }
+// K = 896 (14 groups), whole units of 32 rows, scale and bias blocks 16-byte aligned
+bool head_fits(const QgemmArgs& a) {
+    return a.nseg == 1 && a.M <= 64 && a.K == 896 && a.seg[0].N % 32 == 0 &&
+           reinterpret_cast<uintptr_t>(a.seg[0].s) % 16 == 0 && reinterpret_cast<uintptr_t>(a.seg[0].b) % 16 == 0;
+}
 
 template <int MT, int G, bool OUT, int W, int R>
 hipError_t launch_head_g(hipStream_t st, QgemmArgs a) {
-    static_assert(head_lds_bytes(G, 16 * MT) <= 150 * 1024, "staged rows fit in LDS");
+    constexpr size_t lds = head_lds_bytes(G, 16 * MT) + (size_t)W * head_sb_bytes<G>();
+    static_assert(lds <= 160 * 1024, "staged rows and scale blocks fit in LDS");
     const int units = (a.seg[0].N + 16 * kHeadNW - 1) / (16 * kHeadNW);
     a.nblk = units;
-    const size_t lds = head_lds_bytes(G, 16 * MT);
     static bool raised[64] = {false};  // the kernel's LDS limit, raised once per device
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return hipErrorInvalidDevice;
     if (!raised[dev]) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&qgemm_head_kernel<MT, G, OUT, W, R>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         raised[dev] = true;
     }
@@ -860,16 +913,13 @@ hipError_t launch_head_k(hipStream_t st, const QgemmArgs& a) {
     if (mt == 1) return launch_head_g<1, G, OUT, 8, 6>(st, a);
     if (mt == 2) return launch_head_g<2, G, OUT, 8, 6>(st, a);
     if (mt == 3) return launch_head_g<3, G, OUT, 8, 6>(st, a);
-    // four row tiles: 12 waves (3 a SIMD) with four groups in flight each measured 56.0 us at
-    // N = 151936, K = 896 against 57.6 for 8 waves x 6 groups, 58.0 for 12 x 6, 65-67 for 8 x 10
-    // and 8 x 12, 77 for 16 x 4 (spills)
+    // four row tiles (N = 151936, K = 896, 64 rows): 12 waves (3 a SIMD) with 4 groups in flight
+    // each 42.6 us; 12 x 6 42.5, 8 x 6 45.2, 16 x 4 and 16 x 3 50.3-50.4 (more waves are slower)
     return launch_head_g<4, G, OUT, 12, 4>(st, a);
 }
 
 hipError_t launch_head(hipStream_t st, const QgemmArgs& a) {
-    const bool out = a.y || a.yf;
-    if (a.K == 896) return out ? launch_head_k<14, true>(st, a) : launch_head_k<14, false>(st, a);
-    return out ? launch_head_k<16, true>(st, a) : launch_head_k<16, false>(st, a);
+    return a.y || a.yf ? launch_head_k<14, true>(st, a) : launch_head_k<14, false>(st, a);
 }
 
 // row tiles per workgroup: 2 when MTMAX allows and the row-tile count is even, else 1
