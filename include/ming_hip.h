@@ -81,6 +81,11 @@ int ming_ctx_use_own_stream(ming_ctx* ctx);
  * bounded waits, never as a hang.  No counterpart in the reference: MLX
  * dispatches per op (src/ming_fused.zig has no persistent step). */
 int ming_ctx_set_exclusive(ming_ctx* ctx, int on);
+/* Device bytes the context holds in workspaces it grows on demand (the staging
+ * of ming_qgemm, the attention partials of ming_lm_layer): 0 on a new context.
+ * No counterpart in the reference (MLX owns its allocations); it lets a caller
+ * that must not allocate check that its calls did not. */
+int ming_ctx_workspace_bytes(const ming_ctx* ctx, int64_t* bytes);
 void* ming_ctx_stream(ming_ctx* ctx);
 /* The eval point (mlx_eval, src/ming_model.zig:269-274); also reports any
  * device-side error flag raised since the last call: MING_E_TIMEOUT (a

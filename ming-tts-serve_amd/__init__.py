@@ -160,6 +160,7 @@ def lib():
         "ming_ctx_set_stream": (c_i32, [c_void_p, c_void_p]),
         "ming_ctx_use_own_stream": (c_i32, [c_void_p]),
         "ming_ctx_set_exclusive": (c_i32, [c_void_p, c_i32]),
+        "ming_ctx_workspace_bytes": (c_i32, [c_void_p, P(ctypes.c_int64)]),
         "ming_ctx_stream": (c_void_p, [c_void_p]),
         "ming_sync": (c_i32, [c_void_p]),
         "ming_last_error": (ctypes.c_char_p, [c_void_p]),
@@ -373,6 +374,12 @@ class Context:
 
     def set_exclusive(self, on=True):
         self.check(self.L.ming_ctx_set_exclusive(self.h, int(bool(on))))
+
+    def workspace_bytes(self):
+        """Device bytes of the context's on-demand workspaces (0 on a new context)."""
+        v = ctypes.c_int64(0)
+        self.check(self.L.ming_ctx_workspace_bytes(self.h, ctypes.byref(v)))
+        return int(v.value)
 
     def sync(self):
         self.check(self.L.ming_sync(self.h))

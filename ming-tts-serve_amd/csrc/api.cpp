@@ -314,6 +314,13 @@ int ming_ctx_set_exclusive(ming_ctx* ctx, int on) {
     return MING_OK;
 }
 
+int ming_ctx_workspace_bytes(const ming_ctx* ctx, int64_t* bytes) {
+    if (!ctx || !ctx->alive) return MING_E_NOT_INIT;
+    if (!bytes) return MING_E_ARG;
+    *bytes = (int64_t)(ctx->qstage.bytes + ctx->part.bytes);
+    return MING_OK;
+}
+
 void* ming_ctx_stream(ming_ctx* ctx) { return alive(ctx) ? ctx->stream : nullptr; }
 
 int ming_sync(ming_ctx* ctx) {

@@ -50,11 +50,15 @@ def run(ming, batch, pk, tokens):
     return hid, lg, am
 
 
-def check_teacher_forced(ming, batch, pk, orc, host, lens, tokens, hid, lg, am, tag, seqs=None):
+def check_teacher_forced(ming, batch, pk, orc, host, lens, tokens, hid, lg, am, tag, seqs=None, only=None):
+    """seqs: the sequences whose every layer is checked (default all); only: the sequences
+    checked at all (embedding, appended rows, head; default all)."""
     cfg, layers, norm, head = orc
     tr = {k: host_u16(v) for k, v in batch.trace().items()}
     worst = 0.0
     for i in range(len(lens)):
+        if only is not None and i not in only:
+            continue
         pos = lens[i]
         assert np.array_equal(tr["x"][0, i], oracle.embed(head, tokens[i])), f"{tag} seq {i} embedding"
         gk, gv = pk.gather(i, pos + 1)
@@ -249,6 +253,59 @@ def test_batch_qwen_shape_64_matches_oracle(ming, ctx, qwen):
     seqs = [int(order[j]) for j in (0, 10, 21, 32, 43, 53, 63)]
     worst = check_teacher_forced(ming, b, pk, orc, host, lens, tokens, hid, lg, am, "qwen64", seqs=seqs)
     print(f"[batch] qwen shape 64 sequences worst layer max|d| {worst:.3e}", flush=True)
+
+
+def test_batch_step_beyond_64_sequences(ming, ctx, qwen):
+    """The batched step above 64 sequences (a batch of 512 rows: the LDS-tiled GEMMs, the tiled
+    head with 64-column argmax partials, paged attention and merge beyond 64 sequences): 65
+    sequences in one call equal the same sequences as calls of 64 and 1, bit for bit (hidden,
+    logits, ids, cache rows); 512 sequences with short ragged contexts match the oracle, every
+    layer of 3 of them and the head of 10."""
+    S, syn, m, b, orc = qwen
+    spec = syn.spec
+    big = ming.LmBatch(m, 512, 1024)
+    try:
+        lens = ragged(65, 1, 300, 5)
+        tokens = [int(t) for t in ming.synth_uniform_i32(5, "tok.c5.65", 65, spec.vocab)]
+        tok = torch.tensor(tokens, dtype=torch.int32, device="cuda")
+        print(f"[batch] 65 sequences in one call vs 64 + 1, lens {min(lens)}..{max(lens)}", flush=True)
+        outs = []
+        for split in (False, True):
+            pk = S.PagedKv(spec, 65, 5, seed=5)
+            pk.fill_random(lens, seed=5)
+            hid = torch.empty((65, spec.hidden), dtype=torch.bfloat16, device="cuda")
+            lg = torch.empty((65, spec.vocab), dtype=torch.float32, device="cuda")
+            am = torch.empty(65, dtype=torch.int32, device="cuda")
+            if not split:
+                big.step(pk, pk.table, pk.pos, tokens=tok, hidden=hid, logits=lg, argmax=am)
+            else:
+                for lo, hi in ((0, 64), (64, 65)):
+                    b.step(pk, pk.table[lo:hi], pk.pos[lo:hi], tokens=tok[lo:hi], hidden=hid[lo:hi],
+                           logits=lg[lo:hi], argmax=am[lo:hi])
+            ctx.sync()
+            outs.append((hid, lg, am, pk.gather(64, lens[64] + 1), pk.gather(0, lens[0] + 1)))
+        (h0, l0, a0, c0, d0), (h1, l1, a1, c1, d1) = outs
+        assert torch.equal(h0, h1), "hidden differs between one call of 65 and calls of 64 + 1"
+        assert torch.equal(l0, l1), "logits differ between one call of 65 and calls of 64 + 1"
+        assert torch.equal(a0, a1), "ids differ between one call of 65 and calls of 64 + 1"
+        for x, y in ((c0, c1), (d0, d1)):
+            assert np.array_equal(x[0], y[0]) and np.array_equal(x[1], y[1]), "cache rows differ"
+        del outs, l0, l1
+        n = 512
+        lens = ragged(n, 1, 120, 6)
+        print(f"[batch] 512 sequences, lens {min(lens)}..{max(lens)}", flush=True)
+        pk = S.PagedKv(spec, n, 2, seed=6)
+        host = pk.fill_random(lens, seed=6)
+        tokens = [int(t) for t in ming.synth_uniform_i32(6, "tok.c5.512", n, spec.vocab)]
+        hid, lg, am = run(ming, big, pk, tokens)
+        order = np.argsort(lens)
+        seqs = [int(order[0]), int(order[255]), int(order[-1])]
+        only = set(seqs) | {0, 63, 64, 65, 127, 128, 300, 511}
+        worst = check_teacher_forced(ming, big, pk, orc, host, lens, tokens, hid, lg, am, "qwen512", seqs=seqs,
+                                     only=only)
+        print(f"[batch] 512 sequences worst layer max|d| {worst:.3e}", flush=True)
+    finally:
+        big.close()
 
 
 # ---- multi-token prefill (rows of one sequence as sequences sharing its pages) ----

@@ -1,8 +1,10 @@
 """GPU check of ming_qgemm_noalloc, the batched 4-bit GEMM that stages its
 activations in the device's fixed scratch array instead of allocating:
 through the C ABI, its outputs equal ming_qgemm's bit for bit (same
-kernels) on two calls in a row, the second with a smaller input, and a
-request larger than the fixed scratch is rejected before any launch."""
+kernels) on two calls in a row, the second with a smaller input; on a new
+context it leaves the context's on-demand workspaces at 0 bytes (where
+ming_qgemm then grows them); and a request larger than the fixed scratch is
+rejected before any launch."""
 import numpy as np
 import pytest
 import torch
@@ -38,6 +40,27 @@ def test_qgemm_noalloc_matches_qgemm(ming, ctx):
             assert torch.equal(got.view(torch.int16) if dt == torch.bfloat16 else got.view(torch.int32),
                                ref.view(torch.int16) if dt == torch.bfloat16 else ref.view(torch.int32)), \
                 f"noalloc differs from qgemm at K={K} N={N} M={M} {dt}"
+
+
+def test_qgemm_noalloc_allocates_nothing(ming):
+    K, N, M = 4864, 896, 64
+    own = ming.Context(0)  # a new context: nothing has grown its workspaces yet
+    try:
+        wq, s, b = quantized(ming, own, K, N, 4)
+        x = dev_u16(ming.synth_normal_bf16(54, "noalloc.fresh.x", M * K)).reshape(M, K)
+        got = torch.full((M, N), 3.0, dtype=torch.float32, device="cuda")
+        ref = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        own.sync()
+        assert own.workspace_bytes() == 0
+        own.qgemm_noalloc(x, wq, s, b, got)
+        own.sync()
+        assert own.workspace_bytes() == 0, "ming_qgemm_noalloc allocated a workspace"
+        own.qgemm(x, wq, s, b, ref)  # the allocating entry point grows the staging (the query sees it)
+        own.sync()
+        assert own.workspace_bytes() > 0
+        assert torch.equal(got.view(torch.int32), ref.view(torch.int32))
+    finally:
+        own.close()
 
 
 def test_qgemm_noalloc_rejects_beyond_scratch(ming, ctx):
