@@ -759,9 +759,9 @@ __global__ __launch_bounds__(64 * W) void qgemm_head_kernel(QgemmArgs a) {
             off[t] = fmaf(-128.0f, sc[t], bf2f(SBb[row]));
         }
         load(it + R, h);
-        // the loads stay here, six items ahead of their use (the scheduler would sink them to the
-        // use to save registers, which serialises the ring)
-        __builtin_amdgcn_sched_barrier(0);
+        // the loads stay here, R items ahead of their use (the scheduler would sink them to the use
+        // to save registers, which serialises the ring); ALU, MFMA and LDS work may still cross
+        __builtin_amdgcn_sched_barrier(0x38F);
         // row tile by row tile, tile mt + 1's MFMAs issued before tile mt is folded (group_mma's
         // arithmetic: two MFMAs from zero, then s * sum + (b - 128 s) * sum_k x_k)
         f32x4_t agA[kHeadNW], agB[kHeadNW];  // two row tiles' MFMA sums in flight (named: no indexing)
