@@ -70,16 +70,15 @@ constexpr int kBlkWords = (int)(sizeof(CfmPBlock) / 4);
 constexpr int kLBlk = 0;                                // block table
 constexpr int kLRed = kLBlk + kPMaxBlocks * kBlkWords;  // row-sum partials (12 floats)
 constexpr int kLInv = kLRed + 16;                       // inverse norms of the 6 rows
-constexpr int kLX2 = kLInv + 8;                         // worker: ff2's odd-row outputs [3 pairs][6]
-constexpr int kLY = kLX2 + 32;                          // head: the current latent y (64 bf16)
+constexpr int kLY = kLInv + 8;                          // head: the current latent y (64 bf16)
 constexpr int kLXe = kLY + kPLat / 2;                   // head: x_emb(y) (1024 bf16)
 constexpr int kLFx = kLXe + kD2;                        // head: final-normed rows L-1, 2L-1 [2][512]
 constexpr int kLBx = kLFx + 2 * kD2;                    // head: x_embedder bias (1024 bf16)
 constexpr int kLArea = kLBx + kD2;
-constexpr int kLXs = kLArea;                            // worker: stage image, f32 (<= 6 x 4096 floats)
-constexpr int kLTanh = kLXs + kPR * kPF;                // worker: gelu's tanh table (tanh_tab.h) as bf16
+constexpr int kLXs = kLArea;                            // worker: stage image (<= 6 x 2048 words)
+constexpr int kLTanh = kLXs + kPR * kF2;                // worker: gelu's tanh table (tanh_tab.h)
 constexpr int kLWx = kLArea;                            // head: x_embedder [1024][64] bf16
-constexpr int kLdsW = kLTanh + (kTanhTabN + 1) / 2, kLdsH = kLWx + kPD * kPLat / 2;
+constexpr int kLdsW = kLTanh + kTanhTabN, kLdsH = kLWx + kPD * kPLat / 2;
 constexpr int kLds = kLdsW > kLdsH ? kLdsW : kLdsH;
 static_assert(kLY % 4 == 0 && kLXe % 4 == 0 && kLFx % 4 == 0 && kLXs % 4 == 0 && kLWx % 4 == 0 && kLTanh % 4 == 0,
               "LDS alignment");
@@ -87,38 +86,17 @@ static_assert(kLds * 4 <= 160 * 1024, "LDS of one workgroup");
 static_assert(sizeof(CfmPBlock) % 8 == 0, "block table entries are copied as u64");
 
 typedef uint32_t lds_u32x4_t __attribute__((ext_vector_type(4), aligned(16)));
-typedef float f32x4_l __attribute__((ext_vector_type(4)));
-typedef float lds_f32x4_t __attribute__((ext_vector_type(4), aligned(16)));
-
-// Chunk c (eight bf16 values) of an f32 row of K values in LDS: its first four
-// values at float 4c of the row's first half-plane, the other four at 4c of
-// the second (row base + K/2), so that lanes reading consecutive chunks touch
-// consecutive 16 bytes in each plane (no bank conflicts).
-__device__ __forceinline__ void put8f(float* row, int K, int c, uint4 v) {
-    reinterpret_cast<lds_f32x4_t*>(row)[c] = f32x4_l{bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y)};
-    reinterpret_cast<lds_f32x4_t*>(row + K / 2)[c] = f32x4_l{bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
-}
 
 // (float)tanh((double)u) for every bf16 u in [0, 16] (tanh_tab.h), filled at
 // context creation; each worker copies it into LDS once per launch
 __device__ float cfmp_tanh_tab[kTanhTabN];
 
-// tanh_bf16 (tanh_tab.h) over the LDS copy of the table, whose entries are
-// held rounded to bf16: the chain rounds the table's value to bf16 anyway, so
-// the result is the same and the copy takes half the LDS.
-__device__ __forceinline__ float tanh_bf16_lds(const uint16_t* tab, float u) {
-    const uint32_t b = __float_as_uint(u) >> 16;  // exact: u is a bf16 value
-    const uint32_t m = b & 0x7fffu;
-    const float t = m < (uint32_t)kTanhTabN ? bf2f(tab[m]) : (m > 0x7f80u ? u : 1.0f);
-    return (b & 0x8000u) ? -t : t;
-}
-
 // gelu_approx with every op rounded to bf16 (the launch path's chain), tanh from the LDS table
-__device__ __forceinline__ float gelu_chain_p(const uint16_t* tab, float x) {
+__device__ __forceinline__ float gelu_chain_p(const float* tab, float x) {
     const float c0 = rb(0.044715f), c1 = rb(0.7978845608f);
     const float x3 = rb((float)((double)x * (double)x * (double)x));
     const float inner = rb(x + rb(c0 * x3));
-    const float th = rb(tanh_bf16_lds(tab, rb(c1 * inner)));
+    const float th = rb(tanh_bf16(tab, rb(c1 * inner)));
     return rb(rb(0.5f * x) * rb(1.0f + th));
 }
 
@@ -231,40 +209,36 @@ __device__ __forceinline__ void stores_done() {
 
 // acc[u][r] = team sum over the TEAM lanes of row slot r (6 slots) dotted
 // with unit u's NCH weight chunks of this lane (chunk tl + TEAM j), rows at
-// xs as f32 with K values each: the launch path's inner loop, each product
-// entering the accumulator through an IEEE fused multiply-add in element
-// order, the weight chunk unpacked once for the six slots.  Units share each
-// LDS read.
+// xs with KW4 16-byte chunks each.  Units share each LDS read; chunk j + 1's
+// six reads are issued before chunk j's products, so the reads overlap the
+// math instead of each waiting out its own latency (the chains keep their
+// order: chunk j's four words after chunk j - 1's).
 template <int NCH, int TEAM, int NU>
-__device__ __forceinline__ void dots6(const uint4 (&wr)[NU][NCH], const float* xs, int K, int tl,
+__device__ __forceinline__ void dots6(const uint4 (&wr)[NU][NCH], const uint32_t* xs, int KW4, int tl,
                                       float (&acc)[NU][kPR]) {
-    const lds_f32x4_t* xv4 = reinterpret_cast<const lds_f32x4_t*>(xs);
+    const lds_u32x4_t* xv4 = reinterpret_cast<const lds_u32x4_t*>(xs);
 #pragma unroll
     for (int u = 0; u < NU; u++)
 #pragma unroll
         for (int r = 0; r < kPR; r++) acc[u][r] = 0.0f;
+    u32x4_t xv[2][kPR];  // chunk j's six row words, chunk j + 1's in flight
+#pragma unroll
+    for (int r = 0; r < kPR; r++) xv[0][r] = xv4[r * KW4 + tl];
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
-        const int cj = tl + TEAM * j;
-        f32x4_l xv[kPR][2];  // chunk j of the six rows: all twelve reads issued before the products
+        if (j + 1 < NCH) {
+#pragma unroll
+            for (int r = 0; r < kPR; r++) xv[(j + 1) & 1][r] = xv4[r * KW4 + tl + TEAM * (j + 1)];
+        }
+        const u32x4_t(&x)[kPR] = xv[j & 1];
 #pragma unroll
         for (int r = 0; r < kPR; r++) {
-            xv[r][0] = xv4[r * (K / 4) + cj];
-            xv[r][1] = xv4[r * (K / 4) + K / 8 + cj];
-        }
 #pragma unroll
-        for (int u = 0; u < NU; u++) {
-            const uint4 w = wr[u][j];
-            const float wv[8] = {bf_lo(w.x), bf_hi(w.x), bf_lo(w.y), bf_hi(w.y),
-                                 bf_lo(w.z), bf_hi(w.z), bf_lo(w.w), bf_hi(w.w)};
-#pragma unroll
-            for (int r = 0; r < kPR; r++) {
-                float s = acc[u][r];
-#pragma unroll
-                for (int e = 0; e < 4; e++) s = __builtin_fmaf(wv[e], xv[r][0][e], s);
-#pragma unroll
-                for (int e = 0; e < 4; e++) s = __builtin_fmaf(wv[4 + e], xv[r][1][e], s);
-                acc[u][r] = s;
+            for (int u = 0; u < NU; u++) {
+                float s = dot2(wr[u][j].x, x[r].x, acc[u][r]);
+                s = dot2(wr[u][j].y, x[r].y, s);
+                s = dot2(wr[u][j].z, x[r].z, s);
+                acc[u][r] = dot2(wr[u][j].w, x[r].w, s);
             }
         }
     }
@@ -284,7 +258,7 @@ __device__ __forceinline__ float pick6(const float (&acc)[kPR], int tl) {
 
 // Attention of one (CFG half, head) task as the launch path's attention
 // kernel computes it: lane d owns dimension d; scores sum_d (q/8) k over the
-// wave, p = exp_rep(s - max), o = sum_j p_j v_j / sum_j p_j (rounded by the caller).
+// wave, p = exp(s - max), o = sum_j p_j v_j / sum_j p_j (rounded by the caller).
 __device__ __forceinline__ void attn_math(const float (&qv)[kPL], const float (&kv)[kPL], const float (&vv)[kPL],
                                           float (&r)[kPL]) {
     const float scale = 1.0f / 8.0f;
@@ -399,12 +373,10 @@ __device__ __forceinline__ void own_hh(const Wk& c, int s, int b, int f) {
     uint32_t v[2 * kPR];
     poll_words<2 * kPR>(th + (size_t)u * kPR, [](int i) { return i; }, a.epoch, v, a.flags);
     if (c.w == 0 && c.lane == 0) stamp_at(a, 3, f);
-    // columns 2u .. 2u + 3 of each row: four consecutive f32 of one half-plane of chunk u / 4
-    const int m = u / 2, off = (m & 1) * (kPF / 2) + 4 * (m >> 1);
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
     for (int r = 0; r < kPR; r++)
-        *(MING_GLOBAL f32x4_l*)(c.img + kPImgD + r * kPF + off) =
-            f32x4_l{bf_lo(v[r]), bf_hi(v[r]), bf_lo(v[kPR + r]), bf_hi(v[kPR + r])};
+        *(MING_GLOBAL u32x2*)(c.img + kPImgD + r * kF2 + u) = u32x2{v[r], v[kPR + r]};
     stores_done();
     if (c.lane == 0) gst(c.flg + SD * kPFlagLine + c.j, ftag(a, f));
     if (c.w == 0 && c.lane == 0) stamp_at(a, 0, f);
@@ -415,7 +387,7 @@ __device__ __forceinline__ void own_hh(const Wk& c, int s, int b, int f) {
 // the image holds raw rows whose half-row sums of squares are at `part`:
 // each row is normalised on the way with the weights nw of the thread's
 // chunks (bf16(w * bf16(x * inv)), inv = 1 / sqrt((s0 + s1) / D + eps)).
-template <int NG, bool WIDEN = true>
+template <int NG>
 __device__ __forceinline__ void wait_image(const Wk& c, int kind, int nslices, int f, int off, int words, int part,
                                            const uint4* nw) {
     const CfmPArgs& a = c.a;
@@ -445,31 +417,6 @@ __device__ __forceinline__ void wait_image(const Wk& c, int kind, int nslices, i
         }
         __builtin_amdgcn_s_waitcnt(0);
         lds_sync();
-        if (!WIDEN) {  // the image is f32 in LDS layout already
-            if (c.w == 0 && tix() == 0) stamp_at(a, 1, f);
-            return;
-        }
-        // widen to f32 in place: every chunk is read before any is written
-        // (chunk i's f32 copy covers the bf16 chunks 2i and 2i + 1)
-        uint4 v[NG];
-#pragma unroll
-        for (int k = 0; k < NG; k++) {
-            const int i = tix() + kT * k;
-            if (i < n4) {
-                const u32x4_t q = reinterpret_cast<const lds_u32x4_t*>(c.lds + kLXs)[i];
-                v[k] = make_uint4(q.x, q.y, q.z, q.w);
-            }
-        }
-        lds_sync();
-#pragma unroll
-        for (int k = 0; k < NG; k++) {
-            const int i = tix() + kT * k;
-            if (i < n4) {
-                const int K = 8 * n4 / kPR, cpr = K / 8;  // row length, chunks per row
-                put8f(reinterpret_cast<float*>(c.lds + kLXs) + (i / cpr) * K, K, i % cpr, v[k]);
-            }
-        }
-        lds_sync();
         if (c.w == 0 && tix() == 0) stamp_at(a, 1, f);
         return;
     }
@@ -486,8 +433,7 @@ __device__ __forceinline__ void wait_image(const Wk& c, int kind, int nslices, i
                 for (int e = 0; e < 4; e++)
                     o[e] = pack_bf2(bf_lo(g[e]) * rb(bf_lo(o[e]) * iv), bf_hi(g[e]) * rb(bf_hi(o[e]) * iv));
             }
-            put8f(reinterpret_cast<float*>(c.lds + kLXs) + (i / (kPD / 8)) * kPD, kPD, i % (kPD / 8),
-                  make_uint4(o[0], o[1], o[2], o[3]));
+            reinterpret_cast<lds_u32x4_t*>(c.lds + kLXs)[i] = u32x4_t{o[0], o[1], o[2], o[3]};
         }
     }
     lds_sync();
@@ -537,7 +483,7 @@ __device__ __forceinline__ void wk_qkv(const Wk& c, const CfmPBlock& B, int s, i
     wait_image<2>(c, SA, kNormSlices, f, kPImgA, kPR * kD2, kPImgAp, nw);
     if (!act) return;
     float acc[1][kPR];
-    dots6<4, 32, 1>(wr, reinterpret_cast<const float*>(c.lds + kLXs), kPD, tl, acc);
+    dots6<4, 32, 1>(wr, c.lds + kLXs, kPD / 8, tl, acc);
     const float e = rb(pick6(acc[0], tl) + bias);
     const float other = __shfl(e, c.lane ^ 32, kWave);
     float o = e;
@@ -573,7 +519,7 @@ __device__ __forceinline__ void wk_out(const Wk& c, const CfmPBlock& B, int s, i
     if (!act) return;
     const uint32_t rw = tl < kPR ? raw_word(c, kPImgA, tl, u) : 0u;
     float acc[1][kPR];
-    dots6<4, 32, 1>(wr, reinterpret_cast<const float*>(c.lds + kLXs), kPD, tl, acc);
+    dots6<4, 32, 1>(wr, c.lds + kLXs, kPD / 8, tl, acc);
     const float res = team == 0 ? bf_lo(rw) : bf_hi(rw);
     const float o = res + rb(pick6(acc[0], tl) + bias);
     const float o1 = __shfl(o, c.lane ^ 32, kWave);
@@ -614,14 +560,14 @@ __device__ __forceinline__ void wk_ff1(const Wk& c, const CfmPBlock& B, int s, i
     if (!act0) return;
     float acc[2][kPR];
     if (act1) {
-        dots6<4, 32, 2>(wr, reinterpret_cast<const float*>(c.lds + kLXs), kPD, tl, acc);
+        dots6<4, 32, 2>(wr, c.lds + kLXs, kPD / 8, tl, acc);
     } else {
         const uint4(&w1)[1][4] = reinterpret_cast<const uint4(&)[1][4]>(wr);
         float (&a1)[1][kPR] = reinterpret_cast<float(&)[1][kPR]>(acc);
-        dots6<4, 32, 1>(w1, reinterpret_cast<const float*>(c.lds + kLXs), kPD, tl, a1);
+        dots6<4, 32, 1>(w1, c.lds + kLXs, kPD / 8, tl, a1);
     }
     uint64_t* out = a.th + (size_t)(s * a.nblk + b) * kPTh;
-    const uint16_t* tab = reinterpret_cast<const uint16_t*>(c.lds + kLTanh);
+    const float* tab = reinterpret_cast<const float*>(c.lds + kLTanh);
     {
         const float g = gelu_chain_p(tab, rb(pick6(acc[0], tl) + b0));
         const float g1 = __shfl(g, c.lane ^ 32, kWave);
@@ -636,37 +582,34 @@ __device__ __forceinline__ void wk_ff1(const Wk& c, const CfmPBlock& B, int s, i
 }
 
 // D: x2 = x1 + ff2(h) (E_RES with K = 4096: one 64-lane team per row, 8
-// chunks per lane).  Compute waves 1..6 of worker w take pair u = w + W p,
-// p = (wave - 1) / 2: the even wave row 2u, the odd wave row 2u + 1 (one row
-// per wave halves each wave's chain); the odd row's six outputs reach the
-// even wave through LDS, which stores the tagged pair.
+// chunks per lane).  Compute wave q of worker w takes both rows of pair
+// u = w + W q; the two rows share every image read.
 __device__ __forceinline__ void wk_ff2(const Wk& c, const CfmPBlock& B, int s, int b) {
     const CfmPArgs& a = c.a;
-    const int cw = c.wave - 1, pi = cw >> 1, odd = cw & 1, u = c.w + c.W * pi;
-    const bool act = cw >= 0 && cw < 6 && u < kUD;
-    const int n = 2 * (act ? u : 0) + odd;
-    uint4 wr[1][8];
-    float bn = 0.0f;
+    const int cw = c.wave - 1, u = c.w + c.W * cw;
+    const bool act = cw >= 0 && u < kUD;
+    const int n = 2 * (act ? u : 0);
+    uint4 wr[2][8];
+    float b0 = 0.0f, b1 = 0.0f;
     if (act) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) wr[0][j] = ldg4(B.w2 + (size_t)n * kPF + 8 * (c.lane + 64 * j));
-        bn = bf2f(gld(B.b2 + n));
+        for (int j = 0; j < 8; j++) {
+            wr[0][j] = ldg4(B.w2 + (size_t)n * kPF + 8 * (c.lane + 64 * j));
+            wr[1][j] = ldg4(B.w2 + (size_t)(n + 1) * kPF + 8 * (c.lane + 64 * j));
+        }
+        b0 = bf2f(gld(B.b2 + n));
+        b1 = bf2f(gld(B.b2 + n + 1));
     }
     const int f = fidx(a, s, b, SD);
     if (c.wave == 0) own_hh(c, s, b, f);
-    wait_image<12, false>(c, SD, kHhSlices, f, kPImgD, kPR * kPF, -1, nullptr);
-    float* x2 = reinterpret_cast<float*>(c.lds + kLX2);
-    float o = 0.0f;
-    if (act) {
-        const uint32_t rw = c.lane < kPR ? raw_word(c, kPImgC, c.lane, u) : 0u;
-        float acc[1][kPR];
-        dots6<8, 64, 1>(wr, reinterpret_cast<const float*>(c.lds + kLXs), kPF, c.lane, acc);
-        o = (odd ? bf_hi(rw) : bf_lo(rw)) + rb(pick6(acc[0], c.lane) + bn);
-        if (odd && c.lane < kPR) x2[pi * kPR + c.lane] = o;
-    }
-    lds_sync();
-    if (act && !odd && c.lane < kPR)
-        tstore(a.txo + (size_t)(s * a.nblk + b) * kPTx + c.lane * kD2 + u, pack_bf2(o, x2[pi * kPR + c.lane]), a.epoch);
+    wait_image<6>(c, SD, kHhSlices, f, kPImgD, kPR * kF2, -1, nullptr);
+    if (!act) return;
+    const uint32_t rw = c.lane < kPR ? raw_word(c, kPImgC, c.lane, u) : 0u;
+    float acc[2][kPR];
+    dots6<8, 64, 2>(wr, c.lds + kLXs, kPF / 8, c.lane, acc);
+    const float o0 = bf_lo(rw) + rb(pick6(acc[0], c.lane) + b0);
+    const float o1 = bf_hi(rw) + rb(pick6(acc[1], c.lane) + b1);
+    if (c.lane < kPR) tstore(a.txo + (size_t)(s * a.nblk + b) * kPTx + c.lane * kD2 + u, pack_bf2(o0, o1), a.epoch);
     stamp_stores(c, f);
 }
 
@@ -768,10 +711,10 @@ __device__ __forceinline__ void head_step(const CfmPArgs& a, uint32_t* lds, int 
 #pragma unroll
                 for (int r = 0; r < 2; r++) {
                     const u32x4_t xv = xr[r][jj];
-                    float sacc = fma_bf2(wf[j][jj].x, xv.x, acc[r]);
-                    sacc = fma_bf2(wf[j][jj].y, xv.y, sacc);
-                    sacc = fma_bf2(wf[j][jj].z, xv.z, sacc);
-                    acc[r] = fma_bf2(wf[j][jj].w, xv.w, sacc);
+                    float sacc = dot2(wf[j][jj].x, xv.x, acc[r]);
+                    sacc = dot2(wf[j][jj].y, xv.y, sacc);
+                    sacc = dot2(wf[j][jj].z, xv.z, sacc);
+                    acc[r] = dot2(wf[j][jj].w, xv.w, sacc);
                 }
             }
             acc[0] = team_sum<32>(acc[0]);
@@ -808,10 +751,10 @@ __device__ __forceinline__ void head_step(const CfmPArgs& a, uint32_t* lds, int 
         for (int j = 0; j < 16; j++) {
             const int n = 64 * j + 8 * wave + tm;
             const u32x4_t wv = wvs[j];
-            float acc = fma_bf2(wv.x, yv.x, 0.0f);
-            acc = fma_bf2(wv.y, yv.y, acc);
-            acc = fma_bf2(wv.z, yv.z, acc);
-            acc = fma_bf2(wv.w, yv.w, acc);
+            float acc = dot2(wv.x, yv.x, 0.0f);
+            acc = dot2(wv.y, yv.y, acc);
+            acc = dot2(wv.z, yv.z, acc);
+            acc = dot2(wv.w, yv.w, acc);
             acc = team_sum<8>(acc);
             acc = (acc + 0.0f) + 0.0f;
             if (t8 == 0) xe16[n] = f2bf(rb(acc + bf2f(bx16[n])));
@@ -902,7 +845,7 @@ __global__ __launch_bounds__(kT, 1) void cfm_persistent_kernel(CfmPArgs a) {
         if (tix() == 0) raise_flag(a.flags);
         return;
     }
-    for (int i = tix(); i < kTanhTabN; i += kT) reinterpret_cast<uint16_t*>(lds + kLTanh)[i] = f2bf(gld(cfmp_tanh_tab + i));
+    for (int i = tix(); i < kTanhTabN; i += kT) reinterpret_cast<float*>(lds + kLTanh)[i] = gld(cfmp_tanh_tab + i);
     for (int s = 0; s < a.steps; s++)
         for (int b = 0; b < a.nblk; b++) {
             const CfmPBlock& B = blk(lds, b);

@@ -17,15 +17,14 @@ constexpr int kPMinWorkers = 220;  // 7 compute waves each: the 1536 q/k/v row p
 
 // u32 words of one XCD's stage images: A (the rms1 rows, raw), A's half-row
 // sums of squares, B (attention rows), C (the rms2 rows, raw), C's half-row
-// sums, D (ff1 rows as f32, in the workers' LDS layout: per row, chunk c's
-// first four values at float 4c, the other four at 4c + kPF / 2)
+// sums, D (ff1 rows)
 constexpr int kPImgA = 0;
 constexpr int kPImgAp = kPImgA + kPR * kPD / 2;
 constexpr int kPImgB = kPImgAp + 16;
 constexpr int kPImgC = kPImgB + kPR * kPD / 2;
 constexpr int kPImgCp = kPImgC + kPR * kPD / 2;
 constexpr int kPImgD = kPImgCp + 16;
-constexpr int kPImgWords = kPImgD + kPR * kPF;
+constexpr int kPImgWords = kPImgD + kPR * kPF / 2;
 constexpr int kPFlagLine = 32;     // slice flags of one image (u32 each)
 
 // tagged words {bf16 pair, epoch} per (Euler step, block)

@@ -9,9 +9,10 @@
 //
 // GEMV layout: a workgroup of W waves (W = 2 or 4) owns 2W output rows, one
 // per 32-lane team; a lane holds K/256 16-byte weight chunks in registers.
-// The activation rows are staged in LDS as f32 and every product enters its
-// lane's accumulator through an IEEE fused multiply-add, in element order, so
-// the f32 sums are reproducible on a CPU bit for bit.
+// Each lane adds its products with v_dot2c_f32_bf16 (two products per step,
+// chunks in order), and the team's lane sums meet in the DPP tree; that order
+// and the instruction's own fixed-grid accumulation are what the oracle's
+// device order restates, so the flow head is reproducible on a CPU bit for bit.
 // The weight loads go first, then the epilogue's operands (bias, residual,
 // rotary table, CFM inputs), then the R input rows (R <= 6) in one batch of
 // loads -- every load is issued before the first one is used, so the kernel
@@ -37,10 +38,8 @@ namespace {
 
 constexpr int kMaxR = 6;       // activation rows of a reference-shape block (2 x 3)
 constexpr int kMaxSlots = 20;  // row slots of the widest launch (adaLN modulations: 10 steps x 2 halves)
-// 16-byte LDS vectors (the staged rows are 16-byte aligned: K % 8 == 0)
+// 16-byte LDS vector (the staged rows are 16-byte aligned: K % 8 == 0)
 typedef uint32_t lds_u32x4_t __attribute__((ext_vector_type(4), aligned(16)));
-typedef float f32x4_l __attribute__((ext_vector_type(4)));
-typedef float lds_f32x4_t __attribute__((ext_vector_type(4), aligned(16)));
 constexpr int kMaxL = 8;  // positions per sequence (attention)
 
 enum DitEpi {
@@ -121,19 +120,10 @@ __device__ __forceinline__ float gelu_chain(float x) {
 // branches, so the compiler issues every load, and later every LDS store,
 // back to back.  Threads whose chunk is past the row's end store nothing and
 // add nothing to the sums.
-// Chunk c (eight bf16 values) of an f32 row of K values in LDS: its first four
-// values at float 4c of the row's first half-plane, the other four at 4c of
-// the second (row base + K/2), so that lanes reading consecutive chunks touch
-// consecutive 16 bytes in each plane (no bank conflicts).
-__device__ __forceinline__ void put8f(float* row, int K, int c, uint4 v) {
-    reinterpret_cast<lds_f32x4_t*>(row)[c] = f32x4_l{bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y)};
-    reinterpret_cast<lds_f32x4_t*>(row + K / 2)[c] = f32x4_l{bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
-}
-
 template <int MODE, int RC, int XCH, int T>
-__device__ __forceinline__ void stage_rows(const DitGemv& a, float* xs, float* red, int t) {
+__device__ __forceinline__ void stage_rows(const DitGemv& a, uint32_t* xs, float* red, int t) {
     constexpr bool NORM = MODE != M_PLAIN, ADA = MODE == M_ADANORM;
-    const int K = a.K, NC = K / 8, R = a.R;
+    const int K = a.K, NC = K / 8, K2 = K / 2, R = a.R;
     uint4 xr[RC][XCH];
     uint4 gn[XCH];
     uint4 msh[2][XCH], msc[2][XCH];  // adaLN shift / scale chunks of the (at most 2) CFG halves
@@ -158,7 +148,8 @@ __device__ __forceinline__ void stage_rows(const DitGemv& a, float* xs, float* r
             const int c = t + T * j;
             if (c < NC)
 #pragma unroll
-                for (int r = 0; r < RC; r++) put8f(xs + r * K, K, c, xr[r][j]);
+                for (int r = 0; r < RC; r++)
+                    reinterpret_cast<lds_u32x4_t*>(xs)[r * (K2 / 4) + c] = u32x4_t{xr[r][j].x, xr[r][j].y, xr[r][j].z, xr[r][j].w};
         }
         return;
     }
@@ -222,7 +213,8 @@ __device__ __forceinline__ void stage_rows(const DitGemv& a, float* xs, float* r
         }
         if (c < NC)
 #pragma unroll
-            for (int r = 0; r < RC; r++) put8f(xs + r * K, K, c, o[r]);
+            for (int r = 0; r < RC; r++)
+                reinterpret_cast<lds_u32x4_t*>(xs)[r * (K2 / 4) + c] = u32x4_t{o[r].x, o[r].y, o[r].z, o[r].w};
     }
 }
 
@@ -283,11 +275,11 @@ template <int E, int MODE, int NCH, int W, int RC, int RPW>
 __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
     constexpr int T = 64 * W, TEAM = kWave / RPW, ROWS = RPW * W, XCH = (NCH * TEAM + T - 1) / T;
     static_assert((E != E_QKV && E != E_STOP && E != E_CFMF) || RPW == 2, "per-row lanes live in a half wave");
-    extern __shared__ float xs[];  // [RC][K] f32 (bf16 values), natural order
+    extern __shared__ uint32_t xs[];  // [R][K/2] bf16 pairs, natural order
     __shared__ float red[W * kMaxSlots];
     static_assert(RC <= kMaxSlots, "row slots");
     const int t = threadIdx.x, wave = t / kWave, lane = t % kWave, team = lane / TEAM, tl = lane % TEAM;
-    const int K = a.K, R = a.R, NCk = K / 8;
+    const int K = a.K, R = a.R, NCk = K / 8, K2 = K / 2;
     const int n = blockIdx.x * ROWS + wave * RPW + team;
     const int nn = min(n, a.N - 1);
     // weight matrix and row of output n (q/k/v: D % 8 == 0 keeps a row pair in one matrix)
@@ -304,6 +296,8 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
     const EpiIn ep = epi_load<E>(a, nn, nrow, which, tl, Bv);
     stage_rows<MODE, RC, XCH, T>(a, xs, red, t);
     __syncthreads();
+    // dot products of this team's row with the RC staged row slots: no
+    // branches, so all LDS reads issue ahead of the dot chains
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
         const uint32_t m = tl + TEAM * j < NCk ? 0xffffffffu : 0u;
@@ -312,13 +306,7 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
         wr[j].z &= m;
         wr[j].w &= m;
     }
-    // dot products of this team's row with the RC staged row slots: no
-    // branches, so all LDS reads issue ahead of the chains.  Each product
-    // enters the accumulator through an IEEE fused multiply-add in element
-    // order (bf16 products are exact in f32, so a CPU reproduces every sum
-    // bit for bit); the rows sit in LDS as f32, and the weight chunk is
-    // unpacked once for all row slots.
-    const lds_f32x4_t* xv4 = reinterpret_cast<const lds_f32x4_t*>(xs);
+    const lds_u32x4_t* xv4 = reinterpret_cast<const lds_u32x4_t*>(xs);
     float acc[RC];
 #pragma unroll
     for (int r = 0; r < RC; r++) acc[r] = 0.0f;
@@ -326,14 +314,10 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
     // products, so they overlap the math instead of each waiting out its own
     // latency (wider slot counts would need the registers twice over)
     constexpr int NB = RC <= 6 ? 2 : 1;
-    f32x4_l xv[NB][RC][2];
+    u32x4_t xv[NB][RC];
     if constexpr (NB == 2) {
 #pragma unroll
-        for (int r = 0; r < RC; r++) {
-            const int c0 = min(tl, NCk - 1);
-            xv[0][r][0] = xv4[r * (K / 4) + c0];
-            xv[0][r][1] = xv4[r * (K / 4) + K / 8 + c0];
-        }
+        for (int r = 0; r < RC; r++) xv[0][r] = xv4[r * (K2 / 4) + min(tl, NCk - 1)];
     }
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
@@ -341,22 +325,15 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
         if (jn < NCH) {
             const int c = min(tl + TEAM * jn, NCk - 1);
 #pragma unroll
-            for (int r = 0; r < RC; r++) {
-                xv[jn % NB][r][0] = xv4[r * (K / 4) + c];
-                xv[jn % NB][r][1] = xv4[r * (K / 4) + K / 8 + c];
-            }
+            for (int r = 0; r < RC; r++) xv[jn % NB][r] = xv4[r * (K2 / 4) + c];
         }
-        const float wv[8] = {bf_lo(wr[j].x), bf_hi(wr[j].x), bf_lo(wr[j].y), bf_hi(wr[j].y),
-                             bf_lo(wr[j].z), bf_hi(wr[j].z), bf_lo(wr[j].w), bf_hi(wr[j].w)};
+        const u32x4_t(&x)[RC] = xv[j % NB];
 #pragma unroll
         for (int r = 0; r < RC; r++) {
-            const f32x4_l(&x)[2] = xv[j % NB][r];
-            float s = acc[r];
-#pragma unroll
-            for (int e = 0; e < 4; e++) s = __builtin_fmaf(wv[e], x[0][e], s);
-#pragma unroll
-            for (int e = 0; e < 4; e++) s = __builtin_fmaf(wv[4 + e], x[1][e], s);
-            acc[r] = s;
+            float s = dot2(wr[j].x, x[r].x, acc[r]);
+            s = dot2(wr[j].y, x[r].y, s);
+            s = dot2(wr[j].z, x[r].z, s);
+            acc[r] = dot2(wr[j].w, x[r].w, s);
         }
     }
 #pragma unroll
@@ -459,7 +436,7 @@ __global__ __launch_bounds__(256) void adaln_cond_kernel(const uint16_t* te, con
 // Attention over the L positions of each sequence, one wave per (sequence,
 // head), lane d owning dimension d (lanes past head_dim add zeros): every
 // q/k/v load is issued first; scores sum_d (q/8) k in f32 (wave sums),
-// p = exp_rep(s - max), l = sum p, o = (sum_j p_j v_j) / l rounded once.
+// p = exp(s - max), l = sum p, o = (sum_j p_j v_j) / l rounded once.
 __global__ __launch_bounds__(kWave) void dit_attn_kernel(const uint16_t* qkv, int R, int L, int D, int heads,
                                                          int hd, uint16_t* att) {
     const int b = blockIdx.x / heads, h = blockIdx.x % heads, d = threadIdx.x, dd = min(d, hd - 1);
@@ -499,31 +476,19 @@ __global__ __launch_bounds__(kWave) void dit_attn_kernel(const uint16_t* qkv, in
         }
 }
 
-// Launch with `lds` bytes of dynamic LDS; beyond 64 KB (f32 row slots of long
-// rows: 6 x 4096, 8 x 3584) the kernel's limit is raised first, once per
-// instantiation and size.
-template <class Kern>
-hipError_t launch_lds(Kern kern, int grid, int threads, size_t lds, hipStream_t st, const DitGemv& a) {
-    static size_t raised = 65536;
-    if (lds > raised) {
-        const hipError_t e =
-            hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        raised = lds;
-    }
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(threads), lds, st, a);
-    return hipGetLastError();
-}
-
 template <int E, int MODE, int W, int RC, int RPW>
 hipError_t launch_wr(hipStream_t st, const DitGemv& a) {
     constexpr int ROWS = RPW * W, TEAM = kWave / RPW;
     const int grid = (a.N + ROWS - 1) / ROWS;
-    const size_t lds = sizeof(float) * (size_t)RC * a.K;
-    if (lds > 160 * 1024) return hipErrorInvalidValue;
-    if (a.K <= 8 * TEAM) return launch_lds(dit_gemv_kernel<E, MODE, 1, W, RC, RPW>, grid, 64 * W, lds, st, a);
-    if (a.K <= 32 * TEAM) return launch_lds(dit_gemv_kernel<E, MODE, 4, W, RC, RPW>, grid, 64 * W, lds, st, a);
-    return launch_lds(dit_gemv_kernel<E, MODE, 4096 / (8 * TEAM), W, RC, RPW>, grid, 64 * W, lds, st, a);
+    const size_t lds = sizeof(uint32_t) * (size_t)RC * (a.K / 2);
+    if (a.K <= 8 * TEAM)
+        hipLaunchKernelGGL((dit_gemv_kernel<E, MODE, 1, W, RC, RPW>), dim3(grid), dim3(64 * W), lds, st, a);
+    else if (a.K <= 32 * TEAM)
+        hipLaunchKernelGGL((dit_gemv_kernel<E, MODE, 4, W, RC, RPW>), dim3(grid), dim3(64 * W), lds, st, a);
+    else
+        hipLaunchKernelGGL((dit_gemv_kernel<E, MODE, 4096 / (8 * TEAM), W, RC, RPW>), dim3(grid), dim3(64 * W),
+                           lds, st, a);
+    return hipGetLastError();
 }
 
 // Row slots.  Reference-shape stages: 1, 2 or 6 (3..6 rows run in 6 slots);

@@ -148,16 +148,27 @@ typedef struct {
 
 /* Summation order of every DiT function below (blocks, flow head, aggregator, stop head,
  * adaLN head): OR_DIT_ORDER_MLX (default) sums dot products over 8 interleaved f32 partials and
- * uses libm expf; OR_DIT_ORDER_DEVICE takes each f32 sum in the order of the library's batch-1
- * DiT kernels (team lanes over 16-byte chunks, fused multiply-adds in element order, the pairwise
- * lane tree, wave sums in order) and e^x by or_exp_rep, with the same graph and rounding points. */
-enum { OR_DIT_ORDER_MLX = 0, OR_DIT_ORDER_DEVICE = 1 };
+ * uses libm expf; OR_DIT_ORDER_DEVICE takes each f32 sum in the order and with the arithmetic of
+ * the library's batch-1 DiT kernels (team lanes over 16-byte chunks, v_dot2c_f32_bf16 steps
+ * restated by or_acc_step, the pairwise lane tree, wave sums in order) and e^x by or_exp_rep;
+ * OR_DIT_ORDER_MFMA is the device order with the dot products of the batched flow head's matrix
+ * core GEMM (or_dot_mfma).  Same graph and rounding points in every mode. */
+enum { OR_DIT_ORDER_MLX = 0, OR_DIT_ORDER_DEVICE = 1, OR_DIT_ORDER_MFMA = 2 };
 void or_set_dit_order(int mode);
 int or_get_dit_order(void);
 /* e^x from correctly rounded f32 steps (Cody-Waite reduction, degree-7 Taylor, 2^n scaling). */
 float or_exp_rep(float x);
+/* acc + sum_{i<n} a_i b_i (bf16, n <= 32) as one accumulation step of gfx950's v_dot2c_f32_bf16
+ * (n = 2) or of one 8-k block of v_mfma_f32_16x16x32_bf16 (n = 8); other n for tests. */
+float or_acc_step(float acc, const uint16_t* a, const uint16_t* b, int n);
+/* Batches of or_acc_step: dot2 over u32 bf16 pairs; 16x16x32 matrix tiles (A [t][16][32],
+ * B [t][32][16], C, D [t][16][16]). */
+void or_dot2_batch(const uint32_t* a, const uint32_t* b, const float* c, float* d, int64_t n);
+void or_mfma_batch(const uint16_t* A, const uint16_t* B, const float* C, float* D, int64_t ntests);
 /* One dot product of bf16 w, x [K] in the device order with a team of T (32 or 64) lanes. */
 float or_dot_dev(const uint16_t* w, const uint16_t* x, int64_t K, int T);
+/* One dot product of bf16 w, x [K] in the batched (matrix core) order over vs K slices. */
+float or_dot_mfma(const uint16_t* w, const uint16_t* x, int64_t K, int vs);
 /* Sum of squares of x [K] (K <= 1024) in the device order. */
 float or_sumsq_dev(const uint16_t* x, int64_t K);
 

@@ -6,9 +6,11 @@ compared bit for bit.
   within one f32 ulp over the range, exact at 0, the clamps at -86 / 88.
 - Known answers worked out by hand for inputs where the order decides the result: a team of
   lanes meeting in a pairwise tree (not in lane sequence), a lane's products entering its
-  accumulator one by one (not in rounded pairs), and the sum of squares taken per 64-lane wave
-  tree, then wave by wave.  A plausible slip (sequential lanes, pairs rounded first, the MLX
-  order's 8 partials) gives a different value in each.
+  accumulator two at a time through the dot instruction's step (or_acc_step, pinned against the
+  device in tests/test_oracle_arith.py; IEEE fused multiply-adds one by one give another value),
+  and the sum of squares taken per 64-lane wave tree, then wave by wave.  A plausible slip
+  (sequential lanes, one product at a time, the MLX order's 8 partials) gives a different value
+  in each.
 - Random rows: the device-order dot products and sums of squares against float64, within the
   f32 accumulation bound.
 The DiT functions in this order are pinned by the same float64 restatements, closed forms and
@@ -66,12 +68,14 @@ def test_dot_dev_lane_tree_known_answer():
 
 
 def test_dot_dev_element_order_known_answer():
-    # one chunk [1, 1, 2^24, 1, 0, 0, 0, 0] with unit weights: the products enter the lane's
-    # accumulator one by one, 1 + 1 = 2, 2 + 2^24 = 2^24 + 2, + 1 = 2^24 + 3 -> 2^24 + 4 (tie to
-    # even).  Pairs rounded first, RN(RN(2^24 + 1) + 2): 2^24 + 2.
+    # one chunk [2^24, -0.75, 0, ...] with unit weights: both products enter in one dot2 step, whose
+    # grid (1 here) truncates -0.75 to 0 -> 2^24.  One product at a time (fused multiply-adds):
+    # 2^24 - 0.75 -> 2^24 - 1.
     w = bits(np.ones(8))
-    x = bits([1.0, 1.0, BIG, 1.0, 0, 0, 0, 0])
-    assert oracle.dot_dev(w, x, 32) == BIG + 4
+    assert oracle.dot_dev(w, bits([BIG, -0.75, 0, 0, 0, 0, 0, 0]), 32) == BIG
+    # [1, 1, 2^24, 1, ...]: step 1 gives 2, step 2 adds 2^24 + 1 on the grid 1 -> 2^24 + 3 -> tie to
+    # even 2^24 + 4 (pairs each rounded before the accumulator joins: 2^24 + 2)
+    assert oracle.dot_dev(w, bits([1.0, 1.0, BIG, 1.0, 0, 0, 0, 0]), 32) == BIG + 4
 
 
 def test_sumsq_dev_known_answer():
