@@ -57,6 +57,15 @@ bool alive(const ming_ctx* c) { return c && c->alive; }
 // workgroups read one normalised vector (q/k/v, gate/up, head); o and down
 // (64 workgroups each) are faster staging their inputs themselves.
 // MING_LM_HUB_STAGES (a decimal bit mask) overrides the choice.
+// Attention splits grouped by XCD (StepArgs::att_xl) unless MING_LM_ATT_XL=0.
+bool att_xl_enabled() {
+    static const bool v = [] {
+        const char* e = std::getenv("MING_LM_ATT_XL");
+        return !(e && e[0] == '0' && e[1] == '\0');
+    }();
+    return v;
+}
+
 int hub_stages() {
     static const int v = [] {
         const char* e = std::getenv("MING_LM_HUB_STAGES");
@@ -709,12 +718,12 @@ int ming_lm_model_create(ming_ctx* ctx, const ming_lm_cfg* cfg, const ming_lm_la
     if (e == hipSuccess) e = m->ta.ensure(sizeof(uint64_t) * (size_t)L * (H / 2));
     if (e == hipSuccess) e = m->tx1.ensure(sizeof(uint64_t) * (size_t)L * (H / 2));
     if (e == hipSuccess) e = m->th.ensure(sizeof(uint64_t) * (size_t)L * (I / 2));
-    if (e == hipSuccess) e = m->counters.ensure(sizeof(int32_t) * (size_t)(L * cfg->kv_heads + 1));
+    if (e == hipSuccess) e = m->counters.ensure(sizeof(int32_t) * (size_t)(2 * L * cfg->kv_heads + 1));
     m->img_stride = tagged_img_stride(H, I);
     m->nflag = (4 * L + 1 + 31) / 32 * 32;  // whole 128-byte lines per hub
     if (e == hipSuccess) e = m->img.ensure(sizeof(uint32_t) * (size_t)kMaxHubs * kImgSlots * m->img_stride);
     if (e == hipSuccess) e = m->hflag.ensure(sizeof(uint32_t) * (size_t)kMaxHubs * m->nflag);
-    if (e == hipSuccess) e = m->hubtab.ensure(sizeof(uint64_t) * 32);
+    if (e == hipSuccess) e = m->hubtab.ensure(sizeof(uint64_t) * (kAttXlBase + kAttXlSlots));
     for (DevBuf* b : {&m->tx, &m->tq, &m->ta, &m->tx1, &m->th, &m->counters, &m->img, &m->hflag, &m->hubtab})
         if (e == hipSuccess) e = hipMemset(b->p, 0, b->bytes);
     if (e != hipSuccess) {
@@ -854,6 +863,9 @@ static int lm_step_impl(ming_ctx* ctx, ming_lm_model* m, const int32_t* token_de
         a.hflag = static_cast<uint32_t*>(m->hflag.p);
         a.nflag = m->nflag;
         a.hubtab = static_cast<uint64_t*>(m->hubtab.p);
+        // XCD-grouped splits: split sp of kv head g on worker W-1-(8 sp + g), clear of the front workers
+        a.att_xl = att_xl_enabled() && c->kv_heads <= 8 && 8 * (nsplit - 1) + c->kv_heads <= workers - front &&
+                   8 * nsplit <= kAttXlSlots;
         a.split_len = tsl;
         a.epoch = ++m->epoch;
         if (a.epoch == 0) a.epoch = ++m->epoch;

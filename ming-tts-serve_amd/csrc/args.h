@@ -64,7 +64,8 @@ struct StepArgs {
     uint64_t* ta;             // [n_layers][H/2]       merged attention
     uint64_t* tx1;            // [n_layers][H/2]
     uint64_t* th;             // [n_layers][I/2]
-    int32_t* counters;        // [n_layers * kvh] attention arrivals, [n_layers * kvh] head arrivals
+    int32_t* counters;        // [n_layers * kvh] attention arrivals, [1] head arrivals, [n_layers * kvh] attention
+                              // arrivals of XCD-local splits (L2 atomics)
     uint32_t epoch;
     uint64_t* tstamp;         // optional [n_stamps][grid] wall-clock stamps per stage boundary
     // Hubs of the persistent schedule (one workgroup per XCD): each publishes
@@ -76,8 +77,16 @@ struct StepArgs {
     int img_stride;           // u32 words per image slot
     uint32_t* hflag;          // [kMaxHubs][nflag] epoch of each published image
     int nflag;                // flag words per hub (>= 4 * n_layers + 1)
-    uint64_t* hubtab;         // [kMaxHubs] tagged XCC id of each hub
+    uint64_t* hubtab;         // [kMaxHubs] tagged XCC id of each hub, then [kAttXlSlots] of attention workers
+    // Attention splits grouped by XCD (1): worker W-1-(8 sp + g) runs split sp of kv
+    // head g, so a kv head's splits share an XCD when workgroup b runs on XCD b % 8
+    // (checked per launch); they then meet through that XCD's L2.  0: splits in
+    // unit order across the grid, meeting device-coherently.
+    int att_xl;
 };
+
+constexpr int kAttXlBase = 32;    // hubtab index of the attention workers' XCC ids
+constexpr int kAttXlSlots = 256;
 
 // Stages of the persistent schedule, as bits of StepArgs::hub_stages.
 enum : int { HUB_QKV = 1, HUB_O = 2, HUB_UP = 4, HUB_DOWN = 8, HUB_HEAD = 16 };

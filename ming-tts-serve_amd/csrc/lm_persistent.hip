@@ -477,9 +477,16 @@ __device__ __forceinline__ AttnGeom attn_geom(const Ctx& c) {
     AttnGeom q;
     const int n = a.pos + 1;
     q.ns = attn_splits(a.pos);
-    q.u = c.W - 1 - c.w;  // attention units on the last workers
-    q.g = q.u / q.ns;
-    q.sp = q.u % q.ns;
+    const int d = c.W - 1 - c.w;  // attention units on the last workers
+    if (a.att_xl) {  // split sp of kv head g on worker W-1-(8 sp + g): a kv head's splits 8 workgroups apart
+        q.g = d % 8;
+        q.sp = d / 8;
+        q.u = q.g < a.kvh && q.sp < q.ns ? q.g * q.ns + q.sp : -1;
+    } else {
+        q.u = d;
+        q.g = q.u / q.ns;
+        q.sp = q.u % q.ns;
+    }
     q.j0 = q.sp * kAttP;
     q.j1 = min(n, q.j0 + kAttP);
     return q;
@@ -488,6 +495,32 @@ __device__ __forceinline__ AttnGeom attn_geom(const Ctx& c) {
 __device__ __forceinline__ bool in_attn(const Ctx& c) {
     const AttnGeom q = attn_geom(c);
     return q.u >= 0 && q.u < c.a.kvh * q.ns;
+}
+
+// With XCD-grouped splits (att_xl), every split publishes its XCC id and reads
+// those of its kv head's splits: if all agree, the kv head's partials and its
+// arrival counter go through that XCD's L2 (plain stores, L2 atomics) instead
+// of device-coherent memory.  The same ids give every split of a kv head the
+// same answer; kept in LDS for the launch.
+__device__ __forceinline__ void attn_xl_publish(const Ctx& c, uint32_t xcc) {
+    if (c.a.att_xl && tix() == 0) tstore(c.a.hubtab + kAttXlBase + (c.W - 1 - c.w), xcc, c.a.epoch);
+}
+
+__device__ __forceinline__ void attn_xl_check(const Ctx& c, uint32_t xcc) {
+    const StepArgs& a = c.a;
+    int* xl = reinterpret_cast<int*>(c.lds + kFlagOff + 2);
+    if (tix() < kWave) {
+        bool same = a.att_xl != 0;
+        if (same) {
+            const AttnGeom q = attn_geom(c);
+            const int sp = tix();
+            uint32_t x = xcc;
+            if (sp < q.ns) x = trecv1(a.hubtab + kAttXlBase + 8 * sp + q.g, a.epoch, a.flags);
+            same = __ballot(x != xcc) == 0ull;
+        }
+        if (tix() == 0) *xl = same;
+    }
+    __syncthreads();
 }
 
 // The split's K rows [j0, j0 + kAttP) of layer l into LDS (direct buffer
@@ -678,6 +711,7 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l) {
     // device-coherent stores, completed before the arrival
     const int ntl = min(kAttTiles, (q.j1 - q.j0 + kTile - 1) / kTile);  // tiles holding positions
     const int t = tix();
+    const bool xl = *reinterpret_cast<const int*>(c.lds + kFlagOff + 2) != 0;
     {
         const int h = t / hd, d = t % hd;
         if (h < grp) {
@@ -691,10 +725,18 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l) {
                 Ls += wgt * pi[1];
             }
             float* out = a.part + (((size_t)q.g * q.ns + q.sp) * grp + h) * (hd + 2);
-            cstore(out + 2 + d, o);
-            if (d == 0) {
-                cstore(out, M);
-                cstore(out + 1, Ls);
+            if (xl) {  // to this XCD's L2
+                gst(out + 2 + d, o);
+                if (d == 0) {
+                    gst(out, M);
+                    gst(out + 1, Ls);
+                }
+            } else {
+                cstore(out + 2 + d, o);
+                if (d == 0) {
+                    cstore(out, M);
+                    cstore(out + 1, Ls);
+                }
             }
         }
     }
@@ -702,10 +744,18 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l) {
     __syncthreads();
     int* last = reinterpret_cast<int*>(c.lds + kFlagOff);
     if (t == 0) {
-        int* ctr = a.counters + l * a.kvh + q.g;
-        const int old = __hip_atomic_fetch_add((MING_GLOBAL int*)ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *last = old == q.ns - 1;
-        if (old == q.ns - 1) astore(ctr, 0);
+        if (xl) {  // the kv head's splits share this XCD: an L2 atomic
+            int* ctr = a.counters + a.n_layers * a.kvh + 1 + l * a.kvh + q.g;
+            const int old = __hip_atomic_fetch_add((MING_GLOBAL int*)ctr, 1, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+            *last = old == q.ns - 1;
+            if (old == q.ns - 1) __hip_atomic_store((MING_GLOBAL int*)ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        } else {
+            int* ctr = a.counters + l * a.kvh + q.g;
+            const int old = __hip_atomic_fetch_add((MING_GLOBAL int*)ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *last = old == q.ns - 1;
+            if (old == q.ns - 1) astore(ctr, 0);
+        }
     }
     lds_sync();
     if (!*last) return;
@@ -1086,7 +1136,11 @@ __global__ __launch_bounds__(kT) void decode_tagged_kernel(StepArgs args, const 
     const Ctx c0{a, lds, W, w, wave, lane, lane / 32, lane % 32, hub};
     const bool pq = in_qkv(c0), pa = in_attn(c0), po = in_rowpairs(c0);
     const int L = a.n_layers;
-    if (pa) attn_prefetch(c0, 0);
+    if (pa) {
+        attn_xl_publish(c0, xcc);
+        attn_prefetch(c0, 0);
+        attn_xl_check(c0, xcc);
+    }
     for (int l = 0; l < L; l++) {
         const int ln = tix() % kWave;
         const Ctx c{a, lds, W, w, wave, ln, ln / 32, ln % 32, hub};
