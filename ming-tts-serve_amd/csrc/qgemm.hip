@@ -585,6 +585,247 @@ __global__ __launch_bounds__(256) void qgemm_lds_kernel(QgemmArgs a, int kslices
         }
 }
 
+// One group from packed weight words: as group_mma_pre (the same MFMA chain and
+// fold, so the same bits), with each column tile's two B operands unpacked from
+// its two u32 words (8 nibbles each, pair order) right before their MFMAs.
+template <int MT, int NW>
+__device__ __forceinline__ void group_mma_packed(const AIn<MT>& in, const uint32_t (&bw)[NW][2], const float (&sc)[NW],
+                                                 const float (&off)[NW], f32x4_t (&acc)[MT][NW], uint32_t mask,
+                                                 uint32_t magic) {
+    f32x4_t ag[2][MT];
+    auto unpack = [&](uint32_t w) {
+        return make_uint4((w & mask) | magic, ((w >> 4) & mask) | magic, ((w >> 8) & mask) | magic,
+                          ((w >> 12) & mask) | magic);
+    };
+    auto issue = [&](int t, f32x4_t (&dst)[MT]) {
+        const bf16x8_t b0 = as_a(unpack(bw[t][0])), b1 = as_a(unpack(bw[t][1]));
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+            dst[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_a(in.xa[mt][0]), b0, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+            dst[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_a(in.xa[mt][1]), b1, dst[mt], 0, 0, 0);
+    };
+    auto fold = [&](int t, const f32x4_t (&src)[MT]) {
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const float xv[4] = {in.xsv[mt].x, in.xsv[mt].y, in.xsv[mt].z, in.xsv[mt].w};
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[mt][t][r] = fmaf(off[t], xv[r], fmaf(sc[t], src[mt][r], acc[mt][t][r]));
+        }
+    };
+    issue(0, ag[0]);
+#pragma unroll
+    for (int t = 0; t < NW; t++) {
+        if (t + 1 < NW) issue(t + 1, ag[(t + 1) & 1]);
+        fold(t, ag[t & 1]);
+    }
+}
+
+// More than 64 rows, wide tiles: qgemm_lds_kernel's arithmetic (group order,
+// K slices of the <= 64-row launch, fold) on WM x WN waves with MT x NW tiles
+// each, the weights kept packed in LDS (4 bits a value instead of the 16 of an
+// unpacked B operand) so that a tile of 16 NW WN columns fits: every column
+// and group word is stored word-major, Bp[word][column] with a row of kBPad
+// words, so the 64 lanes of an operand read (16 columns x 4 words 2 j + h)
+// fall in 64 distinct banks.  The activation rows are re-read once per 16 TPS
+// WN output columns instead of once per 32.
+constexpr int kBWords = kLdsGK * 8;  // packed words of one column per chunk
+template <int NC>
+struct BPad {
+    static constexpr int v = NC + 8;  // 2 j rows apart = 16 j banks: with c, 64 distinct banks
+};
+
+template <int WM, int WN, int MT, int NW, int EPI>
+__global__ __launch_bounds__(64 * WM * WN) void qgemm_wide_kernel(QgemmArgs a, int kslices) {
+    constexpr int T = 64 * WM * WN;
+    constexpr int TPS = EPI == QE_SWIGLU ? NW / 2 : NW;
+    constexpr int BM = 16 * WM * MT, NC = 16 * WN * NW;  // rows, weight columns of the tile
+    constexpr int AQ = BM * kLdsGK * 8 / T;              // activation uint4 per thread per chunk
+    constexpr int WQ = NC * kBWords / 4 / T;             // packed weight uint4 per thread per chunk
+    constexpr int SQ = NC * kLdsGK / T;                  // (scale, bias) pairs per thread per chunk
+    constexpr int BP = BPad<NC>::v;
+    static_assert(AQ * T == BM * kLdsGK * 8 && WQ * T * 4 == NC * kBWords && SQ * T == NC * kLdsGK, "whole chunk");
+    __shared__ uint4 As[2][BM * kRowStride];
+    __shared__ __align__(16) float Xs[2][kLdsGK * BM];
+    __shared__ uint32_t Bp[2][kBWords * BP];
+    __shared__ float2 Ss[2][NC * kLdsGK];
+    const int tid = threadIdx.x, lane = tid % kWave, c = lane % 16, j = lane / 16;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int wm = wave / WN, wn = wave % WN;
+    int blk = blockIdx.x, si = 0;
+    if (EPI != QE_SWIGLU && a.nseg > 1 && blk >= a.blocks[0]) {
+        blk -= a.blocks[0];
+        si = 1;
+        if (a.nseg > 2 && blk >= a.blocks[1]) {
+            blk -= a.blocks[1];
+            si = 2;
+        }
+    }
+    const int n0 = blk * 16 * TPS * WN;
+    const int G = a.K / 64, KW8 = a.K / 8, MTT = (a.M + 15) / 16, Mp = 16 * MTT;
+    const int r0 = blockIdx.y * BM;
+    auto wcol = [&](int k, const QSeg*& S) {
+        const int wq = k / (16 * NW), t = (k / 16) % NW;
+        S = &pick(a, EPI == QE_SWIGLU ? (t < TPS ? 0 : 1) : si);
+        return min(n0 + 16 * (wq * TPS + t % TPS) + k % 16, S->N - 1);
+    };
+    // this thread's packed-weight loads: uint4 q = tid + T i -> column q / 4, group (q / 2) % 2, half q % 2
+    const uint32_t* wrow[WQ];
+#pragma unroll
+    for (int i = 0; i < WQ; i++) {
+        const QSeg* WS;
+        const int q = tid + T * i;
+        const int n = wcol(q / 4, WS);
+        wrow[i] = WS->w + (size_t)n * KW8;
+    }
+    const uint16_t* srow[SQ];
+    const uint16_t* brow[SQ];
+#pragma unroll
+    for (int i = 0; i < SQ; i++) {
+        const QSeg* SS;
+        const int q = tid + T * i, n = wcol(q / kLdsGK, SS);
+        srow[i] = SS->s + (size_t)n * G;
+        brow[i] = SS->b + (size_t)n * G;
+    }
+    const bool xload = tid < kLdsGK * BM / 4;
+    const int xgg = tid / (BM / 4), xr = (tid % (BM / 4)) * 4;
+    const uint32_t mask = in_reg(0x000f000fu), magic = in_reg(kQ4Magic);
+    const uint4* xs = static_cast<const uint4*>(a.xs);
+    const int nch = (G + kLdsGK - 1) / kLdsGK;
+    struct Raw {
+        uint4 a[AQ], w[WQ], x;
+        uint32_t s[SQ], b[SQ];
+    };
+    auto fetch = [&](int ch, Raw& R) {
+#pragma unroll
+        for (int i = 0; i < AQ; i++) {
+            const int q = tid + T * i, row = q / (8 * kLdsGK), gg = (q / 8) % kLdsGK, wd = q % 8;
+            const int g = min(ch * kLdsGK + gg, G - 1), m = min(r0 + row, Mp - 1);
+            R.a[i] = ldg4(xs + ((size_t)g * Mp + m) * 8 + wd);
+        }
+        if (xload) {
+            const int g = min(ch * kLdsGK + xgg, G - 1), m = min(r0 + xr, Mp - 4);
+            R.x = ldg4(a.xsum + (size_t)g * Mp + m);
+        }
+#pragma unroll
+        for (int i = 0; i < WQ; i++) {
+            const int q = tid + T * i, gg = (q / 2) % kLdsGK, wh = q % 2, g = min(ch * kLdsGK + gg, G - 1);
+            R.w[i] = ldg4(wrow[i] + 8 * g + 4 * wh);
+        }
+#pragma unroll
+        for (int i = 0; i < SQ; i++) {
+            const int q = tid + T * i, g = min(ch * kLdsGK + q % kLdsGK, G - 1);
+            R.s[i] = gld(srow[i] + g);
+            R.b[i] = gld(brow[i] + g);
+        }
+    };
+    auto store = [&](const Raw& R, int buf) {
+#pragma unroll
+        for (int i = 0; i < AQ; i++) {
+            const int q = tid + T * i, row = q / (8 * kLdsGK), gg = (q / 8) % kLdsGK, wd = q % 8;
+            As[buf][row * kRowStride + gg * 8 + wd] = R.a[i];
+        }
+        if (xload) {
+            Xs[buf][xgg * BM + xr] = __uint_as_float(R.x.x);
+            Xs[buf][xgg * BM + xr + 1] = __uint_as_float(R.x.y);
+            Xs[buf][xgg * BM + xr + 2] = __uint_as_float(R.x.z);
+            Xs[buf][xgg * BM + xr + 3] = __uint_as_float(R.x.w);
+        }
+#pragma unroll
+        for (int i = 0; i < WQ; i++) {
+            const int q = tid + T * i, col = q / 4, gg = (q / 2) % kLdsGK, wh = q % 2, w0 = gg * 8 + 4 * wh;
+            Bp[buf][(w0 + 0) * BP + col] = R.w[i].x;
+            Bp[buf][(w0 + 1) * BP + col] = R.w[i].y;
+            Bp[buf][(w0 + 2) * BP + col] = R.w[i].z;
+            Bp[buf][(w0 + 3) * BP + col] = R.w[i].w;
+        }
+#pragma unroll
+        for (int i = 0; i < SQ; i++) {
+            const int q = tid + T * i;
+            const float sv = bf2f((uint16_t)R.s[i]), bv = bf2f((uint16_t)R.b[i]);
+            Ss[buf][q] = make_float2(sv, fmaf(-128.0f, sv, bv));  // q = column * kLdsGK + group
+        }
+    };
+    f32x4_t acc[MT][NW], run[MT][NW];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int t = 0; t < NW; t++) acc[mt][t] = run[mt][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const int gper = (G + kslices - 1) / kslices;
+    auto chunk = [&](int ch, int buf) {
+#pragma unroll
+        for (int gg = 0; gg < kLdsGK; gg++) {
+            const int g = ch * kLdsGK + gg;
+            if (g >= G) break;
+            AIn<MT> in;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const int row = 16 * (wm * MT + mt);
+                in.xa[mt][0] = As[buf][(row + c) * kRowStride + gg * 8 + 2 * j];
+                in.xa[mt][1] = As[buf][(row + c) * kRowStride + gg * 8 + 2 * j + 1];
+                in.xsv[mt] = *reinterpret_cast<const float4*>(&Xs[buf][gg * BM + row + 4 * j]);
+            }
+            uint32_t bw[NW][2];
+            float sc[NW], off[NW];
+#pragma unroll
+            for (int t = 0; t < NW; t++) {
+                const int col = 16 * (wn * NW + t) + c;
+                bw[t][0] = Bp[buf][(gg * 8 + 2 * j) * BP + col];
+                bw[t][1] = Bp[buf][(gg * 8 + 2 * j + 1) * BP + col];
+                const float2 f = Ss[buf][col * kLdsGK + gg];
+                sc[t] = f.x;
+                off[t] = f.y;
+            }
+            group_mma_packed<MT, NW>(in, bw, sc, off, acc, mask, magic);
+            if ((g + 1) % gper == 0 || g + 1 == G) {
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                    for (int t = 0; t < NW; t++) {
+                        run[mt][t] = run[mt][t] + acc[mt][t];
+                        acc[mt][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                    }
+            }
+        }
+    };
+    Raw R0{}, R1{};
+    fetch(0, R0);
+    store(R0, 0);
+    if (nch > 1) fetch(1, R1);
+    if (nch > 2) fetch(2, R0);
+    __syncthreads();
+    for (int ch = 0; ch < nch; ch += 2) {
+        chunk(ch, 0);
+        if (ch + 1 < nch) store(R1, 1);
+        __syncthreads();
+        if (ch + 3 < nch) fetch(ch + 3, R1);
+        if (ch + 1 >= nch) break;
+        chunk(ch + 1, 1);
+        if (ch + 2 < nch) store(R0, 0);
+        __syncthreads();
+        if (ch + 4 < nch) fetch(ch + 4, R0);
+    }
+    for (int sidx = (G + gper - 1) / gper; sidx < kslices; sidx++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int t = 0; t < NW; t++) run[mt][t] = run[mt][t] + f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const QSeg& S = pick(a, si);
+    const int nw0 = n0 + 16 * wn * TPS;
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = r0 + 16 * (wm * MT + mt) + 4 * j + r;
+            if (m >= a.M) continue;
+            float v[NW];
+#pragma unroll
+            for (int t = 0; t < NW; t++) v[t] = run[mt][t][r];
+            epi_row<MT, NW, EPI>(a, S, si, nw0, c, m, v);
+        }
+}
+
 // kw_in > 0 sets the number of waves splitting K (at most KWMAX).
 template <int MT, int NW, int GPW, int KWMAX, int EPI>
 hipError_t launch_k(hipStream_t st, const QgemmArgs& a, int kw_in = 0) {
@@ -947,6 +1188,32 @@ hipError_t launch_big(hipStream_t st, QgemmArgs a) {
     return hipGetLastError();
 }
 
+// More than 64 rows on qgemm_wide_kernel (same K slices as launch_big); false
+// when the shape does not tile: the caller takes launch_big.
+bool qgemm_wide_enabled() {
+    static const bool v = [] {
+        const char* e = std::getenv("MING_QGEMM_WIDE");
+        return !(e && e[0] == '0' && e[1] == '\0');
+    }();
+    return v;
+}
+
+template <int WM, int WN, int MT, int NW, int GPW, int KWMAX, int EPI>
+bool launch_wide(hipStream_t st, QgemmArgs a, hipError_t& err) {
+    constexpr int TPS = EPI == QE_SWIGLU ? NW / 2 : NW, CB = 16 * TPS * WN, BM = 16 * WM * MT;
+    if (!qgemm_wide_enabled()) return false;
+    for (int i = 0; i < a.nseg; i++)
+        if (a.seg[i].N % CB) return false;
+    const int G = a.K / 64, kw = GPW == 0 ? KWMAX : min(KWMAX, (G + GPW - 1) / GPW);
+    for (int i = 0; i < 3; i++) a.blocks[i] = i < a.nseg ? a.seg[i].N / CB : 0;
+    if (EPI == QE_SWIGLU) a.blocks[1] = 0;
+    const int grid = a.blocks[0] + a.blocks[1] + a.blocks[2];
+    const int mtt = (a.M + 15) / 16, gy = (16 * mtt + BM - 1) / BM;
+    hipLaunchKernelGGL((qgemm_wide_kernel<WM, WN, MT, NW, EPI>), dim3(grid, gy), dim3(64 * WM * WN), 0, st, a, kw);
+    err = hipGetLastError();
+    return true;
+}
+
 }  // namespace
 
 // a.blocks is filled here.  Shapes: the LM head 4 column tiles x 2 row tiles
@@ -984,7 +1251,12 @@ hipError_t launch_qgemm_epi(hipStream_t st, QgemmArgs a, int epi) {
             if (a.nseg != 2 || a.seg[0].N != a.seg[1].N) return hipErrorInvalidValue;
             set_blocks(32);
             a.blocks[1] = 0;
-            return big ? launch_big<2, 2, 2, 2, 0, 2, QE_SWIGLU>(st, a) : launch_mt<4, 0, 2, QE_SWIGLU, 2>(st, a);
+            if (big) {
+                hipError_t e;
+                if (launch_wide<2, 4, 2, 4, 0, 2, QE_SWIGLU>(st, a, e)) return e;
+                return launch_big<2, 2, 2, 2, 0, 2, QE_SWIGLU>(st, a);
+            }
+            return launch_mt<4, 0, 2, QE_SWIGLU, 2>(st, a);
         case QE_QKV:
             if (a.nseg != 3) return hipErrorInvalidValue;
             for (int i = 0; i < 3; i++)
