@@ -653,10 +653,12 @@ int ming_cfm_sample_batch(ming_ctx* ctx, ming_cfm_model* m, int32_t n, const voi
                                       u16(m->bxe.p), n, D, u16(m->brows[0].p));
         int cur = 0;
         for (size_t bl = 0; bl < m->blocks.size() && e == hipSuccess; bl++) {
+            // each block leaves the next one's rms1 of its output in bhn (fused into its ff2 reduce)
             e = launch_dit_block_gemm(s, m->blocks[bl], u16(m->brows[cur].p), R, L,
                                       static_cast<const float*>(m->cos.p), static_cast<const float*>(m->sin.p),
                                       u16(m->bhn.p), u16(m->bqkv.p), u16(m->batt.p), u16(m->bx1.p), u16(m->bhh.p),
-                                      u16(m->brows[cur ^ 1].p), static_cast<float*>(m->bpart.p));
+                                      u16(m->brows[cur ^ 1].p), static_cast<float*>(m->bpart.p), bl > 0,
+                                      bl + 1 < m->blocks.size() ? &m->blocks[bl + 1] : nullptr);
             cur ^= 1;
         }
         if (e == hipSuccess)

@@ -334,12 +334,69 @@ __global__ __launch_bounds__(256) void dreduce_kernel(DGemm a) {
     if constexpr (E == DE_GELU) gst(a.out + off, f2bf(gelu_chain_b(e)));
 }
 
+// Split-K reduce with the residual epilogue (dreduce_kernel<DE_RES>'s arithmetic) followed
+// by the row norm of the result (drms_kernel's): one workgroup per row m, thread t holding
+// the 8-column chunks t, t + 256; writes the row to a.out and its normalised form to hn.
+// The same bits as the two kernels back to back, one launch fewer.
+__global__ __launch_bounds__(256) void dreduce_res_rms_kernel(DGemm a, const uint16_t* __restrict__ w, float eps,
+                                                              uint16_t* __restrict__ hn) {
+    __shared__ float red[4];
+    const int m = blockIdx.x, N = a.N;
+    constexpr int kMaxC = 2;  // chunks per thread: N <= 4096
+    uint32_t xv[kMaxC][4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMaxC; k++) {
+        const int i = threadIdx.x + 256 * k;
+        if (i >= N / 8) break;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            float v[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int n = 8 * i + 2 * p + h;
+                float sum = 0.0f;
+                for (int z = 0; z < a.ks; z++) sum += gld(a.part + ((size_t)z * a.R + m) * a.N + n);
+                const float e = rb(sum + bf2f(gld(a.b[0] + n)));
+                v[h] = rb(bf2f(gld(a.res + (size_t)m * a.ldo + n)) + e);
+            }
+            xv[k][p] = pack_bf2(v[0], v[1]);
+            ss += v[0] * v[0];
+            ss += v[1] * v[1];
+        }
+        gst(reinterpret_cast<uint4*>(a.out + (size_t)m * a.ldo) + i, make_uint4(xv[k][0], xv[k][1], xv[k][2], xv[k][3]));
+    }
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)N + eps);
+#pragma unroll
+    for (int k = 0; k < kMaxC; k++) {
+        const int i = threadIdx.x + 256 * k;
+        if (i >= N / 8) break;
+        const uint4 wv = ldg4(w + 8 * i);
+        const uint32_t we[4] = {wv.x, wv.y, wv.z, wv.w};
+        uint32_t r4[4];
+#pragma unroll
+        for (int p = 0; p < 4; p++)
+            r4[p] = pack_bf2(bf_lo(we[p]) * rb(bf_lo(xv[k][p]) * inv), bf_hi(we[p]) * rb(bf_hi(xv[k][p]) * inv));
+        gst(reinterpret_cast<uint4*>(hn + (size_t)m * N) + i, make_uint4(r4[0], r4[1], r4[2], r4[3]));
+    }
+}
+
 // 64-row tiles when they still give >= 128 workgroups, else 32-row tiles.
 // K >= 2048 (plain epilogues, with a partials buffer) splits four ways across
 // workgroups; the split depends on K alone, so a row's arithmetic does not
 // depend on how many rows are batched.
 template <int E>
-hipError_t dpick(hipStream_t st, DGemm a) {
+void dsplit(DGemm& a) {
+    constexpr bool SPLIT = E == DE_BIAS || E == DE_RES || E == DE_GELU;
+    const int gx = (a.N + kBN - 1) / kBN, tiles = gx * ((a.R + 31) / 32);
+    a.vs = SPLIT && a.K >= 2048 && a.K % (4 * 64) == 0 ? 4 : (SPLIT && a.K >= 1024 && a.K % (2 * 64) == 0 ? 2 : 1);
+    a.ks = !a.part ? 1 : (a.vs == 4 ? 4 : (a.vs == 2 && tiles < 512 ? 2 : 1));
+}
+
+template <int E>
+hipError_t dpick(hipStream_t st, DGemm a, const uint16_t* rms_w = nullptr, float rms_eps = 0.0f,
+                 uint16_t* rms_out = nullptr) {
     const int gx = (a.N + kBN - 1) / kBN;
     // The sum over K is taken in vs slices fixed by K alone (4 from K = 2048, 2 from K = 1024,
     // for the epilogues the reduce kernel applies), so a sequence's bits do not depend on the
@@ -348,10 +405,7 @@ hipError_t dpick(hipStream_t st, DGemm a) {
     // (measured on the 16- and 64-sequence server step: +9-11 %), except where the grid
     // already has >= 512 workgroups (splitting one at 768 loses 5 %); with ks < vs each
     // workgroup folds its slices in the reduce kernel's order.
-    constexpr bool SPLIT = E == DE_BIAS || E == DE_RES || E == DE_GELU;
-    const int tiles = gx * ((a.R + 31) / 32);
-    a.vs = SPLIT && a.K >= 2048 && a.K % (4 * 64) == 0 ? 4 : (SPLIT && a.K >= 1024 && a.K % (2 * 64) == 0 ? 2 : 1);
-    a.ks = !a.part ? 1 : (a.vs == 4 ? 4 : (a.vs == 2 && tiles < 512 ? 2 : 1));
+    dsplit<E>(a);
     if (a.K % (64 * a.vs)) return hipErrorInvalidValue;
     // 128-wide K stages put twice the bytes of each stage in flight (measured: +10 % at 96 rows);
     // slices are whole stages
@@ -360,7 +414,22 @@ hipError_t dpick(hipStream_t st, DGemm a) {
     else
         hipLaunchKernelGGL((dgemm_kernel<32, 64, E>), dim3(gx, (a.R + 31) / 32, a.ks), dim3(256), 0, st, a);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.ks == 1) return e;
+    if (e != hipSuccess) return e;
+    // rms_out: the caller wants the rows' norm next (DE_RES only); with split K the reduce does it
+    if (a.ks == 1) {
+        if (rms_out) {
+            hipLaunchKernelGGL(drms_kernel, dim3(a.R), dim3(256), 0, st, a.out, a.N, 0, rms_w, rms_eps, rms_out);
+            e = hipGetLastError();
+        }
+        return e;
+    }
+    if constexpr (E == DE_RES) {
+        if (rms_out) {
+            if (a.N % 8 || a.N > 4096 || a.ldo != a.N) return hipErrorInvalidValue;
+            hipLaunchKernelGGL(dreduce_res_rms_kernel, dim3(a.R), dim3(256), 0, st, a, rms_w, rms_eps, rms_out);
+            return hipGetLastError();
+        }
+    }
     if constexpr (E == DE_BIAS || E == DE_RES || E == DE_GELU) {
         hipLaunchKernelGGL(dreduce_kernel<E>, dim3((a.R * a.N + 255) / 256), dim3(256), 0, st, a);
         e = hipGetLastError();
@@ -388,14 +457,20 @@ DGemm gemm_args(const uint16_t* x, int R, int N, int K, const uint16_t* w, const
 // One DiT block over R rows of L positions: rms1 -> q/k/v (+ rotary) -> attention
 // -> out_proj + residual -> rms2 -> ff1 + gelu -> ff2 + residual.  x and out may
 // not alias; hn [R][D], qkv [3][R][D], att [R][D], x1 [R][D], hh [R][F] and
-// part f32 scratch of max(4 R D, 2 R F) floats (split-K partials).
+// part f32 scratch of max(4 R D, 2 R F) floats (split-K partials).  hn_ready: hn
+// already holds rms1(x) (the block before wrote it); next: the following block,
+// whose rms1 of this block's output is left in hn.  A residual projection with
+// split K takes the norm after it into its reduce kernel (dreduce_res_rms_kernel).
 hipError_t launch_dit_block_gemm(hipStream_t st, const DitBlockDev& w, const uint16_t* x, int R, int L,
                                  const float* cos_t, const float* sin_t, uint16_t* hn, uint16_t* qkv, uint16_t* att,
-                                 uint16_t* x1, uint16_t* hh, uint16_t* out, float* part) {
+                                 uint16_t* x1, uint16_t* hh, uint16_t* out, float* part, bool hn_ready,
+                                 const DitBlockDev* next) {
     const int D = w.D, F = w.F;
     hipError_t e;
-    hipLaunchKernelGGL(drms_kernel, dim3(R), dim3(256), 0, st, x, D, 0, w.norm1, w.eps, hn);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (!hn_ready) {
+        hipLaunchKernelGGL(drms_kernel, dim3(R), dim3(256), 0, st, x, D, 0, w.norm1, w.eps, hn);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     DGemm a = gemm_args(hn, R, 3 * D, D, w.wq, w.bq, qkv);
     a.w[1] = w.wk;
     a.w[2] = w.wv;
@@ -410,16 +485,14 @@ hipError_t launch_dit_block_gemm(hipStream_t st, const DitBlockDev& w, const uin
     a = gemm_args(att, R, D, D, w.wo, w.bo, x1);
     a.res = x;
     a.part = part;  // [2][R][D] of the [4][R][D] scratch
-    if ((e = dpick<DE_RES>(st, a)) != hipSuccess) return e;
-    hipLaunchKernelGGL(drms_kernel, dim3(R), dim3(256), 0, st, x1, D, 0, w.norm2, w.eps, hn);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = dpick<DE_RES>(st, a, w.norm2, w.eps, hn)) != hipSuccess) return e;  // x1, then rms2(x1) into hn
     a = gemm_args(hn, R, F, D, w.w1, w.b1, hh);
     a.part = part;  // [2][R][F]
     if ((e = dpick<DE_GELU>(st, a)) != hipSuccess) return e;
     a = gemm_args(hh, R, D, F, w.w2, w.b2, out);
     a.res = x1;
     a.part = part;  // [4][R][D] f32: ff2's K = F splits
-    return dpick<DE_RES>(st, a);
+    return next ? dpick<DE_RES>(st, a, next->norm1, next->eps, hn) : dpick<DE_RES>(st, a);
 }
 
 // out [R][N] = bf16(x W^T + b) (x [R][K]).

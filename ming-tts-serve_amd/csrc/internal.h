@@ -109,7 +109,8 @@ hipError_t launch_prefill_rows(hipStream_t st, const int32_t* table, int pps, in
 hipError_t launch_dit_attn(hipStream_t st, const uint16_t* qkv, int B, int L, int D, int heads, int hd, uint16_t* att);
 hipError_t launch_dit_block_gemm(hipStream_t st, const DitBlockDev& w, const uint16_t* x, int R, int L,
                                  const float* cos_t, const float* sin_t, uint16_t* hn, uint16_t* qkv, uint16_t* att,
-                                 uint16_t* x1, uint16_t* hh, uint16_t* out, float* part);
+                                 uint16_t* x1, uint16_t* hh, uint16_t* out, float* part, bool hn_ready = false,
+                                 const DitBlockDev* next = nullptr);
 hipError_t launch_dit_linear_gemm(hipStream_t st, const uint16_t* x, int R, const uint16_t* w, int N, int K,
                                   const uint16_t* b, uint16_t* out);
 hipError_t launch_cfm_rows_batch(hipStream_t st, const uint16_t* te, const uint16_t* ce, const uint16_t* bc,
