@@ -119,7 +119,7 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--ctx", type=int, default=2048)
-    p.add_argument("--mode", choices=["auto", "kernels", "persistent", "direct"], default="auto")
+    p.add_argument("--mode", choices=["auto", "kernels", "persistent", "direct", "xcd"], default="auto")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--stamps", action="store_true",
@@ -165,7 +165,7 @@ def main():
     syn = S.SyntheticLm(ctx, spec, seed=0, quant=True)
     m = syn.model()
     m.set_mode({"auto": ming.LM_AUTO, "kernels": ming.LM_KERNELS, "persistent": ming.LM_PERSISTENT,
-                "direct": ming.LM_PERSISTENT_DIRECT}[args.mode])
+                "direct": ming.LM_PERSISTENT_DIRECT, "xcd": ming.LM_PERSISTENT_XCD}[args.mode])
     # the cache is prefilled so that the timed steps decode at positions ctx .. ctx + steps - 1:
     # the warm-up steps append the rows just before ctx, and every step appends one row
     start = max(1, args.ctx - args.warmup)
@@ -203,7 +203,7 @@ def main():
     bytes_tok = int(round(sum(S.lm_bytes_per_token(spec, args.ctx + i) for i in range(args.steps)) / args.steps))
     achieved = bytes_tok / (launch_ms * 1e-3) / 1e9
 
-    if args.stamps and args.mode in ("auto", "persistent", "direct"):
+    if args.stamps and args.mode in ("auto", "persistent", "direct", "xcd"):
         lm_stage_report(ctx, m, spec, cache, step, args.ctx)
 
     cpu = None
@@ -584,7 +584,7 @@ def bench_c1(args):
     syn = S.SyntheticLm(ctx, spec, seed=0, quant=False)
     m = syn.model()
     m.set_mode({"auto": ming.LM_AUTO, "kernels": ming.LM_KERNELS, "persistent": ming.LM_PERSISTENT,
-                "direct": ming.LM_PERSISTENT_DIRECT}[args.mode])
+                "direct": ming.LM_PERSISTENT_DIRECT, "xcd": ming.LM_PERSISTENT_XCD}[args.mode])
     ids = [int(t) for t in ming.synth_uniform_i32(0, "c1.prompt", C1_PROMPT, spec.vocab)]
     ptok = torch.tensor(ids, dtype=torch.int32, device="cuda")
     cache = S.KvCache(spec, C1_PROMPT + C1_STEPS)

@@ -266,7 +266,9 @@ enum ming_lm_mode {
     MING_LM_AUTO = 0,        /* fastest available */
     MING_LM_KERNELS = 1,     /* one launch per stage (debug / reference schedule) */
     MING_LM_PERSISTENT = 2,  /* one persistent kernel per token */
-    MING_LM_PERSISTENT_DIRECT = 3  /* persistent, every workgroup stages its own inputs (no per-XCD hubs) */
+    MING_LM_PERSISTENT_DIRECT = 3, /* persistent, every workgroup stages its own inputs (no per-XCD hubs) */
+    MING_LM_PERSISTENT_XCD = 4     /* persistent, each kv head's q/k/v, attention and o_proj inside one XCD;
+                                      o_proj and down as split-K partials summed by the per-XCD hubs */
 };
 int ming_lm_model_set_mode(ming_lm_model* m, int32_t mode);
 

@@ -39,7 +39,7 @@ MING_E_TIMEOUT = 7
 
 DT_BF16, DT_F32, DT_U32, DT_I32 = 1, 2, 3, 4
 W_BF16, W_AFFINE = 0, 1
-LM_AUTO, LM_KERNELS, LM_PERSISTENT, LM_PERSISTENT_DIRECT = 0, 1, 2, 3
+LM_AUTO, LM_KERNELS, LM_PERSISTENT, LM_PERSISTENT_DIRECT, LM_PERSISTENT_XCD = 0, 1, 2, 3, 4
 CFM_AUTO, CFM_KERNELS, CFM_PERSISTENT = 0, 1, 2
 
 c_void_p = ctypes.c_void_p

@@ -19,6 +19,9 @@ hipError_t launch_lm_step_kernels(hipStream_t st, const StepArgs& a, const Layer
 hipError_t launch_lm_step_tagged(hipStream_t st, const StepArgs& a, int q4, int grid, bool cooperative);
 hipError_t launch_copy_token(hipStream_t st, const int32_t* src, int32_t* dst);
 int tagged_grid(int num_cus);
+hipError_t launch_lm_step_xcd(hipStream_t st, const StepArgs& a, int grid, bool cooperative);
+bool xcd_fits(int grid, int H, int heads, int kvh, int hd, int I, int n_layers);
+int xcd_slots(int I);
 int tagged_split_len(int n);
 int tagged_hubs(int grid);
 int tagged_img_stride(int H, int I);
@@ -64,6 +67,25 @@ bool att_xl_enabled() {
         return !(e && e[0] == '0' && e[1] == '\0');
     }();
     return v;
+}
+
+// The XCD-local schedule for MING_LM_AUTO unless MING_LM_XCD=0.
+bool xcd_enabled() {
+    static const bool on = [] {
+        const char* e = std::getenv("MING_LM_XCD");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
+// In the XCD-local schedule, hand-offs inside a slot through plain stores
+// (where the slot's workgroups share an XCD) unless MING_LM_XCD_LOCAL=0.
+bool xcd_local_enabled() {
+    static const bool on = [] {
+        const char* e = std::getenv("MING_LM_XCD_LOCAL");
+        return !(e && e[0] == '0');
+    }();
+    return on;
 }
 
 int hub_stages() {
@@ -232,6 +254,10 @@ struct ming_lm_model {
     // workspace
     DevBuf x, x1, att, qkv, hh, part, hidden, amax_v, amax_i;
     DevBuf tx, tq, ta, tx1, th, counters;  // tagged hand-off buffers, arrival counters
+    DevBuf tpo, tpd, tpa;                  // XCD-local schedule: o_proj, down and attention split partials
+    bool xcd_ok = false;                   // the XCD-local schedule takes this model
+    uint32_t xcd_parity = 0;               // epoch parity of the partials' last writes (0: as zeroed)
+    int xnsm = 0;                          // attention split slots per (layer, kv head) in tpa
     DevBuf img, hflag, hubtab;             // per-XCD hub images, their flags, hub XCC ids
     int img_stride = 0, nflag = 0;
 };
@@ -719,18 +745,31 @@ int ming_lm_model_create(ming_ctx* ctx, const ming_lm_cfg* cfg, const ming_lm_la
     if (e == hipSuccess) e = m->tx1.ensure(sizeof(uint64_t) * (size_t)L * (H / 2));
     if (e == hipSuccess) e = m->th.ensure(sizeof(uint64_t) * (size_t)L * (I / 2));
     if (e == hipSuccess) e = m->counters.ensure(sizeof(int32_t) * (size_t)(2 * L * cfg->kv_heads + 1));
+    if (e == hipSuccess) e = m->tpo.ensure(sizeof(uint32_t) * (size_t)L * cfg->kv_heads * H);
+    if (e == hipSuccess) e = m->tpd.ensure(sizeof(uint32_t) * (size_t)L * kMaxHubs * H);
+    m->pgrid = tagged_grid(ctx->num_cus);
+    m->xnsm = m->pgrid / kMaxHubs - 1;  // the attention splits of a kv head on one XCD slot's workers
+    if (e == hipSuccess && m->xnsm > 0)
+        e = m->tpa.ensure(sizeof(uint64_t) * (size_t)L * cfg->kv_heads * m->xnsm * (cfg->heads / cfg->kv_heads) *
+                          (cfg->head_dim + 2));
     m->img_stride = tagged_img_stride(H, I);
     m->nflag = (4 * L + 1 + 31) / 32 * 32;  // whole 128-byte lines per hub
     if (e == hipSuccess) e = m->img.ensure(sizeof(uint32_t) * (size_t)kMaxHubs * kImgSlots * m->img_stride);
     if (e == hipSuccess) e = m->hflag.ensure(sizeof(uint32_t) * (size_t)kMaxHubs * m->nflag);
-    if (e == hipSuccess) e = m->hubtab.ensure(sizeof(uint64_t) * (kAttXlBase + kAttXlSlots));
-    for (DevBuf* b : {&m->tx, &m->tq, &m->ta, &m->tx1, &m->th, &m->counters, &m->img, &m->hflag, &m->hubtab})
-        if (e == hipSuccess) e = hipMemset(b->p, 0, b->bytes);
+    if (e == hipSuccess) e = m->hubtab.ensure(sizeof(uint64_t) * (kXcdBase + kXcdSlots));
+    for (DevBuf* b :
+         {&m->tx, &m->tq, &m->ta, &m->tx1, &m->th, &m->counters, &m->img, &m->hflag, &m->hubtab, &m->tpo, &m->tpd,
+          &m->tpa})
+        if (e == hipSuccess && b->p) e = hipMemset(b->p, 0, b->bytes);
     if (e != hipSuccess) {
         ming_lm_model_destroy(m);
         return hip_check(ctx, e, "lm_model workspace");
     }
-    m->pgrid = tagged_grid(ctx->num_cus);
+    bool all_q4 = m->head.kind == 1;
+    for (const LayerDev& ld : m->layers)
+        for (const LinearDev* l : {&ld.q, &ld.k, &ld.v, &ld.o, &ld.g, &ld.u, &ld.d}) all_q4 = all_q4 && l->kind == 1;
+    m->xcd_ok = all_q4 && m->pgrid > 0 &&
+                xcd_fits(m->pgrid, H, cfg->heads, cfg->kv_heads, cfg->head_dim, I, L);
     *out = m;
     return MING_OK;
 }
@@ -739,7 +778,8 @@ int ming_lm_model_destroy(ming_lm_model* m) {
     if (!m) return MING_E_NOT_INIT;
     if (m->d_layers) (void)hipFree(m->d_layers);
     for (DevBuf* b : {&m->x, &m->x1, &m->att, &m->qkv, &m->hh, &m->part, &m->hidden, &m->amax_v, &m->amax_i,
-                      &m->tx, &m->tq, &m->ta, &m->tx1, &m->th, &m->counters, &m->img, &m->hflag, &m->hubtab})
+                      &m->tx, &m->tq, &m->ta, &m->tx1, &m->th, &m->counters, &m->img, &m->hflag, &m->hubtab,
+                      &m->tpo, &m->tpd, &m->tpa})
         b->release();
     delete m;
     return MING_OK;
@@ -760,7 +800,7 @@ int ming_lm_model_profile_shape(ming_lm_model* m, int32_t* n_stamps, int32_t* gr
 
 int ming_lm_model_set_mode(ming_lm_model* m, int32_t mode) {
     if (!m) return MING_E_NOT_INIT;
-    if (mode < MING_LM_AUTO || mode > MING_LM_PERSISTENT_DIRECT) return set_err(m->ctx, MING_E_ARG, "unknown mode");
+    if (mode < MING_LM_AUTO || mode > MING_LM_PERSISTENT_XCD) return set_err(m->ctx, MING_E_ARG, "unknown mode");
     m->mode = mode;
     return MING_OK;
 }
@@ -842,11 +882,55 @@ static int lm_step_impl(ming_ctx* ctx, ming_lm_model* m, const int32_t* token_de
     const bool persistent = want_persistent && fits;
     if (want_persistent && m->mode != MING_LM_AUTO && !fits)
         return set_err(ctx, MING_E_UNSUPPORTED, "lm_step: context too long for the persistent schedule");
+    // The XCD-local schedule: kv head g's splits on ranks 31..32-nsplit of slot 7-g.
+    const bool xfits = m->xcd_ok && nsplit <= m->pgrid / kMaxHubs - 1;
+    if (m->mode == MING_LM_PERSISTENT_XCD && !xfits)
+        return set_err(ctx, MING_E_UNSUPPORTED, "lm_step: shape or context outside the XCD-local schedule");
+    if (xfits && (m->mode == MING_LM_PERSISTENT_XCD || (m->mode == MING_LM_AUTO && xcd_enabled()))) {
+        if (ctx->timeout_seen) {  // a timed-out step may have left counters raised and partials unwritten
+            for (DevBuf* b : {&m->counters, &m->tpo, &m->tpd})
+                if ((st = hip_check(ctx, hipMemsetAsync(b->p, 0, b->bytes, ctx->stream), "reset counters")))
+                    return st;
+            m->xcd_parity = 0;  // the partials now hold parity 0
+            ctx->timeout_seen = false;
+        }
+        a.tx = static_cast<uint64_t*>(m->tx.p);
+        a.tq = static_cast<uint64_t*>(m->tq.p);
+        a.ta = static_cast<uint64_t*>(m->ta.p);
+        a.tx1 = static_cast<uint64_t*>(m->tx1.p);
+        a.th = static_cast<uint64_t*>(m->th.p);
+        a.tpo = static_cast<uint32_t*>(m->tpo.p);
+        a.tpd = static_cast<uint32_t*>(m->tpd.p);
+        a.tpa = static_cast<uint64_t*>(m->tpa.p);
+        a.xnsm = m->xnsm;
+        a.xslots = xcd_slots(c->inter);
+        a.counters = static_cast<int32_t*>(m->counters.p);
+        a.tstamp = m->tstamp;
+        a.nhubs = kMaxHubs;
+        a.hub_stages = HUB_QKV | HUB_UP | HUB_HEAD;
+        a.img = static_cast<uint32_t*>(m->img.p);
+        a.img_stride = m->img_stride;
+        a.hflag = static_cast<uint32_t*>(m->hflag.p);
+        a.nflag = m->nflag;
+        a.hubtab = static_cast<uint64_t*>(m->hubtab.p);
+        a.att_xl = 1;
+        a.xloc = xcd_local_enabled();
+        a.split_len = tsl;
+        // the partials were last written with parity xcd_parity: this step takes the other one
+        a.epoch = ++m->epoch;
+        while (a.epoch == 0 || (a.epoch & 1u) == m->xcd_parity) a.epoch = ++m->epoch;
+        st = hip_check(ctx, launch_lm_step_xcd(ctx->stream, a, m->pgrid, !ctx->exclusive), "lm_step XCD-local launch");
+        if (st) return st;
+        m->xcd_parity = a.epoch & 1u;
+        kv->len += 1;
+        return MING_OK;
+    }
     if (persistent) {
-        if (ctx->timeout_seen) {  // a timed-out step may have left arrival counters raised
-            if ((st = hip_check(ctx, hipMemsetAsync(m->counters.p, 0, m->counters.bytes, ctx->stream),
-                                "reset counters")))
-                return st;
+        if (ctx->timeout_seen) {  // a timed-out step may have left arrival counters raised and partials unwritten
+            for (DevBuf* b : {&m->counters, &m->tpo, &m->tpd})
+                if ((st = hip_check(ctx, hipMemsetAsync(b->p, 0, b->bytes, ctx->stream), "reset counters")))
+                    return st;
+            m->xcd_parity = 0;
             ctx->timeout_seen = false;
         }
         a.tx = static_cast<uint64_t*>(m->tx.p);

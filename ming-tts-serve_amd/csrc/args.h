@@ -83,10 +83,23 @@ struct StepArgs {
     // (checked per launch); they then meet through that XCD's L2.  0: splits in
     // unit order across the grid, meeting device-coherently.
     int att_xl;
+    // XCD-local schedule: o_proj partials of each kv head and down partials of
+    // each XCD slot, f32 whose lowest mantissa bit carries the epoch's parity
+    // (the reader clears it); xslots = slots that hold SwiGLU groups (and so
+    // down partials).  Every word is written at every step of this schedule,
+    // and consecutive steps of it use epochs of opposite parity.
+    uint32_t* tpo;            // [n_layers][kvh][H]
+    uint32_t* tpd;            // [n_layers][8][H]
+    int xslots;
+    uint64_t* tpa;            // [n_layers][kvh][xnsm][grp][hd + 2] attention split partials, tagged words
+    int xnsm;                 // split slots per (layer, kv head) in tpa
+    int xloc;                 // 1: hand-offs inside an XCD slot use plain stores where the slot is on one XCD
 };
 
 constexpr int kAttXlBase = 32;    // hubtab index of the attention workers' XCC ids
 constexpr int kAttXlSlots = 256;
+constexpr int kXcdBase = kAttXlBase + kAttXlSlots;  // hubtab index of every workgroup's XCC id (XCD-local schedule)
+constexpr int kXcdSlots = 1024;
 
 // Stages of the persistent schedule, as bits of StepArgs::hub_stages.
 enum : int { HUB_QKV = 1, HUB_O = 2, HUB_UP = 4, HUB_DOWN = 8, HUB_HEAD = 16 };

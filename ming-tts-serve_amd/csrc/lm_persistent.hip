@@ -76,6 +76,16 @@ static_assert(kLdsAll * 4 <= 160 * 1024, "LDS of one workgroup");
 static_assert(kAttOt + kAttTiles * 8 * 66 <= kRedOff, "attention partials below the reduction scratch");
 constexpr int kSc1 = 16;         // buffer-load cache policy bit: device scope
 
+// A tagged word for readers on this workgroup's own XCD (loc): a plain store,
+// which stays in the XCD's L2 where the readers' device-scope loads find it;
+// otherwise device-coherent.
+__device__ __forceinline__ void tstore_loc(uint64_t* p, uint32_t payload, uint32_t tag, bool loc) {
+    if (loc)
+        gst(p, ((uint64_t)tag << 32) | payload);
+    else
+        tagged::tstore(p, payload, tag);
+}
+
 template <int Q4>
 struct Nc {
     static constexpr int t32 = Q4 ? 1 : 4;   // chunks per lane, K = hidden
@@ -370,11 +380,12 @@ struct QkvW {
     float cs[2], sn[2];  // rope factors of dims d, d+1 (they do not depend on the input)
 };
 
+// The q/k/v stage for this wave's unit g (every wave of the workgroup calls it).
 template <int Q4>
-__device__ __forceinline__ void st_qkv(const Ctx& c, const LayerDev& Ld, int l) {
+__device__ __forceinline__ void st_qkv_g(const Ctx& c, const LayerDev& Ld, int l, const QkvGeom& g,
+                                         bool loc = false) {
     const StepArgs& a = c.a;
     const int half = a.hd / 2, kvd = a.kvh * a.hd, nq = a.H + 2 * kvd;
-    const QkvGeom g = qkv_geom(c);
     const int cr = g.cr, which = g.which, base = g.base, r0 = g.r0, lr = cr - base;
     const LinearDev& L = which == 0 ? Ld.q : (which == 1 ? Ld.k : Ld.v);
     QkvW<Q4> W;
@@ -422,8 +433,8 @@ __device__ __forceinline__ void st_qkv(const Ctx& c, const LayerDev& Ld, int l) 
     }
     uint64_t* tq = a.tq + (size_t)l * (nq / 2);
     const uint32_t w_lo = pack_bf2(e[0], e[1]), w_hi = pack_bf2(e[2], e[3]);
-    tstore(tq + cr / 2, w_lo, a.epoch);
-    tstore(tq + (cr + half) / 2, w_hi, a.epoch);
+    tstore_loc(tq + cr / 2, w_lo, a.epoch, loc);
+    tstore_loc(tq + (cr + half) / 2, w_hi, a.epoch, loc);
     uint32_t* pq = reinterpret_cast<uint32_t*>(a.qkv + l * a.sq);
     gst(pq + cr / 2, w_lo);
     gst(pq + (cr + half) / 2, w_hi);
@@ -434,6 +445,11 @@ __device__ __forceinline__ void st_qkv(const Ctx& c, const LayerDev& Ld, int l) 
         gst(dst + d / 2, w_lo);
         gst(dst + (d + half) / 2, w_hi);
     }
+}
+
+template <int Q4>
+__device__ __forceinline__ void st_qkv(const Ctx& c, const LayerDev& Ld, int l) {
+    st_qkv_g<Q4>(c, Ld, l, qkv_geom(c));
 }
 
 // ---- LB: split GQA attention over LDS-resident K/V + last-arriver merge ------------------
@@ -626,7 +642,7 @@ __device__ __forceinline__ void attn_recv(const Ctx& c, int l) {
 // C[dim][head], A = V^T rows, B = the probabilities split into bf16 hi + lo
 // (two MFMAs, so P keeps about 16 bits).  The tiles' partials meet through
 // LDS (in tile order) into the split's partial, which leaves as tagged words.
-__device__ __forceinline__ void attn_run(const Ctx& c, int l) {
+__device__ __forceinline__ void attn_run(const Ctx& c, int l, bool loc = false, bool direct = false) {
     const StepArgs& a = c.a;
     const AttnGeom q = attn_geom(c);
     const int grp = a.heads / a.kvh, hd = a.hd;
@@ -708,7 +724,8 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l) {
     }
     lds_sync();
     // the split's partial: per head the max over its tiles, the sum and output rescaled to it;
-    // device-coherent stores, completed before the arrival
+    // device-coherent stores, completed before the arrival (direct: tagged words of the layer's
+    // own partial slots, which the o_proj workers poll and merge; no arrival)
     const int ntl = min(kAttTiles, (q.j1 - q.j0 + kTile - 1) / kTile);  // tiles holding positions
     const int t = tix();
     const bool xl = *reinterpret_cast<const int*>(c.lds + kFlagOff + 2) != 0;
@@ -724,14 +741,22 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l) {
                 o += wgt * pi[2 + d];
                 Ls += wgt * pi[1];
             }
-            float* out = a.part + (((size_t)q.g * q.ns + q.sp) * grp + h) * (hd + 2);
-            if (xl) {  // to this XCD's L2
+            if (direct) {  // tagged words of this layer's partials, merged by the o_proj workers
+                uint64_t* out = a.tpa + ((((size_t)l * a.kvh + q.g) * a.xnsm + q.sp) * grp + h) * (hd + 2);
+                tstore_loc(out + 2 + d, __float_as_uint(o), a.epoch, loc);
+                if (d == 0) {
+                    tstore_loc(out, __float_as_uint(M), a.epoch, loc);
+                    tstore_loc(out + 1, __float_as_uint(Ls), a.epoch, loc);
+                }
+            } else if (xl) {  // to this XCD's L2
+                float* out = a.part + (((size_t)q.g * q.ns + q.sp) * grp + h) * (hd + 2);
                 gst(out + 2 + d, o);
                 if (d == 0) {
                     gst(out, M);
                     gst(out + 1, Ls);
                 }
             } else {
+                float* out = a.part + (((size_t)q.g * q.ns + q.sp) * grp + h) * (hd + 2);
                 cstore(out + 2 + d, o);
                 if (d == 0) {
                     cstore(out, M);
@@ -740,6 +765,7 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l) {
             }
         }
     }
+    if (direct) return;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     int* last = reinterpret_cast<int*>(c.lds + kFlagOff);
@@ -790,7 +816,7 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l) {
         }
         const uint32_t wv = pack_bf2(o0 / L, o1 / L);
         const int cw = (q.g * grp * hd) / 2 + w;
-        tstore(a.ta + (size_t)l * (a.H / 2) + cw, wv, a.epoch);
+        tstore_loc(a.ta + (size_t)l * (a.H / 2) + cw, wv, a.epoch, loc);
         gst(reinterpret_cast<uint32_t*>(a.att + l * a.sx) + cw, wv);
     }
 }
@@ -1174,6 +1200,570 @@ __global__ __launch_bounds__(kT) void decode_tagged_kernel(StepArgs args, const 
     done_stamp(a, slot_in(L, 0) + 1);
 }
 
+// ==== The XCD-local layer (second schedule of the same step) =====================
+// For a grid of 8 R workgroups, workgroup b on XCD slot x = b % 8 with rank
+// r = b / 8 (rank 0 is the slot's hub).  Kv head g's q/k/v rows, its attention
+// splits and its share of o_proj run on the workers of slot 7 - g (the slot
+// that attn_geom's XCD grouping gives kv head g), so those hand-offs stay in
+// one XCD's L2.  o_proj is split over K by kv head: slot 7 - g computes every
+// output row over kv head g's 448 columns.  Gate/up units of slot x are the
+// SwiGLU outputs of its own 64-column groups, and down is split over K the
+// same way: slot x computes every output row over its groups.  The hubs of all
+// slots gather the partials (tagged f32 words), sum them in slot order, apply
+// the global scale, add the residual (which each hub keeps in LDS) and build
+// the normalised stage images.  A layer thus has two grid-wide exchanges (o
+// partials -> hubs, down partials -> hubs) where the first schedule has five.
+// Hand-offs inside a slot use the same device-coherent tagged words, so the
+// results do not depend on where the dispatcher places the workgroups; only
+// the speed does.
+constexpr int kXs = 8;             // XCD slots
+constexpr int kHubRes = kLdsTotal;  // hub LDS, after the layer table: the residual stream, bf16 pairs [H/2] (H <= 1024)
+static_assert(kHubRes + 512 <= kLdsAll, "hub LDS regions");
+constexpr int kSliceT = 8;         // lanes per team of the split-K rows (8 rows per wave)
+constexpr int kON = 2;             // chunks per lane of an o_proj slice (K = grp * hd <= 512)
+constexpr int kDN = 3;             // chunks per lane of a down slice in the first batch
+
+// A partial as an f32 word whose lowest mantissa bit is the epoch's parity
+// (device-coherent store).  A reader that sees the parity of its own epoch
+// has this step's value, since the word was last written a step earlier,
+// with the other parity; it then clears the bit (every partial is thus
+// truncated to 23 mantissa bits, the same way at every step).
+__device__ __forceinline__ void pstore(uint32_t* p, float v, uint32_t epoch) {
+    astore(p, (__float_as_uint(v) & ~1u) | (epoch & 1u));
+}
+
+// SwiGLU groups [gs, ge) of 64 outputs of slot x (slots x < xslots have some).
+__device__ __forceinline__ void xslot_groups(const StepArgs& a, int x, int& gs, int& ge) {
+    const int ng = a.I / 64, n = a.xslots;
+    gs = x < n ? x * ng / n : ng;
+    ge = x < n ? (x + 1) * ng / n : ng;
+}
+
+// A lane's chunks of row n's K slice [32 cb, 32 (cb + nc)) of an affine
+// matrix: slice chunks c0 + tl + T j, clamped to the slice's last chunk (and
+// then not selected), as row_load does for whole rows.
+template <int NCH>
+struct SliceRegs {
+    uint4 w[NCH];
+    uint32_t s[NCH], b[NCH];
+};
+
+template <int T, int NCH>
+__device__ __forceinline__ void slice_load(const LinearDev& L, int n, int cb, int nc, int tl, int c0,
+                                           SliceRegs<NCH>& r) {
+    const int G = L.K / 64;
+    const uint32_t* wrow = L.w + (size_t)n * (L.K / 8);
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+        const int c = cb + min(c0 + tl + T * j, nc - 1);
+        r.w[j] = ldg4(wrow + 4 * c);
+        r.s[j] = gld(L.s + (size_t)n * G + (c >> 1));
+        r.b[j] = gld(L.b + (size_t)n * G + (c >> 1));
+    }
+}
+
+// Partial dot of those chunks with the stage image of the slice (nc chunks).
+template <int T, int NCH>
+__device__ __forceinline__ float slice_compute(const SliceRegs<NCH>& r, const XStage& st, int nc, int tl, int c0) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+        const int cr = c0 + tl + T * j;
+        const bool in = cr < nc;
+        const int c = in ? cr : nc - 1;
+        const uint4 x0 = *reinterpret_cast<const uint4*>(st.xs + (0 * nc + c) * 4);
+        const uint4 x1 = *reinterpret_cast<const uint4*>(st.xs + (1 * nc + c) * 4);
+        const uint4 x2 = *reinterpret_cast<const uint4*>(st.xs + (2 * nc + c) * 4);
+        const uint4 x3 = *reinterpret_cast<const uint4*>(st.xs + (3 * nc + c) * 4);
+        const float xh = st.xh[c];
+        float a0 = q4_word_dot(r.w[j].x, reinterpret_cast<const uint32_t*>(&x0), 0.0f);
+        float a1 = q4_word_dot(r.w[j].y, reinterpret_cast<const uint32_t*>(&x1), 0.0f);
+        a0 = q4_word_dot(r.w[j].z, reinterpret_cast<const uint32_t*>(&x2), a0);
+        a1 = q4_word_dot(r.w[j].w, reinterpret_cast<const uint32_t*>(&x3), a1);
+        const float s = bf2f((uint16_t)r.s[j]), b = bf2f((uint16_t)r.b[j]);
+        const float t = fmaf(b - 128.0f * s, xh, fmaf(s, a0 + a1, acc));
+        acc = in ? t : acc;
+    }
+    return acc;
+}
+
+// Row n's dot over the slice, its first batch of chunks in `first`; team
+// reduced, without the global scale (the hubs apply it to the summed slices).
+template <int T, int NCH>
+__device__ __forceinline__ float slice_dot(const LinearDev& L, int n, const SliceRegs<NCH>& first, const XStage& st,
+                                           int cb, int nc, int tl) {
+    float acc = slice_compute<T, NCH>(first, st, nc, tl, 0);
+    for (int c0 = T * NCH; c0 < nc; c0 += T * NCH) {
+        SliceRegs<NCH> r;
+        slice_load<T, NCH>(L, n, cb, nc, tl, c0, r);
+        acc += slice_compute<T, NCH>(r, st, nc, tl, c0);
+    }
+    return team_sum<T>(acc);
+}
+
+// q/k/v unit u of kv head gh: quads of head blocks [q heads of the group | k | v].
+__device__ __forceinline__ QkvGeom qkv_geom_x(const Ctx& c, int gh, int u) {
+    const StepArgs& a = c.a;
+    const int kvd = a.kvh * a.hd, grp = a.heads / a.kvh, qpb = a.hd / 4;
+    const int nu = (grp + 2) * qpb;
+    QkvGeom g;
+    g.any = true;
+    g.has = c.wave > 0 && u < nu;
+    const int uq = max(0, min(u, nu - 1));
+    const int hb = uq / qpb, qd = uq % qpb;
+    g.cr = (hb < grp ? (gh * grp + hb) * a.hd : (hb == grp ? a.H + gh * a.hd : a.H + kvd + gh * a.hd)) + 2 * qd;
+    g.which = g.cr < a.H ? 0 : (g.cr < a.H + kvd ? 1 : 2);
+    g.base = g.which == 0 ? 0 : (g.which == 1 ? a.H : a.H + kvd);
+    g.r0 = g.cr - g.base + c.team * (a.hd / 2);
+    return g;
+}
+
+// o_proj workers of the XCD-local schedule: kv head g's attention row of layer
+// l (grp heads x hd) merged here from its splits' tagged partials, in split
+// order, as the last arriver merges them in the first schedule (a running
+// (M, L, o): M' = max(M, m_s), L' = L e^(M - M') + l_s e^(m_s - M'), o
+// likewise; the row is o / L), then left in LDS as the stage image of its
+// K = grp hd values.  Every word a thread needs is polled at once, and a
+// split's four words again while any is stale.  With `trace` the row also
+// goes to the attention trace.  All threads call it.
+__device__ __forceinline__ void attn_merge_image(const Ctx& c, int l, int g, bool trace) {
+    const StepArgs& a = c.a;
+    const int grp = a.heads / a.kvh, hd = a.hd, K = grp * hd, ns = attn_splits(a.pos);
+    const size_t sstride = (size_t)grp * (hd + 2);
+    const uint64_t* base = a.tpa + ((size_t)l * a.kvh + g) * a.xnsm * sstride;
+    uint32_t* words = c.lds + kAttOt;
+    const uint32_t ep = a.epoch;
+    for (int w = tix(); w < K / 2; w += kT) {
+        const int h = (2 * w) / hd, d = (2 * w) % hd;
+        const uint64_t* hb = base + (size_t)h * (hd + 2);
+        float M = -INFINITY, L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+        for (int s0 = 0; s0 < ns; s0 += 8) {
+            const int nb = min(8, ns - s0);
+            uint64_t v[8][4];
+            auto load = [&](int i) {
+                const uint64_t* p = hb + (size_t)(s0 + min(i, nb - 1)) * sstride;
+                v[i][0] = tload(p);
+                v[i][1] = tload(p + 1);
+                v[i][2] = tload(p + 2 + d);
+                v[i][3] = tload(p + 3 + d);
+            };
+            auto here = [&](int i) {
+                return ((uint32_t)(v[i][0] >> 32) == ep) & ((uint32_t)(v[i][1] >> 32) == ep) &
+                       ((uint32_t)(v[i][2] >> 32) == ep) & ((uint32_t)(v[i][3] >> 32) == ep);
+            };
+#pragma unroll
+            for (int i = 0; i < 8; i++) load(i);
+            unsigned sp = 0;
+            while (true) {
+                bool ready = true;
+#pragma unroll
+                for (int i = 0; i < 8; i++) ready &= here(i);
+                if (ready) break;
+                if (++sp >= kSpin) {
+                    raise_flag(a.flags);
+                    break;
+                }
+                if ((sp & 255u) == 0 && flag_set(a.flags)) break;
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    if (!here(i)) load(i);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (i >= nb) break;
+                const float mi = __uint_as_float((uint32_t)v[i][0]), li = __uint_as_float((uint32_t)v[i][1]);
+                const float v0 = __uint_as_float((uint32_t)v[i][2]), v1 = __uint_as_float((uint32_t)v[i][3]);
+                const float Mn = fmaxf(M, mi);
+                const float cold = M == -INFINITY ? 0.0f : expf(M - Mn), cnew = expf(mi - Mn);
+                L = L * cold + cnew * li;
+                o0 = o0 * cold + cnew * v0;
+                o1 = o1 * cold + cnew * v1;
+                M = Mn;
+            }
+        }
+        const uint32_t wv = pack_bf2(o0 / L, o1 / L);
+        words[w] = wv;
+        if (trace) gst(reinterpret_cast<uint32_t*>(a.att + l * a.sx) + (g * K) / 2 + w, wv);
+    }
+    lds_sync();
+    uint32_t v[8];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const int gi = tix() + p * kT;
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[4 * p + j] = gi < K / 8 ? words[4 * gi + j] : 0u;
+    }
+    const uint4 nw[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+    image_finish<1, true>(a, c.lds, v, nw, K, nullptr, c.lds + kXsOff, nullptr, -1);
+    lds_sync();
+}
+
+// o_proj partial of kv head g: rows 8 s + lane / 8 over the head's columns
+// [g grp hd, (g + 1) grp hd), from the head's merged attention row.
+template <int Q4>
+__device__ __forceinline__ void st_opart(const Ctx& c, const LayerDev& Ld, int l, int g, int s, bool trace) {
+    const StepArgs& a = c.a;
+    const int K = (a.heads / a.kvh) * a.hd, nc = K / 32, cb = g * nc;
+    const int n = kSliceT * s + c.lane / kSliceT, tl = c.lane % kSliceT;
+    const bool has = c.wave > 0 && n < a.H;
+    SliceRegs<kON> W;
+    if (has) slice_load<kSliceT, kON>(Ld.o, n, cb, nc, tl, 0, W);
+    lds_sync();
+    attn_merge_image(c, l, g, trace);
+    stamp(a, slot_in(l, 2));
+    if (!has) return;
+    const float acc = slice_dot<kSliceT, kON>(Ld.o, n, W, xs_of(c.lds, K), cb, nc, tl);
+    if (tl == 0) pstore(a.tpo + ((size_t)l * a.kvh + g) * a.H + n, acc, a.epoch);
+}
+
+// Gate/up units p in [p0, p1) of this slot: unit p0 + (r - 1) kCW + wave - 1 + i (R - 1) kCW.
+template <int Q4>
+__device__ __forceinline__ void st_up_x(const Ctx& c, const LayerDev& Ld, int l, int p0, int p1, int r, int R,
+                                        bool loc) {
+    const StepArgs& a = c.a;
+    constexpr int MU = Nc<Q4>::up_units;
+    const int step = (R - 1) * kCW, pw = p0 + (r - 1) * kCW + c.wave - 1;
+    if (p0 + (r - 1) * kCW >= p1) return;  // no unit on this workgroup
+    const LinearDev& L = c.team == 0 ? Ld.g : Ld.u;
+    RowRegs<Nc<Q4>::t32> W[MU][2];
+    if (c.wave > 0) {
+#pragma unroll
+        for (int i = 0; i < MU; i++) {
+            const int p = pw + i * step;
+            if (p < p1) {
+                row_load<Q4, 32, Nc<Q4>::t32>(L, 2 * p, c.tl, 0, W[i][0]);
+                row_load<Q4, 32, Nc<Q4>::t32>(L, 2 * p + 1, c.tl, 0, W[i][1]);
+            }
+        }
+    }
+    get_image<Q4>(c, HUB_UP, 4 * l + 2, 2, a.tx1 + (size_t)l * (a.H / 2), a.H, Ld.ln2, nullptr);
+    stamp(a, slot_in(l, 3));
+    if (c.wave == 0) return;
+    const XStage st = xs_of(c.lds, a.H);
+    auto finish = [&](int p, float acc0, float acc1) {
+        const float g0 = rb(__shfl(acc0, 0, kWave)), g1 = rb(__shfl(acc1, 0, kWave));
+        const float u0 = rb(__shfl(acc0, 32, kWave)), u1 = rb(__shfl(acc1, 32, kWave));
+        if (c.lane == 0) {
+            const float s0 = rb(1.0f / (1.0f + expf(-g0))), s1 = rb(1.0f / (1.0f + expf(-g1)));
+            const uint32_t wv = pack_bf2(rb(g0 * s0) * u0, rb(g1 * s1) * u1);
+            tstore_loc(a.th + (size_t)l * (a.I / 2) + p, wv, a.epoch, loc);
+            gst(reinterpret_cast<uint32_t*>(a.hh + l * a.sh) + p, wv);
+        }
+    };
+    float acc[MU][2];
+#pragma unroll
+    for (int i = 0; i < MU; i++) {
+        const int p = pw + i * step;
+        acc[i][0] = acc[i][1] = 0.0f;
+        if (p < p1) {
+            acc[i][0] = row_dot_pf<Q4, 32, Nc<Q4>::t32>(L, 2 * p, st, c.tl, W[i][0]);
+            acc[i][1] = row_dot_pf<Q4, 32, Nc<Q4>::t32>(L, 2 * p + 1, st, c.tl, W[i][1]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < MU; i++) {
+        const int p = pw + i * step;
+        if (p < p1) finish(p, acc[i][0], acc[i][1]);
+    }
+    for (int p = pw + MU * step; p < p1; p += step) {
+        RowRegs<Nc<Q4>::t32> r0, r1;
+        row_load<Q4, 32, Nc<Q4>::t32>(L, 2 * p, c.tl, 0, r0);
+        row_load<Q4, 32, Nc<Q4>::t32>(L, 2 * p + 1, c.tl, 0, r1);
+        const float acc0 = row_dot_pf<Q4, 32, Nc<Q4>::t32>(L, 2 * p, st, c.tl, r0);
+        const float acc1 = row_dot_pf<Q4, 32, Nc<Q4>::t32>(L, 2 * p + 1, st, c.tl, r1);
+        finish(p, acc0, acc1);
+    }
+}
+
+// Down partial of slot x: rows 8 s + lane / 8 over the slot's SwiGLU columns
+// (chunks [cb, cb + nc)); the first batch of weights is loaded before gate/up.
+struct DownX {
+    SliceRegs<kDN> W;
+};
+
+__device__ __forceinline__ void down_pre_x(const Ctx& c, const LayerDev& Ld, int s, int cb, int nc, DownX& d) {
+    const int n = kSliceT * s + c.lane / kSliceT;
+    if (c.wave > 0 && n < c.a.H) slice_load<kSliceT, kDN>(Ld.d, n, cb, nc, c.lane % kSliceT, 0, d.W);
+}
+
+__device__ __forceinline__ void st_dpart(const Ctx& c, const LayerDev& Ld, int l, int x, int s, int cb, int nc,
+                                         const DownX& d) {
+    const StepArgs& a = c.a;
+    const int n = kSliceT * s + c.lane / kSliceT, tl = c.lane % kSliceT;
+    const bool has = c.wave > 0 && n < a.H;
+    lds_sync();
+    build_image<1, true>(a, c.lds, a.th + (size_t)l * (a.I / 2) + 16 * cb, 32 * nc, nullptr, c.lds + kXsOff, nullptr);
+    lds_sync();
+    stamp(a, slot_in(l, 4));
+    if (!has) return;
+    const float acc = slice_dot<kSliceT, kDN>(Ld.d, n, d.W, xs_of(c.lds, 32 * nc), cb, nc, tl);
+    if (tl == 0) pstore(a.tpd + ((size_t)l * kXs + x) * a.H + n, acc, a.epoch);
+}
+
+// Whether all four values of a polled quad carry the epoch's parity.
+__device__ __forceinline__ bool quad_ready(uint4 v, uint32_t par) {
+    return ((v.x & v.y & v.z & v.w & 1u) == par) && (((v.x | v.y | v.z | v.w) & 1u) == par);
+}
+
+// Hub: the next residual from the np partial vectors src[q H ..]: thread t
+// (t < H/4) polls quad t (rows 4t .. 4t + 3) of every partial (device-scope
+// 16-byte loads, all issued at once; stale quads polled again after a short
+// sleep), sums them in partial order with the tag bits cleared, applies the
+// global scale and updates residual words 2t, 2t + 1 in LDS:
+// res = bf16(res + bf16(gs * sum over q of part[q])).  Then v gets the groups
+// t and t + kT of 8 values as image_finish owns them.
+__device__ __forceinline__ void hub_residual(const StepArgs& a, uint32_t* lds, const uint32_t* src, int np, float gs,
+                                             uint32_t (&v)[8]) {
+    uint32_t* res = lds + kHubRes;
+    const int H = a.H, t = tix(), nq = H / 4;
+    const uint32_t par = a.epoch & 1u;
+    if (t < nq) {
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(src), 0, (uint32_t)(np * H) * 4u, 0x00020000);
+        const uint4 ok = make_uint4(par, par, par, par);
+        uint4 w[kXs];
+        auto load = [&](int q) {
+            const auto x = __builtin_amdgcn_raw_buffer_load_b128(rs, (q * nq + t) * 16, 0, kSc1);
+            w[q] = make_uint4(x[0], x[1], x[2], x[3]);
+        };
+#pragma unroll
+        for (int q = 0; q < kXs; q++) {
+            if (q < np)
+                load(q);
+            else
+                w[q] = ok;
+        }
+        unsigned sp = 0;
+        while (true) {
+            bool ready = true;
+#pragma unroll
+            for (int q = 0; q < kXs; q++) ready &= quad_ready(w[q], par);
+            if (ready) break;
+            if (++sp >= kSpin) {
+                raise_flag(a.flags);
+                break;
+            }
+            if ((sp & 255u) == 0 && flag_set(a.flags)) break;
+            __builtin_amdgcn_s_sleep(1);
+            // (one statement per quad: the compiler declines to unroll this loop of conditional loads)
+            auto again = [&](int q) {
+                if (!quad_ready(w[q], par)) load(q);
+            };
+            static_assert(kXs == 8, "the re-poll below names each slot");
+            again(0);
+            again(1);
+            again(2);
+            again(3);
+            again(4);
+            again(5);
+            again(6);
+            again(7);
+        }
+        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int q = 0; q < kXs; q++) {
+            const uint32_t e[4] = {w[q].x, w[q].y, w[q].z, w[q].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) s[j] = q < np ? s[j] + __uint_as_float(e[j] & ~1u) : s[j];
+        }
+        const uint32_t x0 = res[2 * t], x1 = res[2 * t + 1];
+        res[2 * t] = pack_bf2(bf_lo(x0) + rb(s[0] * gs), bf_hi(x0) + rb(s[1] * gs));
+        res[2 * t + 1] = pack_bf2(bf_lo(x1) + rb(s[2] * gs), bf_hi(x1) + rb(s[3] * gs));
+    }
+    lds_sync();
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const int gi = t + p * kT;
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[4 * p + j] = gi < H / 8 ? res[4 * gi + j] : 0u;
+    }
+}
+
+// The hubs also publish each residual as tagged words (for workers that find
+// no hub on their XCD and stage their own inputs) and as the trace copy, hub
+// b the groups gi with gi % 8 == b (so that no hub's next poll queues behind
+// many stores).
+__device__ __forceinline__ void hub_trace(const StepArgs& a, int b, const uint32_t (&v)[8], uint64_t* tdst,
+                                          uint16_t* dst) {
+    const int ng = a.H / 8;
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const int gi = tix() + p * kT;
+        if (gi < ng && gi % kXs == b) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) tstore(tdst + 4 * gi + j, v[4 * p + j], a.epoch);
+            gst(reinterpret_cast<uint4*>(dst) + gi, make_uint4(v[4 * p], v[4 * p + 1], v[4 * p + 2], v[4 * p + 3]));
+        }
+    }
+}
+
+// Hub: this thread's rms weight chunks of norm_w, loaded before the gather
+// whose result they normalise.
+__device__ __forceinline__ void hub_norm_pre(const StepArgs& a, const uint16_t* norm_w, uint4 (&nw)[2]) {
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const int g = tix() + p * kT;
+        nw[p] = g < a.H / 8 ? ldg4(norm_w + 8 * g) : make_uint4(0, 0, 0, 0);
+    }
+}
+
+// Hub: image of the residual v (normalised with norm_w, whose chunks nw
+// holds) into image slot `slot`, then flag fidx.  Stamps as hub_publish.
+template <int Q4>
+__device__ __forceinline__ void hub_image(const StepArgs& a, uint32_t* lds, int b, const uint32_t (&v0)[8],
+                                          const uint16_t* norm_w, const uint4 (&nw)[2], int slot, int fidx,
+                                          uint16_t* hidden, int ss) {
+    uint32_t v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = v0[k];
+    uint32_t* img = a.img + ((size_t)b * kImgSlots + slot) * a.img_stride;
+    image_finish<Q4, false>(a, lds, v, nw, a.H, norm_w, img, hidden, ss);
+    __syncthreads();
+    if (tix() == 0) gst(a.hflag + (size_t)b * a.nflag + fidx, a.epoch);
+    stamp(a, ss + 1);
+}
+
+template <int Q4>
+__device__ __forceinline__ void hub_main_x(const StepArgs& a, const LayerDev* __restrict__ layers, uint32_t* lds, int b,
+                                           uint32_t xcc) {
+    if (tix() == 0) tstore(a.hubtab + b, xcc, a.epoch);
+    const int H = a.H, L = a.n_layers;
+    {  // the layer table into LDS: the stages' norm weights and global scales are then LDS reads
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(layers);
+        for (int i = tix(); i < L * kLayWords; i += kT) lds[kLayOff + i] = gld(src + i);
+    }
+    const LayerDev* lay = reinterpret_cast<const LayerDev*>(lds + kLayOff);
+    uint32_t v[8];
+    uint4 nw[2];
+    hub_norm_pre(a, layers[0].ln1, nw);
+    {  // the embedded row
+        trecv_groups<kT>(a.tx, H / 8, a.epoch, v, a.flags);
+        uint32_t* res = lds + kHubRes;
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const int gi = tix() + p * kT;
+            if (gi < H / 8)
+#pragma unroll
+                for (int j = 0; j < 4; j++) res[4 * gi + j] = v[4 * p + j];
+        }
+    }
+    __syncthreads();  // the layer table and the residual are in LDS
+    for (int l = 0; l <= L; l++) {
+        const uint16_t* n1 = l < L ? lay[l].ln1 : a.final_norm;
+        if (l > 0) {  // layer l - 1's down partials
+            const float gs = lay[l - 1].d.gscale;
+            hub_norm_pre(a, n1, nw);
+            hub_residual(a, lds, a.tpd + (size_t)(l - 1) * kXs * H, a.xslots, gs, v);
+        }
+        if (l == L) {
+            hub_image<Q4>(a, lds, b, v, n1, nw, 4, 4 * L, b == 0 ? a.hidden : nullptr, slot_in(L, 0));
+            hub_trace(a, b, v, a.tx + (size_t)L * (H / 2), a.xo + (size_t)(L - 1) * a.sx);
+            break;
+        }
+        hub_image<Q4>(a, lds, b, v, n1, nw, 0, 4 * l, nullptr, slot_in(l, 0));
+        if (l > 0) hub_trace(a, b, v, a.tx + (size_t)l * (H / 2), a.xo + (size_t)(l - 1) * a.sx);
+        const uint16_t* n2 = lay[l].ln2;
+        const float gs = lay[l].o.gscale;
+        hub_norm_pre(a, n2, nw);
+        hub_residual(a, lds, a.tpo + (size_t)l * a.kvh * H, a.kvh, gs, v);
+        hub_image<Q4>(a, lds, b, v, n2, nw, 2, 4 * l + 2, nullptr, slot_in(l, 3));
+        hub_trace(a, b, v, a.tx1 + (size_t)l * (H / 2), a.x1 + (size_t)l * a.sx);
+    }
+}
+
+// Whether every workgroup of slot x (b = x, x + 8, ..., R of them) runs on
+// this workgroup's XCD, from the XCC ids all workgroups publish at launch; the
+// same answer in every workgroup of the slot.
+__device__ __forceinline__ bool slot_on_one_xcd(const StepArgs& a, uint32_t* lds, int x, int R, uint32_t xcc) {
+    int* res = reinterpret_cast<int*>(lds + kFlagOff + 3);
+    if (tix() < kWave) {
+        bool diff = false;
+        for (int i = tix(); i < R; i += kWave) diff |= trecv1(a.hubtab + kXcdBase + kXs * i + x, a.epoch, a.flags) != xcc;
+        const bool any = __ballot(diff) != 0ull;
+        if (tix() == 0) *res = !any;
+    }
+    __syncthreads();
+    return *res != 0;
+}
+
+template <int Q4>
+__global__ __launch_bounds__(kT) void decode_xcd_kernel(StepArgs args, const LayerDev* __restrict__ layers) {
+    (void)args;
+    const StepArgs& a = *(const StepArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    __shared__ __align__(16) uint32_t lds[kLdsAll];
+    stamp(a, 0);
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xcc &= 0xfu;
+    const int b = blockIdx.x;
+    if (a.xloc && tix() == 0) tstore(a.hubtab + kXcdBase + b, xcc, a.epoch);
+    if (b < kXs) {
+        hub_main_x<Q4>(a, layers, lds, b, xcc);
+        return;
+    }
+    const int lane = tix() % kWave, wave = __builtin_amdgcn_readfirstlane(tix() / kWave);
+    const int W = (int)gridDim.x - kXs, w = b - kXs;
+    const int x = b % kXs, r = b / kXs, R = (int)gridDim.x / kXs;
+    {
+        const Ctx c0{a, lds, W, w, wave, lane, lane / 32, lane % 32, -1};
+        st_embed(c0);
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(layers);
+        for (int i = tix(); i < a.n_layers * kLayWords; i += kT) lds[kLayOff + i] = gld(src + i);
+    }
+    const LayerDev* lay = reinterpret_cast<const LayerDev*>(lds + kLayOff);
+    const int hub = find_hub(a, lds, xcc);
+    const bool loc = a.xloc && slot_on_one_xcd(a, lds, x, R, xcc);
+    const Ctx c0{a, lds, W, w, wave, lane, lane / 32, lane % 32, hub};
+    const int gh = kXs - 1 - x;  // the kv head of this slot, if < kvh
+    const int grp = a.heads / a.kvh, nu = (grp + 2) * (a.hd / 4);
+    const int s0 = (r - 1) * kCW;  // wave slot of this workgroup's wave 1
+    const bool onh = gh < a.kvh;
+    const bool pq = onh && s0 < nu, pa = in_attn(c0), po = onh && kSliceT * s0 < a.H;
+    int gs, ge;
+    xslot_groups(a, x, gs, ge);
+    const bool pd = ge > gs && kSliceT * s0 < a.H;
+    const int L = a.n_layers;
+    if (pa) {
+        attn_xl_publish(c0, xcc);
+        attn_prefetch(c0, 0);
+        attn_xl_check(c0, xcc);
+    }
+    for (int l = 0; l < L; l++) {
+        const int ln = tix() % kWave;
+        const Ctx c{a, lds, W, w, wave, ln, ln / 32, ln % 32, hub};
+        const LayerDev& Ld = lay[l];
+        const int s = s0 + wave - 1;
+        if (pq) {
+            st_qkv_g<Q4>(c, Ld, l, qkv_geom_x(c, gh, s), loc);
+            done_stamp(a, slot_in(l, 0) + 1);
+        }
+        if (pa) {
+            attn_recv(c, l);
+            attn_run(c, l, loc, true);
+            done_stamp(a, slot_in(l, 1) + 1);
+        }
+        if (po) {
+            st_opart<Q4>(c, Ld, l, gh, s, r == 1);
+            done_stamp(a, slot_in(l, 2) + 1);
+        }
+        DownX dx;
+        if (pd) down_pre_x(c, Ld, s, 2 * gs, 2 * (ge - gs), dx);
+        if (ge > gs) {
+            st_up_x<Q4>(c, Ld, l, 32 * gs, 32 * ge, r, R, loc);
+            done_stamp(a, slot_in(l, 3) + 1);
+        }
+        if (pa && l + 1 < L) attn_prefetch(c, l + 1);
+        if (pd) {
+            st_dpart(c, Ld, l, x, s, 2 * gs, 2 * (ge - gs), dx);
+            done_stamp(a, slot_in(l, 4) + 1);
+        }
+    }
+    const int ln = tix() % kWave;
+    const Ctx c{a, lds, W, w, wave, ln, ln / 32, ln % 32, hub};
+    st_head<Q4>(c);
+    done_stamp(a, slot_in(L, 0) + 1);
+}
+
 }  // namespace
 
 // Positions per attention split on this schedule: a workgroup holds the
@@ -1208,6 +1798,34 @@ hipError_t launch_lm_step_tagged(hipStream_t st, const StepArgs& a, int q4, int 
     if (cooperative) return hipLaunchCooperativeKernel(f, dim3(grid), dim3(kT), params, 0, st);
     return hipLaunchKernel(f, dim3(grid), dim3(kT), params, 0, st);
 }
+
+// The XCD-local schedule (decode_xcd_kernel): 4-bit weights, grid of 8 R
+// workgroups.
+hipError_t launch_lm_step_xcd(hipStream_t st, const StepArgs& a, int grid, bool cooperative) {
+    StepArgs args = a;
+    const LayerDev* layers = a.layers;
+    void* params[] = {&args, &layers};
+    const void* f = reinterpret_cast<const void*>(decode_xcd_kernel<1>);
+    if (cooperative) return hipLaunchCooperativeKernel(f, dim3(grid), dim3(kT), params, 0, st);
+    return hipLaunchKernel(f, dim3(grid), dim3(kT), params, 0, st);
+}
+
+// Whether the XCD-local schedule takes this shape on a grid of `grid`
+// workgroups (one per CU); a step also needs at most grid / 8 - 1 attention
+// splits per kv head.
+bool xcd_fits(int grid, int H, int heads, int kvh, int hd, int I, int n_layers) {
+    if (grid % kXs != 0 || grid > kXcdSlots || hd != 64 || kvh < 1 || kvh > kXs || heads % kvh != 0 || heads / kvh > 8) return false;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_xcd_kernel<1>, kT, 0) != hipSuccess || per_cu < 1)
+        return false;
+    const int R = grid / kXs, waves = (R - 1) * kCW, grp = heads / kvh;
+    return R >= 2 && H % 64 == 0 && H <= 1024 && I % 64 == 0 && I <= 8192 && (grp + 2) * hd / 4 <= waves &&
+           H <= kSliceT * waves && n_layers <= kMaxLdsLayers;
+}
+
+// SwiGLU slots of the XCD-local schedule: every slot while there are at
+// least 8 groups of 64 outputs, else one slot per group.
+int xcd_slots(int I) { return I / 64 < kXs ? I / 64 : kXs; }
 
 int tagged_grid(int num_cus) {
     int per_cu = 0;

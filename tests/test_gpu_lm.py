@@ -150,11 +150,13 @@ def check_step_teacher_forced(ming, m, cache_before, cache_after, orc, pos, toke
     return worst, float(d.max()), ram, margin
 
 
-MODES = {"kernels": "LM_KERNELS", "persistent": "LM_PERSISTENT", "direct": "LM_PERSISTENT_DIRECT"}
+MODES = {"kernels": "LM_KERNELS", "persistent": "LM_PERSISTENT", "direct": "LM_PERSISTENT_DIRECT",
+         "xcd": "LM_PERSISTENT_XCD"}
+XCD_MAX_CTX = 31 * 384  # kv head g's attention splits (384 positions each) on the 31 workers of one XCD slot
 
 
-@pytest.mark.parametrize("mode", ["kernels", "persistent", "direct"])
-@pytest.mark.parametrize("ctx_len", [0, 1, 63, 64, 512, 2048, 4095, 8192, 16384])
+@pytest.mark.parametrize("mode", ["kernels", "persistent", "direct", "xcd"])
+@pytest.mark.parametrize("ctx_len", [0, 1, 63, 64, 512, 2048, 4095, 8192, 11903, 16384])
 def test_lm_step_matches_oracle(ming, ctx, q4_model, ctx_len, mode):
     S = syn_mod(ming)
     syn, m, orc = q4_model
@@ -164,6 +166,11 @@ def test_lm_step_matches_oracle(ming, ctx, q4_model, ctx_len, mode):
     cache.fill_random(ctx_len, seed=ctx_len)
     before = cache.host()
     token = 1234
+    if mode == "xcd" and ctx_len + 1 > XCD_MAX_CTX:
+        with pytest.raises(ming.MingError) as e:
+            run_step(ming, syn, m, cache, token, md)
+        assert e.value.status == ming.MING_E_UNSUPPORTED and cache.len == ctx_len
+        return
     am, hid, lg = run_step(ming, syn, m, cache, token, md)
     assert cache.len == ctx_len + 1
     worst, dl, ram, margin = check_step_teacher_forced(ming, m, before, cache.host(), orc, ctx_len, token, am, hid,
@@ -185,7 +192,7 @@ HEAD_SHAPES = [  # (hidden, heads, kv_heads, inter, vocab)
 
 
 @pytest.mark.parametrize("H,heads,kvh,I,V", HEAD_SHAPES)
-@pytest.mark.parametrize("mode", ["kernels", "persistent"])
+@pytest.mark.parametrize("mode", ["kernels", "persistent", "xcd"])
 def test_q4_head_shapes_match_oracle(ming, ctx, H, heads, kvh, I, V, mode):
     S = syn_mod(ming)
     print(f"[lm_head] H={H} heads={heads}/{kvh} I={I} V={V} mode={mode}", flush=True)
@@ -243,7 +250,7 @@ def test_schedules_agree_and_deterministic(ming, ctx, q4_model):
     S = syn_mod(ming)
     syn, m, _ = q4_model
     outs = {}
-    for mode in (ming.LM_KERNELS, ming.LM_PERSISTENT, ming.LM_PERSISTENT_DIRECT):
+    for mode in (ming.LM_KERNELS, ming.LM_PERSISTENT, ming.LM_PERSISTENT_DIRECT, ming.LM_PERSISTENT_XCD):
         for rep in range(3):
             cache = S.KvCache(syn.spec, 1100)
             cache.fill_random(1000, seed=7)
@@ -257,6 +264,8 @@ def test_schedules_agree_and_deterministic(ming, ctx, q4_model):
     k, p, d = outs[ming.LM_KERNELS], outs[ming.LM_PERSISTENT], outs[ming.LM_PERSISTENT_DIRECT]
     assert p[0] == d[0] and np.array_equal(p[1], d[1]) and np.array_equal(p[2], d[2]), "hubs change the result"
     assert_close_bf16(p[1], k[1], "persistent vs kernels hidden", atol=0.2, rtol=0.1)
+    x = outs[ming.LM_PERSISTENT_XCD]
+    assert_close_bf16(x[1], k[1], "XCD-local vs kernels hidden", atol=0.2, rtol=0.1)
 
 
 def test_ordinary_launch_matches_cooperative(ming, ctx, q4_model):
@@ -266,7 +275,7 @@ def test_ordinary_launch_matches_cooperative(ming, ctx, q4_model):
     S = syn_mod(ming)
     syn, m, _ = q4_model
     try:
-        for mode in (ming.LM_PERSISTENT, ming.LM_PERSISTENT_DIRECT):
+        for mode in (ming.LM_PERSISTENT, ming.LM_PERSISTENT_DIRECT, ming.LM_PERSISTENT_XCD):
             got = {}
             for excl in (False, True):
                 ctx.set_exclusive(excl)
