@@ -230,7 +230,7 @@ def main():
             "weights": "MLX affine u32 4-bit, group 64, bf16 scales/biases, global scale 1.0",
             "arithmetic": "4-bit weights unpacked in registers, bf16 activations and KV cache, f32 accumulation",
             "kv_cache": "bf16 in place",
-            "schedule": args.mode,
+            "schedule": args.mode if args.mode != "auto" else f"auto ({lm_schedule(args)})",
             "launch": "cooperative" if args.cooperative else "ordinary (device held by this process alone)",
             "global_batch": 1,
             "seq_len": args.ctx,
@@ -335,11 +335,22 @@ def lm_stage_report(ctx, m, spec, cache, step, pos, reps=5):
               f"span {h[:, 2].mean():5.2f}", file=sys.stderr)
 
 
+def lm_schedule(args):
+    """The decode schedule a step runs: MING_LM_AUTO takes the XCD-local one
+    (4-bit model, attention splits of 384 positions on at most 31 workers of
+    one XCD slot) unless MING_LM_XCD=0, else the first persistent one."""
+    if args.mode != "auto":
+        return args.mode
+    fits = args.ctx + args.steps + 1 <= 31 * 384 and os.environ.get("MING_LM_XCD", "1") != "0"
+    return "xcd" if fits else "persistent"
+
+
 def measured_traffic(args):
     """HBM bytes per launch from the committed rocprofv3 counter runs, for
-    the workload they were taken on (ctx 2048, persistent schedule)."""
-    path = os.path.join(ROOT, "profiles", "decode_tagged_kernel_ctx2048_traffic.json")
-    if args.ctx != 2048 or args.mode not in ("auto", "persistent") or not os.path.exists(path):
+    the workload they were taken on (ctx 2048, each persistent schedule)."""
+    name = {"xcd": "decode_xcd_kernel", "persistent": "decode_tagged_kernel"}.get(lm_schedule(args))
+    path = os.path.join(ROOT, "profiles", f"{name}_ctx2048_traffic.json")
+    if args.ctx != 2048 or name is None or not os.path.exists(path):
         return None
     with open(path) as f:
         return json.load(f)["traffic_bytes_per_dispatch"]
