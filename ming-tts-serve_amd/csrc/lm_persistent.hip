@@ -452,6 +452,11 @@ __device__ __forceinline__ void st_qkv(const Ctx& c, const LayerDev& Ld, int l) 
     st_qkv_g<Q4>(c, Ld, l, qkv_geom(c));
 }
 
+// e^x for the attention softmax and its merges: the native base-2 exponential
+// (v_exp_f32, about one ulp) of x log2(e), two instructions where expf takes
+// about ten (range reduction, special cases); -inf gives 0.
+__device__ __forceinline__ float att_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
 // ---- LB: split GQA attention over LDS-resident K/V + last-arriver merge ------------------
 // Unit = (kv head g, split of kAttP positions), on the last workers.  A
 // split's K rows and V^T stay in this workgroup's LDS: they are loaded one
@@ -681,7 +686,7 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l, bool loc = false, 
         for (int tt = 0; tt < 4; tt++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const float e = sc[tt][r] == -INFINITY ? 0.0f : expf(sc[tt][r] - mx);
+                const float e = att_exp(sc[tt][r] - mx);  // masked scores (-inf) give 0
                 sc[tt][r] = e;
                 lp += e;
             }
@@ -737,7 +742,7 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l, bool loc = false, 
             float o = 0.0f, Ls = 0.0f;
             for (int i = 0; i < ntl; i++) {
                 const float* pi = S.ot + (i * 8 + h) * (hd + 2);
-                const float wgt = expf(pi[0] - M);
+                const float wgt = att_exp(pi[0] - M);
                 o += wgt * pi[2 + d];
                 Ls += wgt * pi[1];
             }
@@ -807,7 +812,7 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l, bool loc = false, 
             for (int i = 0; i < 8; i++) {
                 if (i >= nb) break;
                 const float Mn = fmaxf(M, v[i][0]);
-                const float cold = M == -INFINITY ? 0.0f : expf(M - Mn), cnew = expf(v[i][0] - Mn);
+                const float cold = M == -INFINITY ? 0.0f : att_exp(M - Mn), cnew = att_exp(v[i][0] - Mn);
                 L = L * cold + cnew * v[i][1];
                 o0 = o0 * cold + cnew * v[i][2];
                 o1 = o1 * cold + cnew * v[i][3];
@@ -1374,7 +1379,7 @@ __device__ __forceinline__ void attn_merge_image(const Ctx& c, int l, int g, boo
                 const float mi = __uint_as_float((uint32_t)v[i][0]), li = __uint_as_float((uint32_t)v[i][1]);
                 const float v0 = __uint_as_float((uint32_t)v[i][2]), v1 = __uint_as_float((uint32_t)v[i][3]);
                 const float Mn = fmaxf(M, mi);
-                const float cold = M == -INFINITY ? 0.0f : expf(M - Mn), cnew = expf(mi - Mn);
+                const float cold = M == -INFINITY ? 0.0f : att_exp(M - Mn), cnew = att_exp(mi - Mn);
                 L = L * cold + cnew * li;
                 o0 = o0 * cold + cnew * v0;
                 o1 = o1 * cold + cnew * v1;
