@@ -670,15 +670,20 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l, bool loc = false, 
             sc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(kr[(2 * jj + 1) ^ kswz(pr)]), as_bf8(qb[1]),
                                                             sc[tt], 0, 0, 0);
         }
+        if (cnt < kTile) {  // (wave-uniform) only the tile that holds the newest position is partial
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int p = 32 * (tt / 2) + 8 * jj + 4 * (tt % 2) + r;
+                    if (p >= cnt) sc[tt][r] = -INFINITY;
+                }
+        }
         float mx = -INFINITY;
 #pragma unroll
         for (int tt = 0; tt < 4; tt++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int p = 32 * (tt / 2) + 8 * jj + 4 * (tt % 2) + r;
-                if (p >= cnt) sc[tt][r] = -INFINITY;
-                mx = fmaxf(mx, sc[tt][r]);
-            }
+            for (int r = 0; r < 4; r++) mx = fmaxf(mx, sc[tt][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
         mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
         float lp = 0.0f;
