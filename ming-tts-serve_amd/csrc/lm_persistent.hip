@@ -1053,29 +1053,37 @@ __device__ __forceinline__ void head_rows(const Ctx& c, float& bv, int& bi) {
 
 // The affine head with an even number of groups up to 16 (q4tile_fits) on
 // the matrix cores: 16-row tiles
-// (q4tile_mma / q4tile_finish), one tile per wave in flight (two to four
-// measured slower), and all eight waves computing.  Tile t goes to wave slot
-// t mod 8W, where the compute waves 1..7 of every worker come first and the
-// receiving waves last: a receiving wave starts its loads only once the
-// head's input has arrived, so it gets the fewer tiles.
+// (q4tile_mma / q4tile_finish), DEPTH tiles per wave in flight (two in the
+// XCD-local kernel, whose registers allow it; one in the first schedule's
+// kernel, which two would make spill), and all eight waves computing.  Tile t
+// goes to wave slot t mod 8W, where the compute waves 1..7 of every worker
+// come first and the receiving waves last: a receiving wave starts its loads
+// only once the head's input has arrived, so it gets the fewer tiles.
+template <int DEPTH>
 __device__ __forceinline__ void head_tiles(const Ctx& c, float& bv, int& bi) {
+    static_assert(DEPTH == 1 || DEPTH == 2, "one or two tiles in flight");
     const StepArgs& a = c.a;
     const LinearDev& L = a.head;
     const int V = L.N, G = L.K / 64, ntiles = (V + 15) / 16, nq = c.W * kW;
     const int q = c.wave > 0 ? c.w * kCW + c.wave - 1 : c.W * kCW + c.w;
     const int n16 = c.lane % 16, kq = c.lane / 16;
     const __amdgpu_buffer_rsrc_t rs = q4tile_rsrc(L.s, V, G), rb = q4tile_rsrc(L.b, V, G);
-    Q4Tile r;
-    if (c.wave > 0 && q < ntiles) q4tile_load(L, min(q * 16 + n16, V - 1), kq, rs, rb, r);
+    auto load = [&](int t, Q4Tile& r) { q4tile_load(L, min(t * 16 + n16, V - 1), kq, rs, rb, r); };
+    Q4Tile r0, r1;  // tile t in r0, t + nq in r1 (DEPTH 2)
+    auto first = [&]() {
+        if (q < ntiles) load(q, r0);
+        if (DEPTH == 2 && q + nq < ntiles) load(q + nq, r1);
+    };
+    if (c.wave > 0) first();
     get_image<1>(c, HUB_HEAD, 4 * a.n_layers, 4, a.tx + (size_t)a.n_layers * (a.H / 2), a.H, a.final_norm,
                  !hub_on(a, HUB_HEAD) && c.w == 0 ? a.hidden : nullptr);
     stamp(a, slot_in(a.n_layers, 0));
-    if (c.wave == 0 && q < ntiles) q4tile_load(L, min(q * 16 + n16, V - 1), kq, rs, rb, r);
+    if (c.wave == 0) first();
     const Q4TileX tx = q4tile_x(xs_of(c.lds, a.H), a.H, c.lane);
-    for (int t = q; t < ntiles; t += nq) {
+    auto step = [&](int t, Q4Tile& r) {
         const f32x4_t C = q4tile_mma(L, r, tx, c.lane);
         const uint2 s = r.s, b = r.b;
-        if (t + nq < ntiles) q4tile_load(L, min((t + nq) * 16 + n16, V - 1), kq, rs, rb, r);
+        if (t + DEPTH * nq < ntiles) load(t + DEPTH * nq, r);
         const float y = q4tile_finish(L, C, s, b, tx, c.lane);
         const int n = t * 16 + n16;
         if (kq == 0 && n < V) {
@@ -1085,10 +1093,14 @@ __device__ __forceinline__ void head_tiles(const Ctx& c, float& bv, int& bi) {
                 bi = n;
             }
         }
+    };
+    for (int t = q; t < ntiles; t += DEPTH * nq) {
+        step(t, r0);
+        if (DEPTH == 2 && t + nq < ntiles) step(t + nq, r1);
     }
 }
 
-template <int Q4>
+template <int Q4, int DEPTH = 1>
 __device__ __forceinline__ void st_head(const Ctx& c) {
     const StepArgs& a = c.a;
     if (!a.logits && !a.argmax_out) {  // hidden only: hub 0 (or worker 0) writes it, no head
@@ -1101,7 +1113,7 @@ __device__ __forceinline__ void st_head(const Ctx& c) {
     int bi = 0x7fffffff;
     if constexpr (Q4) {
         if (q4tile_fits(a.head.K))
-            head_tiles(c, bv, bi);
+            head_tiles<DEPTH>(c, bv, bi);
         else
             head_rows<Q4>(c, bv, bi);
     } else {
@@ -1770,7 +1782,7 @@ __global__ __launch_bounds__(kT) void decode_xcd_kernel(StepArgs args, const Lay
     }
     const int ln = tix() % kWave;
     const Ctx c{a, lds, W, w, wave, ln, ln / 32, ln % 32, hub};
-    st_head<Q4>(c);
+    st_head<Q4, 2>(c);
     done_stamp(a, slot_in(L, 0) + 1);
 }
 
