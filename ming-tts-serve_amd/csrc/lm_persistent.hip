@@ -457,6 +457,10 @@ __device__ __forceinline__ void st_qkv(const Ctx& c, const LayerDev& Ld, int l) 
 // about ten (range reduction, special cases); -inf gives 0.
 __device__ __forceinline__ float att_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
+// 1 / (1 + e^-x) from the native exponential and reciprocal (about one ulp
+// each; the SwiGLU rounds the result to bf16).
+__device__ __forceinline__ float sigmoid_fast(float x) { return __builtin_amdgcn_rcpf(1.0f + att_exp(-x)); }
+
 // ---- LB: split GQA attention over LDS-resident K/V + last-arriver merge ------------------
 // Unit = (kv head g, split of kAttP positions), on the last workers.  A
 // split's K rows and V^T stay in this workgroup's LDS: they are loaded one
@@ -893,7 +897,7 @@ __device__ __forceinline__ void st_up(const Ctx& c, const LayerDev& Ld, int l) {
         const float g0 = rb(__shfl(acc0, 0, kWave)), g1 = rb(__shfl(acc1, 0, kWave));
         const float u0 = rb(__shfl(acc0, 32, kWave)), u1 = rb(__shfl(acc1, 32, kWave));
         if (c.lane == 0) {
-            const float s0 = rb(1.0f / (1.0f + expf(-g0))), s1 = rb(1.0f / (1.0f + expf(-g1)));
+            const float s0 = rb(sigmoid_fast(g0)), s1 = rb(sigmoid_fast(g1));
             const uint32_t wv = pack_bf2(rb(g0 * s0) * u0, rb(g1 * s1) * u1);
             tstore(a.th + (size_t)l * (a.I / 2) + p, wv, a.epoch);
             gst(reinterpret_cast<uint32_t*>(a.hh + l * a.sh) + p, wv);
@@ -1466,7 +1470,7 @@ __device__ __forceinline__ void st_up_x(const Ctx& c, const LayerDev& Ld, int l,
         const float g0 = rb(__shfl(acc0, 0, kWave)), g1 = rb(__shfl(acc1, 0, kWave));
         const float u0 = rb(__shfl(acc0, 32, kWave)), u1 = rb(__shfl(acc1, 32, kWave));
         if (c.lane == 0) {
-            const float s0 = rb(1.0f / (1.0f + expf(-g0))), s1 = rb(1.0f / (1.0f + expf(-g1)));
+            const float s0 = rb(sigmoid_fast(g0)), s1 = rb(sigmoid_fast(g1));
             const uint32_t wv = pack_bf2(rb(g0 * s0) * u0, rb(g1 * s1) * u1);
             tstore_loc(a.th + (size_t)l * (a.I / 2) + p, wv, a.epoch, loc);
             gst(reinterpret_cast<uint32_t*>(a.hh + l * a.sh) + p, wv);
