@@ -129,6 +129,24 @@ __device__ __forceinline__ float team_reduce(float v, Op op) {
     return v;
 }
 
+// Combine the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the same place in each
+// 16-lane row) with the permlane swaps: the butterfly of __shfl_xor over 16
+// and 32, bit for bit (add and max are commutative), without LDS round trips.
+template <class Op>
+__device__ __forceinline__ float rows_reduce(float v, Op op) {
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return op(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float rows_sum(float v) { return rows_reduce(v, [](float a, float b) { return a + b; }); }
+__device__ __forceinline__ float rows_max(float v) { return rows_reduce(v, [](float a, float b) { return fmaxf(a, b); }); }
+
+// Lane `lane`'s value (a constant lane) for the whole wave, by v_readlane.
+__device__ __forceinline__ float lane_of(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
 template <int W>
 __device__ __forceinline__ float team_sum(float v) {
     return team_reduce<W>(v, [](float a, float b) { return a + b; });

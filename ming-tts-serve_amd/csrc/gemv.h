@@ -344,8 +344,7 @@ __device__ __forceinline__ float q4tile_finish(const LinearDev& L, f32x4_t C, ui
             p = fmaf(bi - 128.0f * sc, t.xsum[i], p);
         }
     }
-    p += __shfl_xor(p, 16, kWave);
-    p += __shfl_xor(p, 32, kWave);
+    p = rows_sum(p);
     return p * L.gscale;
 }
 

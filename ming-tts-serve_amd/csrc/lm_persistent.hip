@@ -414,8 +414,7 @@ __device__ __forceinline__ void st_qkv_g(const Ctx& c, const LayerDev& Ld, int l
     const XStage st = xs_of(c.lds, a.H);
     const float acc0 = row_dot_pf<Q4, 32, Nc<Q4>::t32>(L, r0, st, c.tl, W.w0);
     const float acc1 = row_dot_pf<Q4, 32, Nc<Q4>::t32>(L, r0 + 1, st, c.tl, W.w1);
-    const float v[4] = {__shfl(acc0, 0, kWave), __shfl(acc1, 0, kWave), __shfl(acc0, 32, kWave),
-                        __shfl(acc1, 32, kWave)};
+    const float v[4] = {lane_of(acc0, 0), lane_of(acc1, 0), lane_of(acc0, 32), lane_of(acc1, 32)};
     if (c.lane != 0) return;
     const float bias[4] = {bf_lo(W.bias[0]), bf_hi(W.bias[0]), bf_lo(W.bias[1]), bf_hi(W.bias[1])};
     float e[4];
@@ -688,8 +687,7 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l, bool loc = false, 
         for (int tt = 0; tt < 4; tt++)
 #pragma unroll
             for (int r = 0; r < 4; r++) mx = fmaxf(mx, sc[tt][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        mx = rows_max(mx);
         float lp = 0.0f;
 #pragma unroll
         for (int tt = 0; tt < 4; tt++)
@@ -699,8 +697,7 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l, bool loc = false, 
                 sc[tt][r] = e;
                 lp += e;
             }
-        lp += __shfl_xor(lp, 16, kWave);
-        lp += __shfl_xor(lp, 32, kWave);
+        lp = rows_sum(lp);
         const uint32_t* vt = c.lds + kVtOffP + (kTile / 2) * tile;
         f32x4_t o[4];
 #pragma unroll
@@ -856,7 +853,7 @@ __device__ __forceinline__ void st_o(const Ctx& c, const LayerDev& Ld, int l) {
     stamp(a, slot_in(l, 2));
     if (!has) return;
     const float acc = row_dot_pf<Q4, 32, Nc<Q4>::t32>(Ld.o, r, xs_of(c.lds, a.H), c.tl, W);
-    const float a0 = __shfl(acc, 0, kWave), a1 = __shfl(acc, 32, kWave);
+    const float a0 = lane_of(acc, 0), a1 = lane_of(acc, 32);
     if (c.lane == 0) {
         const uint32_t xw = tfinish(xsrc, xpre, a.epoch, a.flags);
         const uint32_t w = pack_bf2(bf_lo(xw) + rb(a0), bf_hi(xw) + rb(a1));
@@ -894,8 +891,8 @@ __device__ __forceinline__ void st_up(const Ctx& c, const LayerDev& Ld, int l) {
     if (c.wave == 0) return;
     const XStage st = xs_of(c.lds, a.H);
     auto finish = [&](int p, float acc0, float acc1) {
-        const float g0 = rb(__shfl(acc0, 0, kWave)), g1 = rb(__shfl(acc1, 0, kWave));
-        const float u0 = rb(__shfl(acc0, 32, kWave)), u1 = rb(__shfl(acc1, 32, kWave));
+        const float g0 = rb(lane_of(acc0, 0)), g1 = rb(lane_of(acc1, 0));
+        const float u0 = rb(lane_of(acc0, 32)), u1 = rb(lane_of(acc1, 32));
         if (c.lane == 0) {
             const float s0 = rb(sigmoid_fast(g0)), s1 = rb(sigmoid_fast(g1));
             const uint32_t wv = pack_bf2(rb(g0 * s0) * u0, rb(g1 * s1) * u1);
@@ -962,7 +959,7 @@ __device__ __forceinline__ void st_down(const Ctx& c, const LayerDev& Ld, int l,
     stamp(a, slot_in(l, 4));
     if (!has) return;
     const float acc = row_dot_pf<Q4, 32, Nc<Q4>::down>(Ld.d, r, xs_of(c.lds, a.I), c.tl, d.W);
-    const float a0 = __shfl(acc, 0, kWave), a1 = __shfl(acc, 32, kWave);
+    const float a0 = lane_of(acc, 0), a1 = lane_of(acc, 32);
     if (c.lane == 0) {
         const uint32_t xw = tfinish(xsrc, xpre, a.epoch, a.flags);
         const uint32_t w2 = pack_bf2(bf_lo(xw) + rb(a0), bf_hi(xw) + rb(a1));
@@ -1467,8 +1464,8 @@ __device__ __forceinline__ void st_up_x(const Ctx& c, const LayerDev& Ld, int l,
     if (c.wave == 0) return;
     const XStage st = xs_of(c.lds, a.H);
     auto finish = [&](int p, float acc0, float acc1) {
-        const float g0 = rb(__shfl(acc0, 0, kWave)), g1 = rb(__shfl(acc1, 0, kWave));
-        const float u0 = rb(__shfl(acc0, 32, kWave)), u1 = rb(__shfl(acc1, 32, kWave));
+        const float g0 = rb(lane_of(acc0, 0)), g1 = rb(lane_of(acc1, 0));
+        const float u0 = rb(lane_of(acc0, 32)), u1 = rb(lane_of(acc1, 32));
         if (c.lane == 0) {
             const float s0 = rb(sigmoid_fast(g0)), s1 = rb(sigmoid_fast(g1));
             const uint32_t wv = pack_bf2(rb(g0 * s0) * u0, rb(g1 * s1) * u1);
