@@ -211,19 +211,17 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(PagedAttnArgs a) {
                 if (base + p >= len) sc[t][r] = -INFINITY;
                 mx = fmaxf(mx, sc[t][r]);
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = rows_max(mx);
         float l = 0.0f;
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const float e = expf(sc[t][r] - mx);
+                const float e = att_exp(sc[t][r] - mx);  // masked scores (-inf) give 0
                 sc[t][r] = e;
                 l += e;
             }
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
+        l = rows_sum(l);
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             uint32_t hi[4], lo[4];
@@ -262,7 +260,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(PagedAttnArgs a) {
     float f[4], L = 0.0f;
 #pragma unroll
     for (int w = 0; w < 4; w++) {
-        f[w] = sm[w][c] == -INFINITY ? 0.0f : expf(sm[w][c] - M);
+        f[w] = sm[w][c] == -INFINITY ? 0.0f : att_exp(sm[w][c] - M);
         L += f[w] * sl[w][c];
     }
     if (c >= a.grp) return;
@@ -303,7 +301,7 @@ __global__ __launch_bounds__(256) void merge_stage_kernel(MergeArgs a) {
     float o = 0.0f, L = 0.0f;
     for (int s = 0; s < nsplit; s++) {
         const float ms = gld(pp + s * stride + 64), ls = gld(pp + s * stride + 65);
-        const float f = ms == -INFINITY ? 0.0f : expf(ms - M);
+        const float f = ms == -INFINITY ? 0.0f : att_exp(ms - M);
         L += f * ls;
         o += f * gld(pp + s * stride + lane);
     }

@@ -345,7 +345,7 @@ __device__ __forceinline__ void attn_task(const CfmPArgs& a, uint32_t* img, int 
     attn_math(qv, kv, vv, o);
 #pragma unroll
     for (int i = 0; i < kPL; i++) {
-        const float o1 = __shfl(o[i], d ^ 1, kWave);
+        const float o1 = lane_xor1(o[i]);  // d is the lane
         if ((d & 1) == 0) gst(img + kPImgB + (3 * hb + i) * kD2 + col / 2, pack_bf2(o[i], o1));
     }
 }
@@ -485,14 +485,14 @@ __device__ __forceinline__ void wk_qkv(const Wk& c, const CfmPBlock& B, int s, i
     float acc[1][kPR];
     dots6<4, 32, 1>(wr, c.lds + kLXs, kPD / 8, tl, acc);
     const float e = rb(pick6(acc[0], tl) + bias);
-    const float other = __shfl(e, c.lane ^ 32, kWave);
+    const float other = lane_xor32(e, c.lane);
     float o = e;
     if (which < 2) {
         const float ev = team == 0 ? e : other, od = team == 0 ? other : e;
         const float p = ev * cs, q = od * sn, s2 = ev * sn, uu = od * cs;
         o = team == 0 ? p - q : s2 + uu;
     }
-    const float o1 = __shfl(o, c.lane ^ 32, kWave);
+    const float o1 = lane_xor32(o, c.lane);
     if (team == 0 && tl < kPR)
         tstore(a.tq + (size_t)(s * a.nblk + b) * kPTq + ((size_t)which * kD2 + nrow / 2) * kPR + tl, pack_bf2(o, o1),
                a.epoch);
@@ -522,7 +522,7 @@ __device__ __forceinline__ void wk_out(const Wk& c, const CfmPBlock& B, int s, i
     dots6<4, 32, 1>(wr, c.lds + kLXs, kPD / 8, tl, acc);
     const float res = team == 0 ? bf_lo(rw) : bf_hi(rw);
     const float o = res + rb(pick6(acc[0], tl) + bias);
-    const float o1 = __shfl(o, c.lane ^ 32, kWave);
+    const float o1 = lane_xor32(o, c.lane);
     if (team == 0 && tl < kPR)
         tstore(a.tx1 + (size_t)(s * a.nblk + b) * kPTx + tl * kD2 + u, pack_bf2(o, o1), a.epoch);
     stamp_stores(c, f);
@@ -570,12 +570,12 @@ __device__ __forceinline__ void wk_ff1(const Wk& c, const CfmPBlock& B, int s, i
     const float* tab = reinterpret_cast<const float*>(c.lds + kLTanh);
     {
         const float g = gelu_chain_p(tab, rb(pick6(acc[0], tl) + b0));
-        const float g1 = __shfl(g, c.lane ^ 32, kWave);
+        const float g1 = lane_xor32(g, c.lane);
         if (team == 0 && tl < kPR) tstore(out + (size_t)u0 * kPR + tl, pack_bf2(g, g1), a.epoch);
     }
     if (act1) {
         const float g = gelu_chain_p(tab, rb(pick6(acc[1], tl) + b1));
-        const float g1 = __shfl(g, c.lane ^ 32, kWave);
+        const float g1 = lane_xor32(g, c.lane);
         if (team == 0 && tl < kPR) tstore(out + (size_t)u1 * kPR + tl, pack_bf2(g, g1), a.epoch);
     }
     stamp_stores(c, f);

@@ -142,6 +142,21 @@ __device__ __forceinline__ float rows_reduce(float v, Op op) {
 __device__ __forceinline__ float rows_sum(float v) { return rows_reduce(v, [](float a, float b) { return a + b; }); }
 __device__ __forceinline__ float rows_max(float v) { return rows_reduce(v, [](float a, float b) { return fmaxf(a, b); }); }
 
+// e^x for attention softmaxes and their merges: the native base-2 exponential
+// (v_exp_f32, about one ulp) of x log2(e), two instructions where expf takes
+// about ten (range reduction, special cases); -inf gives 0.
+__device__ __forceinline__ float att_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
+// The value of lane l ^ 1 (DPP quad_perm [1,0,3,2]) and of lane l ^ 32
+// (v_permlane32_swap: its first result holds the low half twice, its second the
+// high half twice), exactly what __shfl(v, l ^ 1) and __shfl(v, l ^ 32) read,
+// without an LDS round trip.
+__device__ __forceinline__ float lane_xor1(float v) { return dpp<0xB1>(v); }
+__device__ __forceinline__ float lane_xor32(float v, int lane) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(lane < 32 ? p[1] : p[0]);
+}
+
 // Lane `lane`'s value (a constant lane) for the whole wave, by v_readlane.
 __device__ __forceinline__ float lane_of(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));

@@ -347,7 +347,7 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
     if (E == E_QKV) {
         // the rotary pair (2i, 2i+1) is (team 0, team 1) of this wave: D and 2W are even
         const float e = rb(v + ep.b);
-        const float other = __shfl(e, lane ^ 32, kWave);
+        const float other = lane_xor32(e, lane);
         if (r >= R || n >= a.N) return;
         float o = e;
         if (which < 2) {
@@ -388,7 +388,7 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
     if (E == E_STOP) {
         // lane 0 holds logit 0 (bias 0), lane 32 logit 1 (bias 1)
         const float x = rb(v + ep.b);
-        const float x1 = __shfl(x, lane ^ 32, kWave);
+        const float x1 = lane_xor32(x, lane);
         if (blockIdx.x != 0 || wave != 0 || lane != 0) return;
         const float m = fmaxf(x, x1), e0 = exp_rep(x - m), e1 = exp_rep(x1 - m);
         gst(a.p_out, e1 / (e0 + e1));

@@ -451,11 +451,6 @@ __device__ __forceinline__ void st_qkv(const Ctx& c, const LayerDev& Ld, int l) 
     st_qkv_g<Q4>(c, Ld, l, qkv_geom(c));
 }
 
-// e^x for the attention softmax and its merges: the native base-2 exponential
-// (v_exp_f32, about one ulp) of x log2(e), two instructions where expf takes
-// about ten (range reduction, special cases); -inf gives 0.
-__device__ __forceinline__ float att_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
-
 // 1 / (1 + e^-x) from the native exponential and reciprocal (about one ulp
 // each; the SwiGLU rounds the result to bf16).
 __device__ __forceinline__ float sigmoid_fast(float x) { return __builtin_amdgcn_rcpf(1.0f + att_exp(-x)); }
