@@ -1057,7 +1057,7 @@ __device__ __forceinline__ void head_rows(const Ctx& c, float& bv, int& bi) {
 // only once the head's input has arrived, so it gets the fewer tiles.
 template <int DEPTH>
 __device__ __forceinline__ void head_tiles(const Ctx& c, float& bv, int& bi) {
-    static_assert(DEPTH == 1 || DEPTH == 2, "one or two tiles in flight");
+    static_assert(DEPTH >= 1 && DEPTH <= 3, "one to three tiles in flight");
     const StepArgs& a = c.a;
     const LinearDev& L = a.head;
     const int V = L.N, G = L.K / 64, ntiles = (V + 15) / 16, nq = c.W * kW;
@@ -1065,10 +1065,11 @@ __device__ __forceinline__ void head_tiles(const Ctx& c, float& bv, int& bi) {
     const int n16 = c.lane % 16, kq = c.lane / 16;
     const __amdgpu_buffer_rsrc_t rs = q4tile_rsrc(L.s, V, G), rb = q4tile_rsrc(L.b, V, G);
     auto load = [&](int t, Q4Tile& r) { q4tile_load(L, min(t * 16 + n16, V - 1), kq, rs, rb, r); };
-    Q4Tile r0, r1;  // tile t in r0, t + nq in r1 (DEPTH 2)
+    Q4Tile r0, r1, r2;  // tile t in r0, t + nq in r1 (DEPTH >= 2), t + 2 nq in r2 (DEPTH 3)
     auto first = [&]() {
         if (q < ntiles) load(q, r0);
-        if (DEPTH == 2 && q + nq < ntiles) load(q + nq, r1);
+        if (DEPTH >= 2 && q + nq < ntiles) load(q + nq, r1);
+        if (DEPTH >= 3 && q + 2 * nq < ntiles) load(q + 2 * nq, r2);
     };
     if (c.wave > 0) first();
     get_image<1>(c, HUB_HEAD, 4 * a.n_layers, 4, a.tx + (size_t)a.n_layers * (a.H / 2), a.H, a.final_norm,
@@ -1092,7 +1093,8 @@ __device__ __forceinline__ void head_tiles(const Ctx& c, float& bv, int& bi) {
     };
     for (int t = q; t < ntiles; t += DEPTH * nq) {
         step(t, r0);
-        if (DEPTH == 2 && t + nq < ntiles) step(t + nq, r1);
+        if (DEPTH >= 2 && t + nq < ntiles) step(t + nq, r1);
+        if (DEPTH >= 3 && t + 2 * nq < ntiles) step(t + 2 * nq, r2);
     }
 }
 
@@ -1778,7 +1780,7 @@ __global__ __launch_bounds__(kT) void decode_xcd_kernel(StepArgs args, const Lay
     }
     const int ln = tix() % kWave;
     const Ctx c{a, lds, W, w, wave, ln, ln / 32, ln % 32, hub};
-    st_head<Q4, 2>(c);
+    st_head<Q4, 3>(c);
     done_stamp(a, slot_in(L, 0) + 1);
 }
 
