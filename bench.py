@@ -667,7 +667,9 @@ def bench_c1(args):
                                   f"inter 4864, vocab 151936, tied head), {C1_PROMPT}-token uniform prompt (seed 0) fed "
                                   f"one position at a time, then {C1_STEPS} greedy ids fed back on the device; one job "
                                   f"per step, cache emptied at its start",
-                      "global_batch": 1, "seq_len": C1_PROMPT + C1_STEPS, "schedule": args.mode,
+                      "global_batch": 1, "seq_len": C1_PROMPT + C1_STEPS,
+                      "schedule": args.mode if args.mode != "auto" else
+                      f"auto ({'xcd' if os.environ.get('MING_LM_XCD', '1') != '0' else 'persistent'})",
                       "prompt_ms": round(prompt_ms, 3),
                       "greedy_steps_tok_s": round(C1_STEPS * 1000.0 / (ms - prompt_ms), 2),
                       "steps_per_job": C1_PROMPT + C1_STEPS - 1},

@@ -19,8 +19,8 @@ hipError_t launch_lm_step_kernels(hipStream_t st, const StepArgs& a, const Layer
 hipError_t launch_lm_step_tagged(hipStream_t st, const StepArgs& a, int q4, int grid, bool cooperative);
 hipError_t launch_copy_token(hipStream_t st, const int32_t* src, int32_t* dst);
 int tagged_grid(int num_cus);
-hipError_t launch_lm_step_xcd(hipStream_t st, const StepArgs& a, int grid, bool cooperative);
-bool xcd_fits(int grid, int H, int heads, int kvh, int hd, int I, int n_layers);
+hipError_t launch_lm_step_xcd(hipStream_t st, const StepArgs& a, int q4, int grid, bool cooperative);
+bool xcd_fits(int q4, int grid, int H, int heads, int kvh, int hd, int I, int n_layers);
 int xcd_slots(int I);
 int tagged_split_len(int n);
 int tagged_hubs(int grid);
@@ -765,11 +765,13 @@ int ming_lm_model_create(ming_ctx* ctx, const ming_lm_cfg* cfg, const ming_lm_la
         ming_lm_model_destroy(m);
         return hip_check(ctx, e, "lm_model workspace");
     }
-    bool all_q4 = m->head.kind == 1;
+    // the XCD-local kernel is instantiated for one weight format throughout (as the first schedule's)
+    bool same_kind = true;
     for (const LayerDev& ld : m->layers)
-        for (const LinearDev* l : {&ld.q, &ld.k, &ld.v, &ld.o, &ld.g, &ld.u, &ld.d}) all_q4 = all_q4 && l->kind == 1;
-    m->xcd_ok = all_q4 && m->pgrid > 0 &&
-                xcd_fits(m->pgrid, H, cfg->heads, cfg->kv_heads, cfg->head_dim, I, L);
+        for (const LinearDev* l : {&ld.q, &ld.k, &ld.v, &ld.o, &ld.g, &ld.u, &ld.d})
+            same_kind = same_kind && l->kind == m->head.kind;
+    m->xcd_ok = same_kind && m->pgrid > 0 &&
+                xcd_fits(m->head.kind == 1, m->pgrid, H, cfg->heads, cfg->kv_heads, cfg->head_dim, I, L);
     *out = m;
     return MING_OK;
 }
@@ -919,7 +921,8 @@ static int lm_step_impl(ming_ctx* ctx, ming_lm_model* m, const int32_t* token_de
         // the partials were last written with parity xcd_parity: this step takes the other one
         a.epoch = ++m->epoch;
         while (a.epoch == 0 || (a.epoch & 1u) == m->xcd_parity) a.epoch = ++m->epoch;
-        st = hip_check(ctx, launch_lm_step_xcd(ctx->stream, a, m->pgrid, !ctx->exclusive), "lm_step XCD-local launch");
+        st = hip_check(ctx, launch_lm_step_xcd(ctx->stream, a, m->head.kind == 1, m->pgrid, !ctx->exclusive),
+                       "lm_step XCD-local launch");
         if (st) return st;
         m->xcd_parity = a.epoch & 1u;
         kv->len += 1;

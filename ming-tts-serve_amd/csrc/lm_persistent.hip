@@ -1240,8 +1240,6 @@ constexpr int kXs = 8;             // XCD slots
 constexpr int kHubRes = kLdsTotal;  // hub LDS, after the layer table: the residual stream, bf16 pairs [H/2] (H <= 1024)
 static_assert(kHubRes + 512 <= kLdsAll, "hub LDS regions");
 constexpr int kSliceT = 8;         // lanes per team of the split-K rows (8 rows per wave)
-constexpr int kON = 2;             // chunks per lane of an o_proj slice (K = grp * hd <= 512)
-constexpr int kDN = 3;             // chunks per lane of a down slice in the first batch
 
 // A partial as an f32 word whose lowest mantissa bit is the epoch's parity
 // (device-coherent store).  A reader that sees the parity of its own epoch
@@ -1259,64 +1257,98 @@ __device__ __forceinline__ void xslot_groups(const StepArgs& a, int x, int& gs, 
     ge = x < n ? (x + 1) * ng / n : ng;
 }
 
-// A lane's chunks of row n's K slice [32 cb, 32 (cb + nc)) of an affine
-// matrix: slice chunks c0 + tl + T j, clamped to the slice's last chunk (and
-// then not selected), as row_load does for whole rows.
-template <int NCH>
+// A lane's chunks of row n's K slice: chunks [cb, cb + nc) of the row, a chunk
+// being 32 values of an affine matrix (Q4) or 8 of a bf16 one; the lane takes
+// slice chunks c0 + tl + T j, clamped to the slice's last chunk (and then not
+// selected), as row_load does for whole rows.  Affine chunks carry their
+// group's scale and bias.
+template <int Q4, int NCH>
 struct SliceRegs {
     uint4 w[NCH];
     uint32_t s[NCH], b[NCH];
 };
+template <int NCH>
+struct SliceRegs<0, NCH> {
+    uint4 w[NCH];
+};
 
-template <int T, int NCH>
+// Values per chunk and the chunks per lane of the split-K rows (8-lane
+// teams): o_proj over a kv head's grp hd <= 512 columns, down over a slot's
+// SwiGLU columns (<= 10 groups of 64 for Qwen2-0.5B; more run in further
+// batches).
+template <int Q4>
+struct XcdN {
+    static constexpr int cv = Q4 ? 32 : 8;
+    static constexpr int o = Q4 ? 2 : 7;
+    static constexpr int d = Q4 ? 3 : 10;
+};
+
+template <int Q4, int T, int NCH>
 __device__ __forceinline__ void slice_load(const LinearDev& L, int n, int cb, int nc, int tl, int c0,
-                                           SliceRegs<NCH>& r) {
-    const int G = L.K / 64;
-    const uint32_t* wrow = L.w + (size_t)n * (L.K / 8);
+                                           SliceRegs<Q4, NCH>& r) {
+    const uint32_t* wrow = L.w + (size_t)n * (Q4 ? L.K / 8 : L.K / 2);
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
         const int c = cb + min(c0 + tl + T * j, nc - 1);
         r.w[j] = ldg4(wrow + 4 * c);
-        r.s[j] = gld(L.s + (size_t)n * G + (c >> 1));
-        r.b[j] = gld(L.b + (size_t)n * G + (c >> 1));
+        if constexpr (Q4 != 0) {
+            const int G = L.K / 64;
+            r.s[j] = gld(L.s + (size_t)n * G + (c >> 1));
+            r.b[j] = gld(L.b + (size_t)n * G + (c >> 1));
+        }
     }
 }
 
 // Partial dot of those chunks with the stage image of the slice (nc chunks).
-template <int T, int NCH>
-__device__ __forceinline__ float slice_compute(const SliceRegs<NCH>& r, const XStage& st, int nc, int tl, int c0) {
+template <int Q4, int T, int NCH>
+__device__ __forceinline__ float slice_compute(const SliceRegs<Q4, NCH>& r, const XStage& st, int nc, int tl, int c0) {
     float acc = 0.0f;
+    if constexpr (Q4 != 0) {
 #pragma unroll
-    for (int j = 0; j < NCH; j++) {
-        const int cr = c0 + tl + T * j;
-        const bool in = cr < nc;
-        const int c = in ? cr : nc - 1;
-        const uint4 x0 = *reinterpret_cast<const uint4*>(st.xs + (0 * nc + c) * 4);
-        const uint4 x1 = *reinterpret_cast<const uint4*>(st.xs + (1 * nc + c) * 4);
-        const uint4 x2 = *reinterpret_cast<const uint4*>(st.xs + (2 * nc + c) * 4);
-        const uint4 x3 = *reinterpret_cast<const uint4*>(st.xs + (3 * nc + c) * 4);
-        const float xh = st.xh[c];
-        float a0 = q4_word_dot(r.w[j].x, reinterpret_cast<const uint32_t*>(&x0), 0.0f);
-        float a1 = q4_word_dot(r.w[j].y, reinterpret_cast<const uint32_t*>(&x1), 0.0f);
-        a0 = q4_word_dot(r.w[j].z, reinterpret_cast<const uint32_t*>(&x2), a0);
-        a1 = q4_word_dot(r.w[j].w, reinterpret_cast<const uint32_t*>(&x3), a1);
-        const float s = bf2f((uint16_t)r.s[j]), b = bf2f((uint16_t)r.b[j]);
-        const float t = fmaf(b - 128.0f * s, xh, fmaf(s, a0 + a1, acc));
-        acc = in ? t : acc;
+        for (int j = 0; j < NCH; j++) {
+            const int cr = c0 + tl + T * j;
+            const bool in = cr < nc;
+            const int c = in ? cr : nc - 1;
+            const uint4 x0 = *reinterpret_cast<const uint4*>(st.xs + (0 * nc + c) * 4);
+            const uint4 x1 = *reinterpret_cast<const uint4*>(st.xs + (1 * nc + c) * 4);
+            const uint4 x2 = *reinterpret_cast<const uint4*>(st.xs + (2 * nc + c) * 4);
+            const uint4 x3 = *reinterpret_cast<const uint4*>(st.xs + (3 * nc + c) * 4);
+            const float xh = st.xh[c];
+            float a0 = q4_word_dot(r.w[j].x, reinterpret_cast<const uint32_t*>(&x0), 0.0f);
+            float a1 = q4_word_dot(r.w[j].y, reinterpret_cast<const uint32_t*>(&x1), 0.0f);
+            a0 = q4_word_dot(r.w[j].z, reinterpret_cast<const uint32_t*>(&x2), a0);
+            a1 = q4_word_dot(r.w[j].w, reinterpret_cast<const uint32_t*>(&x3), a1);
+            const float s = bf2f((uint16_t)r.s[j]), b = bf2f((uint16_t)r.b[j]);
+            const float t = fmaf(b - 128.0f * s, xh, fmaf(s, a0 + a1, acc));
+            acc = in ? t : acc;
+        }
+    } else {  // bf16 rows: the image holds the values in order, two accumulators as row_compute
+        float a1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int cr = c0 + tl + T * j;
+            const bool in = cr < nc;
+            const uint4 x = *reinterpret_cast<const uint4*>(st.xs + 4 * (in ? cr : nc - 1));
+            const float t0 = dot2(r.w[j].z, x.z, dot2(r.w[j].x, x.x, acc));
+            const float t1 = dot2(r.w[j].w, x.w, dot2(r.w[j].y, x.y, a1));
+            acc = in ? t0 : acc;
+            a1 = in ? t1 : a1;
+        }
+        acc += a1;
     }
     return acc;
 }
 
 // Row n's dot over the slice, its first batch of chunks in `first`; team
 // reduced, without the global scale (the hubs apply it to the summed slices).
-template <int T, int NCH>
-__device__ __forceinline__ float slice_dot(const LinearDev& L, int n, const SliceRegs<NCH>& first, const XStage& st,
-                                           int cb, int nc, int tl) {
-    float acc = slice_compute<T, NCH>(first, st, nc, tl, 0);
+template <int Q4, int T, int NCH>
+__device__ __forceinline__ float slice_dot(const LinearDev& L, int n, const SliceRegs<Q4, NCH>& first,
+                                           const XStage& st, int cb, int nc, int tl) {
+    float acc = slice_compute<Q4, T, NCH>(first, st, nc, tl, 0);
     for (int c0 = T * NCH; c0 < nc; c0 += T * NCH) {
-        SliceRegs<NCH> r;
-        slice_load<T, NCH>(L, n, cb, nc, tl, c0, r);
-        acc += slice_compute<T, NCH>(r, st, nc, tl, c0);
+        SliceRegs<Q4, NCH> r;
+        slice_load<Q4, T, NCH>(L, n, cb, nc, tl, c0, r);
+        acc += slice_compute<Q4, T, NCH>(r, st, nc, tl, c0);
     }
     return team_sum<T>(acc);
 }
@@ -1346,6 +1378,7 @@ __device__ __forceinline__ QkvGeom qkv_geom_x(const Ctx& c, int gh, int u) {
 // K = grp hd values.  Every word a thread needs is polled at once, and a
 // split's four words again while any is stale.  With `trace` the row also
 // goes to the attention trace.  All threads call it.
+template <int Q4>
 __device__ __forceinline__ void attn_merge_image(const Ctx& c, int l, int g, bool trace) {
     const StepArgs& a = c.a;
     const int grp = a.heads / a.kvh, hd = a.hd, K = grp * hd, ns = attn_splits(a.pos);
@@ -1414,7 +1447,7 @@ __device__ __forceinline__ void attn_merge_image(const Ctx& c, int l, int g, boo
         for (int j = 0; j < 4; j++) v[4 * p + j] = gi < K / 8 ? words[4 * gi + j] : 0u;
     }
     const uint4 nw[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-    image_finish<1, true>(a, c.lds, v, nw, K, nullptr, c.lds + kXsOff, nullptr, -1);
+    image_finish<Q4, true>(a, c.lds, v, nw, K, nullptr, c.lds + kXsOff, nullptr, -1);
     lds_sync();
 }
 
@@ -1423,16 +1456,17 @@ __device__ __forceinline__ void attn_merge_image(const Ctx& c, int l, int g, boo
 template <int Q4>
 __device__ __forceinline__ void st_opart(const Ctx& c, const LayerDev& Ld, int l, int g, int s, bool trace) {
     const StepArgs& a = c.a;
-    const int K = (a.heads / a.kvh) * a.hd, nc = K / 32, cb = g * nc;
+    constexpr int NO = XcdN<Q4>::o;
+    const int K = (a.heads / a.kvh) * a.hd, nc = K / XcdN<Q4>::cv, cb = g * nc;
     const int n = kSliceT * s + c.lane / kSliceT, tl = c.lane % kSliceT;
     const bool has = c.wave > 0 && n < a.H;
-    SliceRegs<kON> W;
-    if (has) slice_load<kSliceT, kON>(Ld.o, n, cb, nc, tl, 0, W);
+    SliceRegs<Q4, NO> W;
+    if (has) slice_load<Q4, kSliceT, NO>(Ld.o, n, cb, nc, tl, 0, W);
     lds_sync();
-    attn_merge_image(c, l, g, trace);
+    attn_merge_image<Q4>(c, l, g, trace);
     stamp(a, slot_in(l, 2));
     if (!has) return;
-    const float acc = slice_dot<kSliceT, kON>(Ld.o, n, W, xs_of(c.lds, K), cb, nc, tl);
+    const float acc = slice_dot<Q4, kSliceT, NO>(Ld.o, n, W, xs_of(c.lds, K), cb, nc, tl);
     if (tl == 0) pstore(a.tpo + ((size_t)l * a.kvh + g) * a.H + n, acc, a.epoch);
 }
 
@@ -1497,26 +1531,33 @@ __device__ __forceinline__ void st_up_x(const Ctx& c, const LayerDev& Ld, int l,
 
 // Down partial of slot x: rows 8 s + lane / 8 over the slot's SwiGLU columns
 // (chunks [cb, cb + nc)); the first batch of weights is loaded before gate/up.
+template <int Q4>
 struct DownX {
-    SliceRegs<kDN> W;
+    SliceRegs<Q4, XcdN<Q4>::d> W;
 };
 
-__device__ __forceinline__ void down_pre_x(const Ctx& c, const LayerDev& Ld, int s, int cb, int nc, DownX& d) {
+// The slot's SwiGLU values [v0, v0 + K) are chunks [v0 / cv, (v0 + K) / cv) of a down row.
+template <int Q4>
+__device__ __forceinline__ void down_pre_x(const Ctx& c, const LayerDev& Ld, int s, int v0, int K, DownX<Q4>& d) {
+    constexpr int CV = XcdN<Q4>::cv;
     const int n = kSliceT * s + c.lane / kSliceT;
-    if (c.wave > 0 && n < c.a.H) slice_load<kSliceT, kDN>(Ld.d, n, cb, nc, c.lane % kSliceT, 0, d.W);
+    if (c.wave > 0 && n < c.a.H)
+        slice_load<Q4, kSliceT, XcdN<Q4>::d>(Ld.d, n, v0 / CV, K / CV, c.lane % kSliceT, 0, d.W);
 }
 
-__device__ __forceinline__ void st_dpart(const Ctx& c, const LayerDev& Ld, int l, int x, int s, int cb, int nc,
-                                         const DownX& d) {
+template <int Q4>
+__device__ __forceinline__ void st_dpart(const Ctx& c, const LayerDev& Ld, int l, int x, int s, int v0, int K,
+                                         const DownX<Q4>& d) {
     const StepArgs& a = c.a;
+    constexpr int CV = XcdN<Q4>::cv;
     const int n = kSliceT * s + c.lane / kSliceT, tl = c.lane % kSliceT;
     const bool has = c.wave > 0 && n < a.H;
     lds_sync();
-    build_image<1, true>(a, c.lds, a.th + (size_t)l * (a.I / 2) + 16 * cb, 32 * nc, nullptr, c.lds + kXsOff, nullptr);
+    build_image<Q4, true>(a, c.lds, a.th + (size_t)l * (a.I / 2) + v0 / 2, K, nullptr, c.lds + kXsOff, nullptr);
     lds_sync();
     stamp(a, slot_in(l, 4));
     if (!has) return;
-    const float acc = slice_dot<kSliceT, kDN>(Ld.d, n, d.W, xs_of(c.lds, 32 * nc), cb, nc, tl);
+    const float acc = slice_dot<Q4, kSliceT, XcdN<Q4>::d>(Ld.d, n, d.W, xs_of(c.lds, K), v0 / CV, K / CV, tl);
     if (tl == 0) pstore(a.tpd + ((size_t)l * kXs + x) * a.H + n, acc, a.epoch);
 }
 
@@ -1766,15 +1807,15 @@ __global__ __launch_bounds__(kT) void decode_xcd_kernel(StepArgs args, const Lay
             st_opart<Q4>(c, Ld, l, gh, s, r == 1);
             done_stamp(a, slot_in(l, 2) + 1);
         }
-        DownX dx;
-        if (pd) down_pre_x(c, Ld, s, 2 * gs, 2 * (ge - gs), dx);
+        DownX<Q4> dx;
+        if (pd) down_pre_x<Q4>(c, Ld, s, 64 * gs, 64 * (ge - gs), dx);
         if (ge > gs) {
             st_up_x<Q4>(c, Ld, l, 32 * gs, 32 * ge, r, R, loc);
             done_stamp(a, slot_in(l, 3) + 1);
         }
         if (pa && l + 1 < L) attn_prefetch(c, l + 1);
         if (pd) {
-            st_dpart(c, Ld, l, x, s, 2 * gs, 2 * (ge - gs), dx);
+            st_dpart<Q4>(c, Ld, l, x, s, 64 * gs, 64 * (ge - gs), dx);
             done_stamp(a, slot_in(l, 4) + 1);
         }
     }
@@ -1819,13 +1860,14 @@ hipError_t launch_lm_step_tagged(hipStream_t st, const StepArgs& a, int q4, int 
     return hipLaunchKernel(f, dim3(grid), dim3(kT), params, 0, st);
 }
 
-// The XCD-local schedule (decode_xcd_kernel): 4-bit weights, grid of 8 R
-// workgroups.
-hipError_t launch_lm_step_xcd(hipStream_t st, const StepArgs& a, int grid, bool cooperative) {
+// The XCD-local schedule (decode_xcd_kernel): 4-bit (q4) or bf16 weights,
+// grid of 8 R workgroups.
+hipError_t launch_lm_step_xcd(hipStream_t st, const StepArgs& a, int q4, int grid, bool cooperative) {
     StepArgs args = a;
     const LayerDev* layers = a.layers;
     void* params[] = {&args, &layers};
-    const void* f = reinterpret_cast<const void*>(decode_xcd_kernel<1>);
+    const void* f = q4 ? reinterpret_cast<const void*>(decode_xcd_kernel<1>)
+                       : reinterpret_cast<const void*>(decode_xcd_kernel<0>);
     if (cooperative) return hipLaunchCooperativeKernel(f, dim3(grid), dim3(kT), params, 0, st);
     return hipLaunchKernel(f, dim3(grid), dim3(kT), params, 0, st);
 }
@@ -1833,10 +1875,12 @@ hipError_t launch_lm_step_xcd(hipStream_t st, const StepArgs& a, int grid, bool 
 // Whether the XCD-local schedule takes this shape on a grid of `grid`
 // workgroups (one per CU); a step also needs at most grid / 8 - 1 attention
 // splits per kv head.
-bool xcd_fits(int grid, int H, int heads, int kvh, int hd, int I, int n_layers) {
+bool xcd_fits(int q4, int grid, int H, int heads, int kvh, int hd, int I, int n_layers) {
     if (grid % kXs != 0 || grid > kXcdSlots || hd != 64 || kvh < 1 || kvh > kXs || heads % kvh != 0 || heads / kvh > 8) return false;
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_xcd_kernel<1>, kT, 0) != hipSuccess || per_cu < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, q4 ? decode_xcd_kernel<1> : decode_xcd_kernel<0>, kT,
+                                                     0) != hipSuccess ||
+        per_cu < 1)
         return false;
     const int R = grid / kXs, waves = (R - 1) * kCW, grp = heads / kvh;
     return R >= 2 && H % 64 == 0 && H <= 1024 && I % 64 == 0 && I <= 8192 && (grp + 2) * hd / 4 <= waves &&

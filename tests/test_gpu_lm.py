@@ -223,7 +223,7 @@ def bf16_model(ming, ctx):
     m.close()
 
 
-@pytest.mark.parametrize("mode", ["kernels", "persistent", "direct"])
+@pytest.mark.parametrize("mode", ["kernels", "persistent", "direct", "xcd"])
 def test_bf16_lm_step_matches_oracle(ming, ctx, bf16_model, mode):
     """bf16 weights (the persistent kernel's second instance, plain bf16 rows
     instead of 4-bit chunks) at hidden 896, 14/2 heads, inter 4864, vocab
