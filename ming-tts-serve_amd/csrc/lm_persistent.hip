@@ -60,11 +60,14 @@ constexpr int kMaxLdsLayers = 32;
 constexpr int kLayWords = (int)(sizeof(LayerDev) / 4);
 constexpr int kLdsTotal = kLayOff + kMaxLdsLayers * kLayWords;
 static_assert(sizeof(LayerDev) % 8 == 0, "layer table entries must keep 8-byte alignment in LDS");
-constexpr int kTile = 64;
-// Attention: a split of kAttTiles 64-position tiles per workgroup, its K rows
-// and V^T resident in LDS after the layer table.
-constexpr int kAttTiles = 6;
-constexpr int kAttP = kAttTiles * kTile;      // positions per split
+// Attention: a split of kAttTiles tiles of kTileP positions per workgroup, its
+// K rows and V^T resident in LDS after the layer table.  Four tiles of 96
+// positions take one compute wave on each SIMD (six of 64 put two on two SIMDs).
+constexpr int kTileP = 96;
+constexpr int kTileSub = kTileP / 16;  // 16-position score sub-tiles of a tile
+constexpr int kTileU = kTileP / 32;    // 32-position P.V chunks of a tile
+constexpr int kAttTiles = 4;
+constexpr int kAttP = kAttTiles * kTileP;     // positions per split
 constexpr int kVtRowP = kAttP / 2 + 4;        // u32 per V^T row (position pairs), padded: conflict-free reads
 constexpr int kKvOff = kLdsTotal;             // K rows [kAttP][64] bf16
 constexpr int kVtOffP = kKvOff + kAttP * 32;  // V^T [64][kVtRowP]
@@ -459,8 +462,8 @@ __device__ __forceinline__ float sigmoid_fast(float x) { return __builtin_amdgcn
 // Unit = (kv head g, split of kAttP positions), on the last workers.  A
 // split's K rows and V^T stay in this workgroup's LDS: they are loaded one
 // layer ahead (attn_prefetch, after the workgroup's gate/up stage of the
-// layer before, or at launch for layer 0), so that once q arrives the six
-// 64-position tiles of the split are computed at once, one per compute wave,
+// layer before, or at launch for layer 0), so that once q arrives the four
+// 96-position tiles of the split are computed at once, one per compute wave,
 // on the matrix cores, and merged through LDS into one partial per split
 // (per q head: max, sum, unnormalised output).  The splits of a kv head meet
 // through a per-(layer, kv head) arrival counter: every split stores its
@@ -651,16 +654,16 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l, bool loc = false, 
     const int grp = a.heads / a.kvh, hd = a.hd;
     const ALds S = alds(c.lds);
     lds_sync();  // q and the new row staged
-    const int tile = c.wave - 1, p0 = q.j0 + kTile * tile;
-    const int cnt = (c.wave >= 1 && c.wave <= kAttTiles) ? max(0, min(kTile, q.j1 - p0)) : 0;
+    const int tile = c.wave - 1, p0 = q.j0 + kTileP * tile;
+    const int cnt = (c.wave >= 1 && c.wave <= kAttTiles) ? max(0, min(kTileP, q.j1 - p0)) : 0;
     const int cc = c.lane % 16, jj = c.lane / 16;
     if (cnt > 0) {
         const uint4 qb[2] = {S.qb[2 * c.lane], S.qb[2 * c.lane + 1]};
-        const uint4* kt = reinterpret_cast<const uint4*>(c.lds + kKvOff) + (size_t)kTile * tile * 8;  // 8 chunks a row
-        f32x4_t sc[4];
+        const uint4* kt = reinterpret_cast<const uint4*>(c.lds + kKvOff) + (size_t)kTileP * tile * 8;  // 8 chunks a row
+        f32x4_t sc[kTileSub];
 #pragma unroll
-        for (int tt = 0; tt < 4; tt++) {
-            const int p = 32 * (tt / 2) + 8 * (cc / 4) + 4 * (tt % 2) + cc % 4, pr = kTile * tile + p;
+        for (int tt = 0; tt < kTileSub; tt++) {
+            const int p = 32 * (tt / 2) + 8 * (cc / 4) + 4 * (tt % 2) + cc % 4, pr = kTileP * tile + p;
             const uint4* kr = kt + 8 * p;
             sc[tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
             sc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(kr[(2 * jj) ^ kswz(pr)]), as_bf8(qb[0]), sc[tt],
@@ -668,9 +671,9 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l, bool loc = false, 
             sc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(kr[(2 * jj + 1) ^ kswz(pr)]), as_bf8(qb[1]),
                                                             sc[tt], 0, 0, 0);
         }
-        if (cnt < kTile) {  // (wave-uniform) only the tile that holds the newest position is partial
+        if (cnt < kTileP) {  // (wave-uniform) only the tile that holds the newest position is partial
 #pragma unroll
-            for (int tt = 0; tt < 4; tt++)
+            for (int tt = 0; tt < kTileSub; tt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int p = 32 * (tt / 2) + 8 * jj + 4 * (tt % 2) + r;
@@ -679,13 +682,13 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l, bool loc = false, 
         }
         float mx = -INFINITY;
 #pragma unroll
-        for (int tt = 0; tt < 4; tt++)
+        for (int tt = 0; tt < kTileSub; tt++)
 #pragma unroll
             for (int r = 0; r < 4; r++) mx = fmaxf(mx, sc[tt][r]);
         mx = rows_max(mx);
         float lp = 0.0f;
 #pragma unroll
-        for (int tt = 0; tt < 4; tt++)
+        for (int tt = 0; tt < kTileSub; tt++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const float e = att_exp(sc[tt][r] - mx);  // masked scores (-inf) give 0
@@ -693,12 +696,12 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l, bool loc = false, 
                 lp += e;
             }
         lp = rows_sum(lp);
-        const uint32_t* vt = c.lds + kVtOffP + (kTile / 2) * tile;
+        const uint32_t* vt = c.lds + kVtOffP + (kTileP / 2) * tile;
         f32x4_t o[4];
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) o[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
+        for (int u = 0; u < kTileU; u++) {
             uint32_t hi[4], lo[4];
 #pragma unroll
             for (int k = 0; k < 4; k++) {
@@ -732,7 +735,7 @@ __device__ __forceinline__ void attn_run(const Ctx& c, int l, bool loc = false, 
     // the split's partial: per head the max over its tiles, the sum and output rescaled to it;
     // device-coherent stores, completed before the arrival (direct: tagged words of the layer's
     // own partial slots, which the o_proj workers poll and merge; no arrival)
-    const int ntl = min(kAttTiles, (q.j1 - q.j0 + kTile - 1) / kTile);  // tiles holding positions
+    const int ntl = min(kAttTiles, (q.j1 - q.j0 + kTileP - 1) / kTileP);  // tiles holding positions
     const int t = tix();
     const bool xl = *reinterpret_cast<const int*>(c.lds + kFlagOff + 2) != 0;
     {
@@ -1828,7 +1831,7 @@ __global__ __launch_bounds__(kT) void decode_xcd_kernel(StepArgs args, const Lay
 }  // namespace
 
 // Positions per attention split on this schedule: a workgroup holds the
-// split's K rows and V^T in LDS, one 64-position tile per compute wave.
+// split's K rows and V^T in LDS, one 96-position tile on each of four compute waves.
 int tagged_split_len(int) { return kAttP; }
 
 // Hubs for a grid of `grid` workgroups: one per XCD when the grid is large
