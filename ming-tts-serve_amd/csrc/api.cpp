@@ -79,13 +79,12 @@ bool xcd_enabled() {
 }
 
 // In the XCD-local schedule, hand-offs inside a slot through plain stores
-// (where the slot's workgroups share an XCD) unless MING_LM_XCD_LOCAL=0.
+// (where the slot's workgroups share an XCD) unless MING_LM_XCD_LOCAL=0, read
+// at every step (the device-coherent form is what a slot split over XCDs
+// runs; tests force it to check that it gives the same bits).
 bool xcd_local_enabled() {
-    static const bool on = [] {
-        const char* e = std::getenv("MING_LM_XCD_LOCAL");
-        return !(e && e[0] == '0');
-    }();
-    return on;
+    const char* e = std::getenv("MING_LM_XCD_LOCAL");
+    return !(e && e[0] == '0');
 }
 
 int hub_stages() {

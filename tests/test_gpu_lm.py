@@ -268,6 +268,24 @@ def test_schedules_agree_and_deterministic(ming, ctx, q4_model):
     assert_close_bf16(x[1], k[1], "XCD-local vs kernels hidden", atol=0.2, rtol=0.1)
 
 
+def test_xcd_coherent_handoffs_same_bits(ming, ctx, q4_model, monkeypatch):
+    """The XCD-local schedule's hand-offs inside a slot go through that XCD's L2
+    (plain stores) where the slot's workgroups share an XCD, else through
+    device-coherent stores; MING_LM_XCD_LOCAL=0 forces the second form, which
+    must give the same bits (the store kind changes no arithmetic)."""
+    S = syn_mod(ming)
+    syn, m, _ = q4_model
+    outs = []
+    for local in ("1", "0"):
+        monkeypatch.setenv("MING_LM_XCD_LOCAL", local)
+        cache = S.KvCache(syn.spec, 2100)
+        cache.fill_random(2048, seed=21)
+        outs.append([run_step(ming, syn, m, cache, t, ming.LM_PERSISTENT_XCD) for t in (5, 77777)])
+    for a, b in zip(*outs):
+        assert a[0] == b[0] and np.array_equal(a[1], b[1]) and np.array_equal(a[2], b[2]), \
+            "device-coherent hand-offs change the result"
+
+
 def test_ordinary_launch_matches_cooperative(ming, ctx, q4_model):
     """With the device held exclusively the persistent step is an ordinary
     launch; the kernel is the same, so the bits are the same, in both the hub
