@@ -861,7 +861,7 @@ static int lm_step_impl(ming_ctx* ctx, ming_lm_model* m, const int32_t* token_de
     a.amax_v = static_cast<float*>(m->amax_v.p);
     a.amax_i = static_cast<int32_t*>(m->amax_i.p);
     a.flags = ctx->dev_flags;
-    if (!token_dev &&
+    if (!token_dev && x_in != a.x &&
         (st = hip_check(ctx,
                         hipMemcpyAsync(a.x, x_in, sizeof(uint16_t) * c->hidden, hipMemcpyDeviceToDevice, ctx->stream),
                         "copy x_in")))
@@ -992,3 +992,7 @@ int ming_lm_generate(ming_ctx* ctx, ming_lm_model* m, ming_kv* kv, int32_t n_ste
 }
 
 }  // extern "C"
+
+// Layer 0's input row of the model's step (where an input row is copied
+// unless the caller wrote it there already, as the TTS loop's aggregator does).
+uint16_t* ming::lm_input_row(ming_lm_model* m) { return static_cast<uint16_t*>(m->x.p); }

@@ -5,6 +5,7 @@
 // cfmSample / aggregate / stopProb (src/ming_model.zig:1033-1053, :1143-1203).
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -17,7 +18,7 @@ hipError_t launch_dit_stage(hipStream_t st, int which, const DitBlockDev& w, con
                             int B, int L, const float* cos_t, const float* sin_t, uint16_t* qkv, uint16_t* out);
 hipError_t launch_dit_block(hipStream_t st, const DitBlockDev& w, const uint16_t* x, int B, int L,
                             const float* cos_t, const float* sin_t, uint16_t* qkv, uint16_t* att, uint16_t* x1,
-                            uint16_t* hh, uint16_t* x2);
+                            uint16_t* hh, uint16_t* x2, bool fuse_attn);
 hipError_t launch_dit_linear(hipStream_t st, const uint16_t* x, int64_t xrow0, int64_t xstride, int R,
                              const uint16_t* norm, float eps, const uint16_t* w, int N, int K, const uint16_t* bias,
                              uint16_t* out, bool silu);
@@ -27,7 +28,8 @@ hipError_t launch_cfm_final(hipStream_t st, const uint16_t* h, int L, int D, con
                             const uint16_t* wf, const uint16_t* bf, int latent, const uint16_t* y, const uint16_t* dt,
                             const uint16_t* sq, const uint16_t* sde, int step, float cfg, float shift,
                             uint16_t* y_out);
-hipError_t launch_stop_prob(hipStream_t st, const uint16_t* z, const uint16_t* w, const uint16_t* b, int K, float* p);
+hipError_t launch_stop_prob(hipStream_t st, const uint16_t* z, const uint16_t* w, const uint16_t* b, int K, float* p,
+                            const int32_t* flags_in);
 hipError_t launch_cfm_persistent(hipStream_t st, const CfmPArgs& a, int grid, bool cooperative);
 int cfmp_grid(int num_cus);
 hipError_t launch_adaln_block(hipStream_t st, const DitBlockDev& w, const uint16_t* mod, const uint16_t* x, int B,
@@ -171,16 +173,20 @@ struct StackBufs {
 };
 
 // The blocks of a stack on rows[0] (B x L rows); returns the buffer holding the output.
+// The blocks in order on rows ping-ponging between b.rows[0] and [1]; the
+// first block reads `first` when given (else b.rows[0]).
 hipError_t run_stack(hipStream_t st, const std::vector<DitBlockDev>& blocks, StackBufs& b, int B, int L,
-                     const float* cos_t, const float* sin_t, uint16_t** out) {
+                     const float* cos_t, const float* sin_t, uint16_t** out, uint16_t* first = nullptr) {
     int cur = 0;
+    uint16_t* in = first ? first : u16(b.rows[0].p);
     for (const DitBlockDev& w : blocks) {
-        hipError_t e = launch_dit_block(st, w, u16(b.rows[cur].p), B, L, cos_t, sin_t, u16(b.qkv.p), u16(b.att.p),
-                                        u16(b.x1.p), u16(b.hh.p), u16(b.rows[cur ^ 1].p));
+        hipError_t e = launch_dit_block(st, w, in, B, L, cos_t, sin_t, u16(b.qkv.p), u16(b.att.p), u16(b.x1.p),
+                                        u16(b.hh.p), u16(b.rows[cur ^ 1].p), true);
         if (e != hipSuccess) return e;
         cur ^= 1;
+        in = u16(b.rows[cur].p);
     }
-    *out = u16(b.rows[cur].p);
+    *out = in;
     return hipSuccess;
 }
 
@@ -282,6 +288,7 @@ struct ming_agg_model {
                    *final_norm = nullptr;
     int latent = 0, lm_hidden = 0;
     DevBuf cos, sin;
+    DevBuf in;  // the first block's input rows [cls; x_emb(latent)]: cls written once at creation
     StackBufs s;
 };
 
@@ -340,7 +347,7 @@ int ming_dit_block(ming_ctx* ctx, const ming_dit_cfg* cfg, const ming_dit_block_
     const DitBlockDev d = block_dev(cfg, w);
     return hip_check(ctx,
                      launch_dit_block(ctx->stream, d, u16(x), B, L, cos_dev, sin_dev, u16(out->qkv), u16(out->att),
-                                      u16(out->x1), u16(out->hh), u16(out->x2)),
+                                      u16(out->x1), u16(out->hh), u16(out->x2), false),
                      "dit_block launch");
 }
 
@@ -439,6 +446,10 @@ int ming_cfm_model_create(ming_ctx* ctx, const ming_cfm_w* w, ming_cfm_model** o
     if (e == hipSuccess) e = m->y.ensure(sizeof(uint16_t) * (size_t)latent);
     if (e == hipSuccess) e = m->s.alloc(2 * L, D, c->ff);
     if (e == hipSuccess) e = hipMemsetAsync(m->zc.p, 0, m->zc.bytes, s);
+    // c_emb of the unconditional half's zero row, once: row 1 of ce (cfm_sample computes row 0)
+    if (e == hipSuccess)
+        e = launch_dit_linear(s, u16(m->zc.p) + H, 0, 1, 1, nullptr, c->eps, m->wc, D, H, m->bc, u16(m->ce.p) + D,
+                              false);
     if (e != hipSuccess) {
         ming_cfm_model_destroy(m);
         return hip_check(ctx, e, "cfm_model_create");
@@ -529,10 +540,16 @@ int ming_cfm_sample(ming_ctx* ctx, ming_cfm_model* m, const void* z, const void*
     hipStream_t s = ctx->stream;
     const int D = m->cfg.hidden, H = m->lm_hidden, lat = m->latent, L = 3;
     const float eps = m->cfg.eps;
-    // once per sample: c_emb([z, 0]) and x_emb(hist) (:1196-1197)
-    hipError_t e = hipMemcpyAsync(m->zc.p, z, sizeof(uint16_t) * H, hipMemcpyDeviceToDevice, s);
-    if (e == hipSuccess)
-        e = launch_dit_linear(s, u16(m->zc.p), 0, 1, 2, nullptr, eps, m->wc, D, H, m->bc, u16(m->ce.p), false);
+    // once per sample: c_emb([z, 0]) and x_emb(hist) (:1196-1197).  Row 1 of ce, c_emb of the zero
+    // row, is computed at creation; row 0 reads z in place when it is 16-byte aligned (a row's
+    // result does not depend on how many rows a launch takes).
+    hipError_t e = hipSuccess;
+    const uint16_t* zin = u16(z);
+    if (reinterpret_cast<uintptr_t>(z) % 16 != 0) {
+        e = hipMemcpyAsync(m->zc.p, z, sizeof(uint16_t) * H, hipMemcpyDeviceToDevice, s);
+        zin = u16(m->zc.p);
+    }
+    if (e == hipSuccess) e = launch_dit_linear(s, zin, 0, 1, 1, nullptr, eps, m->wc, D, H, m->bc, u16(m->ce.p), false);
     if (e == hipSuccess)
         e = launch_dit_linear(s, u16(hist), 0, 1, 1, nullptr, eps, m->wx, D, lat, m->bx, u16(m->xh.p), false);
     // AUTO takes the persistent kernel wherever its shape fits: 1.51 ms per sample against the
@@ -706,6 +723,8 @@ int ming_agg_model_create(ming_ctx* ctx, const ming_agg_w* w, ming_agg_model** o
     hipError_t e = m->cos.ensure(sizeof(float) * L * half);
     if (e == hipSuccess) e = m->sin.ensure(sizeof(float) * L * half);
     if (e == hipSuccess) e = m->s.alloc(L, D, c->ff);
+    if (e == hipSuccess) e = m->in.ensure(sizeof(uint16_t) * 2 * (size_t)D);
+    if (e == hipSuccess) e = hipMemcpy(m->in.p, m->cls, sizeof(uint16_t) * D, hipMemcpyDeviceToDevice);
     if (e != hipSuccess) {
         ming_agg_model_destroy(m);
         return hip_check(ctx, e, "agg_model_create");
@@ -722,6 +741,7 @@ int ming_agg_model_destroy(ming_agg_model* m) {
     if (!m) return MING_E_NOT_INIT;
     m->cos.release();
     m->sin.release();
+    m->in.release();
     m->s.release();
     delete m;
     return MING_OK;
@@ -745,27 +765,25 @@ int aggregate_impl(ming_ctx* ctx, ming_agg_model* m, const void* latent, void* o
                                          hipMemcpyDeviceToDevice, s)
                         : hipSuccess;
     };
-    // h = [cls, x_emb(latent)] (:1046-1050)
-    hipError_t e = hipMemcpyAsync(m->s.rows[0].p, m->cls, sizeof(uint16_t) * D, hipMemcpyDeviceToDevice, s);
-    if (e == hipSuccess)
-        e = launch_dit_linear(s, u16(latent), 0, 1, 1, nullptr, 0.0f, m->wx, D, m->latent, m->bx,
-                              u16(m->s.rows[0].p) + D, false);
+    // h = [cls, x_emb(latent)] (:1046-1050): row 0 of m->in holds cls since creation
+    uint16_t* in = u16(m->in.p);
+    hipError_t e = launch_dit_linear(s, u16(latent), 0, 1, 1, nullptr, 0.0f, m->wx, D, m->latent, m->bx, in + D, false);
     uint16_t* h = nullptr;
     if (e == hipSuccess && !rows_out) {
         e = run_stack(s, m->blocks, m->s, 1, 2, static_cast<const float*>(m->cos.p),
-                      static_cast<const float*>(m->sin.p), &h);
+                      static_cast<const float*>(m->sin.p), &h, in);
     } else if (e == hipSuccess) {  // run_stack's launches one block at a time, keeping each input
         int cur = 0;
+        h = in;
         for (size_t i = 0; i < m->blocks.size() && e == hipSuccess; i++) {
-            e = keep((int)i, m->s.rows[cur].p);
+            e = keep((int)i, h);
             if (e == hipSuccess)
-                e = launch_dit_block(s, m->blocks[i], u16(m->s.rows[cur].p), 1, 2,
-                                     static_cast<const float*>(m->cos.p), static_cast<const float*>(m->sin.p),
-                                     u16(m->s.qkv.p), u16(m->s.att.p), u16(m->s.x1.p), u16(m->s.hh.p),
-                                     u16(m->s.rows[cur ^ 1].p));
+                e = launch_dit_block(s, m->blocks[i], h, 1, 2, static_cast<const float*>(m->cos.p),
+                                     static_cast<const float*>(m->sin.p), u16(m->s.qkv.p), u16(m->s.att.p),
+                                     u16(m->s.x1.p), u16(m->s.hh.p), u16(m->s.rows[cur ^ 1].p), true);
             cur ^= 1;
+            h = u16(m->s.rows[cur].p);
         }
-        h = u16(m->s.rows[cur].p);
         if (e == hipSuccess) e = keep((int)m->blocks.size(), h);
     }
     // final(rms(h)) on row 0 (:1051-1052)
@@ -790,16 +808,26 @@ int ming_aggregate_trace(ming_ctx* ctx, ming_agg_model* m, const void* latent, v
 }
 
 int ming_stop_prob(ming_ctx* ctx, const ming_linear* head, const void* bias, const void* z, float* p_dev) {
+    return stop_prob_impl(ctx, head, bias, z, p_dev, false);
+}
+
+}  // extern "C"
+
+// stopProb; with_flags: the context's three error flags follow p in p_dev[1..3]
+// (as int32), read after every earlier launch on the stream, so that one copy
+// brings both to the host.
+int ming::stop_prob_impl(ming_ctx* ctx, const ming_linear* head, const void* bias, const void* z, float* p_dev,
+                         bool with_flags) {
     if (!alive(ctx)) return MING_E_NOT_INIT;
     if (!head || !bias || !z || !p_dev) return set_err(ctx, MING_E_ARG, "stop_prob: null argument");
     int st;
     if ((st = check_bf16(ctx, *head, 2, head->in_features, "stop_head"))) return st;
     if (head->in_features > 4096) return set_err(ctx, MING_E_UNSUPPORTED, "stop_prob: hidden > 4096");
-    return hip_check(ctx, launch_stop_prob(ctx->stream, u16(z), u16(head->w), u16(bias), head->in_features, p_dev),
+    return hip_check(ctx,
+                     launch_stop_prob(ctx->stream, u16(z), u16(head->w), u16(bias), head->in_features, p_dev,
+                                      with_flags ? ctx->dev_flags : nullptr),
                      "stop_prob launch");
 }
-
-}  // extern "C"
 
 // ---- adaLN flow head (config 4) ---------------------------------------------------------
 

@@ -155,13 +155,14 @@ int ming_sample_latents(ming_ctx* ctx, ming_lm_model* lm, ming_cfm_model* cfm, m
     hipError_t e = b.z.ensure(sizeof(uint16_t) * H);
     if (e == hipSuccess) e = b.xrow.ensure(sizeof(uint16_t) * H);
     if (e == hipSuccess) e = b.hist.ensure(sizeof(uint16_t) * lat);
-    if (e == hipSuccess) e = b.stop.ensure(sizeof(float) * 2);
+    if (e == hipSuccess) e = b.stop.ensure(sizeof(StopSlot) * 2);
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&b.host_stop), sizeof(StopSlot) * 2);
     for (hipEvent_t& ev : b.ev)
         if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
     if ((st = hip_check(ctx, e, "sample_latents workspace"))) return st;
     uint16_t* z = static_cast<uint16_t*>(b.z.p);
-    uint16_t* xrow = static_cast<uint16_t*>(b.xrow.p);
+    // the aggregator writes the LM step's input row in place
+    uint16_t* xrow = lm_input_row(lm) ? lm_input_row(lm) : static_cast<uint16_t*>(b.xrow.p);
     float* stop_dev = static_cast<float*>(b.stop.p);
     const uint16_t* emb = static_cast<const uint16_t*>(embeds);
     uint16_t* lats = static_cast<uint16_t*>(latents_out);
@@ -183,16 +184,16 @@ int ming_sample_latents(ming_ctx* ctx, ming_lm_model* lm, ming_cfm_model* cfm, m
                       : hipMemsetAsync(b.hist.p, 0, sizeof(uint16_t) * lat, s);
     if ((st = hip_check(ctx, e, "sample_latents history"))) return st;
     const uint16_t* hist = static_cast<const uint16_t*>(b.hist.p);
-    // stop_k and the error flags on their way to the host into slot k & 1
+    // stop_k and the error flags (written beside it by the stop launch) on their way to the host
+    // into slot k & 1, in one copy
     auto send_stop = [&](int slot) {
-        hipError_t r = hipMemcpyAsync(&b.host_stop[slot].p, stop_dev + slot, sizeof(float), hipMemcpyDeviceToHost, s);
-        if (r == hipSuccess)
-            r = hipMemcpyAsync(b.host_stop[slot].flags, ctx->dev_flags, sizeof(b.host_stop[slot].flags),
-                               hipMemcpyDeviceToHost, s);
+        hipError_t r = hipMemcpyAsync(&b.host_stop[slot], stop_dev + 4 * slot, sizeof(StopSlot), hipMemcpyDeviceToHost,
+                                      s);
         if (r == hipSuccess) r = hipEventRecord(b.ev[slot], s);
         return hip_check(ctx, r, "sample_latents stop copy");
     };
-    if ((st = ming_stop_prob(ctx, stop_head, stop_bias, z, stop_dev))) return st;
+    static_assert(sizeof(StopSlot) == 4 * sizeof(float), "p and three flags");
+    if ((st = stop_prob_impl(ctx, stop_head, stop_bias, z, stop_dev, true))) return st;
     if ((st = send_stop(0))) return st;
     int n = 0;
     for (int k = 0; k < steps; k++) {
@@ -210,7 +211,7 @@ int ming_sample_latents(ming_ctx* ctx, ming_lm_model* lm, ming_cfm_model* cfm, m
         if (k + 1 < steps) {  // the next position, queued before the host reads stop_k
             if ((st = ming_aggregate(ctx, agg, latent, xrow)) ||
                 (st = ming_lm_step(ctx, lm, nullptr, xrow, kv, z, nullptr, nullptr)) ||
-                (st = ming_stop_prob(ctx, stop_head, stop_bias, z, stop_dev + nxt)))
+                (st = stop_prob_impl(ctx, stop_head, stop_bias, z, stop_dev + 4 * nxt, true)))
                 return st;
             if ((st = send_stop(nxt))) return st;
         }

@@ -23,6 +23,7 @@
 // wave short: native bf16 rounding, one reciprocal square root per row shared
 // by readlane, no loads after the reduction.  Team sums use DPP; rows past N
 // load the last row again and write nothing.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -41,6 +42,7 @@ constexpr int kMaxSlots = 20;  // row slots of the widest launch (adaLN modulati
 // 16-byte LDS vector (the staged rows are 16-byte aligned: K % 8 == 0)
 typedef uint32_t lds_u32x4_t __attribute__((ext_vector_type(4), aligned(16)));
 constexpr int kMaxL = 8;  // positions per sequence (attention)
+constexpr int kMaxH = 4;  // heads per wave in dit_attn_out_kernel (16 heads, 4 waves)
 
 enum DitEpi {
     E_BIAS = 0,     // out[r][n] = bf16(acc + b)
@@ -94,6 +96,7 @@ struct DitGemv {
     float cfg, shift;
     uint16_t* y_out;
     float* p_out;          // E_STOP
+    const int32_t* flags_in;  // E_STOP: when set, flags_in[0..2] are copied to p_out[1..3] (as int32)
 };
 
 // (float)tanh((double)u) for every bf16 u in [0, 16] (tanh_tab.h), filled at
@@ -120,28 +123,16 @@ __device__ __forceinline__ float gelu_chain(float x) {
 // branches, so the compiler issues every load, and later every LDS store,
 // back to back.  Threads whose chunk is past the row's end store nothing and
 // add nothing to the sums.
+//
+// stage_finish is the arithmetic on operands already in registers (xr the
+// rows' chunks c = min(t + T j, K/8 - 1), gn the norm weight's, msh / msc the
+// adaLN shift and scale of the two CFG halves); stage_rows loads them first.
 template <int MODE, int RC, int XCH, int T>
-__device__ __forceinline__ void stage_rows(const DitGemv& a, uint32_t* xs, float* red, int t) {
+__device__ __forceinline__ void stage_finish(const DitGemv& a, uint32_t* xs, float* red, int t,
+                                             const uint4 (&xr)[RC][XCH], const uint4 (&gn)[XCH],
+                                             const uint4 (&msh)[2][XCH], const uint4 (&msc)[2][XCH]) {
     constexpr bool NORM = MODE != M_PLAIN, ADA = MODE == M_ADANORM;
     const int K = a.K, NC = K / 8, K2 = K / 2, R = a.R;
-    uint4 xr[RC][XCH];
-    uint4 gn[XCH];
-    uint4 msh[2][XCH], msc[2][XCH];  // adaLN shift / scale chunks of the (at most 2) CFG halves
-    const int nh = ADA ? (R + a.rph - 1) / a.rph : 1;
-#pragma unroll
-    for (int j = 0; j < XCH; j++) {
-        const int c = min(t + T * j, NC - 1);
-        if (NORM) gn[j] = ldg4(a.norm + 8 * c);
-#pragma unroll
-        for (int r = 0; r < RC; r++) xr[r][j] = ldg4(a.x + (a.xrow0 + min(r, R - 1) * a.xstride) * K + 8 * c);
-        if (ADA)
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const uint16_t* mh = a.mod + min(h, nh - 1) * a.mstride;
-                msh[h][j] = ldg4(mh + (size_t)a.soff * K + 8 * c);
-                msc[h][j] = ldg4(mh + (size_t)a.coff * K + 8 * c);
-            }
-    }
     if (!NORM) {
 #pragma unroll
         for (int j = 0; j < XCH; j++) {
@@ -218,6 +209,31 @@ __device__ __forceinline__ void stage_rows(const DitGemv& a, uint32_t* xs, float
     }
 }
 
+template <int MODE, int RC, int XCH, int T>
+__device__ __forceinline__ void stage_rows(const DitGemv& a, uint32_t* xs, float* red, int t) {
+    constexpr bool NORM = MODE != M_PLAIN, ADA = MODE == M_ADANORM;
+    const int K = a.K, NC = K / 8, R = a.R;
+    uint4 xr[RC][XCH];
+    uint4 gn[XCH];
+    uint4 msh[2][XCH], msc[2][XCH];  // adaLN shift / scale chunks of the (at most 2) CFG halves
+    const int nh = ADA ? (R + a.rph - 1) / a.rph : 1;
+#pragma unroll
+    for (int j = 0; j < XCH; j++) {
+        const int c = min(t + T * j, NC - 1);
+        if (NORM) gn[j] = ldg4(a.norm + 8 * c);
+#pragma unroll
+        for (int r = 0; r < RC; r++) xr[r][j] = ldg4(a.x + (a.xrow0 + min(r, R - 1) * a.xstride) * K + 8 * c);
+        if (ADA)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint16_t* mh = a.mod + min(h, nh - 1) * a.mstride;
+                msh[h][j] = ldg4(mh + (size_t)a.soff * K + 8 * c);
+                msc[h][j] = ldg4(mh + (size_t)a.coff * K + 8 * c);
+            }
+    }
+    stage_finish<MODE, RC, XCH, T>(a, xs, red, t, xr, gn, msh, msc);
+}
+
 // Operands of the epilogue of lane tl (row r = tl, output n), loaded at
 // kernel start so that no load waits at the end.
 struct EpiIn {
@@ -267,37 +283,14 @@ __device__ __forceinline__ EpiIn epi_load(const DitGemv& a, int n, int nrow, int
     return p;
 }
 
-// ---- the GEMV kernel ----------------------------------------------------------------
-
-// W waves, RPW output rows per wave (a team of 64 / RPW lanes per row), NCH
-// 16-byte weight chunks per lane, RC row slots.
-template <int E, int MODE, int NCH, int W, int RC, int RPW>
-__global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
-    constexpr int T = 64 * W, TEAM = kWave / RPW, ROWS = RPW * W, XCH = (NCH * TEAM + T - 1) / T;
-    static_assert((E != E_QKV && E != E_STOP && E != E_CFMF) || RPW == 2, "per-row lanes live in a half wave");
-    extern __shared__ uint32_t xs[];  // [R][K/2] bf16 pairs, natural order
-    __shared__ float red[W * kMaxSlots];
-    static_assert(RC <= kMaxSlots, "row slots");
-    const int t = threadIdx.x, wave = t / kWave, lane = t % kWave, team = lane / TEAM, tl = lane % TEAM;
-    const int K = a.K, R = a.R, NCk = K / 8, K2 = K / 2;
-    const int n = blockIdx.x * ROWS + wave * RPW + team;
-    const int nn = min(n, a.N - 1);
-    // weight matrix and row of output n (q/k/v: D % 8 == 0 keeps a row pair in one matrix)
-    const int which = E == E_QKV ? nn / a.D : 0;
-    const int nrow = E == E_QKV ? nn % a.D : nn;
-    const uint16_t* Wm = E == E_QKV ? (which == 0 ? a.w3[0] : which == 1 ? a.w3[1] : a.w3[2]) : a.w;
-    const uint16_t* Bv = E == E_QKV ? (which == 0 ? a.b3[0] : which == 1 ? a.b3[1] : a.b3[2]) : a.bias;
-    // weight loads first (lanes past the row's end reload its last chunk and
-    // zero it below), then the epilogue's operands, then the rows
-    uint4 wr[NCH];
-    const uint16_t* wrow = Wm + (size_t)nrow * K;
-#pragma unroll
-    for (int j = 0; j < NCH; j++) wr[j] = ldg4(wrow + 8 * min(tl + TEAM * j, NCk - 1));
-    const EpiIn ep = epi_load<E>(a, nn, nrow, which, tl, Bv);
-    stage_rows<MODE, RC, XCH, T>(a, xs, red, t);
-    __syncthreads();
-    // dot products of this team's row with the RC staged row slots: no
-    // branches, so all LDS reads issue ahead of the dot chains
+// Dot products of a team's weight chunks (chunk tl + TEAM j of its row;
+// chunks past the row's end are zeroed here) with the RC row slots staged in
+// LDS: each lane's products in chunk order by v_dot2c, then the team's DPP
+// tree, so every lane of the team holds acc[r].  No branches, so all LDS
+// reads issue ahead of the dot chains.
+template <int NCH, int RC, int TEAM>
+__device__ __forceinline__ void gemv_dots(uint4 (&wr)[NCH], const uint32_t* xs, int tl, int K, float (&acc)[RC]) {
+    const int NCk = K / 8, K2 = K / 2;
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
         const uint32_t m = tl + TEAM * j < NCk ? 0xffffffffu : 0u;
@@ -307,7 +300,6 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
         wr[j].w &= m;
     }
     const lds_u32x4_t* xv4 = reinterpret_cast<const lds_u32x4_t*>(xs);
-    float acc[RC];
 #pragma unroll
     for (int r = 0; r < RC; r++) acc[r] = 0.0f;
     // up to 6 row slots, chunk j + 1's row reads are issued before chunk j's
@@ -338,6 +330,39 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
     }
 #pragma unroll
     for (int r = 0; r < RC; r++) acc[r] = team_sum<TEAM>(acc[r]);
+}
+
+// ---- the GEMV kernel ----------------------------------------------------------------
+
+// W waves, RPW output rows per wave (a team of 64 / RPW lanes per row), NCH
+// 16-byte weight chunks per lane, RC row slots.
+template <int E, int MODE, int NCH, int W, int RC, int RPW>
+__global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
+    constexpr int T = 64 * W, TEAM = kWave / RPW, ROWS = RPW * W, XCH = (NCH * TEAM + T - 1) / T;
+    static_assert((E != E_QKV && E != E_STOP && E != E_CFMF) || RPW == 2, "per-row lanes live in a half wave");
+    extern __shared__ uint32_t xs[];  // [R][K/2] bf16 pairs, natural order
+    __shared__ float red[W * kMaxSlots];
+    static_assert(RC <= kMaxSlots, "row slots");
+    const int t = threadIdx.x, wave = t / kWave, lane = t % kWave, team = lane / TEAM, tl = lane % TEAM;
+    const int K = a.K, R = a.R, NCk = K / 8, K2 = K / 2;
+    const int n = blockIdx.x * ROWS + wave * RPW + team;
+    const int nn = min(n, a.N - 1);
+    // weight matrix and row of output n (q/k/v: D % 8 == 0 keeps a row pair in one matrix)
+    const int which = E == E_QKV ? nn / a.D : 0;
+    const int nrow = E == E_QKV ? nn % a.D : nn;
+    const uint16_t* Wm = E == E_QKV ? (which == 0 ? a.w3[0] : which == 1 ? a.w3[1] : a.w3[2]) : a.w;
+    const uint16_t* Bv = E == E_QKV ? (which == 0 ? a.b3[0] : which == 1 ? a.b3[1] : a.b3[2]) : a.bias;
+    // weight loads first (lanes past the row's end reload its last chunk and
+    // zero it below), then the epilogue's operands, then the rows
+    uint4 wr[NCH];
+    const uint16_t* wrow = Wm + (size_t)nrow * K;
+#pragma unroll
+    for (int j = 0; j < NCH; j++) wr[j] = ldg4(wrow + 8 * min(tl + TEAM * j, NCk - 1));
+    const EpiIn ep = epi_load<E>(a, nn, nrow, which, tl, Bv);
+    stage_rows<MODE, RC, XCH, T>(a, xs, red, t);
+    __syncthreads();
+    float acc[RC];
+    gemv_dots<NCH, RC, TEAM>(wr, xs, tl, K, acc);
     // epilogue: lane tl = r of each team handles row r
     float v = 0.0f;
 #pragma unroll
@@ -392,6 +417,8 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
         if (blockIdx.x != 0 || wave != 0 || lane != 0) return;
         const float m = fmaxf(x, x1), e0 = exp_rep(x - m), e1 = exp_rep(x1 - m);
         gst(a.p_out, e1 / (e0 + e1));
+        if (a.flags_in)
+            for (int i = 0; i < 3; i++) gst(reinterpret_cast<int32_t*>(a.p_out) + 1 + i, gld(a.flags_in + i));
         return;
     }
     if (r >= R || n >= a.N) return;
@@ -433,10 +460,39 @@ __global__ __launch_bounds__(256) void adaln_cond_kernel(const uint16_t* te, con
     gst(out + i, f2bf(v * sg));
 }
 
+// Attention of one (sequence, head) over its L positions on the wave, lane d
+// holding dimension d of q, k and v (lanes past head_dim: on = false, adding
+// zeros): scores sum_d (q/8) k in f32 (wave sums), p = exp(s - max),
+// l = sum p, o[i] = (sum_j p_j v_j) / l, to be rounded once by the caller.
+__device__ __forceinline__ void attn_math(const float (&qv)[kMaxL], const float (&kv)[kMaxL],
+                                          const float (&vv)[kMaxL], int L, bool on, float (&o)[kMaxL]) {
+    const float scale = 1.0f / 8.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxL; i++)
+        if (i < L) {
+            const float qd = on ? scale * qv[i] : 0.0f;
+            float sc[kMaxL], m = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < kMaxL; j++)
+                if (j < L) {
+                    sc[j] = team_sum<kWave>(qd * kv[j]);
+                    m = fmaxf(m, sc[j]);
+                }
+            float l = 0.0f, acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kMaxL; j++)
+                if (j < L) {
+                    const float p = exp_rep(sc[j] - m);
+                    l += p;
+                    acc += p * vv[j];
+                }
+            o[i] = acc / l;
+        }
+}
+
 // Attention over the L positions of each sequence, one wave per (sequence,
-// head), lane d owning dimension d (lanes past head_dim add zeros): every
-// q/k/v load is issued first; scores sum_d (q/8) k in f32 (wave sums),
-// p = exp(s - max), l = sum p, o = (sum_j p_j v_j) / l rounded once.
+// head), lane d owning dimension d: every q/k/v load is issued first, then
+// attn_math, each output rounded once.
 __global__ __launch_bounds__(kWave) void dit_attn_kernel(const uint16_t* qkv, int R, int L, int D, int heads,
                                                          int hd, uint16_t* att) {
     const int b = blockIdx.x / heads, h = blockIdx.x % heads, d = threadIdx.x, dd = min(d, hd - 1);
@@ -452,28 +508,11 @@ __global__ __launch_bounds__(kWave) void dit_attn_kernel(const uint16_t* qkv, in
             kv[i] = bf2f(gld(k + (size_t)i * D));
             vv[i] = bf2f(gld(v + (size_t)i * D));
         }
-    const float scale = 1.0f / 8.0f;
+    float o[kMaxL];
+    attn_math(qv, kv, vv, L, on, o);
 #pragma unroll
     for (int i = 0; i < kMaxL; i++)
-        if (i < L) {
-            const float qd = on ? scale * qv[i] : 0.0f;
-            float sc[kMaxL], m = -INFINITY;
-#pragma unroll
-            for (int j = 0; j < kMaxL; j++)
-                if (j < L) {
-                    sc[j] = team_sum<kWave>(qd * kv[j]);
-                    m = fmaxf(m, sc[j]);
-                }
-            float l = 0.0f, o = 0.0f;
-#pragma unroll
-            for (int j = 0; j < kMaxL; j++)
-                if (j < L) {
-                    const float p = exp_rep(sc[j] - m);
-                    l += p;
-                    o += p * vv[j];
-                }
-            if (on) gst(att + (size_t)(b * L + i) * D + h * hd + d, f2bf(o / l));
-        }
+        if (i < L && on) gst(att + (size_t)(b * L + i) * D + h * hd + d, f2bf(o[i]));
 }
 
 template <int E, int MODE, int W, int RC, int RPW>
@@ -529,7 +568,7 @@ hipError_t launch_gemv(hipStream_t st, const DitGemv& a) {
     return (a.N + 7) / 8 >= 256 ? launch_w<E, MODE, 4>(st, a) : launch_w<E, MODE, 2>(st, a);
 }
 
-DitGemv gemv_args(const uint16_t* x, int R, const uint16_t* w, int N, int K, const uint16_t* bias, uint16_t* out) {
+__host__ __device__ DitGemv gemv_args(const uint16_t* x, int R, const uint16_t* w, int N, int K, const uint16_t* bias, uint16_t* out) {
     DitGemv a{};
     a.x = x;
     a.xrow0 = 0;
@@ -543,6 +582,108 @@ DitGemv gemv_args(const uint16_t* x, int R, const uint16_t* w, int N, int K, con
     a.ostride = N;
     a.eps = 1e-6f;
     return a;
+}
+
+// ---- attention + out_proj in one launch (one sequence of two rows) ------------------
+// The aggregator's blocks (one sequence, L = 2) run stage B without the
+// attention launch before it: each out_proj workgroup of four waves computes
+// the attention of every head itself (heads wave, wave + 4, ...: attn_math,
+// the attention kernel's arithmetic, rounded once, so the same bits) into
+// its staged rows, then the E_RES stage as dit_gemv_kernel computes it (rows
+// of 32 lanes, chunk split and dot order by K alone: plain staged rows make
+// the bits independent of the workgroup's width).  Eight launches fewer per
+// aggregate; a workgroup's attention work (16 heads x 2 rows) is a few
+// hundred cycles.
+constexpr int kAoW = 4;  // waves per workgroup
+
+template <int NCH>
+__global__ __launch_bounds__(64 * kAoW) void dit_attn_out_kernel(DitGemv a) {
+    constexpr int RPW = 2, TEAM = kWave / RPW, ROWS = RPW * kAoW, RC = 2;
+    extern __shared__ uint32_t xs[];  // [2][D/2] the attention rows
+    const int t = threadIdx.x, wave = t / kWave, lane = t % kWave, team = lane / TEAM, tl = lane % TEAM;
+    const int D = a.K, NCk = D / 8, hd = a.hd, heads = D / hd;
+    const int n = blockIdx.x * ROWS + wave * RPW + team, nn = min(n, a.N - 1);
+    uint4 wr[NCH];
+    const uint16_t* wrow = a.w + (size_t)nn * D;
+#pragma unroll
+    for (int j = 0; j < NCH; j++) wr[j] = ldg4(wrow + 8 * min(tl + TEAM * j, NCk - 1));
+    const EpiIn ep = epi_load<E_RES>(a, nn, nn, 0, tl, a.bias);
+    // q, k, v of rows 0 and 1 at a.x = qkv [3][2][D]; waves past the last head repeat it (not stored)
+    const int d = lane, dd = min(d, hd - 1);
+    float o[kMaxH][kMaxL];
+#pragma unroll
+    for (int k = 0; k < kMaxH; k++) {
+        const int h = min(wave + kAoW * k, heads - 1);
+        float qv[kMaxL], kv[kMaxL], vv[kMaxL];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint16_t* p = a.x + (size_t)i * D + h * hd + dd;
+            qv[i] = bf2f(gld(p));
+            kv[i] = bf2f(gld(p + (size_t)2 * D));
+            vv[i] = bf2f(gld(p + (size_t)4 * D));
+        }
+        attn_math(qv, kv, vv, 2, d < hd, o[k]);
+    }
+    uint16_t* xh = reinterpret_cast<uint16_t*>(xs);
+#pragma unroll
+    for (int k = 0; k < kMaxH; k++) {
+        const int h = wave + kAoW * k;
+        if (h < heads && d < hd)
+#pragma unroll
+            for (int i = 0; i < 2; i++) xh[i * D + h * hd + d] = f2bf(o[k][i]);
+    }
+    __syncthreads();
+    float acc[RC];
+    gemv_dots<NCH, RC, TEAM>(wr, xs, tl, D, acc);
+    float v = 0.0f;
+#pragma unroll
+    for (int r = 0; r < RC; r++)
+        if (tl == r) v = acc[r];
+    const int r = tl;
+    if (r >= 2 || n >= a.N) return;
+    gst(a.out + r * a.ostride + n, f2bf(ep.res + rb(v + ep.b)));
+}
+
+// Stage A's GEMV: rms1 + q/k/v + bias + rotary of R rows (sequences of L) -> qkv [3][R][D].
+hipError_t launch_dit_qkv(hipStream_t st, const DitBlockDev& w, const uint16_t* x, int R, int L, const float* cos_t,
+                          const float* sin_t, uint16_t* qkv) {
+    const int D = w.D;
+    DitGemv a = gemv_args(x, R, nullptr, 3 * D, D, nullptr, qkv);
+    a.w3[0] = w.wq;
+    a.w3[1] = w.wk;
+    a.w3[2] = w.wv;
+    a.b3[0] = w.bq;
+    a.b3[1] = w.bk;
+    a.b3[2] = w.bv;
+    a.norm = w.norm1;
+    a.eps = w.eps;
+    a.cos_t = cos_t;
+    a.sin_t = sin_t;
+    a.L = L;
+    a.D = D;
+    a.hd = w.hd;
+    return launch_gemv<E_QKV, M_NORM>(st, a);
+}
+
+// Attention + out_proj + residual of one sequence of two rows (dit_attn_out_kernel), where its
+// shape allows: hidden <= 1024 in chunks of 8, at most 16 heads of at most 64.
+bool attn_out_fits(const DitBlockDev& w) {
+    return w.D <= 1024 && w.D % 8 == 0 && w.hd >= 1 && w.hd <= kWave && w.D % w.hd == 0 && w.D / w.hd <= kAoW * kMaxH;
+}
+
+hipError_t launch_attn_out(hipStream_t st, const DitBlockDev& w, const uint16_t* qkv, const uint16_t* x,
+                           uint16_t* out) {
+    const int D = w.D;
+    DitGemv a = gemv_args(qkv, 2, w.wo, D, D, w.bo, out);
+    a.res = x;
+    a.hd = w.hd;
+    const int grid = (D + 2 * kAoW - 1) / (2 * kAoW);
+    const size_t lds = sizeof(uint32_t) * (size_t)D;  // two rows of D bf16
+    if (D <= 8 * (kWave / 2))
+        hipLaunchKernelGGL(dit_attn_out_kernel<1>, dim3(grid), dim3(64 * kAoW), lds, st, a);
+    else
+        hipLaunchKernelGGL(dit_attn_out_kernel<4>, dim3(grid), dim3(64 * kAoW), lds, st, a);
+    return hipGetLastError();
 }
 
 }  // namespace
@@ -560,21 +701,7 @@ hipError_t launch_dit_stage(hipStream_t st, int which, const DitBlockDev& w, con
     DitGemv a;
     switch (which) {
         case 0: {
-            a = gemv_args(x, R, nullptr, 3 * D, D, nullptr, qkv);
-            a.w3[0] = w.wq;
-            a.w3[1] = w.wk;
-            a.w3[2] = w.wv;
-            a.b3[0] = w.bq;
-            a.b3[1] = w.bk;
-            a.b3[2] = w.bv;
-            a.norm = w.norm1;
-            a.eps = w.eps;
-            a.cos_t = cos_t;
-            a.sin_t = sin_t;
-            a.L = L;
-            a.D = D;
-            a.hd = w.hd;
-            hipError_t e = launch_gemv<E_QKV, M_NORM>(st, a);
+            hipError_t e = launch_dit_qkv(st, w, x, R, L, cos_t, sin_t, qkv);
             if (e != hipSuccess) return e;
             hipLaunchKernelGGL(dit_attn_kernel, dim3(B * w.heads), dim3(kWave), 0, st, qkv, R, L, D, w.heads, w.hd,
                                out);
@@ -603,13 +730,20 @@ hipError_t launch_dit_attn(hipStream_t st, const uint16_t* qkv, int B, int L, in
     return hipGetLastError();
 }
 
-// One DiT block: the four stages in order.
+// One DiT block: the four stages in order.  fuse_attn: for one sequence of
+// two rows, attention and out_proj in one launch where the shape allows
+// (dit_attn_out_kernel: the same bits; att is then not written).
 hipError_t launch_dit_block(hipStream_t st, const DitBlockDev& w, const uint16_t* x, int B, int L,
                             const float* cos_t, const float* sin_t, uint16_t* qkv, uint16_t* att, uint16_t* x1,
-                            uint16_t* hh, uint16_t* x2) {
+                            uint16_t* hh, uint16_t* x2, bool fuse_attn) {
     hipError_t e;
-    if ((e = launch_dit_stage(st, 0, w, x, nullptr, B, L, cos_t, sin_t, qkv, att)) != hipSuccess) return e;
-    if ((e = launch_dit_stage(st, 1, w, x, att, B, L, cos_t, sin_t, qkv, x1)) != hipSuccess) return e;
+    if (fuse_attn && B == 1 && L == 2 && attn_out_fits(w)) {
+        if ((e = launch_dit_qkv(st, w, x, 2, 2, cos_t, sin_t, qkv)) != hipSuccess) return e;
+        if ((e = launch_attn_out(st, w, qkv, x, x1)) != hipSuccess) return e;
+    } else {
+        if ((e = launch_dit_stage(st, 0, w, x, nullptr, B, L, cos_t, sin_t, qkv, att)) != hipSuccess) return e;
+        if ((e = launch_dit_stage(st, 1, w, x, att, B, L, cos_t, sin_t, qkv, x1)) != hipSuccess) return e;
+    }
     if ((e = launch_dit_stage(st, 2, w, x1, nullptr, B, L, cos_t, sin_t, qkv, hh)) != hipSuccess) return e;
     return launch_dit_stage(st, 3, w, x1, hh, B, L, cos_t, sin_t, qkv, x2);
 }
@@ -779,9 +913,11 @@ hipError_t launch_adaln_final(hipStream_t st, const uint16_t* h, int F, int D, c
 }
 
 // stopProb: p = softmax(f32(bf16(W z + b)))[1] (W [2][K]).
-hipError_t launch_stop_prob(hipStream_t st, const uint16_t* z, const uint16_t* w, const uint16_t* b, int K, float* p) {
+hipError_t launch_stop_prob(hipStream_t st, const uint16_t* z, const uint16_t* w, const uint16_t* b, int K, float* p,
+                            const int32_t* flags_in) {
     DitGemv a = gemv_args(z, 1, w, 2, K, b, nullptr);
     a.p_out = p;
+    a.flags_in = flags_in;
     return launch_gemv<E_STOP, M_PLAIN>(st, a);
 }
 

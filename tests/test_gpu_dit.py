@@ -340,6 +340,32 @@ def test_aggregate(ming, ctx, flow, flow_oracle, flow_oracle_dev):
     m.close()
 
 
+def test_aggregate_fused_attention_matches_unfused(ming, ctx, flow):
+    """The aggregator's blocks (one sequence of two rows) run attention and out_proj as one launch;
+    every block's output rows equal the unfused launches' (ming_dit_block: q/k/v, attention,
+    out_proj, ff1, ff2) bit for bit on the same input rows, over consecutive calls."""
+    spec = flow.spec
+    D, F, nb = spec.hidden, spec.ff, spec.agg_blocks
+    m = flow.agg_model()
+    cos, sin = rotary_dev(ctx, spec, 2)
+    rows = bf16_empty(nb + 1, 2, D)
+    out_t, out_a = bf16_empty(spec.lm_hidden), bf16_empty(spec.lm_hidden)
+    buf = dict(qkv=bf16_empty(3, 2, D), att=bf16_empty(2, D), x1=bf16_empty(2, D), hh=bf16_empty(2, F),
+               x2=bf16_empty(2, D))
+    o = ming.DitOut(*(buf[k].data_ptr() for k in ("qkv", "att", "x1", "hh", "x2")))
+    for seed in (71, 72, 73):
+        latent = dev_u16(ming.synth_normal_bf16(seed, "agg.latent", spec.latent))
+        m.aggregate_trace(latent, rows, out_t)
+        m.aggregate(latent, out_a)
+        ctx.sync()
+        assert_bits(host_u16(out_a), host_u16(out_t), f"aggregate vs its trace, seed {seed}")
+        for b in range(nb):
+            ctx.dit_block(spec.cfg(), flow.agg_blocks[b], rows[b], 1, 2, cos, sin, o)
+            ctx.sync()
+            assert_bits(host_u16(buf["x2"]), host_u16(rows[b + 1]), f"block {b} output, seed {seed}")
+    m.close()
+
+
 def test_stop_prob(ming, ctx, flow):
     H = flow.spec.lm_hidden
     head = olin(flow, "stop_head")
