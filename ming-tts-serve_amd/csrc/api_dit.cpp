@@ -30,6 +30,9 @@ hipError_t launch_cfm_final(hipStream_t st, const uint16_t* h, int L, int D, con
                             uint16_t* y_out);
 hipError_t launch_stop_prob(hipStream_t st, const uint16_t* z, const uint16_t* w, const uint16_t* b, int K, float* p,
                             const int32_t* flags_in);
+bool launch_cfm_pre(hipStream_t st, const uint16_t* z, int H, const uint16_t* wc, const uint16_t* bc, int D,
+                    uint16_t* ce, const uint16_t* hist, int lat, const uint16_t* wx, const uint16_t* bx, uint16_t* xh,
+                    const uint16_t* ws, const uint16_t* bs, float* p_out, const int32_t* flags_in, hipError_t* err);
 hipError_t launch_cfm_persistent(hipStream_t st, const CfmPArgs& a, int grid, bool cooperative);
 int cfmp_grid(int num_cus);
 hipError_t launch_adaln_block(hipStream_t st, const DitBlockDev& w, const uint16_t* mod, const uint16_t* x, int B,
@@ -532,6 +535,15 @@ int ming_cfm_model_tables(ming_cfm_model* m, uint16_t* t, uint16_t* dt, uint16_t
 
 int ming_cfm_sample(ming_ctx* ctx, ming_cfm_model* m, const void* z, const void* hist, const void* noise,
                     const void* sde, float cfg, float sigma, float temperature, void* latent_out, void* y_steps) {
+    return ming::cfm_sample_impl(ctx, m, z, hist, noise, sde, cfg, sigma, temperature, latent_out, y_steps, false);
+}
+
+}  // extern "C"
+
+// cfmSample; pre_done: c_emb(z) and x_emb(hist) are already in the model's rows (cfm_pre).
+int ming::cfm_sample_impl(ming_ctx* ctx, ming_cfm_model* m, const void* z, const void* hist, const void* noise,
+                          const void* sde, float cfg, float sigma, float temperature, void* latent_out, void* y_steps,
+                          bool pre_done) {
     if (!alive(ctx)) return MING_E_NOT_INIT;
     if (!m) return set_err(ctx, MING_E_NOT_INIT, "cfm_sample: null model");
     const float shift = sigma * std::sqrt(temperature);
@@ -544,14 +556,17 @@ int ming_cfm_sample(ming_ctx* ctx, ming_cfm_model* m, const void* z, const void*
     // row, is computed at creation; row 0 reads z in place when it is 16-byte aligned (a row's
     // result does not depend on how many rows a launch takes).
     hipError_t e = hipSuccess;
-    const uint16_t* zin = u16(z);
-    if (reinterpret_cast<uintptr_t>(z) % 16 != 0) {
-        e = hipMemcpyAsync(m->zc.p, z, sizeof(uint16_t) * H, hipMemcpyDeviceToDevice, s);
-        zin = u16(m->zc.p);
+    if (!pre_done) {
+        const uint16_t* zin = u16(z);
+        if (reinterpret_cast<uintptr_t>(z) % 16 != 0) {
+            e = hipMemcpyAsync(m->zc.p, z, sizeof(uint16_t) * H, hipMemcpyDeviceToDevice, s);
+            zin = u16(m->zc.p);
+        }
+        if (e == hipSuccess)
+            e = launch_dit_linear(s, zin, 0, 1, 1, nullptr, eps, m->wc, D, H, m->bc, u16(m->ce.p), false);
+        if (e == hipSuccess)
+            e = launch_dit_linear(s, u16(hist), 0, 1, 1, nullptr, eps, m->wx, D, lat, m->bx, u16(m->xh.p), false);
     }
-    if (e == hipSuccess) e = launch_dit_linear(s, zin, 0, 1, 1, nullptr, eps, m->wc, D, H, m->bc, u16(m->ce.p), false);
-    if (e == hipSuccess)
-        e = launch_dit_linear(s, u16(hist), 0, 1, 1, nullptr, eps, m->wx, D, lat, m->bx, u16(m->xh.p), false);
     // AUTO takes the persistent kernel wherever its shape fits: 1.51 ms per sample against the
     // launch path's 1.92 ms at hidden 1024, 8 blocks
     if (e == hipSuccess && (m->mode == MING_CFM_PERSISTENT || m->mode == MING_CFM_AUTO) && m->pgrid > 0) {
@@ -621,6 +636,37 @@ int ming_cfm_sample(ming_ctx* ctx, ming_cfm_model* m, const void* z, const void*
         e = hipMemcpyAsync(latent_out, m->y.p, sizeof(uint16_t) * lat, hipMemcpyDeviceToDevice, s);
     return hip_check(ctx, e, "cfm_sample");
 }
+
+// The step's one-row GEMVs before a flow-head sample: c_emb(z) and x_emb(hist)
+// into the model's rows (for cfm_sample_impl with pre_done) and the stop head
+// on z into p_out[0] with the error flags in p_out[1..3] -- one launch where
+// the shapes allow it, else three.
+int ming::cfm_pre(ming_ctx* ctx, ming_cfm_model* m, const void* z, const void* hist, const ming_linear* stop_head,
+                  const void* stop_bias, float* p_out) {
+    if (!alive(ctx)) return MING_E_NOT_INIT;
+    if (!m || !z || !hist || !stop_head || !stop_bias || !p_out) return set_err(ctx, MING_E_ARG, "cfm_pre: null argument");
+    int st;
+    if ((st = check_bf16(ctx, *stop_head, 2, m->lm_hidden, "stop_head"))) return st;
+    hipStream_t s = ctx->stream;
+    const int D = m->cfg.hidden, H = m->lm_hidden, lat = m->latent;
+    hipError_t e = hipSuccess;
+    if (launch_cfm_pre(s, u16(z), H, m->wc, m->bc, D, u16(m->ce.p), u16(hist), lat, m->wx, m->bx, u16(m->xh.p),
+                       u16(stop_head->w), u16(stop_bias), p_out, ctx->dev_flags, &e))
+        return hip_check(ctx, e, "cfm_pre launch");
+    if ((st = stop_prob_impl(ctx, stop_head, stop_bias, z, p_out, true))) return st;
+    const uint16_t* zin = u16(z);
+    if (reinterpret_cast<uintptr_t>(z) % 16 != 0) {
+        e = hipMemcpyAsync(m->zc.p, z, sizeof(uint16_t) * H, hipMemcpyDeviceToDevice, s);
+        zin = u16(m->zc.p);
+    }
+    if (e == hipSuccess)
+        e = launch_dit_linear(s, zin, 0, 1, 1, nullptr, m->cfg.eps, m->wc, D, H, m->bc, u16(m->ce.p), false);
+    if (e == hipSuccess)
+        e = launch_dit_linear(s, u16(hist), 0, 1, 1, nullptr, m->cfg.eps, m->wx, D, lat, m->bx, u16(m->xh.p), false);
+    return hip_check(ctx, e, "cfm_pre launches");
+}
+
+extern "C" {
 
 // cfmSample of n sequences in one pass (the flow head of a batched server
 // step): the rows of every sequence go through each DiT linear as one GEMM.

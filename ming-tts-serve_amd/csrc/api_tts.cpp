@@ -34,12 +34,12 @@ struct StopSlot {
 // return can leave queued work that still reads it).
 struct LoopBufs {
     hipStream_t s = nullptr;
-    DevBuf z, xrow, hist, stop;
-    StopSlot* host_stop = nullptr;  // pinned [2]
+    DevBuf z, xrow, hist;
+    StopSlot* host_stop = nullptr;  // pinned [2], written by the stop launch
     hipEvent_t ev[2] = {nullptr, nullptr};
     ~LoopBufs() {
         if (s) (void)hipStreamSynchronize(s);
-        for (DevBuf* b : {&z, &xrow, &hist, &stop}) b->release();
+        for (DevBuf* b : {&z, &xrow, &hist}) b->release();
         if (host_stop) (void)hipHostFree(host_stop);
         for (hipEvent_t& e : ev)
             if (e) (void)hipEventDestroy(e);
@@ -155,15 +155,16 @@ int ming_sample_latents(ming_ctx* ctx, ming_lm_model* lm, ming_cfm_model* cfm, m
     hipError_t e = b.z.ensure(sizeof(uint16_t) * H);
     if (e == hipSuccess) e = b.xrow.ensure(sizeof(uint16_t) * H);
     if (e == hipSuccess) e = b.hist.ensure(sizeof(uint16_t) * lat);
-    if (e == hipSuccess) e = b.stop.ensure(sizeof(StopSlot) * 2);
-    if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&b.host_stop), sizeof(StopSlot) * 2);
+    // coherent pinned memory: the stop launch stores into it directly
+    if (e == hipSuccess)
+        e = hipHostMalloc(reinterpret_cast<void**>(&b.host_stop), sizeof(StopSlot) * 2,
+                          hipHostMallocMapped | hipHostMallocCoherent);
     for (hipEvent_t& ev : b.ev)
         if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
     if ((st = hip_check(ctx, e, "sample_latents workspace"))) return st;
     uint16_t* z = static_cast<uint16_t*>(b.z.p);
     // the aggregator writes the LM step's input row in place
     uint16_t* xrow = lm_input_row(lm) ? lm_input_row(lm) : static_cast<uint16_t*>(b.xrow.p);
-    float* stop_dev = static_cast<float*>(b.stop.p);
     const uint16_t* emb = static_cast<const uint16_t*>(embeds);
     uint16_t* lats = static_cast<uint16_t*>(latents_out);
     const uint16_t* bank = static_cast<const uint16_t*>(noise_bank);
@@ -184,17 +185,16 @@ int ming_sample_latents(ming_ctx* ctx, ming_lm_model* lm, ming_cfm_model* cfm, m
                       : hipMemsetAsync(b.hist.p, 0, sizeof(uint16_t) * lat, s);
     if ((st = hip_check(ctx, e, "sample_latents history"))) return st;
     const uint16_t* hist = static_cast<const uint16_t*>(b.hist.p);
-    // stop_k and the error flags (written beside it by the stop launch) on their way to the host
-    // into slot k & 1, in one copy
-    auto send_stop = [&](int slot) {
-        hipError_t r = hipMemcpyAsync(&b.host_stop[slot], stop_dev + 4 * slot, sizeof(StopSlot), hipMemcpyDeviceToHost,
-                                      s);
-        if (r == hipSuccess) r = hipEventRecord(b.ev[slot], s);
-        return hip_check(ctx, r, "sample_latents stop copy");
-    };
+    // Before each flow-head sample, one launch (cfm_pre) runs its c_emb(z) and x_emb(hist) and the
+    // stop head on z, whose probability and the error flags land directly in the pinned host slot
+    // k & 1; an event after it tells the host when they are there.
     static_assert(sizeof(StopSlot) == 4 * sizeof(float), "p and three flags");
-    if ((st = stop_prob_impl(ctx, stop_head, stop_bias, z, stop_dev, true))) return st;
-    if ((st = send_stop(0))) return st;
+    auto pre = [&](int slot, const uint16_t* h) {
+        int r = cfm_pre(ctx, cfm, z, h, stop_head, stop_bias, reinterpret_cast<float*>(&b.host_stop[slot]));
+        if (r) return r;
+        return hip_check(ctx, hipEventRecord(b.ev[slot], s), "sample_latents stop event");
+    };
+    if ((st = pre(0, hist))) return st;
     int n = 0;
     for (int k = 0; k < steps; k++) {
         if (z_trace && (st = hip_check(ctx,
@@ -204,16 +204,14 @@ int ming_sample_latents(ming_ctx* ctx, ming_lm_model* lm, ming_cfm_model* cfm, m
             return st;
         const uint16_t* noise = bank + (size_t)k * (kFlowSteps + 1) * lat;
         uint16_t* latent = lats + (size_t)k * lat;
-        if ((st = ming_cfm_sample(ctx, cfm, z, hist, noise, noise + lat, p->cfg, p->sigma, p->temperature, latent,
-                                  nullptr)))
+        if ((st = cfm_sample_impl(ctx, cfm, z, hist, noise, noise + lat, p->cfg, p->sigma, p->temperature, latent,
+                                  nullptr, true)))
             return st;
         const int nxt = (k + 1) & 1;
         if (k + 1 < steps) {  // the next position, queued before the host reads stop_k
             if ((st = ming_aggregate(ctx, agg, latent, xrow)) ||
-                (st = ming_lm_step(ctx, lm, nullptr, xrow, kv, z, nullptr, nullptr)) ||
-                (st = stop_prob_impl(ctx, stop_head, stop_bias, z, stop_dev + 4 * nxt, true)))
+                (st = ming_lm_step(ctx, lm, nullptr, xrow, kv, z, nullptr, nullptr)) || (st = pre(nxt, latent)))
                 return st;
-            if ((st = send_stop(nxt))) return st;
         }
         if ((st = hip_check(ctx, hipEventSynchronize(b.ev[k & 1]), "sample_latents stop wait"))) return st;
         const StopSlot& slot = b.host_stop[k & 1];

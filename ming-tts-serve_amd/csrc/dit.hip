@@ -336,16 +336,16 @@ __device__ __forceinline__ void gemv_dots(uint4 (&wr)[NCH], const uint32_t* xs, 
 
 // W waves, RPW output rows per wave (a team of 64 / RPW lanes per row), NCH
 // 16-byte weight chunks per lane, RC row slots.
+// (workgroup vb of the launch; xs the staged rows [R][K/2] as bf16 pairs in
+// natural order, red W * kMaxSlots floats)
 template <int E, int MODE, int NCH, int W, int RC, int RPW>
-__global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
+__device__ __forceinline__ void gemv_body(const DitGemv& a, int vb, uint32_t* xs, float* red) {
     constexpr int T = 64 * W, TEAM = kWave / RPW, ROWS = RPW * W, XCH = (NCH * TEAM + T - 1) / T;
     static_assert((E != E_QKV && E != E_STOP && E != E_CFMF) || RPW == 2, "per-row lanes live in a half wave");
-    extern __shared__ uint32_t xs[];  // [R][K/2] bf16 pairs, natural order
-    __shared__ float red[W * kMaxSlots];
     static_assert(RC <= kMaxSlots, "row slots");
     const int t = threadIdx.x, wave = t / kWave, lane = t % kWave, team = lane / TEAM, tl = lane % TEAM;
     const int K = a.K, R = a.R, NCk = K / 8, K2 = K / 2;
-    const int n = blockIdx.x * ROWS + wave * RPW + team;
+    const int n = vb * ROWS + wave * RPW + team;
     const int nn = min(n, a.N - 1);
     // weight matrix and row of output n (q/k/v: D % 8 == 0 keeps a row pair in one matrix)
     const int which = E == E_QKV ? nn / a.D : 0;
@@ -414,7 +414,7 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
         // lane 0 holds logit 0 (bias 0), lane 32 logit 1 (bias 1)
         const float x = rb(v + ep.b);
         const float x1 = lane_xor32(x, lane);
-        if (blockIdx.x != 0 || wave != 0 || lane != 0) return;
+        if (vb != 0 || wave != 0 || lane != 0) return;
         const float m = fmaxf(x, x1), e0 = exp_rep(x - m), e1 = exp_rep(x1 - m);
         gst(a.p_out, e1 / (e0 + e1));
         if (a.flags_in)
@@ -447,6 +447,31 @@ __global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
         gst(a.out + (size_t)4 * a.N + n, ep.xh);
         gst(a.out + (size_t)5 * a.N + n, xe);
     }
+}
+
+template <int E, int MODE, int NCH, int W, int RC, int RPW>
+__global__ __launch_bounds__(64 * W) void dit_gemv_kernel(DitGemv a) {
+    extern __shared__ uint32_t xs[];
+    __shared__ float red[W * kMaxSlots];
+    gemv_body<E, MODE, NCH, W, RC, RPW>(a, blockIdx.x, xs, red);
+}
+
+// The three one-row GEMVs that sit between an LM step and the next flow-head
+// sample, in one launch: c_emb(z) (row 0 of the flow head's c_emb rows;
+// workgroups [0, nc)), x_emb(hist) ([nc, nc + nx)) and the stop head on z
+// (the last workgroup) -- each workgroup runs the body that its own launch
+// would (two waves, rows of 32 lanes, chunks by K), so the same bits.
+template <int NCHC, int NCHX>
+__global__ __launch_bounds__(128) void dit_pre_kernel(DitGemv c, DitGemv x, DitGemv s, int nc, int nx) {
+    extern __shared__ uint32_t xs[];
+    __shared__ float red[2 * kMaxSlots];
+    const int b = blockIdx.x;
+    if (b < nc)
+        gemv_body<E_BIAS, M_PLAIN, NCHC, 2, 1, 2>(c, b, xs, red);
+    else if (b < nc + nx)
+        gemv_body<E_BIAS, M_PLAIN, NCHX, 2, 1, 2>(x, b - nc, xs, red);
+    else
+        gemv_body<E_STOP, M_PLAIN, NCHC, 2, 1, 2>(s, 0, xs, red);
 }
 
 // adaLN conditions of every Euler step and CFG half: out [steps][2][D] =
@@ -919,6 +944,27 @@ hipError_t launch_stop_prob(hipStream_t st, const uint16_t* z, const uint16_t* w
     a.p_out = p;
     a.flags_in = flags_in;
     return launch_gemv<E_STOP, M_PLAIN>(st, a);
+}
+
+// c_emb(z) -> ce row 0, x_emb(hist) -> xh and the stop head on z -> p_out (with the error flags
+// beside it when flags_in is set) as one launch where the shapes allow it (z of 256 < K <= 1024,
+// hist of K <= 256, hidden < 2041, all 16-byte aligned); false: the caller launches them apart.
+bool launch_cfm_pre(hipStream_t st, const uint16_t* z, int H, const uint16_t* wc, const uint16_t* bc, int D,
+                    uint16_t* ce, const uint16_t* hist, int lat, const uint16_t* wx, const uint16_t* bx, uint16_t* xh,
+                    const uint16_t* ws, const uint16_t* bs, float* p_out, const int32_t* flags_in, hipError_t* err) {
+    auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (H <= 256 || H > 1024 || H % 8 || lat < 8 || lat > 256 || lat % 8 || (D + 7) / 8 >= 256 || !al(z) || !al(hist))
+        return false;
+    DitGemv c = gemv_args(z, 1, wc, D, H, bc, ce);
+    DitGemv x = gemv_args(hist, 1, wx, D, lat, bx, xh);
+    DitGemv s = gemv_args(z, 1, ws, 2, H, bs, nullptr);
+    s.p_out = p_out;
+    s.flags_in = flags_in;
+    const int nb = (D + 3) / 4;  // rows of two waves x 2
+    const size_t lds = sizeof(uint32_t) * (size_t)(H / 2);
+    hipLaunchKernelGGL((dit_pre_kernel<4, 1>), dim3(2 * nb + 1), dim3(128), lds, st, c, x, s, nb, nb);
+    *err = hipGetLastError();
+    return true;
 }
 
 hipError_t tanh_upload_dit(const float* host) {

@@ -109,6 +109,11 @@ hipError_t launch_prefill_rows(hipStream_t st, const int32_t* table, int pps, in
 int stop_prob_impl(ming_ctx* ctx, const ming_linear* head, const void* bias, const void* z, float* p_dev,
                    bool with_flags);
 uint16_t* lm_input_row(ming_lm_model* m);
+int cfm_sample_impl(ming_ctx* ctx, ming_cfm_model* m, const void* z, const void* hist, const void* noise,
+                    const void* sde, float cfg, float sigma, float temperature, void* latent_out, void* y_steps,
+                    bool pre_done);
+int cfm_pre(ming_ctx* ctx, ming_cfm_model* m, const void* z, const void* hist, const ming_linear* stop_head,
+            const void* stop_bias, float* p_out);
 hipError_t launch_dit_attn(hipStream_t st, const uint16_t* qkv, int B, int L, int D, int heads, int hd, uint16_t* att);
 hipError_t launch_dit_block_gemm(hipStream_t st, const DitBlockDev& w, const uint16_t* x, int R, int L,
                                  const float* cos_t, const float* sin_t, uint16_t* hn, uint16_t* qkv, uint16_t* att,
