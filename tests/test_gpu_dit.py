@@ -382,6 +382,31 @@ def test_stop_prob(ming, ctx, flow):
         assert 0.0 <= float(p.item()) <= 1.0
 
 
+def test_cfm_sample_unaligned_z(ming, ctx, flow):
+    """c_emb reads z in place when it is 16-byte aligned and copies it first otherwise: a z two
+    bytes off alignment gives the aligned call's latent and Euler steps bit for bit."""
+    spec = flow.spec
+    lat, H = spec.latent, spec.lm_hidden
+    zh = ming.synth_normal_bf16(49, "unaligned.z", H)
+    z = dev_u16(zh)
+    zbuf = torch.zeros(H + 8, dtype=torch.bfloat16, device="cuda")
+    zbuf[1:H + 1].copy_(z)
+    zu = zbuf[1:H + 1]
+    assert zu.data_ptr() % 16 != 0 and z.data_ptr() % 16 == 0
+    hist = dev_u16(ming.synth_normal_bf16(46, "det.hist", lat))
+    noise = dev_u16(ming.synth_normal_bf16(47, "det.noise", lat))
+    sde = dev_u16(ming.synth_normal_bf16(48, "det.sde", 10 * lat).reshape(10, lat))
+    m = flow.cfm_model()
+    steps_a, steps_u = bf16_empty(10, lat), bf16_empty(10, lat)
+    out_a, out_u = bf16_empty(lat), bf16_empty(lat)
+    m.sample(z, hist, noise, sde, 2.0, 0.25, 1.0, out_a, steps_a)
+    m.sample(zu, hist, noise, sde, 2.0, 0.25, 1.0, out_u, steps_u)
+    ctx.sync()
+    assert_bits(host_u16(steps_u), host_u16(steps_a), "Euler steps, unaligned z vs aligned")
+    assert_bits(host_u16(out_u), host_u16(out_a), "latent, unaligned z vs aligned")
+    m.close()
+
+
 def test_cfm_sample_deterministic(ming, ctx, flow):
     """30 repeated samples of the same inputs are bit-identical to the first
     (the reference's flow-head determinism check, src/ming_fused_bench.zig:158-169),
